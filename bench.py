@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""DP-SGD clip + noise throughput on one MI355X.
+
+Workload: Llama-3-8B-shaped LoRA r=16 on q
+(4096->4096), k/v (4096->1024), o (4096->4096), gate/up (4096->14336) and
+down (14336->4096) across 32 layers; batch 16 x seq 1024 bf16 with ragged
+lengths uniform in [256, 1024]; AUTO-S clipping (R = 1, gamma = 0.01),
+normalize_by = batch, Gaussian noise with noise multiplier 1.0.
+
+A step is the DP core with the captured activations a and output
+gradients g already resident in HBM: per-example norms (project + factor
+kernels), clip factors, clipped sum and noise.  Model forward/backward is not
+part of the step.  Prints one JSON line (the driver's contract).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+LAYER_SHAPES = {  # name: (d_in, d_out); q/k/v share an input, gate/up share an input
+    "q": (4096, 4096), "k": (4096, 1024), "v": (4096, 1024), "o": (4096, 4096),
+    "gate": (4096, 14336), "up": (4096, 14336), "down": (14336, 4096),
+}
+SHARED_INPUT = {"q": "qkv", "k": "qkv", "v": "qkv", "o": "o", "gate": "gu", "up": "gu", "down": "down"}
+MI355X_HBM_PEAK_GBS = 8000.0
+MI355X_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--seq", type=int, default=1024)
+    ap.add_argument("--rank", type=int, default=16)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    return ap.parse_args()
+
+
+def build_workload(layers, B, T, r, seed, device):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    lengths = torch.randint(256, T + 1, (B,), generator=g).tolist() if T >= 256 else [T] * B
+    gd = torch.Generator(device=device).manual_seed(seed + 1)
+    N = B * T
+    sites = []
+    mask = torch.zeros(N, 1, dtype=torch.bfloat16, device=device)
+    for i, ln in enumerate(lengths):
+        mask[i * T : i * T + ln] = 1
+    for _ in range(layers):
+        xs = {}
+        for name, (d_in, d_out) in LAYER_SHAPES.items():
+            key = SHARED_INPUT[name]
+            if key not in xs:
+                xs[key] = torch.randn(N, d_in, dtype=torch.bfloat16, device=device, generator=gd)
+            x = xs[key]
+            gt = torch.randn(N, d_out, dtype=torch.bfloat16, device=device, generator=gd) * mask
+            A = (torch.randn(d_in, r, device=device, generator=gd) / math.sqrt(d_in)).to(torch.bfloat16)
+            Bm = (torch.randn(r, d_out, device=device, generator=gd) * 0.02).to(torch.bfloat16)
+            sites.append((name, x, gt, A, Bm))
+    return lengths, sites
+
+
+def algorithmic_bytes(sites, lengths, n_leaf_params):
+    """One read of the unique a and g rows that carry tokens, plus the per-example
+    factor gradients written (fp32) and the bf16 clipped sum; per step."""
+    valid = sum(lengths)
+    seen = set()
+    ab = 0
+    for name, x, gt, A, Bm in sites:
+        if x.data_ptr() not in seen:
+            seen.add(x.data_ptr())
+            ab += valid * x.shape[1] * 2
+        ab += valid * gt.shape[1] * 2
+    return ab
+
+
+def cpu_baseline(r, seed):
+    """The reference algorithm on the host: vmap(grad) per-example LoRA
+    gradients of one Llama layer for a few examples, reference AUTO-S scaling,
+    fp32-accumulated sum and mt19937 inverse-CDF noise (oracle.dp_ref)."""
+    from oracle import dp_ref
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    T, n_ex = 1024, 2
+    g = torch.Generator().manual_seed(seed)
+    params, xs, gs = {}, {}, {}
+    for name, (d_in, d_out) in LAYER_SHAPES.items():
+        params[name + ".A"] = (torch.randn(d_in, r, generator=g) / math.sqrt(d_in)).to(torch.bfloat16)
+        params[name + ".B"] = (torch.randn(r, d_out, generator=g) * 0.02).to(torch.bfloat16)
+    for key, d in (("qkv", 4096), ("o", 4096), ("gu", 4096), ("down", 14336)):
+        xs[key] = torch.randn(n_ex, T, d, generator=g).to(torch.bfloat16)
+    for name, (d_in, d_out) in LAYER_SHAPES.items():
+        gs[name] = torch.randn(n_ex, T, d_out, generator=g).to(torch.bfloat16)
+
+    def loss(p, xq, xo, xg, xd, gq, gk, gv, go, gg, gu, gd):
+        xin = {"q": xq, "k": xq, "v": xq, "o": xo, "gate": xg, "up": xg, "down": xd}
+        gin = {"q": gq, "k": gk, "v": gv, "o": go, "gate": gg, "up": gu, "down": gd}
+        tot = 0.0
+        for name in LAYER_SHAPES:
+            y = 2.0 * (xin[name] @ p[name + ".A"]) @ p[name + ".B"]
+            tot = tot + (y.float() * gin[name].float()).sum()
+        return tot
+
+    batch = (xs["qkv"], xs["o"], xs["gu"], xs["down"], *(gs[n] for n in LAYER_SHAPES))
+
+    def once():
+        res, _ = dp_ref.clipped_grad(loss, params, batch, clipping_norm=1.0, normalize_by=float(n_ex), autos=True)
+        sigma = 1.0 * 1.0 / n_ex
+        dp_ref.gaussian_noise_reference(res, sigma, key=42, step=0)
+
+    once()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    # n_ex examples through 1 of the 32 layers -> examples/sec of the whole model.
+    value = n_ex / (t * 32)
+    return {
+        "value": value,
+        "unit": "examples/sec",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"1 of 32 Llama-3-8B LoRA r={r} layers, {n_ex} examples x {T} tokens, bf16 on CPU "
+                  f"(oracle vmap(grad) + AUTO-S + mt19937 noise), median of 3 after 1 warm-up, "
+                  f"scaled by 1/32; cpu={platform.processor() or platform.machine()}",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1",
+                          "gpus_requested": args.gpus}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+
+    from opaque_amd import _native as N
+    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments
+    from opaque_amd.guard import guard_constants, leaf_guards
+    from opaque_amd.noise import add_noise_tree
+    from opaque_amd.random import fold_in, key
+
+    N.load()
+    dev = torch.device("cuda", 0)
+    B, T, r = args.batch, args.seq, args.rank
+    lengths, sites = build_workload(args.layers, B, T, r, args.seed, dev)
+    seg = Segments.padded(B, T, lengths)
+
+    leaves, lsites, shapes = [], [], []
+    for name, x, gt, A, Bm in sites:
+        ia, ib = len(leaves), len(leaves) + 1
+        leaves += [LeafOut(tuple(A.shape), torch.bfloat16), LeafOut(tuple(Bm.shape), torch.bfloat16)]
+        shapes += [tuple(A.shape), tuple(Bm.shape)]
+        lsites.append(LoraSite(x, gt, A, Bm, 2.0, a_leaf=ia, b_leaf=ib))
+    _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=N.CLIP_AUTOS, thresholds=[1.0], effective=1.0, gamma=0.01,
+                    normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
+    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev)
+    n_params = sum(math.prod(lf.shape) for lf in leaves)
+    sigma = 1.0 * 1.0 / B  # noise_multiplier * max_norm, max_norm = R / normalize_by
+    k0 = key(42)
+
+    def step(i, events=None):
+        res = plan.run(events)
+        flat = res.flat[torch.bfloat16]
+        if events and "noise" in events:
+            events["noise"][0].record()
+        add_noise_tree({"flat": flat[:n_params]}, sigma, fold_in(k0, i).seed)
+        if events and "noise" in events:
+            events["noise"][1].record()
+        return res
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    stages = ("project", "factor", "clip", "scale_sum", "noise")
+    ev = [{s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for s in stages}
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, ev[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1000.0 / args.steps
+    stage_ms = {s: sum(e[s][0].elapsed_time(e[s][1]) for e in ev) / args.steps for s in stages}
+
+    valid = sum(lengths)
+    ab_factor = algorithmic_bytes(sites, lengths, n_params) + B * n_params * 4
+    factor_gbs = ab_factor / (stage_ms["factor"] * 1e-3) / 1e9
+    flops = 3 * 2 * valid * r * sum(d_in + d_out for d_in, d_out in LAYER_SHAPES.values()) * args.layers
+    res = plan.run()
+    torch.cuda.synchronize()
+
+    out = {
+        "metric": "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16",
+        "value": B / (ms * 1e-3),
+        "unit": "examples/sec",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C3: Llama-3-8B-shaped LoRA r=16, 32 layers x 7 linears, batch 16 x seq 1024, "
+                        "ragged lengths U[256,1024], AUTO-S R=1 gamma=0.01, noise multiplier 1.0",
+            "global_batch": B, "seq_len": T, "layers": args.layers, "rank": r,
+            "valid_tokens": valid, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "odp_seg_factor (k_factor_bf16)",
+            "achieved": factor_gbs,
+            "peak": MI355X_HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": factor_gbs / MI355X_HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": ab_factor,
+        },
+        "stage_ms": stage_ms,
+        "mfma_frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
+        "algorithmic_tflops": flops / (ms * 1e-3) / 1e12,
+        "clipped_fraction": float(res.clipped_total.float().mean().item()),
+    }
+    if args.cpu_baseline == "on":
+        out["cpu_baseline"] = cpu_baseline(r, args.seed)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

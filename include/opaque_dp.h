@@ -1,0 +1,219 @@
+/*
+ * opaque_dp.h — C ABI of the MI355X (gfx950) DP-SGD clip + noise core.
+ *
+ * Every entry point is asynchronous on the caller's HIP stream, takes plain
+ * device pointers and sizes, allocates nothing, never throws, and returns an
+ * odp_status (0 = success).  On failure odp_last_error() returns a
+ * human-readable message for the calling thread.
+ *
+ * Work is described by "problem tables": device arrays of int64_t rows whose
+ * field indices are listed below.  One launch processes every problem of its
+ * table, so a whole model's DP step is five launches regardless of depth.
+ * Each table comes with a device int32 array work_start[n_prob + 1] holding
+ * the cumulative number of workgroups per problem (work_start[0] == 0);
+ * the *_blocks() helpers give the per-problem workgroup counts.
+ *
+ * The reference (JetBrains-Research/opaque) is Python; these entry points
+ * replace the following internals of its DP-SGD hot path
+ * (paths relative to packages/):
+ *   odp_project + odp_seg_factor  -> per-sample LoRA factor gradients,
+ *       opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176
+ *       (dA[i] = s X[i]^T (G[i] B^T), dB[i] = s (X[i] A)^T G[i]) and the
+ *       per-example squared norms of clip_pytree,
+ *       opaque-engine/src/opaque/api/engine/clipping/_pytree.py:224-265,520-540
+ *   odp_linear_sqnorm             -> per-example squared norm of a full
+ *       weight gradient G[i]^T X[i] without materialising it (the reference
+ *       materialises it under vmap(grad), clipping/_clipped_fun.py:756-762)
+ *   odp_clip_factors              -> clip_pytree / auto_scale_pytree ratio,
+ *       guard and finalisation, clipping/_pytree.py:106-142,345-431,475-564
+ *       and the clipped counts of clipping/_clipped_fun.py:472-523
+ *   odp_scale_sum                 -> per-leaf scale, batch sum and
+ *       normalize_by, clipping/_pytree.py:553 and
+ *       clipping/_clipped_fun.py:115-134,777-782,821-824
+ *   odp_linear_clipped_sum        -> the same sum for a full weight,
+ *       sum_i c_i G[i]^T X[i] as one GEMM
+ *   odp_gaussian_noise            -> the sampler of
+ *       opaque-dpsgd/src/opaque/api/dpsgd/noise/_gaussian.py:235-301
+ *       (inverse-CDF Gaussian; uniforms from a counter-based Philox4x32-10
+ *       stream keyed by the 64-bit RngKey seed instead of a CPU mt19937)
+ */
+#ifndef OPAQUE_DP_H_
+#define OPAQUE_DP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* odp_stream_t; /* == hipStream_t */
+
+typedef enum odp_status {
+  ODP_OK = 0,
+  ODP_ERR_INVALID_ARGUMENT = 1,
+  ODP_ERR_UNSUPPORTED = 2,
+  ODP_ERR_HIP = 3
+} odp_status;
+
+typedef enum odp_dtype { ODP_DTYPE_F32 = 0, ODP_DTYPE_BF16 = 1 } odp_dtype;
+
+typedef enum odp_clip_mode {
+  ODP_CLIP_FIXED = 0, /* ratio = C / ||g||, clamped to 1 (clip_pytree) */
+  ODP_CLIP_AUTOS = 1  /* ratio = R / (||g|| + gamma), no clamp (auto_scale_pytree) */
+} odp_clip_mode;
+
+typedef enum odp_norm_form {
+  ODP_FORM_OUTER = 0, /* ||sum_t g_t a_t^T||_F^2 */
+  ODP_FORM_GRAM = 1   /* sum_{t,s} (g_t . g_s)(a_t . a_s) */
+} odp_norm_form;
+
+/* ---- segments -----------------------------------------------------------
+ * Rows of a layer's activations a [n_rows, d_in] and output gradients
+ * g [n_rows, d_out] are grouped into segments: seg_row_start[s],
+ * seg_row_len[s] (rows of one example, or of one (example, expert) pair),
+ * sorted by start and non-overlapping, and seg_example[s] names the example
+ * whose norm and clip factor the segment contributes to.  A problem refers
+ * to the slice [seg_first, seg_first + n_seg) of these device arrays.      */
+
+/* ---- odp_project: Q^T[k][row] = sum_j P[row][j] * W[k][j] --------------
+ * The LoRA rank-space projections U = G B^T and V = X A for rows
+ * [0, n_rows); rows outside the problem's segments get 0.  Only columns
+ * k < r are written.  bf16 P writes two bf16 planes, hi at ODP_PJ_Q and
+ * lo at ODP_PJ_QLO (hi + lo carries ~16 mantissa bits of the fp32 sum),
+ * each [k][ldq]; f32 P writes one f32 plane at ODP_PJ_Q.                  */
+enum {
+  ODP_PJ_P = 0,      /* address of P, row-major, ld = ODP_PJ_LDP elements     */
+  ODP_PJ_LDP = 1,
+  ODP_PJ_D = 2,      /* contraction length (multiple of 8 for bf16, 4 for f32) */
+  ODP_PJ_W = 3,      /* address of W [r][d] row-major, same dtype as P         */
+  ODP_PJ_R = 4,      /* r <= 64                                               */
+  ODP_PJ_Q = 5,      /* address of the output planes                          */
+  ODP_PJ_LDQ = 6,    /* row pitch of Q planes, multiple of 8, >= n_rows + 32   */
+  ODP_PJ_NROWS = 7,
+  ODP_PJ_SEG_FIRST = 8,
+  ODP_PJ_NSEG = 9,
+  ODP_PJ_QLO = 10,   /* address of the lo plane (bf16 only)                   */
+  ODP_PJ_FIELDS = 12
+};
+int64_t odp_project_blocks(int64_t n_rows);
+int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
+                const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                const int32_t* seg_row_start, const int32_t* seg_row_len);
+
+/* ---- odp_seg_factor: per-segment factor gradients and norm partials -----
+ * For every segment s and column k < r of Q (up to 4 leaves laid side by
+ * side in Q's columns):  pe_leaf[s][k - col0][m] = scaling * sum_{t in s}
+ * Q[k][t] * P[t][m],  m < M.  Each workgroup covers FACTOR_MTILE values of
+ * m and writes, per leaf, its fp64 sum of squares to
+ * part[seg_example[s] * part_stride + slot_base + tile].  Requirements: M
+ * and the P row pitch are multiples of 8 (bf16) or 4 (f32); Q is the output
+ * of odp_project (ldq a multiple of 8 and >= n_rows + 32), readable for
+ * 16*ceil(r/16) rows; rows k >= r may hold anything (they are discarded). */
+enum {
+  ODP_FT_P = 0, ODP_FT_LDP = 1, ODP_FT_M = 2,
+  ODP_FT_Q = 3, ODP_FT_LDQ = 4, ODP_FT_R = 5,
+  ODP_FT_SEG_FIRST = 6, ODP_FT_NSEG = 7,
+  ODP_FT_SCALING = 8, /* double bit pattern                                  */
+  ODP_FT_NLEAF = 9,   /* 1..4                                                */
+  ODP_FT_LEAF0 = 10,  /* per leaf l: [10+3l] pe address (f32 [n_seg][rank][M]),
+                         [11+3l] col0 | rank << 16, [12+3l] slot_base;
+                         leaves sorted by col0                               */
+  ODP_FT_QLO = 22,    /* lo plane of Q (bf16 only)                           */
+  ODP_FT_FIELDS = 24
+};
+int64_t odp_seg_factor_tiles(int64_t M);
+int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
+                   const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                   const int32_t* seg_row_start, const int32_t* seg_row_len,
+                   const int32_t* seg_example, double* part, int64_t part_stride);
+
+/* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
+ * For leaves that are not behind a captured linear op, the per-example
+ * gradients X[n_seg][n] are materialised; each workgroup sums
+ * f32(x)^2 (non-finite x counted as 0) over a chunk of one segment in fp64
+ * and writes part[seg_example[s] * part_stride + slot + chunk]; a problem
+ * uses odp_sqnorm_blocks(n) slots.                                        */
+enum {
+  ODP_SQ_X = 0, ODP_SQ_N = 1, ODP_SQ_NSEG = 2, ODP_SQ_SEG_FIRST = 3,
+  ODP_SQ_SLOT = 4, ODP_SQ_DTYPE = 5,
+  ODP_SQ_FIELDS = 8
+};
+int64_t odp_sqnorm_blocks(int64_t n);
+int odp_sqnorm(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+               int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
+               double* part, int64_t part_stride);
+
+/* ---- odp_clip_factors ----------------------------------------------------
+ * part[n_ex][n_slots] (fp64 squared-norm partials; every slot must have
+ * been written or zeroed), group_slot_start[n_groups + 1] (int64, device:
+ * group g owns slots [start[g], start[g+1])), thresholds[n_groups] (C_g or
+ * R_g, device), guard[2 * n_cls] and cls_dtype[n_cls] (device).  Per example:
+ * group squared norms in fp64, ratio per group (mode), then per dtype class
+ * c: scale = ratio * guard[2c] - guard[2c+1]; min(1, .) for FIXED;
+ * non-finite -> 0; max(0, .); rounded to cls_dtype[c].
+ * Outputs: scale_out[c][g][ex] (f32 holding the rounded value),
+ * norm_out[ex] = f32(sqrt(total)), group_norm_out[g][ex] (may be null),
+ * clipped_out[g][ex] = f32(group norm) > f32(threshold) (uint8, may be
+ * null), clipped_total_out[ex] = norm_out > f32(effective threshold).       */
+int odp_clip_factors(odp_stream_t stream, const double* part, int64_t n_slots, int32_t n_ex,
+                     const int64_t* group_slot_start, int32_t n_groups, const double* thresholds,
+                     double effective_threshold, int32_t mode, double gamma,
+                     int32_t n_cls, const double* guard, const int32_t* cls_dtype,
+                     float* scale_out, float* norm_out, float* group_norm_out,
+                     uint8_t* clipped_out, uint8_t* clipped_total_out);
+
+/* ---- odp_scale_sum: clipped batch sum of stored per-segment gradients ----
+ * out = round_out(sum_s scale[cls][grp][seg_example[s]] * pe[s]) and then,
+ * if normalize_by != 1, round_out(out / normalize_by).  Optional second
+ * output out2 = same for (scale * pe)^2.                                   */
+enum {
+  ODP_SS_PE = 0,        /* address of f32 [n_seg][rank][M]                  */
+  ODP_SS_M = 1, ODP_SS_RANK = 2,
+  ODP_SS_SEG_FIRST = 3, ODP_SS_NSEG = 4,
+  ODP_SS_OUT = 5,       /* address of the output leaf                       */
+  ODP_SS_FLAGS = 6,     /* out dtype | transpose << 8 | group << 16 | cls << 40
+                           | pe dtype << 56; transpose 0 writes [rank][M],
+                           1 writes [M][rank]; non-finite pe values count 0 */
+  ODP_SS_OUT2 = 7,      /* address of the second-moment output or 0         */
+  ODP_SS_FIELDS = 8
+};
+int64_t odp_scale_sum_blocks(int64_t n_elems);
+int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                  int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
+                  const float* scales, int32_t n_ex, int32_t n_groups, float normalize_by);
+
+/* ---- odp_gaussian_noise --------------------------------------------------
+ * out[i] = round_out(in[i] + f32(sigma * sqrt 2) * erfinv(2u - 1)) with
+ * u = clamp((x >> 8) * 2^-24, eps, 1 - eps), x = word (e & 3) of
+ * Philox4x32-10(counter = {e >> 2 (64-bit), stream_tag, 0}, key = seed)
+ * and e = flat_offset + i the element's index in the flattened pytree.
+ * sigma == 0 copies the input.  With the bounded flag the Gaussian is
+ * renormalised over [low, high] (u -> Phi(za) + u (Phi(zb) - Phi(za))) and
+ * the result clamped, as the reference's bounded mode does.  in and out may
+ * alias.                                                                   */
+enum {
+  ODP_NZ_IN = 0, ODP_NZ_OUT = 1, ODP_NZ_N = 2, ODP_NZ_FLAT_OFFSET = 3,
+  ODP_NZ_SIGMA = 4,     /* double bit pattern                               */
+  ODP_NZ_DTYPES = 5,    /* in dtype | out dtype << 8 | bounded << 16        */
+  ODP_NZ_LOW = 6,       /* double bit pattern (bounded only)                */
+  ODP_NZ_HIGH = 7,      /* double bit pattern (bounded only)                */
+  ODP_NZ_FIELDS = 8
+};
+int64_t odp_gaussian_noise_blocks(int64_t flat_offset, int64_t n);
+int odp_gaussian_noise(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                       int32_t n_prob, int32_t total_blocks, uint64_t seed, uint32_t stream_tag);
+
+/* Raw Philox4x32-10 words for counters [ctr0, ctr0 + n), key = seed: for
+ * known-answer and determinism tests of the device stream.               */
+int odp_philox_words(odp_stream_t stream, uint64_t ctr0, uint32_t ctr2, uint32_t ctr3,
+                     uint64_t seed, int64_t n, uint32_t* out /* [n][4] */);
+
+/* ---- library -------------------------------------------------------------- */
+int odp_abi_version(void);
+const char* odp_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPAQUE_DP_H_ */

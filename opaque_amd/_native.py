@@ -1,0 +1,113 @@
+"""ctypes binding of ``libopaque_dp.so`` (declared in ``include/opaque_dp.h``).
+
+The library must be built (``python -m opaque_amd.build``); there is no
+fallback implementation, so a missing library raises immediately.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libopaque_dp.so"
+
+ODP_OK = 0
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+CLIP_FIXED = 0
+CLIP_AUTOS = 1
+
+# Problem-table field layouts (must match include/opaque_dp.h).
+PJ_FIELDS = 12
+PJ_P, PJ_LDP, PJ_D, PJ_W, PJ_R, PJ_Q, PJ_LDQ, PJ_NROWS, PJ_SEG_FIRST, PJ_NSEG, PJ_QLO = range(11)
+FT_FIELDS = 24
+FT_P, FT_LDP, FT_M, FT_Q, FT_LDQ, FT_R, FT_SEG_FIRST, FT_NSEG, FT_SCALING, FT_NLEAF = range(10)
+FT_LEAF0 = 10
+FT_QLO = 22
+SS_FIELDS = 8
+SS_PE, SS_M, SS_RANK, SS_SEG_FIRST, SS_NSEG, SS_OUT, SS_FLAGS, SS_OUT2 = range(8)
+NZ_FIELDS = 8
+NZ_IN, NZ_OUT, NZ_N, NZ_FLAT_OFFSET, NZ_SIGMA, NZ_DTYPES = range(6)
+SQ_FIELDS = 8
+SQ_X, SQ_N, SQ_NSEG, SQ_SEG_FIRST, SQ_SLOT, SQ_DTYPE = range(6)
+LN_FIELDS = 16
+
+_c_int = ctypes.c_int
+_c_i32 = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_u32 = ctypes.c_uint32
+_c_u64 = ctypes.c_uint64
+_c_f32 = ctypes.c_float
+_c_f64 = ctypes.c_double
+_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes)
+_SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "odp_abi_version": (_c_int, []),
+    "odp_last_error": (ctypes.c_char_p, []),
+    "odp_project_blocks": (_c_i64, [_c_i64]),
+    "odp_project": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr]),
+    "odp_seg_factor_tiles": (_c_i64, [_c_i64]),
+    "odp_seg_factor": (
+        _c_int,
+        [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64],
+    ),
+    "odp_sqnorm_blocks": (_c_i64, [_c_i64]),
+    "odp_sqnorm": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i64]),
+    "odp_clip_factors": (
+        _c_int,
+        [
+            _ptr, _ptr, _c_i64, _c_i32, _ptr, _c_i32, _ptr, _c_f64, _c_i32, _c_f64,
+            _c_i32, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+        ],
+    ),
+    "odp_scale_sum_blocks": (_c_i64, [_c_i64]),
+    "odp_scale_sum": (
+        _c_int,
+        [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i32, _c_i32, _c_f32],
+    ),
+    "odp_gaussian_noise_blocks": (_c_i64, [_c_i64, _c_i64]),
+    "odp_gaussian_noise": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _c_u64, _c_u32]),
+    "odp_philox_words": (_c_int, [_ptr, _c_u64, _c_u32, _c_u32, _c_u64, _c_i64, _ptr]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGNATURES)
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load the native library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"opaque_amd native library not found at {p}. Build it with "
+            "`python -m opaque_amd.build` (hipcc, gfx950); there is no fallback path."
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if the symbol is missing
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().odp_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != ODP_OK:
+        raise RuntimeError(f"{what} failed with status {rc}: {last_error()}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,70 @@
+"""Builds ``libopaque_dp.so`` (HIP kernels + C ABI) in-tree for gfx950.
+
+Usage: ``python -m opaque_amd.build`` (or ``__graft_entry__.build()``).
+The library is written next to this file so it travels with the source tree.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = PKG_DIR.parent / "include"
+LIB_NAME = "libopaque_dp.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+SOURCES = ["odp_abi.hip", "odp_lora.hip", "odp_clip.hip", "odp_noise.hip", "odp_linear.hip"]
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed-FP32 instructions are kept out of generated code on this target.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; the HIP toolchain is required to build opaque_amd")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source into one shared library. Always recompiles."""
+    srcs = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
+    tmp = LIB_PATH.with_name(LIB_NAME + f".tmp{os.getpid()}")
+    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        tmp.unlink(missing_ok=True)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    if verbose:
+        noise = [
+            ln
+            for ln in proc.stderr.splitlines()
+            if "packed-fp32-ops" not in ln and ln.strip()
+        ]
+        if noise:
+            print("\n".join(noise), file=sys.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

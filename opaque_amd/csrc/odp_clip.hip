@@ -1,0 +1,273 @@
+// Clip factors (fixed / AUTO-S, global or per group) and the clipped batch
+// sum of stored per-segment gradients.
+//
+// The scale arithmetic follows clip_pytree / auto_scale_pytree
+// (opaque-engine/.../clipping/_pytree.py:106-142, 345-431, 475-564): fp64
+// norms, ratio C/||g|| (or R/(||g||+gamma)), the storage guard
+// ratio*rel - abs evaluated as two separately rounded fp64 operations,
+// min(1, .) for fixed clipping with NaN propagating as in torch.minimum,
+// non-finite -> 0, clamp at 0, then rounded to the leaf dtype the way
+// torch casts a float64 tensor (to float32, then to bfloat16).
+#include "odp_internal.h"
+
+namespace {
+
+constexpr int CL_THREADS = 256;
+constexpr int CL_MAX_GROUPS = 1024;
+constexpr int SS_THREADS = 256;
+constexpr int SS_ELEMS = 4;  // elements per thread
+
+__device__ __forceinline__ double block_sum_fixed(double v, double* red) {
+  const int t = threadIdx.x;
+  red[t] = v;
+  __syncthreads();
+#pragma unroll
+  for (int w = CL_THREADS / 2; w > 0; w >>= 1) {
+    if (t < w) red[t] = red[t] + red[t + w];
+    __syncthreads();
+  }
+  const double out = red[0];
+  __syncthreads();
+  return out;
+}
+
+__device__ __forceinline__ float finalize_scale(double ratio, double rel, double abs_, int clamp_one,
+                                                int dtype) {
+  double s = __dsub_rn(__dmul_rn(ratio, rel), abs_);
+  if (clamp_one && !(s < 1.0) && !isnan(s)) s = 1.0;
+  if (!isfinite(s)) s = 0.0;
+  if (s < 0.0) s = 0.0;
+  return odp_round_to((float)s, dtype);
+}
+
+// One workgroup per example.  Group g owns slots [gstart[g], gstart[g+1]).
+__global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
+    const double* __restrict__ part, int64_t n_slots, int n_ex, const int64_t* __restrict__ gstart, int n_groups,
+    const double* __restrict__ thr, double eff_thr, int mode, double gamma, int n_cls,
+    const double* __restrict__ guard, const int32_t* __restrict__ cls_dtype,
+    float* __restrict__ scale_out, float* __restrict__ norm_out, float* __restrict__ gnorm_out,
+    uint8_t* __restrict__ clip_out, uint8_t* __restrict__ clip_total_out) {
+  const int ex = blockIdx.x;
+  const int t = threadIdx.x;
+  __shared__ double red[CL_THREADS];
+  __shared__ double gsq[CL_MAX_GROUPS];
+
+  for (int g = 0; g < n_groups; ++g) {
+    double acc = 0.0;
+    for (int64_t s = gstart[g] + t; s < gstart[g + 1]; s += CL_THREADS)
+      acc += part[(int64_t)ex * n_slots + s];
+    const double tot = block_sum_fixed(acc, red);
+    if (t == 0) gsq[g] = tot;
+  }
+  __syncthreads();
+
+  if (t == 0) {
+    double total = 0.0;
+    for (int g = 0; g < n_groups; ++g) total += gsq[g];
+    const double norm = sqrt(total);
+    const float normf = (float)norm;
+    norm_out[ex] = normf;
+    if (clip_total_out) clip_total_out[ex] = normf > (float)eff_thr ? 1 : 0;
+  }
+  for (int g = t; g < n_groups; g += CL_THREADS) {
+    const double gn = sqrt(gsq[g]);
+    if (gnorm_out) gnorm_out[(int64_t)g * n_ex + ex] = (float)gn;
+    if (clip_out) clip_out[(int64_t)g * n_ex + ex] = (float)gn > (float)thr[g] ? 1 : 0;
+    const double c = thr[g] > 0.0 ? thr[g] : 0.0;
+    const double ratio = mode == ODP_CLIP_AUTOS ? c / (gn + gamma) : c / gn;
+    for (int k = 0; k < n_cls; ++k)
+      scale_out[((int64_t)k * n_groups + g) * n_ex + ex] =
+          finalize_scale(ratio, guard[2 * k], guard[2 * k + 1], mode == ODP_CLIP_FIXED, cls_dtype[k]);
+  }
+}
+
+// Clipped sum of one leaf per problem: 4 consecutive elements per thread,
+// summed over the leaf's segments in segment order.
+__global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
+    const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
+    const int32_t* __restrict__ sex, const float* __restrict__ scales, int n_ex, int n_groups,
+    float normalize_by) {
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_SS_FIELDS;
+  const float* pe = (const float*)f[ODP_SS_PE];
+  const int64_t M = f[ODP_SS_M];
+  const int rank = (int)f[ODP_SS_RANK];
+  const int seg_first = (int)f[ODP_SS_SEG_FIRST], n_seg = (int)f[ODP_SS_NSEG];
+  void* out = (void*)f[ODP_SS_OUT];
+  void* out2 = (void*)f[ODP_SS_OUT2];
+  const int64_t flags = f[ODP_SS_FLAGS];
+  const int odt = (int)(flags & 0xff);
+  const int transpose = (int)((flags >> 8) & 0xff);
+  const int grp = (int)((flags >> 16) & 0xffffff);
+  const int cls = (int)((flags >> 40) & 0xffff);
+  const int pdt = (int)((flags >> 56) & 0xff);
+  const int64_t E = M * rank;
+  const int64_t e0 = ((int64_t)(bid - ws[p]) * SS_THREADS + threadIdx.x) * SS_ELEMS;
+  if (e0 >= E) return;
+  const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
+  const bool vec = pdt == ODP_DTYPE_F32 && (E & 3) == 0;
+
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc2 = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < n_seg; ++s) {
+    const float c = sc[sex[seg_first + s]];
+    f32x4_t v;
+    if (vec) {
+      v = *(const f32x4_t*)(pe + (int64_t)s * E + e0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = e0 + i < E ? odp_load_as_float(pe, (int64_t)s * E + e0 + i, pdt) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!isfinite(v[i])) v[i] = 0.f;  // nan_to_num of the per-example value
+      const float y = __fmul_rn(c, v[i]);
+      acc[i] = __fadd_rn(acc[i], y);
+      acc2[i] = __fadd_rn(acc2[i], __fmul_rn(y, y));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t e = e0 + i;
+    if (e >= E) break;
+    const int64_t k = e / M, m = e - k * M;
+    const int64_t o = transpose ? m * rank + k : e;
+    float x = odp_round_to(acc[i], odt);
+    if (normalize_by != 1.0f) x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
+    odp_store_from_float(out, o, odt, x);
+    if (out2) {
+      float x2 = odp_round_to(acc2[i], odt);
+      if (normalize_by != 1.0f) x2 = odp_round_to(__fdiv_rn(x2, normalize_by), odt);
+      odp_store_from_float(out2, o, odt, x2);
+    }
+  }
+}
+
+// Per-segment sums of squares of materialised per-example tensors
+// (x^2 in fp32 as clip_pytree squares in its float32 accumulation dtype,
+// summed in fp64).  Each workgroup reduces SQ_CHUNK elements of one
+// segment and writes one slot.
+constexpr int SQ_THREADS = 256;
+constexpr int64_t SQ_CHUNK = 8192;
+
+__global__ __launch_bounds__(SQ_THREADS) void k_sqnorm(const int64_t* __restrict__ probs,
+                                                       const int32_t* __restrict__ ws, int n_prob,
+                                                       const int32_t* __restrict__ sex,
+                                                       double* __restrict__ part,
+                                                       int64_t part_stride) {
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_SQ_FIELDS;
+  const void* X = (const void*)f[ODP_SQ_X];
+  const int64_t n = f[ODP_SQ_N];
+  const int seg_first = (int)f[ODP_SQ_SEG_FIRST];
+  const int64_t slot = f[ODP_SQ_SLOT];
+  const int dt = (int)f[ODP_SQ_DTYPE];
+  const int64_t nchunk = (n + SQ_CHUNK - 1) / SQ_CHUNK;
+  const int64_t local = bid - ws[p];
+  const int64_t seg = local / nchunk, chunk = local % nchunk;
+  const int64_t lo = chunk * SQ_CHUNK, hi = lo + SQ_CHUNK < n ? lo + SQ_CHUNK : n;
+  double acc = 0.0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += SQ_THREADS) {
+    float x = odp_load_as_float(X, seg * n + i, dt);
+    if (!isfinite(x)) x = 0.f;  // nan_to_num before the norm
+    acc += (double)__fmul_rn(x, x);
+  }
+  __shared__ double red[SQ_THREADS];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = SQ_THREADS / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[(int64_t)sex[seg_first + seg] * part_stride + slot + chunk] = red[0];
+}
+
+}  // namespace
+
+extern "C" int64_t odp_sqnorm_blocks(int64_t n) {
+  return n <= 0 ? 0 : (n + SQ_CHUNK - 1) / SQ_CHUNK;
+}
+
+extern "C" int odp_sqnorm(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                          int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
+                          double* part, int64_t part_stride) {
+  int rc = odp_check_table("odp_sqnorm", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_example == nullptr || part == nullptr || part_stride <= 0) {
+    odp_set_error("odp_sqnorm: null seg_example/part or part_stride <= 0");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_sqnorm, dim3(total_blocks), dim3(SQ_THREADS), 0, odp_hip_stream(stream),
+                     problems, work_start, n_prob, seg_example, part, part_stride);
+  return odp_check_launch("odp_sqnorm");
+}
+
+extern "C" int odp_clip_factors(odp_stream_t stream, const double* part, int64_t n_slots,
+                                int32_t n_ex, const int64_t* group_slot_start, int32_t n_groups,
+                                const double* thresholds, double effective_threshold, int32_t mode,
+                                double gamma, int32_t n_cls, const double* guard,
+                                const int32_t* cls_dtype, float* scale_out, float* norm_out,
+                                float* group_norm_out, uint8_t* clipped_out,
+                                uint8_t* clipped_total_out) {
+  if (n_ex < 0 || n_slots < 0) {
+    odp_set_error("odp_clip_factors: negative n_ex or n_slots");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (n_groups < 1 || n_groups > CL_MAX_GROUPS) {
+    odp_set_error("odp_clip_factors: n_groups=%d outside [1, %d]", n_groups, CL_MAX_GROUPS);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  if (n_cls < 1 || n_cls > 8) {
+    odp_set_error("odp_clip_factors: n_cls=%d outside [1, 8]", n_cls);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  if (mode != ODP_CLIP_FIXED && mode != ODP_CLIP_AUTOS) {
+    odp_set_error("odp_clip_factors: unknown mode %d", mode);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (mode == ODP_CLIP_AUTOS && !(gamma > 0.0)) {
+    odp_set_error("odp_clip_factors: gamma must be positive, got %g", gamma);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (n_ex == 0) return ODP_OK;
+  if ((n_slots > 0 && part == nullptr) || group_slot_start == nullptr || thresholds == nullptr ||
+      guard == nullptr || cls_dtype == nullptr || scale_out == nullptr || norm_out == nullptr) {
+    odp_set_error("odp_clip_factors: null required pointer");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_clip_factors, dim3(n_ex), dim3(CL_THREADS), 0, odp_hip_stream(stream), part,
+                     n_slots, n_ex, group_slot_start, n_groups, thresholds, effective_threshold, mode,
+                     gamma, n_cls, guard, cls_dtype, scale_out, norm_out, group_norm_out,
+                     clipped_out, clipped_total_out);
+  return odp_check_launch("odp_clip_factors");
+}
+
+extern "C" int64_t odp_scale_sum_blocks(int64_t n_elems) {
+  const int64_t per = (int64_t)SS_THREADS * SS_ELEMS;
+  return n_elems <= 0 ? 0 : (n_elems + per - 1) / per;
+}
+
+extern "C" int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                             int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
+                             const float* scales, int32_t n_ex, int32_t n_groups,
+                             float normalize_by) {
+  int rc = odp_check_table("odp_scale_sum", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (!(normalize_by > 0.0f)) {
+    odp_set_error("odp_scale_sum: normalize_by must be > 0, got %g", (double)normalize_by);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_example == nullptr || scales == nullptr || n_ex <= 0 || n_groups <= 0) {
+    odp_set_error("odp_scale_sum: null seg_example/scales or non-positive n_ex/n_groups");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_scale_sum, dim3(total_blocks), dim3(SS_THREADS), 0, odp_hip_stream(stream),
+                     problems, work_start, n_prob, seg_example, scales, n_ex, n_groups,
+                     normalize_by);
+  return odp_check_launch("odp_scale_sum");
+}

@@ -1,0 +1,636 @@
+"""Host orchestration of the DP clip kernels.
+
+A ``GhostPlan`` turns one batch's captured layer inputs into problem tables
+for the native kernels and runs the DP step as a fixed sequence of launches
+on the current HIP stream:
+
+    odp_project     U_i = G_i B_i^T, V = X [A_1 .. A_k]   (LoRA rank space)
+    odp_seg_factor  per-example dA, dB and their squared-norm partials
+    odp_sqnorm      squared norms of materialised per-example leaves
+    odp_clip_factors  per-example norms -> clip / AUTO-S scales
+    odp_scale_sum   clipped sum, cast and normalize_by, into one flat buffer
+
+LoRA adapters that read the same activation tensor (q/k/v, gate/up) share
+one pass over it: their ranks are laid side by side (up to 4 leaves and 64
+columns per pass).  All metadata of a step is packed into one pinned host
+buffer and uploaded with one asynchronous copy.
+"""
+
+from __future__ import annotations
+
+import math
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from opaque_amd import _native as N
+
+_DTYPE_CODE = {torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
+_ALIGN = {torch.float32: 4, torch.bfloat16: 8}  # element multiple for 16-byte rows
+MAX_RANK_PER_PASS = 64
+MAX_LEAVES_PER_PASS = 4
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise TypeError(f"opaque_amd kernels support float32 and bfloat16, got {dt}") from None
+
+
+def _f64_bits(x: float) -> int:
+    return struct.unpack("<q", struct.pack("<d", float(x)))[0]
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """2-D row view [rows, d] with unit column stride and a 16-byte aligned pitch."""
+    t2 = t.reshape(-1, t.shape[-1])
+    align = _ALIGN[t.dtype]
+    if t2.stride(-1) != 1 or t2.stride(0) % align != 0 or t2.data_ptr() % 16 != 0:
+        t2 = t2.contiguous()
+    return t2
+
+
+def supports_rows(t: torch.Tensor) -> bool:
+    """Whether a [.., d] activation can go through the LoRA kernels."""
+    return t.dtype in _ALIGN and t.shape[-1] % _ALIGN[t.dtype] == 0 and t.shape[-1] > 0
+
+
+# ---------------------------------------------------------------------------
+# Segments
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Segments:
+    """Row ranges of examples (or (example, expert) pairs) in a row tensor."""
+
+    starts: list[int]
+    lengths: list[int]
+    examples: list[int]
+    n_ex: int
+    n_rows: int
+
+    def __post_init__(self) -> None:
+        if not (len(self.starts) == len(self.lengths) == len(self.examples)):
+            raise ValueError("segment arrays must have equal length")
+        prev_end = 0
+        for s, ln, e in zip(self.starts, self.lengths, self.examples):
+            if ln < 0 or s < prev_end or s + ln > self.n_rows:
+                raise ValueError(
+                    f"segments must be sorted, non-overlapping and inside [0, {self.n_rows}); "
+                    f"got start={s} len={ln} after end={prev_end}"
+                )
+            if not 0 <= e < self.n_ex:
+                raise ValueError(f"segment example {e} outside [0, {self.n_ex})")
+            prev_end = s + ln
+        if self.n_rows >= 2**31 - 64:
+            raise ValueError("row count exceeds the int32 segment range")
+
+    @property
+    def n_seg(self) -> int:
+        return len(self.starts)
+
+    @classmethod
+    def padded(cls, n_ex: int, seq_len: int, lengths: list[int] | None = None) -> Segments:
+        """Example i owns rows [i*seq_len, i*seq_len + lengths[i])."""
+        lens = [seq_len] * n_ex if lengths is None else [int(x) for x in lengths]
+        if len(lens) != n_ex or any(not 0 <= x <= seq_len for x in lens):
+            raise ValueError("lengths must give one value in [0, seq_len] per example")
+        return cls([i * seq_len for i in range(n_ex)], lens, list(range(n_ex)), n_ex, n_ex * seq_len)
+
+
+# ---------------------------------------------------------------------------
+# Inputs and outputs of a plan
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class LoraSite:
+    """One LoRA application y = x W^T + s (x A) B over the batch rows.
+
+    ``A`` is [d_in, r] and ``B`` is [r, d_out] (kernel convention).  The
+    gradient leaves are indices into the plan's leaf list (None when the
+    factor is frozen); ``a_transposed`` / ``b_transposed`` say that the leaf
+    is stored as [r, d_in] / [d_out, r] (PEFT's lora_A.weight/lora_B.weight).
+    """
+
+    x: torch.Tensor
+    g: torch.Tensor
+    A: torch.Tensor
+    B: torch.Tensor
+    scaling: float
+    a_leaf: int | None
+    b_leaf: int | None
+    a_transposed: bool = False
+    b_transposed: bool = False
+
+
+@dataclass
+class MaterializedLeaf:
+    """A leaf whose per-example gradients are already materialised: [n_seg, *shape]."""
+
+    per_example: torch.Tensor
+    leaf: int
+
+
+@dataclass
+class LeafOut:
+    shape: tuple[int, ...]
+    out_dtype: torch.dtype
+    group: int = 0
+    cls: int = 0
+
+
+@dataclass
+class ClipSpec:
+    mode: int  # N.CLIP_FIXED or N.CLIP_AUTOS
+    thresholds: list[float]  # per group
+    effective: float
+    gamma: float = 0.01
+    normalize_by: float = 1.0
+    guards: list[tuple[float, float, torch.dtype]] = field(default_factory=list)  # per cls
+
+
+@dataclass
+class GhostResult:
+    leaves: list[torch.Tensor]
+    norms: torch.Tensor  # [n_ex] f32
+    group_norms: torch.Tensor  # [G, n_ex] f32
+    clipped: torch.Tensor  # [G, n_ex] uint8
+    clipped_total: torch.Tensor  # [n_ex] uint8
+    scales: torch.Tensor  # [n_cls, G, n_ex] f32
+    second_moment: list[torch.Tensor] | None
+    flat: dict[torch.dtype, torch.Tensor]
+
+
+class _Pack:
+    """Collects host arrays and uploads them with one pinned async copy."""
+
+    def __init__(self) -> None:
+        self._chunks: list[np.ndarray] = []
+        self._offsets: list[int] = []
+        self._size = 0
+
+    def add(self, arr: np.ndarray) -> int:
+        arr = np.ascontiguousarray(arr)
+        off = (self._size + 255) // 256 * 256
+        self._chunks.append(arr)
+        self._offsets.append(off)
+        self._size = off + arr.nbytes
+        return len(self._chunks) - 1
+
+    def upload(self, device: torch.device) -> list[torch.Tensor]:
+        host = torch.empty(max(self._size, 1), dtype=torch.uint8, pin_memory=True)
+        hn = host.numpy()
+        for arr, off in zip(self._chunks, self._offsets):
+            hn[off : off + arr.nbytes] = arr.view(np.uint8).reshape(-1)
+        dev = host.to(device, non_blocking=True)
+        self._host = host  # keep the pinned source alive until the copy is done
+        views = []
+        for arr, off in zip(self._chunks, self._offsets):
+            tdt = {
+                np.dtype(np.int64): torch.int64,
+                np.dtype(np.int32): torch.int32,
+                np.dtype(np.float64): torch.float64,
+            }[arr.dtype]
+            views.append(dev[off : off + arr.nbytes].view(tdt))
+        return views
+
+
+class _Table:
+    def __init__(self, fields: int) -> None:
+        self.fields = fields
+        self.rows: list[list[int]] = []
+        self.blocks: list[int] = []
+
+    def add(self, row: dict[int, int], blocks: int) -> None:
+        if blocks <= 0:
+            return
+        r = [0] * self.fields
+        for k, v in row.items():
+            r[k] = int(v)
+        self.rows.append(r)
+        self.blocks.append(int(blocks))
+
+    def arrays(self) -> tuple[np.ndarray, np.ndarray, int]:
+        probs = np.asarray(self.rows, dtype=np.int64).reshape(-1, self.fields)
+        ws = np.zeros(len(self.blocks) + 1, dtype=np.int64)
+        np.cumsum(self.blocks, out=ws[1:])
+        total = int(ws[-1])
+        if total >= 2**31 - 1:
+            raise ValueError("launch exceeds the int32 workgroup range; split the batch")
+        return probs, ws.astype(np.int32), total
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---------------------------------------------------------------------------
+# The plan
+# ---------------------------------------------------------------------------
+
+
+class GhostPlan:
+    """Buffers and problem tables of one DP clip step.  Build, then ``run()``.
+
+    A plan may be run repeatedly (the bench does) as long as the tensors it
+    was built from stay alive and unchanged in shape.
+    """
+
+    def __init__(
+        self,
+        *,
+        segments: Segments,
+        leaves: list[LeafOut],
+        clip: ClipSpec,
+        lora_sites: list[LoraSite] = (),
+        materialized: list[MaterializedLeaf] = (),
+        device: torch.device | str = "cuda",
+        second_moment: bool = False,
+    ) -> None:
+        N.load()
+        self.device = torch.device(device)
+        self.segments = segments
+        self.leaves = leaves
+        self.clip = clip
+        self.second_moment = second_moment
+        self.n_groups = len(clip.thresholds)
+        self.n_cls = max(1, len(clip.guards))
+        if self.n_groups < 1:
+            raise ValueError("at least one clip group is required")
+        for lf in leaves:
+            if not 0 <= lf.group < self.n_groups or not 0 <= lf.cls < self.n_cls:
+                raise ValueError("leaf group/class out of range")
+        self._keep: list[torch.Tensor] = []
+        self._build(list(lora_sites), list(materialized))
+
+    # -- construction --------------------------------------------------------
+    def _build(self, sites: list[LoraSite], mats: list[MaterializedLeaf]) -> None:
+        seg = self.segments
+        dev = self.device
+        n_rows, n_seg = seg.n_rows, seg.n_seg
+        ldq = (n_rows + 32 + 7) // 8 * 8
+
+        # Group sites by activation tensor, then chunk by rank/leaf budget.
+        for s in sites:
+            if s.x.device != dev or s.g.device != dev:
+                raise ValueError("LoRA site tensors must be on the plan device")
+            if s.x.dtype != s.g.dtype:
+                raise TypeError("x and g of a LoRA site must share a dtype")
+            if s.x.reshape(-1, s.x.shape[-1]).shape[0] != n_rows or s.g.reshape(-1, s.g.shape[-1]).shape[0] != n_rows:
+                raise ValueError("LoRA site row count does not match the segments")
+            if not (supports_rows(s.x) and supports_rows(s.g)):
+                raise ValueError("LoRA site feature sizes must be multiples of 8 (bf16) / 4 (f32)")
+        groups: dict[tuple, list[LoraSite]] = {}
+        for s in sites:
+            if s.a_leaf is None and s.b_leaf is None:
+                continue
+            k = (s.x.data_ptr(), tuple(s.x.shape), tuple(s.x.stride()), s.x.dtype)
+            groups.setdefault(k, []).append(s)
+        chunks: list[list[LoraSite]] = []
+        for members in groups.values():
+            cur: list[LoraSite] = []
+            rtot = 0
+            for s in members:
+                r = s.A.shape[1]
+                if r > MAX_RANK_PER_PASS:
+                    raise ValueError(f"LoRA rank {r} exceeds {MAX_RANK_PER_PASS}")
+                if cur and (len(cur) == MAX_LEAVES_PER_PASS or rtot + r > MAX_RANK_PER_PASS):
+                    chunks.append(cur)
+                    cur, rtot = [], 0
+                cur.append(s)
+                rtot += r
+            if cur:
+                chunks.append(cur)
+
+        # Slot allocation: leaf -> number of partial slots, assigned in group order.
+        leaf_slots: dict[int, int] = {}
+        pe_elems: dict[int, int] = {}
+        leaf_rank_m: dict[int, tuple[int, int]] = {}
+        for ch in chunks:
+            for s in ch:
+                d_in, r = s.A.shape
+                d_out = s.B.shape[1]
+                if s.a_leaf is not None:
+                    leaf_slots[s.a_leaf] = int(N.load().odp_seg_factor_tiles(d_in))
+                    leaf_rank_m[s.a_leaf] = (r, d_in)
+                    pe_elems[s.a_leaf] = n_seg * r * d_in
+                if s.b_leaf is not None:
+                    leaf_slots[s.b_leaf] = int(N.load().odp_seg_factor_tiles(d_out))
+                    leaf_rank_m[s.b_leaf] = (r, d_out)
+                    pe_elems[s.b_leaf] = n_seg * r * d_out
+        for m in mats:
+            n = int(math.prod(m.per_example.shape[1:]))
+            if m.per_example.shape[0] != n_seg:
+                raise ValueError("materialised leaves need one row per segment")
+            leaf_slots[m.leaf] = int(N.load().odp_sqnorm_blocks(n))
+        covered = set(leaf_slots)
+        if len(covered) != len(leaf_slots) or covered != set(range(len(self.leaves))):
+            missing = sorted(set(range(len(self.leaves))) - covered)
+            raise ValueError(f"every output leaf needs exactly one producer; missing {missing}")
+        order = sorted(leaf_slots, key=lambda i: (self.leaves[i].group, i))
+        slot_base: dict[int, int] = {}
+        gstart = np.zeros(self.n_groups + 1, dtype=np.int64)
+        pos = 0
+        for i in order:
+            slot_base[i] = pos
+            pos += leaf_slots[i]
+            gstart[self.leaves[i].group + 1] = pos
+        for g in range(1, self.n_groups + 1):  # empty groups
+            gstart[g] = max(gstart[g], gstart[g - 1])
+        self.n_slots = max(pos, 1)
+
+        # Device buffers.
+        pe_off: dict[int, int] = {}
+        off = 0
+        for i in sorted(pe_elems):
+            pe_off[i] = off
+            off += (pe_elems[i] + 63) // 64 * 64
+        self.pe = torch.empty(max(off, 1), dtype=torch.float32, device=dev)
+        self.part = torch.zeros((seg.n_ex, self.n_slots), dtype=torch.float64, device=dev)
+
+        # Output leaves: one flat buffer per output dtype, views in leaf order.
+        self.flat: dict[torch.dtype, torch.Tensor] = {}
+        sizes: dict[torch.dtype, int] = {}
+        for lf in self.leaves:
+            sizes[lf.out_dtype] = sizes.get(lf.out_dtype, 0) + (math.prod(lf.shape) + 63) // 64 * 64
+        for dt, n in sizes.items():
+            self.flat[dt] = torch.empty(max(n, 1), dtype=dt, device=dev)
+        self.out: list[torch.Tensor] = []
+        cursor = dict.fromkeys(sizes, 0)
+        for lf in self.leaves:
+            n = math.prod(lf.shape)
+            c = cursor[lf.out_dtype]
+            self.out.append(self.flat[lf.out_dtype][c : c + n].view(lf.shape))
+            cursor[lf.out_dtype] = c + (n + 63) // 64 * 64
+        self.out2: list[torch.Tensor] | None = None
+        if self.second_moment:
+            self.out2 = [torch.empty(lf.shape, dtype=lf.out_dtype, device=dev) for lf in self.leaves]
+
+        G, C, E = self.n_groups, self.n_cls, seg.n_ex
+        self.scales = torch.empty((C, G, E), dtype=torch.float32, device=dev)
+        self.norms = torch.empty(E, dtype=torch.float32, device=dev)
+        self.group_norms = torch.empty((G, E), dtype=torch.float32, device=dev)
+        self.clipped = torch.empty((G, E), dtype=torch.uint8, device=dev)
+        self.clipped_total = torch.empty(E, dtype=torch.uint8, device=dev)
+
+        # Q planes (U and V) for every chunk, carved from one allocation per dtype.
+        q_need: dict[torch.dtype, int] = {}
+        chunk_layout = []
+        for ch in chunks:
+            dt = ch[0].x.dtype
+            rtot = sum(s.A.shape[1] for s in ch)
+            rows_alloc = (rtot + 15) // 16 * 16 + 16
+            planes = 2 if dt == torch.bfloat16 else 1
+            per = planes * rows_alloc * ldq
+            base = q_need.get(dt, 0)
+            chunk_layout.append((dt, rtot, rows_alloc, planes, base, base + per))
+            q_need[dt] = base + 2 * per
+        self.qbuf = {dt: torch.empty(max(n, 1), dtype=dt, device=dev) for dt, n in q_need.items()}
+
+        # Problem tables, per activation dtype.
+        pj = {dt: _Table(N.PJ_FIELDS) for dt in q_need}
+        ft = {dt: _Table(N.FT_FIELDS) for dt in q_need}
+        lib = N.load()
+        elem = {torch.bfloat16: 2, torch.float32: 4}
+        for ch, (dt, rtot, rows_alloc, planes, vbase, ubase) in zip(chunks, chunk_layout):
+            qb = self.qbuf[dt]
+            es = elem[dt]
+            plane = rows_alloc * ldq
+
+            def qaddr(base: int, row: int, lo: bool) -> int:
+                return qb.data_ptr() + (base + (plane if lo else 0) + row * ldq) * es
+
+            x = _rows(ch[0].x)
+            self._keep.append(x)
+            d_in = x.shape[1]
+            # V = X [A_1 .. A_k]
+            wx = torch.cat([s.A.detach().to(dt).t() for s in ch], dim=0).contiguous()
+            self._keep.append(wx)
+            pj[dt].add(
+                {
+                    N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
+                    N.PJ_W: wx.data_ptr(), N.PJ_R: rtot,
+                    N.PJ_Q: qaddr(vbase, 0, False), N.PJ_QLO: qaddr(vbase, 0, True),
+                    N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: 0, N.PJ_NSEG: n_seg,
+                },
+                lib.odp_project_blocks(n_rows),
+            )
+            c0 = 0
+            a_leaves = []
+            for s in ch:
+                r = s.A.shape[1]
+                g = _rows(s.g)
+                self._keep.append(g)
+                wb = s.B.detach().to(dt).contiguous()
+                self._keep.append(wb)
+                d_out = g.shape[1]
+                # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
+                pj[dt].add(
+                    {
+                        N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
+                        N.PJ_W: wb.data_ptr(), N.PJ_R: r,
+                        N.PJ_Q: qaddr(ubase, c0, False), N.PJ_QLO: qaddr(ubase, c0, True),
+                        N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: 0, N.PJ_NSEG: n_seg,
+                    },
+                    lib.odp_project_blocks(n_rows),
+                )
+                if s.a_leaf is not None:
+                    a_leaves.append((s.a_leaf, c0, r))
+                if s.b_leaf is not None:
+                    # dB_i^T rows: pe[s][k][m] = scaling * sum_t V[k][t] G[t][m]
+                    row = {
+                        N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
+                        N.FT_Q: qaddr(vbase, c0, False), N.FT_QLO: qaddr(vbase, c0, True),
+                        N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: 0, N.FT_NSEG: n_seg,
+                        N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
+                        N.FT_LEAF0: self.pe.data_ptr() + pe_off[s.b_leaf] * 4,
+                        N.FT_LEAF0 + 1: 0 | (r << 16),
+                        N.FT_LEAF0 + 2: slot_base[s.b_leaf],
+                    }
+                    ft[dt].add(row, n_seg * lib.odp_seg_factor_tiles(d_out))
+                c0 += r
+            if a_leaves:
+                scal = {s.scaling for s in ch if s.a_leaf is not None}
+                if len(scal) != 1:
+                    # Different scalings cannot share one pass: split them.
+                    for s_leaf, col0, r in a_leaves:
+                        sc = next(s.scaling for s in ch if s.a_leaf == s_leaf)
+                        ft[dt].add(self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, n_seg, sc,
+                                               [(s_leaf, col0, r)], pe_off, slot_base),
+                                   n_seg * lib.odp_seg_factor_tiles(d_in))
+                else:
+                    ft[dt].add(self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, n_seg, scal.pop(),
+                                           a_leaves, pe_off, slot_base),
+                               n_seg * lib.odp_seg_factor_tiles(d_in))
+
+        sq = _Table(N.SQ_FIELDS)
+        mat_pe: dict[int, torch.Tensor] = {}
+        for m in mats:
+            pe_m = m.per_example.detach()
+            if pe_m.dtype not in _DTYPE_CODE:
+                pe_m = pe_m.float()
+            pe_m = pe_m.reshape(n_seg, -1).contiguous()
+            self._keep.append(pe_m)
+            n = pe_m.shape[1]
+            sq.add(
+                {
+                    N.SQ_X: pe_m.data_ptr(), N.SQ_N: n, N.SQ_NSEG: n_seg, N.SQ_SEG_FIRST: 0,
+                    N.SQ_SLOT: slot_base[m.leaf], N.SQ_DTYPE: dtype_code(pe_m.dtype),
+                },
+                n_seg * lib.odp_sqnorm_blocks(n),
+            )
+            mat_pe[m.leaf] = pe_m
+
+        ss = _Table(N.SS_FIELDS)
+        for i, lf in enumerate(self.leaves):
+            out = self.out[i]
+            out2 = self.out2[i].data_ptr() if self.out2 is not None else 0
+            if i in mat_pe:
+                pe_m = mat_pe[i]
+                rank, M, transpose, pdt, pe_addr = 1, pe_m.shape[1], 0, dtype_code(pe_m.dtype), pe_m.data_ptr()
+            else:
+                rank, M = leaf_rank_m[i]
+                transpose = 1 if self._leaf_transposed(i, sites) else 0
+                pdt, pe_addr = N.DTYPE_F32, self.pe.data_ptr() + pe_off[i] * 4
+            flags = dtype_code(lf.out_dtype) | (transpose << 8) | (lf.group << 16) | (lf.cls << 40) | (pdt << 56)
+            ss.add(
+                {
+                    N.SS_PE: pe_addr, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: 0,
+                    N.SS_NSEG: n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2,
+                },
+                lib.odp_scale_sum_blocks(rank * M),
+            )
+
+        # Upload everything in one copy.
+        pack = _Pack()
+        idx = {}
+        idx["seg_start"] = pack.add(np.asarray(seg.starts, dtype=np.int32).reshape(-1))
+        idx["seg_len"] = pack.add(np.asarray(seg.lengths, dtype=np.int32).reshape(-1))
+        idx["seg_ex"] = pack.add(np.asarray(seg.examples, dtype=np.int32).reshape(-1))
+        self._launch: list[tuple] = []
+        tabs = []
+        for dt in q_need:
+            tabs.append(("project", dt, pj[dt]))
+            tabs.append(("factor", dt, ft[dt]))
+        tabs.append(("sqnorm", None, sq))
+        tabs.append(("scale_sum", None, ss))
+        tab_idx = []
+        for name, dt, t in tabs:
+            probs, ws, total = t.arrays()
+            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total))
+        idx["gstart"] = pack.add(gstart)
+        idx["thr"] = pack.add(np.asarray(self.clip.thresholds, dtype=np.float64))
+        guards = self.clip.guards or [(1.0, 0.0, torch.float32)]
+        idx["guard"] = pack.add(np.asarray([[g[0], g[1]] for g in guards], dtype=np.float64).reshape(-1))
+        idx["cls_dt"] = pack.add(np.asarray([dtype_code(g[2]) for g in guards], dtype=np.int32))
+        views = pack.upload(dev)
+        self._views = views
+        self._host = pack._host
+        self.seg_start, self.seg_len, self.seg_ex = (views[idx[k]] for k in ("seg_start", "seg_len", "seg_ex"))
+        self.gstart, self.thr = views[idx["gstart"]], views[idx["thr"]]
+        self.guard, self.cls_dt = views[idx["guard"]], views[idx["cls_dt"]]
+        self.tables = [(name, dt, views[pi], views[wi], n, total) for name, dt, pi, wi, n, total in tab_idx]
+
+    def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, n_seg, scaling, leaves, pe_off, slot_base):
+        row = {
+            N.FT_P: x.data_ptr(), N.FT_LDP: x.stride(0), N.FT_M: d_in,
+            N.FT_Q: qaddr(ubase, col0, False), N.FT_QLO: qaddr(ubase, col0, True),
+            N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: 0, N.FT_NSEG: n_seg,
+            N.FT_SCALING: _f64_bits(scaling), N.FT_NLEAF: len(leaves),
+        }
+        for li, (leaf, c, rk) in enumerate(sorted(leaves, key=lambda t: t[1])):
+            row[N.FT_LEAF0 + 3 * li] = self.pe.data_ptr() + pe_off[leaf] * 4
+            row[N.FT_LEAF0 + 3 * li + 1] = (c - col0) | (rk << 16)
+            row[N.FT_LEAF0 + 3 * li + 2] = slot_base[leaf]
+        return row
+
+    def _leaf_transposed(self, i: int, sites: list[LoraSite]) -> bool:
+        # pe rows are [r][M]; A leaves [d_in, r] need the transpose, B leaves [r, d_out] do not.
+        for s in sites:
+            if s.a_leaf == i:
+                return not s.a_transposed
+            if s.b_leaf == i:
+                return s.b_transposed
+        return False
+
+    # -- execution -------------------------------------------------------------
+    def run(self, events: dict | None = None) -> GhostResult:
+        """Launch the step on the current stream.
+
+        ``events`` may map a stage name ("project", "factor", "sqnorm",
+        "clip", "scale_sum") to a (start, end) pair of torch.cuda.Event that
+        are recorded around that stage's launch.
+        """
+        lib = N.load()
+        stream = _stream()
+        seg = self.segments
+        ev = events or {}
+        self.part.zero_()
+        for name, dt, probs, ws, n, total in self.tables:
+            if total == 0 or name == "scale_sum":
+                continue
+            if name in ev:
+                ev[name][0].record()
+            if name == "project":
+                N.check(lib.odp_project(stream, dtype_code(dt), probs.data_ptr(), ws.data_ptr(), n, total,
+                                        self.seg_start.data_ptr(), self.seg_len.data_ptr()), name)
+            elif name == "factor":
+                N.check(lib.odp_seg_factor(stream, dtype_code(dt), probs.data_ptr(), ws.data_ptr(), n, total,
+                                           self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                           self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
+            elif name == "sqnorm":
+                N.check(lib.odp_sqnorm(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                       self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
+            if name in ev:
+                ev[name][1].record()
+        if "clip" in ev:
+            ev["clip"][0].record()
+        N.check(
+            lib.odp_clip_factors(
+                stream, self.part.data_ptr(), self.n_slots, seg.n_ex, self.gstart.data_ptr(), self.n_groups,
+                self.thr.data_ptr(), float(self.clip.effective), int(self.clip.mode), float(self.clip.gamma),
+                self.n_cls, self.guard.data_ptr(), self.cls_dt.data_ptr(), self.scales.data_ptr(),
+                self.norms.data_ptr(), self.group_norms.data_ptr(), self.clipped.data_ptr(),
+                self.clipped_total.data_ptr(),
+            ),
+            "odp_clip_factors",
+        )
+        if "clip" in ev:
+            ev["clip"][1].record()
+        for name, dt, probs, ws, n, total in self.tables:
+            if name == "scale_sum" and total:
+                if name in ev:
+                    ev[name][0].record()
+                N.check(lib.odp_scale_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                          self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
+                                          self.n_groups, float(self.clip.normalize_by)), name)
+                if name in ev:
+                    ev[name][1].record()
+        return GhostResult(
+            leaves=self.out,
+            norms=self.norms,
+            group_norms=self.group_norms,
+            clipped=self.clipped,
+            clipped_total=self.clipped_total,
+            scales=self.scales,
+            second_moment=self.out2,
+            flat=self.flat,
+        )
+
+
+__all__ = [
+    "ClipSpec",
+    "GhostPlan",
+    "GhostResult",
+    "LeafOut",
+    "LoraSite",
+    "MaterializedLeaf",
+    "Segments",
+    "dtype_code",
+    "supports_rows",
+]
