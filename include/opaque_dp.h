@@ -98,7 +98,8 @@ enum {
 int64_t odp_project_blocks(int64_t n_rows);
 int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
                 const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
-                const int32_t* seg_row_start, const int32_t* seg_row_len);
+                const int32_t* seg_row_start, const int32_t* seg_row_len,
+                int32_t max_rank /* max ODP_PJ_R over the table, <= 64 */);
 
 /* ---- odp_seg_factor: per-segment factor gradients and norm partials -----
  * For every segment s and column k < r of Q (up to 4 leaves laid side by

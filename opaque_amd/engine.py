@@ -253,7 +253,10 @@ class GhostPlan:
         second_moment: bool = False,
     ) -> None:
         N.load()
-        self.device = torch.device(device)
+        dev = torch.device(device)
+        if dev.type == "cuda" and dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.device = dev
         self.segments = segments
         self.leaves = leaves
         self.clip = clip
@@ -520,6 +523,7 @@ class GhostPlan:
         tabs.append(("sqnorm", None, sq))
         tabs.append(("scale_sum", None, ss))
         tab_idx = []
+        self.max_rank = {dt: max([row[N.PJ_R] for row in pj[dt].rows] or [1]) for dt in q_need}
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
             tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total))
@@ -578,7 +582,8 @@ class GhostPlan:
                 ev[name][0].record()
             if name == "project":
                 N.check(lib.odp_project(stream, dtype_code(dt), probs.data_ptr(), ws.data_ptr(), n, total,
-                                        self.seg_start.data_ptr(), self.seg_len.data_ptr()), name)
+                                        self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                        self.max_rank[dt]), name)
             elif name == "factor":
                 N.check(lib.odp_seg_factor(stream, dtype_code(dt), probs.data_ptr(), ws.data_ptr(), n, total,
                                            self.seg_start.data_ptr(), self.seg_len.data_ptr(),
