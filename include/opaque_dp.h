@@ -96,10 +96,10 @@ enum {
   ODP_PJ_FIELDS = 12
 };
 int64_t odp_project_blocks(int64_t n_rows);
+/* Every problem of one table must have ceil(ODP_PJ_R / 16) == nkb (1..4). */
 int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
                 const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
-                const int32_t* seg_row_start, const int32_t* seg_row_len,
-                int32_t max_rank /* max ODP_PJ_R over the table, <= 64 */);
+                const int32_t* seg_row_start, const int32_t* seg_row_len, int32_t nkb);
 
 /* ---- odp_seg_factor: per-segment factor gradients and norm partials -----
  * For every segment s and column k < r of Q (up to 4 leaves laid side by
@@ -122,11 +122,14 @@ enum {
   ODP_FT_QLO = 22,    /* lo plane of Q (bf16 only)                           */
   ODP_FT_FIELDS = 24
 };
-int64_t odp_seg_factor_tiles(int64_t M);
+/* M-tiles (and partial slots per leaf) of a problem; the bf16 tile width
+ * depends on the rank.  Every problem of one table must have
+ * ceil(ODP_FT_R / 16) == nkb (1..4).                                       */
+int64_t odp_seg_factor_tiles(int dtype, int64_t M, int32_t r);
 int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
                    const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                    const int32_t* seg_row_start, const int32_t* seg_row_len,
-                   const int32_t* seg_example, double* part, int64_t part_stride);
+                   const int32_t* seg_example, double* part, int64_t part_stride, int32_t nkb);
 
 /* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
  * For leaves that are not behind a captured linear op, the per-example

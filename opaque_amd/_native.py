@@ -47,10 +47,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_last_error": (ctypes.c_char_p, []),
     "odp_project_blocks": (_c_i64, [_c_i64]),
     "odp_project": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i32]),
-    "odp_seg_factor_tiles": (_c_i64, [_c_i64]),
+    "odp_seg_factor_tiles": (_c_i64, [_c_int, _c_i64, _c_i32]),
     "odp_seg_factor": (
         _c_int,
-        [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64],
+        [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64, _c_i32],
     ),
     "odp_sqnorm_blocks": (_c_i64, [_c_i64]),
     "odp_sqnorm": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i64]),

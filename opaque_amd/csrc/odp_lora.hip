@@ -7,8 +7,10 @@
 // materialised with torch.bmm under vmap).  Both are skinny products whose
 // long dimension is a row of X or G, so the work is HBM-bound: each kernel
 // streams X or G and keeps the rank-r side (U, V, the r x M output tile) on
-// chip.  Both kernels keep two pipeline steps of loads in flight per wave so
-// that enough bytes are outstanding per CU to approach HBM bandwidth.
+// chip.  The bf16 kernels are instantiated per rank block count NKB =
+// ceil(r / 16) so that registers match the rank, and keep two pipeline steps
+// of loads in flight per wave so that enough bytes are outstanding per CU to
+// approach HBM bandwidth.
 //
 //   k_project_*  : Q^T = (P W^T)^T for every row of a segment      (U, V)
 //   k_factor_*   : pe[s] = s * Q_s^T P_s per segment, plus fp64 sums of
@@ -20,31 +22,63 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 namespace {
 
-constexpr int PJ_ROWS = 64;             // rows per project workgroup (4 waves x 16)
-constexpr int PJ_KS = 128;              // contraction elements per bf16 pipeline step
-constexpr int PJ_WPITCH = PJ_KS + 8;    // u16 per staged W row
-constexpr int FT_M = 128;               // M columns per factor workgroup
-constexpr int FT_T = 32;                // tokens per bf16 factor step (MFMA K)
-constexpr int FT_PP = FT_M + 4;         // u16 pitch of the staged P tile [t][m]
-constexpr int FT_QP = FT_T + 8;         // u16 pitch of the staged Q tile [k][t]
-constexpr int FT_QROWS = 64;            // staged Q rows per plane (r <= 64)
-constexpr int FT_PTILE = FT_T * FT_PP;  // u16 per staged P tile
-constexpr int FT_STAGE = FT_PTILE + 2 * FT_QROWS * FT_QP;
+#ifndef ODP_PJ_KS
+#define ODP_PJ_KS 128  // contraction elements per bf16 project step
+#endif
+#ifndef ODP_PJ_DEPTH
+#define ODP_PJ_DEPTH 2  // project steps of P loads in flight per wave (1 or 2)
+#endif
+#ifndef ODP_FT_T
+#define ODP_FT_T 32  // tokens per bf16 factor step (a multiple of the MFMA K, 32)
+#endif
+constexpr int PJ_ROWS = 64;   // rows per project workgroup (4 waves x 16)
+constexpr int FT_T = ODP_FT_T;
+constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 
-__device__ __forceinline__ u32x4_t ld16(const void* p) { return *(const u32x4_t*)p; }
+// bf16 project: contraction elements per pipeline step, by rank blocks.
+__host__ __device__ constexpr int pj_ks(int nkb) { return nkb <= 2 ? 256 : 128; }
+__host__ __device__ constexpr int pj_pitch(int nkb) { return pj_ks(nkb) + 8; }
+// bf16 factor: 16-wide m blocks per wave (M-tile = 64 * NJ), by rank blocks.
+__host__ __device__ constexpr int ft_nj(int nkb) { return nkb > 0 ? 2 : 2; }  // 128-wide M-tile
+
+// Table pointers arrive as integers (generic address space); loads through
+// them are issued as global (not flat) loads so that they only count in
+// vmcnt and the compiler can keep a prefetch in flight across LDS traffic.
+#define ODP_GLOBAL __attribute__((address_space(1)))
+__device__ __forceinline__ u32x4_t ld16(const void* p) {
+  return *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)p;
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16
+// lanes, lane i receives v[j] = (4 x b16 chunk addressed by lane (i >> 2) + 4j)
+// element (i & 3).  If lane c of the group addresses row (c >> 2), columns
+// 4 (c & 3) .. +3 of a row-major [t][m] tile, lane i therefore receives
+// column i of 4 consecutive rows: the K-contiguous MFMA operand layout.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+#define ODP_LDS __attribute__((address_space(3)))
+__device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((ODP_LDS v4i16_t*)(ODP_LDS void*)p);
+}
 
 // ---------------------------------------------------------------------------
 // Projection, bf16: MFMA 16x16x32 bf16 with fp32 accumulation.  Each wave
-// owns 16 rows and the full contraction; P rows feed the MFMA A operand
-// straight from global memory (row-major P already has the K-contiguous
-// layout the operand needs), W is staged through LDS once per workgroup per
-// 128-wide step.  Loads of step s+1 are issued before step s is computed.
+// owns 16 rows and the full contraction.  P is read with fully coalesced
+// loads (each instruction covers 4 rows x 256 contiguous bytes) into
+// registers one step ahead, then written to a wave-private LDS tile from
+// which each lane picks its MFMA A operand (row lane & 15, 8 consecutive k).
+// W is staged through LDS once per workgroup per step.  All loads are
+// branch-free (clamped addresses, data zeroed when consumed).
 // ---------------------------------------------------------------------------
+template <int NKB>
 __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict__ probs,
                                                       const int32_t* __restrict__ ws, int n_prob,
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t wlds[];  // [2][rp][PJ_WPITCH]
+  constexpr int KS = ODP_PJ_KS, WPITCH = KS + 8, PPITCH = KS + 8, RP = 16 * NKB;
+  constexpr int NPR = KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
+  constexpr int NW = (RP * (KS / 8) + 255) / 256;  // W pieces per thread per step
+  __shared__ __attribute__((aligned(16))) uint16_t wlds[2 * RP * WPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t plds[4 * 16 * PPITCH];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_PJ_FIELDS;
@@ -59,88 +93,131 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row0 = (int64_t)(bid - ws[p]) * PJ_ROWS + 16 * wave;
-  const int64_t my_row = row0 + (lane & 15);
-  const bool valid = my_row < n_rows &&
-                     odp_row_in_segments(my_row, sstart + seg_first, slen + seg_first, n_seg);
-  if (!__syncthreads_or(valid ? 1 : 0)) return;  // whole block is padding
+  // Lane i < 16 tests row row0 + i; the wave shares the answers as a bit mask.
+  const int64_t test_row = row0 + (lane & 15);
+  const bool tvalid = test_row < n_rows &&
+                      odp_row_in_segments(test_row, sstart + seg_first, slen + seg_first, n_seg);
+  const uint64_t vmask = __ballot(tvalid && lane < 16);
+  if (!__syncthreads_or(vmask != 0 ? 1 : 0)) return;  // the whole block is padding
 
-  const int nkb = (r + 15) >> 4, rp = nkb * 16;
-  const int kq = (lane >> 4) * 8;
-  const uint16_t* prow = P + (valid ? my_row : 0) * ldp;
-  const int64_t nsteps = (d + PJ_KS - 1) / PJ_KS;
-
-  f32x4_t acc[4];
+  // Load mapping: instruction i covers rows 4(i % 4) + (lane >> 4), 16 lanes x
+  // 16 B per row, at column block i / 4 of the step.
+  const int lr = lane >> 4, piece = lane & 15;
+  const uint16_t* prow[4];
+  bool rowok[4];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) acc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto load_p = [&](int64_t s, u32x4_t(&pa)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t k = s * PJ_KS + 32 * i + kq;
-      pa[i] = (valid && k < d) ? ld16(prow + k) : u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  auto load_w = [&](int64_t s, u32x4_t(&wr)[4]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int id = tid + 256 * q;
-      const int row = id >> 4, col = (id & 15) * 8;
-      const int64_t k = s * PJ_KS + col;
-      wr[q] = (row < r && k < d) ? ld16(W + (int64_t)row * d + k) : u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store_w = [&](int b, const u32x4_t(&wr)[4]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int id = tid + 256 * q;
-      if (id < rp * 16) {
-        const int row = id >> 4, col = (id & 15) * 8;
-        *(u32x4_t*)&wlds[(b * rp + row) * PJ_WPITCH + col] = wr[q];
-      }
-    }
-  };
-  auto compute = [&](int b, const u32x4_t(&pa)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, pa[i]);
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        if (kb < nkb) {
-          const u32x4_t bv = *(const u32x4_t*)&wlds[(b * rp + kb * 16 + (lane & 15)) * PJ_WPITCH + 32 * i + kq];
-          acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv),
-                                                            acc[kb], 0, 0, 0);
-        }
-      }
-    }
-  };
-
-  u32x4_t pa0[4], pa1[4], wr[4];
-  load_p(0, pa0);
-  load_w(0, wr);
-  for (int64_t s = 0; s < nsteps; s += 2) {
-    store_w(0, wr);
-    __syncthreads();
-    if (s + 1 < nsteps) {
-      load_p(s + 1, pa1);
-      load_w(s + 1, wr);
-    }
-    compute(0, pa0);
-    if (s + 1 >= nsteps) break;
-    store_w(1, wr);
-    __syncthreads();
-    if (s + 2 < nsteps) {
-      load_p(s + 2, pa0);
-      load_w(s + 2, wr);
-    }
-    compute(1, pa1);
+  for (int i = 0; i < 4; ++i) {
+    const int rl = 4 * i + lr;
+    rowok[i] = (vmask >> rl) & 1;
+    prow[i] = P + (rowok[i] ? row0 + rl : 0) * ldp;
   }
+  uint16_t* pw = plds + wave * 16 * PPITCH;
+  const int kq = (lane >> 4) * 8;
+  const int64_t nsteps = (d + KS - 1) / KS;
+
+  f32x4_t acc[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) acc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto load_p = [&](int64_t s, u32x4_t(&pr)[NPR]) {
+#pragma unroll
+    for (int i = 0; i < NPR; ++i) {
+      const int64_t k = s * KS + 128 * (i / 4) + 8 * piece;
+      pr[i] = ld16(prow[i % 4] + (k < d ? k : d - 8));
+    }
+  };
+  auto store_p = [&](int64_t s, const u32x4_t(&pr)[NPR]) {
+#pragma unroll
+    for (int i = 0; i < NPR; ++i) {
+      const int c = 128 * (i / 4) + 8 * piece;
+      const bool ok = rowok[i % 4] && s * KS + c < d;
+      *(u32x4_t*)&pw[(4 * (i % 4) + lr) * PPITCH + c] = ok ? pr[i] : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto load_w = [&](int64_t s, u32x4_t(&wr)[NW]) {
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const int id = (tid + 256 * q) % (RP * (KS / 8));
+      const int row = id / (KS / 8), col = (id % (KS / 8)) * 8;
+      const int64_t k = s * KS + col;
+      wr[q] = ld16(W + (int64_t)(row < r ? row : 0) * d + (k < d ? k : d - 8));
+    }
+  };
+  auto store_w = [&](int b, int64_t s, const u32x4_t(&wr)[NW]) {
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const int id = tid + 256 * q;
+      if (id < RP * (KS / 8)) {
+        const int row = id / (KS / 8), col = (id % (KS / 8)) * 8;
+        const bool ok = row < r && s * KS + col < d;
+        *(u32x4_t*)&wlds[(b * RP + row) * WPITCH + col] = ok ? wr[q] : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto compute = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < KS / 32; ++i) {
+      const u32x4_t av = *(const u32x4_t*)&pw[(lane & 15) * PPITCH + 32 * i + kq];
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const u32x4_t bv =
+            *(const u32x4_t*)&wlds[(b * RP + kb * 16 + (lane & 15)) * WPITCH + 32 * i + kq];
+        acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv),
+                                                          acc[kb], 0, 0, 0);
+      }
+    }
+  };
+
+  // W of a step is issued before its P rows; prefetch indices are clamped to
+  // the last step instead of branching (surplus loads are discarded).
+  const int64_t last = nsteps - 1;
+#if ODP_PJ_DEPTH == 1
+  u32x4_t pr[NPR], wr[NW];
+  load_w(0, wr);
+  load_p(0, pr);
+  for (int64_t s = 0; s < nsteps; ++s) {
+    const int b = (int)(s & 1);
+    store_w(b, s, wr);
+    store_p(s, pr);
+    __syncthreads();
+    const int64_t nx = s + 1 < last ? s + 1 : last;
+    load_w(nx, wr);
+    load_p(nx, pr);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    compute(b);
+  }
+#else
+  // Two steps of P in flight: P(s+2) is issued while P(s+1) is still loading.
+  u32x4_t pa[NPR], pb[NPR], wr[NW];
+  load_w(0, wr);
+  load_p(0, pa);
+  load_p(1 < last ? 1 : last, pb);
+  for (int64_t s = 0; s < nsteps; s += 2) {
+    store_w(0, s, wr);
+    store_p(s, pa);
+    __syncthreads();
+    load_w(s + 1 < last ? s + 1 : last, wr);
+    load_p(s + 2 < last ? s + 2 : last, pa);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    compute(0);
+    if (s + 1 >= nsteps) break;
+    store_w(1, s + 1, wr);
+    store_p(s + 1, pb);
+    __syncthreads();
+    load_w(s + 2 < last ? s + 2 : last, wr);
+    load_p(s + 3 < last ? s + 3 : last, pb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+  }
+#endif
 
   // lane holds D[4*(lane>>4) + i][lane & 15] of each 16x16 block
   const int64_t rb = row0 + 4 * (lane >> 4);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
+  for (int kb = 0; kb < NKB; ++kb) {
     const int col = kb * 16 + (lane & 15);
-    if (kb < nkb && col < r) {
+    if (col < r) {
       uint16_t* qhi = Q + (int64_t)col * ldq;
       uint16_t* qlo = Qlo + (int64_t)col * ldq;
 #pragma unroll
@@ -218,6 +295,10 @@ __global__ __launch_bounds__(256) void k_project_f32(const int64_t* __restrict__
 
 // Shared epilogue of the factor kernels: scale, store per-leaf rows, and
 // reduce the squared values per leaf in a fixed order.
+
+// Shared epilogue of the factor kernels: scale, store per-leaf rows, and
+// reduce the squared values per leaf in a fixed order.  Wave w owns the
+// 16-wide m blocks w*NJ .. w*NJ + NJ - 1 of the workgroup's M-tile.
 struct FactorLeaves {
   int n;
   float* pe[4];
@@ -241,31 +322,38 @@ __device__ __forceinline__ FactorLeaves read_leaves(const int64_t* f) {
   return L;
 }
 
-__device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[2][4], int nkb, int r,
-                                                float scale, int64_t M, int64_t m_base,
-                                                int seg, int tile, int ex, int64_t part_stride,
+template <int NJ, int NKB>
+__device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], int r, float scale,
+                                                int64_t M, int64_t m_base, int seg, int tile,
+                                                int ex, int64_t part_stride,
                                                 const FactorLeaves& L, double* __restrict__ part) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ double colsq[4][64];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    if (kb >= nkb) continue;
+  for (int kb = 0; kb < NKB; ++kb) {
     double cs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       cs[i] = 0.0;
       const int k = kb * 16 + 4 * (lane >> 4) + i;
       if (k >= r) continue;
-      int l = 0;
+      // Leaf owning column k (leaves are sorted by col0); selected without
+      // dynamic indexing so the descriptor stays in registers.
+      float* lpe = L.pe[0];
+      int lc0 = L.col0[0], lrk = L.rank[0];
 #pragma unroll
       for (int q = 1; q < 4; ++q)
-        if (q < L.n && k >= L.col0[q]) l = q;
+        if (q < L.n && k >= L.col0[q]) {
+          lpe = L.pe[q];
+          lc0 = L.col0[q];
+          lrk = L.rank[q];
+        }
       // Columns of frozen factors between leaves belong to no leaf.
-      if (k < L.col0[l] || k - L.col0[l] >= L.rank[l]) continue;
-      float* dst = L.pe[l] + ((int64_t)seg * L.rank[l] + (k - L.col0[l])) * M;
+      if (k < lc0 || k - lc0 >= lrk) continue;
+      float* dst = lpe + ((int64_t)seg * lrk + (k - lc0)) * M;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t m = m_base + (2 * wave + j) * 16 + (lane & 15);
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
         if (m < M) {
           const float v = scale * acc[j][kb][i];
           dst[m] = v;
@@ -289,33 +377,39 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[2][4], int 
   }
   __syncthreads();
   const int t = threadIdx.x;
-  if (t < L.n) {
-    double total = 0.0;
-    for (int k = L.col0[t]; k < L.col0[t] + L.rank[t]; ++k)
-      for (int w = 0; w < 4; ++w) total += colsq[w][k];
-    part[(int64_t)ex * part_stride + L.slot[t] + tile] = total;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (t == q && q < L.n) {
+      double total = 0.0;
+      for (int k = L.col0[q]; k < L.col0[q] + L.rank[q]; ++k)
+        for (int w = 0; w < 4; ++w) total += colsq[w][k];
+      part[(int64_t)ex * part_stride + L.slot[q] + tile] = total;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Factor gradients, bf16 P: MFMA 16x16x32 with K = 32 tokens.  Per step the
-// workgroup stages the P tile [32 tokens x 128 m] and the Q^T tile (hi and
-// lo planes, [rp x 32 tokens]) through LDS; each lane then gathers its 8
-// consecutive tokens of one column for the B operand.  Two steps of loads
-// are in flight while a third is computed.
+// Factor gradients, bf16 P: MFMA 16x16x32 with K = 32 tokens per step.  Per
+// step the workgroup stages the P tile [32 tokens x 128 m] and the Q^T tile
+// (hi and lo planes, [16*NKB x 32 tokens]) through LDS; each lane gathers its
+// 8 consecutive tokens of one column for the B operand.  Loads run two steps
+// ahead of the compute; the token mask is applied when a stage is written to
+// LDS (never right after its load, which would stall the prefetch).
 // ---------------------------------------------------------------------------
-struct FactorStage {
-  u32x4_t p[2];
-  u32x4_t q[2];
-};
-
-__global__ __launch_bounds__(256, 4) void k_factor_bf16(const int64_t* __restrict__ probs,
+template <int NKB>
+__global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__ probs,
                                                      const int32_t* __restrict__ ws, int n_prob,
                                                      const int32_t* __restrict__ sstart,
                                                      const int32_t* __restrict__ slen,
                                                      const int32_t* __restrict__ sex,
                                                      double* __restrict__ part, int64_t part_stride) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * FT_STAGE];
+  constexpr int NJ = ft_nj(NKB), MT = 64 * NJ, PP = MT + 4;
+  constexpr int QP = FT_T + 8, QROWS = 16 * NKB;
+  constexpr int PTILE = FT_T * PP, STAGE = PTILE + 2 * QROWS * QP;
+  constexpr int NPP = NJ * FT_T / 32;                 // P pieces per thread per step
+  constexpr int QPC = FT_T / 8;                       // Q pieces per row per step
+  constexpr int NQP = (2 * QPC * QROWS + 255) / 256;  // Q pieces per thread per step
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_FT_FIELDS;
@@ -328,120 +422,133 @@ __global__ __launch_bounds__(256, 4) void k_factor_bf16(const int64_t* __restric
   const int seg_first = (int)f[ODP_FT_SEG_FIRST];
   const float scale = (float)__longlong_as_double(f[ODP_FT_SCALING]);
 
-  const int ntile = (int)((M + FT_M - 1) / FT_M);
+  const int ntile = (int)((M + MT - 1) / MT);
   const int local = bid - ws[p];
   const int seg = local / ntile, tile = local % ntile;
   const int gs = seg_first + seg;
   const int64_t rs = sstart[gs], t_hi = rs + slen[gs];
   const int ex = sex[gs];
-  const int64_t m_base = (int64_t)tile * FT_M;
-  const int nkb = (r + 15) >> 4, rp = nkb * 16;
+  const int64_t m_base = (int64_t)tile * MT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t_lo = rs & ~(int64_t)7;
   const int64_t nchunk = t_hi > rs ? (t_hi - t_lo + FT_T - 1) / FT_T : 0;
 
-  auto load = [&](int64_t c, FactorStage& S) {
+  struct Stage {
+    u32x4_t p[NPP];
+    u32x4_t q[NQP];
+  };
+  // Loads are branch-free (addresses clamped in bounds); rows outside the
+  // segment and columns past M are zeroed when the stage is written to LDS.
+  auto load = [&](int64_t c, Stage& S) {
     const int64_t t0 = t_lo + c * FT_T;
 #pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
+    for (int ps = 0; ps < NPP; ++ps) {
       const int id = tid + 256 * ps;
-      const int64_t t = t0 + (id >> 4);
-      const int64_t m = m_base + (id & 15) * 8;
-      S.p[ps] = (t >= rs && t < t_hi && m < M) ? ld16(P + t * ldp + m) : u32x4_t{0u, 0u, 0u, 0u};
+      int64_t t = t0 + id / (MT / 8);
+      t = t < rs ? rs : (t >= t_hi ? t_hi - 1 : t);
+      const int64_t m = m_base + (id % (MT / 8)) * 8;
+      S.p[ps] = ld16(P + t * ldp + (m < M ? m : M - 8));
     }
 #pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
+    for (int ps = 0; ps < NQP; ++ps) {
+      const int id = (tid + 256 * ps) % (2 * QPC * QROWS);
+      const int plane = id / (QPC * QROWS), rem = id % (QPC * QROWS);
+      const int row = rem / QPC, pc = rem % QPC;
+      S.q[ps] = ld16((plane ? Qlo : Q) + (int64_t)row * ldq + t0 + 8 * pc);
+    }
+  };
+  auto store = [&](int b, int64_t c, const Stage& S) {
+    uint16_t* st = lds + b * STAGE;
+    const int64_t t0 = t_lo + c * FT_T;
+#pragma unroll
+    for (int ps = 0; ps < NPP; ++ps) {
       const int id = tid + 256 * ps;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (id < 8 * rp) {
-        const int plane = id / (4 * rp), rem = id - plane * 4 * rp;
-        const int row = rem >> 2, pc = rem & 3;
+      const int64_t t = t0 + id / (MT / 8);
+      const bool ok = t >= rs && t < t_hi && m_base + (id % (MT / 8)) * 8 < M;
+      const u32x4_t v = ok ? S.p[ps] : u32x4_t{0u, 0u, 0u, 0u};
+      u32x2_t* dst = (u32x2_t*)&st[(id / (MT / 8)) * PP + (id % (MT / 8)) * 8];
+      dst[0] = u32x2_t{v[0], v[1]};
+      dst[1] = u32x2_t{v[2], v[3]};
+    }
+#pragma unroll
+    for (int ps = 0; ps < NQP; ++ps) {
+      const int id = tid + 256 * ps;
+      if (id < 2 * QPC * QROWS) {
+        const int plane = id / (QPC * QROWS), rem = id % (QPC * QROWS);
+        const int row = rem / QPC, pc = rem % QPC;
         const int64_t tq = t0 + 8 * pc;
-        v = ld16((plane ? Qlo : Q) + (int64_t)row * ldq + tq);
+        u32x4_t v = S.q[ps];
+        // Tokens outside [rs, t_hi) contribute nothing.
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const int64_t ta = tq + 2 * w;
-          const uint32_t lo_ok = (ta >= rs && ta < t_hi) ? 0x0000ffffu : 0u;
-          const uint32_t hi_ok = (ta + 1 >= rs && ta + 1 < t_hi) ? 0xffff0000u : 0u;
-          v[w] &= lo_ok | hi_ok;
+          v[w] &= ((ta >= rs && ta < t_hi) ? 0x0000ffffu : 0u) |
+                  ((ta + 1 >= rs && ta + 1 < t_hi) ? 0xffff0000u : 0u);
         }
-      }
-      S.q[ps] = v;
-    }
-  };
-  auto store = [&](int b, const FactorStage& S) {
-    uint16_t* st = lds + b * FT_STAGE;
-#pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
-      const int id = tid + 256 * ps;
-      u32x2_t* dst = (u32x2_t*)&st[(id >> 4) * FT_PP + (id & 15) * 8];
-      dst[0] = u32x2_t{S.p[ps][0], S.p[ps][1]};
-      dst[1] = u32x2_t{S.p[ps][2], S.p[ps][3]};
-    }
-#pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
-      const int id = tid + 256 * ps;
-      if (id < 8 * rp) {
-        const int plane = id / (4 * rp), rem = id - plane * 4 * rp;
-        const int row = rem >> 2, pc = rem & 3;
-        *(u32x4_t*)&st[FT_PTILE + (plane * FT_QROWS + row) * FT_QP + 8 * pc] = S.q[ps];
+        *(u32x4_t*)&st[PTILE + (plane * QROWS + row) * QP + 8 * pc] = v;
       }
     }
   };
 
-  f32x4_t acc[2][4];
+  f32x4_t acc[NJ][NKB];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) acc[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < NKB; ++kb) acc[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int b) {
-    const uint16_t* st = lds + b * FT_STAGE;
-    bf16x8_t bop[2];
+    const uint16_t* st = lds + b * STAGE;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int m = (2 * wave + j) * 16 + (lane & 15);
-      const uint16_t* col = st + (8 * (lane >> 4)) * FT_PP + m;
-      u32x4_t v;
+    for (int u = 0; u < FT_T / 32; ++u)
 #pragma unroll
-      for (int w = 0; w < 4; ++w)
-        v[w] = (uint32_t)col[(2 * w) * FT_PP] | ((uint32_t)col[(2 * w + 1) * FT_PP] << 16);
-      bop[j] = __builtin_bit_cast(bf16x8_t, v);
-    }
+    for (int j = 0; j < NJ; ++j) {
+      // B operand: lane gets tokens 32u + 8*(lane>>4) + 0..7 of column m0 + (lane&15),
+      // as two transposing reads of 4 tokens each.
+      const int m0 = (NJ * wave + j) * 16, c = lane & 15;
+      const uint16_t* src = st + (32 * u + 8 * (lane >> 4) + (c >> 2)) * PP + m0 + 4 * (c & 3);
+      const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
+      const v4i16_t tt[2] = {t0, t1};
+      const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      if (kb < nkb) {
+      for (int kb = 0; kb < NKB; ++kb) {
         const int row = kb * 16 + (lane & 15);
-        const u32x4_t hv = *(const u32x4_t*)&st[FT_PTILE + row * FT_QP + 8 * (lane >> 4)];
-        const u32x4_t lv = *(const u32x4_t*)&st[FT_PTILE + (FT_QROWS + row) * FT_QP + 8 * (lane >> 4)];
-        const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, hv);
-        const bf16x8_t al = __builtin_bit_cast(bf16x8_t, lv);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bop[j], acc[j][kb], 0, 0, 0);
-          acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bop[j], acc[j][kb], 0, 0, 0);
-        }
+        const int tc = 32 * u + 8 * (lane >> 4);
+        const u32x4_t hv = *(const u32x4_t*)&st[PTILE + row * QP + tc];
+        const u32x4_t lv = *(const u32x4_t*)&st[PTILE + (QROWS + row) * QP + tc];
+        acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hv), bop,
+                                                             acc[j][kb], 0, 0, 0);
+        acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lv), bop,
+                                                             acc[j][kb], 0, 0, 0);
       }
     }
   };
 
-  FactorStage SA, SB;
-  if (nchunk > 0) load(0, SA);
-  if (nchunk > 1) load(1, SB);
+  // Prefetch indices are clamped to the last chunk instead of branching.
+  Stage SA, SB;
+  const int64_t last = nchunk - 1;
+  if (nchunk > 0) {
+    load(0, SA);
+    load(1 < last ? 1 : last, SB);
+  }
   for (int64_t c = 0; c < nchunk; c += 2) {
-    store(0, SA);
+    store(0, c, SA);
     __syncthreads();
-    if (c + 2 < nchunk) load(c + 2, SA);
+    load(c + 2 < last ? c + 2 : last, SA);
+    // Keep the prefetch issued here: left alone, the scheduler sinks these
+    // loads past the compute to shorten live ranges, which leaves only one
+    // stage in flight.
+    __builtin_amdgcn_sched_barrier(0);
     compute(0);
     if (c + 1 >= nchunk) break;
-    store(1, SB);
+    store(1, c + 1, SB);
     __syncthreads();
-    if (c + 3 < nchunk) load(c + 3, SB);
+    load(c + 3 < last ? c + 3 : last, SB);
+    __builtin_amdgcn_sched_barrier(0);
     compute(1);
   }
 
   const FactorLeaves L = read_leaves(f);
-  factor_epilogue(acc, nkb, r, scale, M, m_base, seg, tile, ex, part_stride, L, part);
+  factor_epilogue<NJ, NKB>(acc, r, scale, M, m_base, seg, tile, ex, part_stride, L, part);
 }
 
 // ---------------------------------------------------------------------------
@@ -466,13 +573,13 @@ __global__ __launch_bounds__(256) void k_factor_f32(const int64_t* __restrict__ 
   const int seg_first = (int)f[ODP_FT_SEG_FIRST];
   const float scale = (float)__longlong_as_double(f[ODP_FT_SCALING]);
 
-  const int ntile = (int)((M + FT_M - 1) / FT_M);
+  const int ntile = (int)((M + FT_M_F32 - 1) / FT_M_F32);
   const int local = bid - ws[p];
   const int seg = local / ntile, tile = local % ntile;
   const int gs = seg_first + seg;
   const int64_t rs = sstart[gs], t_hi = rs + slen[gs];
   const int ex = sex[gs];
-  const int64_t m_base = (int64_t)tile * FT_M;
+  const int64_t m_base = (int64_t)tile * FT_M_F32;
   const int nkb = (r + 15) >> 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4;
@@ -516,8 +623,9 @@ __global__ __launch_bounds__(256) void k_factor_f32(const int64_t* __restrict__ 
   }
 
   const FactorLeaves L = read_leaves(f);
-  factor_epilogue(acc, nkb, r, scale, M, m_base, seg, tile, ex, part_stride, L, part);
+  factor_epilogue<2, 4>(acc, r, scale, M, m_base, seg, tile, ex, part_stride, L, part);
 }
+
 
 }  // namespace
 
@@ -525,22 +633,23 @@ extern "C" int64_t odp_project_blocks(int64_t n_rows) {
   return n_rows <= 0 ? 0 : (n_rows + PJ_ROWS - 1) / PJ_ROWS;
 }
 
-extern "C" int64_t odp_seg_factor_tiles(int64_t M) {
-  return M <= 0 ? 0 : (M + FT_M - 1) / FT_M;
+extern "C" int64_t odp_seg_factor_tiles(int dtype, int64_t M, int32_t r) {
+  if (M <= 0 || r <= 0) return 0;
+  const int64_t mt = dtype == ODP_DTYPE_BF16 ? 64 * ft_nj((r + 15) / 16) : FT_M_F32;
+  return (M + mt - 1) / mt;
 }
 
 extern "C" int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
                            const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
-                           const int32_t* seg_row_start, const int32_t* seg_row_len,
-                           int32_t max_rank) {
+                           const int32_t* seg_row_start, const int32_t* seg_row_len, int32_t nkb) {
   int rc = odp_check_table("odp_project", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
   if (dtype != ODP_DTYPE_BF16 && dtype != ODP_DTYPE_F32) {
     odp_set_error("odp_project: unsupported dtype %d", dtype);
     return ODP_ERR_UNSUPPORTED;
   }
-  if (max_rank < 1 || max_rank > 64) {
-    odp_set_error("odp_project: max_rank=%d outside [1, 64]", max_rank);
+  if (nkb < 1 || nkb > 4) {
+    odp_set_error("odp_project: nkb=%d outside [1, 4] (rank must be <= 64)", nkb);
     return ODP_ERR_UNSUPPORTED;
   }
   if (total_blocks == 0) return ODP_OK;
@@ -549,13 +658,17 @@ extern "C" int odp_project(odp_stream_t stream, int dtype, const int64_t* proble
     return ODP_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = odp_hip_stream(stream);
+  const dim3 grid(total_blocks), block(256);
   if (dtype == ODP_DTYPE_BF16) {
-    const size_t lds = (size_t)2 * ((max_rank + 15) / 16 * 16) * PJ_WPITCH * sizeof(uint16_t);
-    hipLaunchKernelGGL(k_project_bf16, dim3(total_blocks), dim3(256), lds, s, problems, work_start,
-                       n_prob, seg_row_start, seg_row_len);
+    switch (nkb) {
+      case 1: hipLaunchKernelGGL(k_project_bf16<1>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      case 2: hipLaunchKernelGGL(k_project_bf16<2>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      case 3: hipLaunchKernelGGL(k_project_bf16<3>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      default: hipLaunchKernelGGL(k_project_bf16<4>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+    }
   } else {
-    hipLaunchKernelGGL(k_project_f32, dim3(total_blocks), dim3(256), 0, s, problems, work_start,
-                       n_prob, seg_row_start, seg_row_len);
+    hipLaunchKernelGGL(k_project_f32, grid, block, 0, s, problems, work_start, n_prob,
+                       seg_row_start, seg_row_len);
   }
   return odp_check_launch("odp_project");
 }
@@ -563,11 +676,16 @@ extern "C" int odp_project(odp_stream_t stream, int dtype, const int64_t* proble
 extern "C" int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
                               const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                               const int32_t* seg_row_start, const int32_t* seg_row_len,
-                              const int32_t* seg_example, double* part, int64_t part_stride) {
+                              const int32_t* seg_example, double* part, int64_t part_stride,
+                              int32_t nkb) {
   int rc = odp_check_table("odp_seg_factor", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
   if (dtype != ODP_DTYPE_BF16 && dtype != ODP_DTYPE_F32) {
     odp_set_error("odp_seg_factor: unsupported dtype %d", dtype);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  if (nkb < 1 || nkb > 4) {
+    odp_set_error("odp_seg_factor: nkb=%d outside [1, 4] (rank must be <= 64)", nkb);
     return ODP_ERR_UNSUPPORTED;
   }
   if (total_blocks == 0) return ODP_OK;
@@ -577,11 +695,17 @@ extern "C" int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* pro
     return ODP_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = odp_hip_stream(stream);
-  if (dtype == ODP_DTYPE_BF16)
-    hipLaunchKernelGGL(k_factor_bf16, dim3(total_blocks), dim3(256), 0, s, problems, work_start,
-                       n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride);
-  else
-    hipLaunchKernelGGL(k_factor_f32, dim3(total_blocks), dim3(256), 0, s, problems, work_start,
-                       n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride);
+  const dim3 grid(total_blocks), block(256);
+  if (dtype == ODP_DTYPE_BF16) {
+    switch (nkb) {
+      case 1: hipLaunchKernelGGL(k_factor_bf16<1>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+      case 2: hipLaunchKernelGGL(k_factor_bf16<2>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+      case 3: hipLaunchKernelGGL(k_factor_bf16<3>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+      default: hipLaunchKernelGGL(k_factor_bf16<4>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+    }
+  } else {
+    hipLaunchKernelGGL(k_factor_f32, grid, block, 0, s, problems, work_start, n_prob,
+                       seg_row_start, seg_row_len, seg_example, part, part_stride);
+  }
   return odp_check_launch("odp_seg_factor");
 }

@@ -314,16 +314,21 @@ class GhostPlan:
         leaf_slots: dict[int, int] = {}
         pe_elems: dict[int, int] = {}
         leaf_rank_m: dict[int, tuple[int, int]] = {}
+        lib = N.load()
         for ch in chunks:
+            dcode = dtype_code(ch[0].x.dtype)
+            rtot = sum(s.A.shape[1] for s in ch)
+            fused = len({s.scaling for s in ch if s.a_leaf is not None}) <= 1
             for s in ch:
                 d_in, r = s.A.shape
                 d_out = s.B.shape[1]
                 if s.a_leaf is not None:
-                    leaf_slots[s.a_leaf] = int(N.load().odp_seg_factor_tiles(d_in))
+                    # dA leaves of one activation share a pass of width rtot.
+                    leaf_slots[s.a_leaf] = int(lib.odp_seg_factor_tiles(dcode, d_in, rtot if fused else r))
                     leaf_rank_m[s.a_leaf] = (r, d_in)
                     pe_elems[s.a_leaf] = n_seg * r * d_in
                 if s.b_leaf is not None:
-                    leaf_slots[s.b_leaf] = int(N.load().odp_seg_factor_tiles(d_out))
+                    leaf_slots[s.b_leaf] = int(lib.odp_seg_factor_tiles(dcode, d_out, r))
                     leaf_rank_m[s.b_leaf] = (r, d_out)
                     pe_elems[s.b_leaf] = n_seg * r * d_out
         for m in mats:
@@ -396,9 +401,13 @@ class GhostPlan:
         self.qbuf = {dt: torch.empty(max(n, 1), dtype=dt, device=dev) for dt, n in q_need.items()}
 
         # Problem tables, per activation dtype.
-        pj = {dt: _Table(N.PJ_FIELDS) for dt in q_need}
-        ft = {dt: _Table(N.FT_FIELDS) for dt in q_need}
-        lib = N.load()
+        # Tables are keyed by (dtype, rank blocks): one launch per key.
+        pj: dict[tuple, _Table] = {}
+        ft: dict[tuple, _Table] = {}
+
+        def tab(tables: dict, dt: torch.dtype, r: int, fields: int) -> _Table:
+            return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
+
         elem = {torch.bfloat16: 2, torch.float32: 4}
         for ch, (dt, rtot, rows_alloc, planes, vbase, ubase) in zip(chunks, chunk_layout):
             qb = self.qbuf[dt]
@@ -414,7 +423,7 @@ class GhostPlan:
             # V = X [A_1 .. A_k]
             wx = torch.cat([s.A.detach().to(dt).t() for s in ch], dim=0).contiguous()
             self._keep.append(wx)
-            pj[dt].add(
+            tab(pj, dt, rtot, N.PJ_FIELDS).add(
                 {
                     N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
                     N.PJ_W: wx.data_ptr(), N.PJ_R: rtot,
@@ -433,7 +442,7 @@ class GhostPlan:
                 self._keep.append(wb)
                 d_out = g.shape[1]
                 # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
-                pj[dt].add(
+                tab(pj, dt, r, N.PJ_FIELDS).add(
                     {
                         N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
                         N.PJ_W: wb.data_ptr(), N.PJ_R: r,
@@ -455,7 +464,7 @@ class GhostPlan:
                         N.FT_LEAF0 + 1: 0 | (r << 16),
                         N.FT_LEAF0 + 2: slot_base[s.b_leaf],
                     }
-                    ft[dt].add(row, n_seg * lib.odp_seg_factor_tiles(d_out))
+                    tab(ft, dt, r, N.FT_FIELDS).add(row, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r))
                 c0 += r
             if a_leaves:
                 scal = {s.scaling for s in ch if s.a_leaf is not None}
@@ -463,13 +472,15 @@ class GhostPlan:
                     # Different scalings cannot share one pass: split them.
                     for s_leaf, col0, r in a_leaves:
                         sc = next(s.scaling for s in ch if s.a_leaf == s_leaf)
-                        ft[dt].add(self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, n_seg, sc,
-                                               [(s_leaf, col0, r)], pe_off, slot_base),
-                                   n_seg * lib.odp_seg_factor_tiles(d_in))
+                        tab(ft, dt, r, N.FT_FIELDS).add(
+                            self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, n_seg, sc,
+                                        [(s_leaf, col0, r)], pe_off, slot_base),
+                            n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r))
                 else:
-                    ft[dt].add(self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, n_seg, scal.pop(),
-                                           a_leaves, pe_off, slot_base),
-                               n_seg * lib.odp_seg_factor_tiles(d_in))
+                    tab(ft, dt, rtot, N.FT_FIELDS).add(
+                        self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, n_seg, scal.pop(),
+                                    a_leaves, pe_off, slot_base),
+                        n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot))
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
@@ -517,13 +528,13 @@ class GhostPlan:
         idx["seg_ex"] = pack.add(np.asarray(seg.examples, dtype=np.int32).reshape(-1))
         self._launch: list[tuple] = []
         tabs = []
-        for dt in q_need:
-            tabs.append(("project", dt, pj[dt]))
-            tabs.append(("factor", dt, ft[dt]))
+        for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
+            tabs.append(("project", key, pj[key]))
+        for key in sorted(ft, key=lambda k: (str(k[0]), k[1])):
+            tabs.append(("factor", key, ft[key]))
         tabs.append(("sqnorm", None, sq))
         tabs.append(("scale_sum", None, ss))
         tab_idx = []
-        self.max_rank = {dt: max([row[N.PJ_R] for row in pj[dt].rows] or [1]) for dt in q_need}
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
             tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total))
@@ -575,23 +586,24 @@ class GhostPlan:
         seg = self.segments
         ev = events or {}
         self.part.zero_()
-        for name, dt, probs, ws, n, total in self.tables:
-            if total == 0 or name == "scale_sum":
-                continue
-            if name in ev:
+        live = [t for t in self.tables if t[5] > 0 and t[0] != "scale_sum"]
+        for idx, (name, dt, probs, ws, n, total) in enumerate(live):
+            first = idx == 0 or live[idx - 1][0] != name
+            last = idx == len(live) - 1 or live[idx + 1][0] != name
+            if name in ev and first:
                 ev[name][0].record()
             if name == "project":
-                N.check(lib.odp_project(stream, dtype_code(dt), probs.data_ptr(), ws.data_ptr(), n, total,
-                                        self.seg_start.data_ptr(), self.seg_len.data_ptr(),
-                                        self.max_rank[dt]), name)
+                N.check(lib.odp_project(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
+                                        self.seg_start.data_ptr(), self.seg_len.data_ptr(), dt[1]), name)
             elif name == "factor":
-                N.check(lib.odp_seg_factor(stream, dtype_code(dt), probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_seg_factor(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                            self.seg_start.data_ptr(), self.seg_len.data_ptr(),
-                                           self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
+                                           self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots,
+                                           dt[1]), name)
             elif name == "sqnorm":
                 N.check(lib.odp_sqnorm(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                        self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
-            if name in ev:
+            if name in ev and last:
                 ev[name][1].record()
         if "clip" in ev:
             ev["clip"][0].record()
