@@ -1,0 +1,232 @@
+"""Capture of (activation, output-gradient) pairs at LoRA seams.
+
+The reference computes per-example LoRA gradients inside the ``vmap`` rule of
+its LoRA autograd Functions (``opaque-patches/.../kernels/lora.py:145-184``,
+fed by ``PAT/peft/components/linear.py:60-68``).  Here the same seam records
+what the DP kernels need instead: the activations ``x`` of the whole batch
+and, during one ordinary backward pass, the output gradients ``g``.  The
+per-example factor gradients are then never materialised by autograd.
+
+Outside a capture pass the ops are plain differentiable torch math
+(``y = x W^T + s (x A) B``), so the same model code runs under the
+reference's ``vmap(grad)``, under ordinary autograd and under the engine.
+"""
+
+from __future__ import annotations
+
+import threading
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+_STATE = threading.local()
+
+
+@dataclass
+class SiteRecord:
+    """One LoRA application seen during a capture pass."""
+
+    x: torch.Tensor  # physical activations [B, *, d_in]
+    A: torch.Tensor  # kernel-layout [d_in, r] values
+    B: torch.Tensor  # kernel-layout [r, d_out] values
+    scaling: float
+    a_obj: torch.Tensor | None  # the tensor the model passed (identity used for leaf lookup)
+    b_obj: torch.Tensor | None
+    a_transposed: bool
+    b_transposed: bool
+    g: torch.Tensor | None = None  # physical output gradients, filled by backward
+
+
+@dataclass
+class CaptureSession:
+    """Active while the engine runs a loss function to capture its LoRA seams.
+
+    ``mode`` is "discover" (record which tensors feed LoRA seams, keep them out
+    of autograd) or "capture" (record x and, in backward, g).
+    """
+
+    mode: str
+    anchor: torch.Tensor | None = None
+    sites: list[SiteRecord] = field(default_factory=list)
+    uses: dict[int, int] = field(default_factory=dict)  # id(tensor) -> number of seam uses
+    pairs: list[tuple[int, int, int, int]] = field(default_factory=list)  # ids of (A, B, W, bias) per call
+    eligible: set[int] = field(default_factory=set)  # ids allowed to be captured
+
+    def __enter__(self) -> CaptureSession:
+        if getattr(_STATE, "session", None) is not None:
+            raise RuntimeError("nested opaque_amd capture sessions are not supported")
+        _STATE.session = self
+        return self
+
+    def __exit__(self, *exc: Any) -> None:
+        _STATE.session = None
+
+
+def active_session() -> CaptureSession | None:
+    return getattr(_STATE, "session", None)
+
+
+def _plain(x, W, A, B, scaling, bias):
+    out = F.linear(x, W) + scaling * ((x @ A) @ B)
+    return out if bias is None else out + bias
+
+
+class _TapLoRA(torch.autograd.Function):
+    """Physical (batch-merged) LoRA op that records x now and g in backward."""
+
+    @staticmethod
+    def forward(x, W, A, B, scaling, bias, anchor, record):
+        return _plain(x, W, A, B, scaling, bias)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        x, W, A, B, scaling, bias, anchor, record = inputs
+        ctx.save_for_backward(W, A, B)
+        ctx.scaling = scaling
+        ctx.record = record
+        ctx.has_bias = bias is not None
+        ctx.bias_batched = bias is not None and bias.dim() > 1
+
+    @staticmethod
+    def backward(ctx, g):
+        W, A, B = ctx.saved_tensors
+        ctx.record.g = g.detach()
+        dx = None
+        if ctx.needs_input_grad[0]:
+            gb = g @ B.t()
+            dx = g @ W + ctx.scaling * (gb @ A.t())
+        dbias = None
+        if ctx.has_bias and ctx.needs_input_grad[5]:
+            # A batched (per-example, [B, 1.., d_out]) bias keeps its example axis.
+            if ctx.bias_batched:
+                red = tuple(range(1, g.dim() - 1))
+                dbias = g.sum(dim=red, keepdim=True) if red else g
+            else:
+                dbias = g.reshape(-1, g.shape[-1]).sum(0)
+        danchor = torch.zeros((), dtype=g.dtype, device=g.device) if ctx.needs_input_grad[6] else None
+        return dx, None, None, None, None, dbias, danchor, None
+
+
+class _SeamLoRA(torch.autograd.Function):
+    """Per-example LoRA op whose vmap rule merges the batch and taps the seam."""
+
+    generate_vmap_rule = False
+
+    @staticmethod
+    def forward(x, W, A, B, scaling, bias, a_obj, b_obj, a_t, b_t):
+        return _plain(x, W, A, B, scaling, bias)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        pass
+
+    @staticmethod
+    def backward(ctx, g):
+        raise RuntimeError("the capture seam is differentiated through its vmap rule only")
+
+    @staticmethod
+    def vmap(info, in_dims, x, W, A, B, scaling, bias, a_obj, b_obj, a_t, b_t):
+        sess = active_session()
+        xd, wd, ad, bd = in_dims[0], in_dims[1], in_dims[2], in_dims[3]
+        bias_d = in_dims[5]
+        if xd is None:
+            x = x.unsqueeze(0).expand(info.batch_size, *x.shape)
+        elif xd != 0:
+            x = x.movedim(xd, 0)
+        if bias is not None and bias_d is not None and bias_d != 0:
+            bias = bias.movedim(bias_d, 0)
+        if wd is not None or ad is not None or bd is not None or sess is None or sess.mode != "capture":
+            # A batched (expanded) weight or no capture: plain batched math.
+            if wd is not None:
+                W = W.movedim(wd, 0)
+                out = torch.einsum("b...i,boi->b...o", x, W)
+            else:
+                out = F.linear(x, W)
+            Ab = A.movedim(ad, 0) if ad is not None else A
+            Bb = B.movedim(bd, 0) if bd is not None else B
+            xa = torch.einsum("b...i,bir->b...r", x, Ab) if ad is not None else x @ Ab
+            xab = torch.einsum("b...r,bro->b...o", xa, Bb) if bd is not None else xa @ Bb
+            out = out + scaling * xab
+            if bias is not None:
+                out = out + (bias.view(bias.shape[0], *([1] * (out.dim() - 2)), bias.shape[-1])
+                             if bias_d is not None else bias)
+            return out, 0
+        rec = SiteRecord(x=x, A=A, B=B, scaling=float(scaling), a_obj=a_obj, b_obj=b_obj,
+                         a_transposed=a_t, b_transposed=b_t)
+        sess.sites.append(rec)
+        if bias is not None and bias_d is not None:
+            bias = bias.view(bias.shape[0], *([1] * (x.dim() - 2)), bias.shape[-1])
+        out = _TapLoRA.apply(x, W, A, B, float(scaling), bias, sess.anchor, rec)
+        return out, 0
+
+
+def _lora(x, W, A, B, scaling, bias, a_obj, b_obj, a_t, b_t):
+    sess = active_session()
+    if sess is None:
+        return _plain(x, W, A, B, scaling, bias)
+    if sess.mode == "discover":
+        for t in (a_obj, b_obj):
+            if t is not None:
+                sess.uses[id(t)] = sess.uses.get(id(t), 0) + 1
+        sess.pairs.append((id(a_obj), id(b_obj), id(W), id(bias) if bias is not None else 0))
+        # Seam parameters are hidden from autograd here, so a gradient that still
+        # reaches them afterwards reveals a use outside a seam.
+        return _plain(x, W, A.detach(), B.detach(), scaling, bias)
+    if id(a_obj) not in sess.eligible and id(b_obj) not in sess.eligible:
+        return _plain(x, W, A, B, scaling, bias)
+    return _SeamLoRA.apply(x, W, A, B, scaling, bias, a_obj, b_obj, a_t, b_t)
+
+
+def lora_linear(x: torch.Tensor, W: torch.Tensor, A: torch.Tensor, B: torch.Tensor,
+                scaling: float, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``x W^T + bias + scaling (x A) B`` with A [d_in, r], B [r, d_out].
+
+    Same computation as the reference's ``Opaque_LoRA_W`` (lora.py:217-293).
+    """
+    return _lora(x, W, A, B, scaling, bias, A, B, False, False)
+
+
+def peft_lora_linear(x: torch.Tensor, W: torch.Tensor, lora_A_weight: torch.Tensor,
+                     lora_B_weight: torch.Tensor, scaling: float,
+                     bias: torch.Tensor | None = None) -> torch.Tensor:
+    """LoRA with PEFT's storage: lora_A.weight [r, d_in], lora_B.weight [d_out, r].
+
+    The reference transposes these before its kernels (PAT/peft/components/linear.py:60-65).
+    """
+    return _lora(x, W, lora_A_weight.t(), lora_B_weight.t(), scaling, bias,
+                 lora_A_weight, lora_B_weight, True, True)
+
+
+class LoRALinear(torch.nn.Module):
+    """A frozen ``Linear`` with a trainable LoRA adapter routed through the seam.
+
+    Parameters ``lora_A`` [r, in] and ``lora_B`` [out, r] use PEFT's layout;
+    ``scaling = alpha / r`` as in PEFT (PAT/peft/components/_utils.py:43).
+    """
+
+    def __init__(self, in_features: int, out_features: int, r: int, alpha: float = 16.0,
+                 bias: bool = False, device=None, dtype=None) -> None:
+        super().__init__()
+        kw = {"device": device, "dtype": dtype}
+        self.weight = torch.nn.Parameter(torch.empty(out_features, in_features, **kw), requires_grad=False)
+        self.bias = torch.nn.Parameter(torch.zeros(out_features, **kw), requires_grad=False) if bias else None
+        self.lora_A = torch.nn.Parameter(torch.empty(r, in_features, **kw))
+        self.lora_B = torch.nn.Parameter(torch.zeros(out_features, r, **kw))
+        self.scaling = alpha / r
+        torch.nn.init.kaiming_uniform_(self.weight, a=5**0.5)
+        torch.nn.init.kaiming_uniform_(self.lora_A, a=5**0.5)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return peft_lora_linear(x, self.weight, self.lora_A, self.lora_B, self.scaling, self.bias)
+
+
+__all__ = [
+    "CaptureSession",
+    "LoRALinear",
+    "SiteRecord",
+    "active_session",
+    "lora_linear",
+    "peft_lora_linear",
+]

@@ -359,6 +359,7 @@ class GhostPlan:
             pe_off[i] = off
             off += (pe_elems[i] + 63) // 64 * 64
         self.pe = torch.empty(max(off, 1), dtype=torch.float32, device=dev)
+        self._pe_slices = [(pe_off[i], pe_elems[i]) for i in sorted(pe_elems)]
         self.part = torch.zeros((seg.n_ex, self.n_slots), dtype=torch.float64, device=dev)
 
         # Output leaves: one flat buffer per output dtype, views in leaf order.
@@ -572,6 +573,10 @@ class GhostPlan:
             if s.b_leaf == i:
                 return s.b_transposed
         return False
+
+    def pe_views(self) -> list[torch.Tensor]:
+        """The per-example factor gradients each LoRA leaf stored ([n_seg * r * M] fp32)."""
+        return [self.pe[o : o + n] for o, n in self._pe_slices]
 
     # -- execution -------------------------------------------------------------
     def run(self, events: dict | None = None) -> GhostResult:

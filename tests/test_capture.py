@@ -1,0 +1,161 @@
+"""Seam capture on the CPU: discovery, the batched capture pass and what it records.
+
+The per-example factor gradients rebuilt from the recorded (x, g) pairs
+(dA_i = s X_i^T G_i B^T, dB_i = s (X_i A)^T G_i) must equal torch.func's
+vmap(grad) of the same loss; non-captured leaves get theirs from the
+batch-expanded copies.  No kernel runs here.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from opaque_amd import capture
+from opaque_amd import clipping as C
+from opaque_amd.pytree import tree_flatten_with_paths, tree_unflatten
+
+
+class _Model(torch.nn.Module):
+    def __init__(self, bias: bool = True) -> None:
+        super().__init__()
+        self.q = capture.LoRALinear(16, 24, 4, alpha=8)
+        self.o = capture.LoRALinear(24, 16, 4, alpha=8, bias=bias)
+        self.ln = torch.nn.LayerNorm(24)
+        torch.nn.init.normal_(self.q.lora_B, std=0.1)
+        torch.nn.init.normal_(self.o.lora_B, std=0.1)
+
+    def forward(self, x):
+        return self.o(torch.tanh(self.ln(self.q(x))))
+
+
+def _engine(loss_fn, batch_argnums=(1, 2)):
+    return C._ClipEngine(
+        loss_fn, (0,), 0, False, clipping_norm=1.0, autos=False, gamma=0.0, normalize_by=1.0,
+        batch_argnums=batch_argnums, want_aux=False, want_stats=False, second_moment=False,
+        pre_clipping_transform=C._identity, microbatch_size=None, dtype=None, compute_dtype=None,
+        scale_fn=None,
+    )
+
+
+def _capture_per_example(eng, args, n):
+    """The capture pass of the engine, returning per-example grads by leaf path."""
+    paths, leaves, td = tree_flatten_with_paths(eng._grad_tree(args))
+    disc = eng._discover(args, {}, leaves, td)
+    expanded, passed, dims = {}, [], []
+    for k, t in enumerate(leaves):
+        if k in disc.eligible:
+            passed.append(t)
+            dims.append(None)
+        else:
+            e = t.detach().unsqueeze(0).expand(n, *t.shape).requires_grad_()
+            expanded[k] = e
+            passed.append(e)
+            dims.append(0)
+    cargs = eng._with_grad_tree(args, tree_unflatten(td, passed))
+    in_dims = eng._in_dims(cargs, tree_unflatten(td, dims))
+    anchor = torch.zeros((), requires_grad=True)
+    obj_leaf = {id(leaves[k]): k for k in disc.eligible}
+    sess = capture.CaptureSession(mode="capture", anchor=anchor, eligible=set(obj_leaf))
+    with torch.enable_grad(), sess:
+        values, _ = torch.func.vmap(lambda *a: eng._loss(*a), in_dims=in_dims, randomness="same")(*cargs)
+    grads = torch.autograd.grad(values.sum(), [anchor] + [expanded[k] for k in sorted(expanded)],
+                                allow_unused=True)
+    got = {paths[k]: g for k, g in zip(sorted(expanded), grads[1:])}
+    for r in sess.sites:
+        ka, kb = obj_leaf.get(id(r.a_obj)), obj_leaf.get(id(r.b_obj))
+        for k, pe in C._site_per_example(r, ka, kb, leaves):
+            got[paths[k]] = pe
+    return disc, sess, got, paths
+
+
+def _check(ref, got):
+    rp, rl, _ = tree_flatten_with_paths(ref)
+    assert set(got) == set(rp)
+    for p, t in zip(rp, rl):
+        torch.testing.assert_close(got[p], t, rtol=1e-5, atol=1e-6)
+
+
+def test_capture_reproduces_vmap_grad():
+    torch.manual_seed(0)
+    m = _Model()
+    train = {k: v for k, v in m.named_parameters() if v.requires_grad}
+    train["ln.weight"] = m.ln.weight
+    frozen = {k: v for k, v in m.named_parameters() if k not in train}
+
+    def loss_fn(params, x, y):
+        out = torch.func.functional_call(m, {**frozen, **params}, (x,))
+        return ((out - y) ** 2).mean()
+
+    n = 3
+    x, y = torch.randn(n, 5, 16), torch.randn(n, 5, 16)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0, 0))(train, x, y)
+    eng = _engine(loss_fn)
+    disc, sess, got, paths = _capture_per_example(eng, (train, x, y), n)
+    eligible = {paths[k][0] for k in disc.eligible}
+    assert eligible == {"q.lora_A", "q.lora_B", "o.lora_A", "o.lora_B"}
+    assert len(sess.sites) == 2
+    assert all(r.g is not None and r.x.shape[0] == n for r in sess.sites)
+    _check(ref, got)
+
+
+def test_trainable_bias_and_base_weight():
+    torch.manual_seed(1)
+    m = _Model(bias=True)
+    # The o-projection's bias is trainable (a per-example leaf through the seam's
+    # batched bias path); the q-projection's base weight is trainable, which
+    # keeps its whole seam off the capture route.
+    train = {k: v for k, v in m.named_parameters() if "lora" in k}
+    train["o.bias"] = m.o.bias
+    train["q.weight"] = m.q.weight
+    frozen = {k: v for k, v in m.named_parameters() if k not in train}
+
+    def loss_fn(params, x, y):
+        out = torch.func.functional_call(m, {**frozen, **params}, (x,))
+        return ((out - y) ** 2).sum()
+
+    n = 4
+    x, y = torch.randn(n, 3, 16), torch.randn(n, 3, 16)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0, 0))(train, x, y)
+    disc, sess, got, paths = _capture_per_example(_engine(loss_fn), (train, x, y), n)
+    assert {paths[k][0] for k in disc.eligible} == {"o.lora_A", "o.lora_B"}
+    _check(ref, got)
+
+
+def test_factor_used_outside_the_seam_is_not_captured():
+    g = torch.Generator().manual_seed(2)
+    W = torch.randn(8, 8, generator=g)
+    params = {"A": torch.randn(8, 2, generator=g), "B": torch.randn(2, 8, generator=g)}
+
+    def loss_fn(p, x):
+        y = capture.lora_linear(x, W, p["A"], p["B"], 0.5)
+        return (y**2).sum() + (p["A"] ** 2).sum() * x.sum()
+
+    x = torch.randn(3, 8, generator=g)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0))(params, x)
+    disc, sess, got, paths = _capture_per_example(_engine(loss_fn, batch_argnums=(1,)), (params, x), 3)
+    assert disc.eligible == frozenset()
+    assert sess.sites == []
+    _check(ref, got)
+
+
+def test_seam_ops_are_plain_math_outside_capture():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 5, 8, generator=g)
+    W = torch.randn(6, 8, generator=g)
+    a_w = torch.randn(3, 8, generator=g)
+    b_w = torch.randn(6, 3, generator=g)
+    bias = torch.randn(6, generator=g)
+    y = capture.peft_lora_linear(x, W, a_w, b_w, 1.5, bias)
+    torch.testing.assert_close(y, x @ W.t() + bias + 1.5 * (x @ a_w.t()) @ b_w.t())
+    y2 = capture.lora_linear(x, W, a_w.t(), b_w.t(), 1.5)
+    torch.testing.assert_close(y2, x @ W.t() + 1.5 * (x @ a_w.t()) @ b_w.t())
+
+
+def test_nested_sessions_rejected():
+    import pytest
+
+    with capture.CaptureSession(mode="discover"):
+        with pytest.raises(RuntimeError, match="nested"):
+            with capture.CaptureSession(mode="discover"):
+                pass
+    assert capture.active_session() is None

@@ -1,0 +1,286 @@
+"""GPU parity of the drop-in ``clipped_grad`` / ``auto_clipped_grad`` against the CPU oracle.
+
+Both sides differentiate the same per-example loss; the oracle restates the
+reference's vmap(grad) + clip_pytree + fp32 sum on the CPU, the product runs
+the HIP kernels (seam capture for LoRA factors, materialised leaves for the
+rest).  Tolerances: fp32 rel <= 1e-5, bf16 rel <= 2e-2 (global relative
+error of each leaf and of the norms).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import dp_ref
+from opaque_amd import capture
+from opaque_amd.clipping import (
+    AutoClippedGradAux,
+    ClippedGradAux,
+    ClippingStats,
+    auto_clipped_grad,
+    clipped_grad,
+    per_group,
+)
+from opaque_amd.types import ClippedPytree, PerGroup, SecondMomentClippingOutput
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    den = b.norm().item()
+    return (a - b).norm().item() / den if den > 0 else (a - b).norm().item()
+
+
+def _plain_lora(x, W, A, B, s, bias=None):
+    out = x @ W.t() + s * ((x @ A) @ B)
+    return out if bias is None else out + bias
+
+
+def _peft(op):
+    def f(x, W, a_w, b_w, s, bias=None):
+        if op is None:
+            return _plain_lora(x, W, a_w.t(), b_w.t(), s, bias)
+        return op(x, W, a_w, b_w, s, bias)
+
+    return f
+
+
+def make_model(dtype, d=32, h=64, r=8, seed=0, layers=2):
+    """A small transformer-ish MLP stack: LoRA on in/out projections, trainable norm weights."""
+    g = torch.Generator().manual_seed(seed)
+
+    def rn(*s, scale=1.0):
+        return (torch.randn(*s, generator=g) * scale).to(dtype)
+
+    frozen, train = {}, {}
+    for li in range(layers):
+        frozen[f"l{li}.up.W"] = rn(h, d, scale=d**-0.5)
+        frozen[f"l{li}.down.W"] = rn(d, h, scale=h**-0.5)
+        train[f"l{li}.up.lora_A"] = rn(r, d, scale=d**-0.5)
+        train[f"l{li}.up.lora_B"] = rn(h, r, scale=0.2)
+        train[f"l{li}.down.lora_A"] = rn(r, h, scale=h**-0.5)
+        train[f"l{li}.down.lora_B"] = rn(d, r, scale=0.2)
+        train[f"l{li}.norm"] = (1.0 + 0.1 * torch.randn(d, generator=g)).to(dtype)
+    return frozen, train
+
+
+def model_loss(op, frozen, layers=2, s=2.0):
+    lora = _peft(op)
+
+    def loss(params, x, y):
+        hcur = x
+        for li in range(layers):
+            z = hcur * params[f"l{li}.norm"]
+            u = lora(z, frozen[f"l{li}.up.W"], params[f"l{li}.up.lora_A"], params[f"l{li}.up.lora_B"], s)
+            u = torch.nn.functional.gelu(u)
+            hcur = hcur + lora(u, frozen[f"l{li}.down.W"], params[f"l{li}.down.lora_A"],
+                               params[f"l{li}.down.lora_B"], s)
+        return ((hcur.float() - y.float()) ** 2).mean()
+
+    return loss
+
+
+def to(tree, dev):
+    return {k: v.to(dev) for k, v in tree.items()}
+
+
+def run_both(dtype, *, n=6, T=16, autos=False, C=None, normalize_by=1.0, second_moment=False,
+             return_aux=True, microbatch=None, out_dtype=None, seed=0):
+    frozen, train = make_model(dtype, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(n, T, 32, generator=g).to(dtype)
+    y = torch.randn(n, T, 32, generator=g).to(dtype)
+    # Per-example scale so that some examples clip and some do not.
+    x = x * torch.logspace(-1, 0.5, n).view(n, 1, 1).to(dtype)
+    fz_d = to(frozen, DEV)
+    prod_loss = model_loss(capture.peft_lora_linear, fz_d)
+    ref_loss = model_loss(None, frozen)
+    # Oracle on the CPU in float32 copies of the same values.
+    if C is None:
+        _, aux0 = dp_ref.clipped_grad(ref_loss, train, (x, y), clipping_norm=float("inf"))
+        C = float(aux0["norms"].median())
+    kw = dict(normalize_by=normalize_by, second_moment=second_moment, dtype=out_dtype)
+    if autos:
+        fn, st = auto_clipped_grad(prod_loss, R=C, batch_argnums=(1, 2), return_aux=return_aux,
+                                   microbatch_size=microbatch, **kw)
+    else:
+        fn, st = clipped_grad(prod_loss, clipping_norm=C, batch_argnums=(1, 2), return_aux=return_aux,
+                              microbatch_size=microbatch, **kw)
+    out, st2 = fn(to(train, DEV), x.to(DEV), y.to(DEV), state=st)
+    torch.cuda.synchronize()
+    summed, aux = dp_ref.clipped_grad(ref_loss, train, (x, y), clipping_norm=C, autos=autos,
+                                      normalize_by=normalize_by, second_moment=second_moment,
+                                      dtype=out_dtype)
+    return out, st, st2, summed, aux, C
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("autos", [False, True])
+def test_lora_capture_matches_oracle(dtype, tol, autos):
+    out, st, st2, summed, aux, C = run_both(dtype, autos=autos)
+    assert st2 is st
+    grads, gaux = out
+    assert isinstance(grads, ClippedPytree)
+    assert grads.max_norm == C
+    assert isinstance(gaux, AutoClippedGradAux if autos else ClippedGradAux)
+    for k, ref in summed.items():
+        got = grads.pytree[k]
+        assert got.dtype == dtype and got.shape == ref.shape, k
+        assert rel(got, ref) <= tol, (k, rel(got, ref))
+    assert rel(gaux.grad_norms, aux["norms"]) <= tol
+    assert rel(gaux.loss_values, aux["loss_values"]) <= tol
+    assert rel(gaux.clipped_grad_norms, aux["clipped_norms"]) <= max(tol, 1e-5)
+    assert gaux.batch_size == 6
+    # Masks agree away from the threshold.
+    band = 1e-3 if dtype == torch.bfloat16 else 1e-6
+    ref_n = aux["norms"].double()
+    far = ((ref_n - C).abs() / C) > band
+    ref_rate = float((ref_n[far] > C).sum()) / len(ref_n)
+    if bool(far.all()):
+        assert gaux.clipping_rate == pytest.approx(ref_rate)
+
+
+def test_capture_route_was_taken():
+    frozen, train = make_model(torch.float32)
+    fz_d = to(frozen, DEV)
+    loss = model_loss(capture.peft_lora_linear, fz_d)
+    fn, st = clipped_grad(loss, clipping_norm=1.0, batch_argnums=(1, 2))
+    x = torch.randn(3, 8, 32, device=DEV)
+    fn(to(train, DEV), x, x, state=st)
+    disc = fn.engine._discovery[1]
+    # All eight LoRA factors are captured at the seam; the norm weights are not.
+    assert len(disc.eligible) == 8
+
+
+def test_shared_factor_falls_back_to_materialised():
+    frozen, train = make_model(torch.float32, layers=1)
+    fz_d = to(frozen, DEV)
+
+    def loss(params, x, y):
+        a = params["l0.up.lora_A"]
+        u = capture.peft_lora_linear(x, fz_d["l0.up.W"], a, params["l0.up.lora_B"], 2.0)
+        # lora_A is also used outside the seam: its per-example gradient must
+        # come from autograd, and the seam it feeds cannot be captured.
+        u = u + (x @ a.t()).sum(-1, keepdim=True)
+        v = capture.peft_lora_linear(torch.tanh(u), fz_d["l0.down.W"], params["l0.down.lora_A"],
+                                     params["l0.down.lora_B"], 2.0)
+        return ((v * params["l0.norm"] - y) ** 2).mean()
+
+    def ref_loss(params, x, y):
+        a = params["l0.up.lora_A"]
+        u = _plain_lora(x, frozen["l0.up.W"], a.t(), params["l0.up.lora_B"].t(), 2.0)
+        u = u + (x @ a.t()).sum(-1, keepdim=True)
+        v = _plain_lora(torch.tanh(u), frozen["l0.down.W"], params["l0.down.lora_A"].t(),
+                        params["l0.down.lora_B"].t(), 2.0)
+        return ((v * params["l0.norm"] - y) ** 2).mean()
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4, 8, 32, generator=g)
+    y = torch.randn(4, 8, 32, generator=g)
+    fn, st = clipped_grad(loss, clipping_norm=0.5, batch_argnums=(1, 2))
+    out, _ = fn(to(train, DEV), x.to(DEV), y.to(DEV), state=st)
+    disc = fn.engine._discovery[1]
+    assert len(disc.eligible) == 2  # only the down projection's factors
+    ref, _ = dp_ref.clipped_grad(ref_loss, train, (x, y), clipping_norm=0.5)
+    for k, r in ref.items():
+        assert rel(out.pytree[k], r) <= 1e-5, k
+
+
+def test_materialised_route_linear_regression():
+    # The reference docstring example (_clipped_grad.py:112-129): theta = 3, data [0, 7, -2].
+    def f(theta, d):
+        return 0.5 * ((d - theta) ** 2).mean()
+
+    fn, st = clipped_grad(f, clipping_norm=float("inf"), return_aux=True)
+    (res, aux), _ = fn(torch.tensor(3.0, device=DEV), torch.tensor([0.0, 7.0, -2.0], device=DEV), state=st)
+    # Per-example gradients 3, -4, 5 pass unclipped; their sum is 4 (mean 4/3).
+    assert res.pytree.item() == pytest.approx(4.0, rel=1e-6)
+    assert aux.loss_values.cpu().tolist() == pytest.approx([4.5, 8.0, 12.5])
+    assert aux.grad_norms.cpu().tolist() == pytest.approx([3.0, 4.0, 5.0])
+    fn3, st3 = clipped_grad(f, clipping_norm=float("inf"), normalize_by=3.0)
+    res3, _ = fn3(torch.tensor(3.0, device=DEV), torch.tensor([0.0, 7.0, -2.0], device=DEV), state=st3)
+    assert res3.pytree.item() == pytest.approx(4.0 / 3.0, rel=1e-6)
+    assert res3.max_norm == math.inf
+
+
+def test_materialised_route_matches_oracle_fixed_clip():
+    g = torch.Generator().manual_seed(3)
+    params = {"w": torch.randn(12, 5, generator=g), "b": torch.randn(5, generator=g)}
+    x = torch.randn(9, 12, generator=g) * torch.logspace(-1, 1, 9).view(9, 1)
+    y = torch.randn(9, 5, generator=g)
+
+    def f(p, xi, yi):
+        return ((xi @ p["w"] + p["b"] - yi) ** 2).sum()
+
+    fn, st = clipped_grad(f, clipping_norm=3.0, batch_argnums=(1, 2), return_aux=True, normalize_by=4.0)
+    (res, aux), _ = fn({k: v.to(DEV) for k, v in params.items()}, x.to(DEV), y.to(DEV), state=st)
+    ref, raux = dp_ref.clipped_grad(f, params, (x, y), clipping_norm=3.0, normalize_by=4.0)
+    for k in params:
+        assert rel(res.pytree[k], ref[k]) <= 1e-5
+    assert rel(aux.grad_norms, raux["norms"]) <= 1e-6
+    assert res.max_norm == 3.0 / 4.0
+
+
+def test_per_group_matches_oracle():
+    frozen, train = make_model(torch.float32)
+    pg = per_group(train, up=0.3, down=0.2, norm=0.5)
+    fz_d = to(frozen, DEV)
+    prod_loss = model_loss(capture.peft_lora_linear, fz_d)
+    ref_loss = model_loss(None, frozen)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(5, 8, 32, generator=g)
+    y = torch.randn(5, 8, 32, generator=g)
+    fn, st = clipped_grad(prod_loss, clipping_norm=pg, batch_argnums=(1, 2), return_aux=True)
+    (res, aux), _ = fn(to(train, DEV), x.to(DEV), y.to(DEV), state=st)
+    ref, raux = dp_ref.clipped_grad(ref_loss, train, (x, y), clipping_norm=pg)
+    assert isinstance(res.max_norm, PerGroup)
+    for k in train:
+        assert rel(res.pytree[k], ref[k]) <= 1e-5, k
+    assert set(aux.group_norms) == set(raux["group_norms"])
+    for name, v in raux["group_norms"].items():
+        assert rel(aux.group_norms[name], v) <= 1e-5
+    assert aux.clipping_rate is None
+
+
+def test_second_moment_microbatch_stats():
+    out, st, _, summed, aux, C = run_both(torch.float32, second_moment=True, normalize_by=2.0)
+    res, _ = out
+    assert isinstance(res, SecondMomentClippingOutput)
+    assert res.squared_grads.max_norm == pytest.approx(C * C / 2.0)
+    for k, ref in aux["squared"].items():
+        assert rel(res.squared_grads.pytree[k], ref) <= 1e-5, k
+    for k, ref in summed.items():
+        assert rel(res.grads.pytree[k], ref) <= 1e-5, k
+    # Microbatching gives the same sum.
+    out_mb, _, _, summed_mb, _, _ = run_both(torch.float32, microbatch=4, return_aux=False, normalize_by=2.0)
+    for k, ref in summed_mb.items():
+        assert rel(out_mb.pytree[k], ref) <= 1e-5, k
+
+
+def test_return_stats_and_output_dtype():
+    frozen, train = make_model(torch.bfloat16)
+    fz_d = to(frozen, DEV)
+    loss = model_loss(capture.peft_lora_linear, fz_d)
+    fn, st = clipped_grad(loss, clipping_norm=1e-3, batch_argnums=(1, 2), return_stats=True,
+                          dtype=torch.float32)
+    x = torch.randn(4, 8, 32, device=DEV, dtype=torch.bfloat16)
+    (res, stats), _ = fn(to(train, DEV), x, x, state=st)
+    assert isinstance(stats, ClippingStats)
+    assert stats.batch_size == 4 and stats.num_clipped == 4.0 and stats.clipping_rate == 1.0
+    assert stats.all_finite is True
+    assert all(v.dtype == torch.float32 for v in res.pytree.values())
+
+
+def test_empty_batch():
+    fn, st = clipped_grad(lambda p, x: (p * x).sum(), clipping_norm=1.0, return_aux=True)
+    p = torch.ones(3, device=DEV)
+    (res, aux), _ = fn(p, torch.zeros(0, 3, device=DEV), state=st)
+    assert torch.equal(res.pytree, torch.zeros(3, device=DEV))
+    assert aux.batch_size == 0 and aux.clipping_rate == 0.0

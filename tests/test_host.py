@@ -1,0 +1,204 @@
+"""Host-side logic of the drop-in API (no GPU): types, per_group, keys, guard, validation."""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import pytest
+import torch
+
+from oracle import dp_ref
+from opaque_amd import guard
+from opaque_amd.clipping import auto_clipped_grad, clipped_grad, per_group
+from opaque_amd.noise import gaussian_noise
+from opaque_amd.noise_allocation import paired_noise_stddevs, per_group_noise_stddev
+from opaque_amd.pytree import param_path, tree_flatten_with_paths, tree_unflatten
+from opaque_amd.random import RngKey, fold_in, key, split
+from opaque_amd.types import ClippedPytree, NoisedPytree, PerGroup, clipped
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+with open(os.path.join(HERE, "golden", "reference_vectors.json")) as _f:
+    CASES = {c["name"]: c for c in json.load(_f)["cases"]}
+
+
+# -- golden values through the product's host code ----------------------------
+
+
+def test_noise_per_group_sigma_golden():
+    case = CASES["noise_per_group_sigma"]
+    pg = PerGroup(groups={"w": "small", "b": "large"}, values=case["values"])
+    sd = per_group_noise_stddev(pg, case["noise_multiplier"])
+    assert sd.values == {k: pytest.approx(v, rel=1e-15) for k, v in case["expected"].items()}
+    assert sd.groups == pg.groups
+
+
+def test_noise_stddev_for_golden():
+    case = CASES["noise_stddev_for_scalar"]
+    cg = clipped(torch.zeros(8), max_norm=case["max_norm"])
+    assert cg.noise_stddev_for(noise_multiplier=case["noise_multiplier"]) == pytest.approx(case["expected"])
+    assert cg.noise_stddev_for(noise_multiplier=case["noise_multiplier"], allocation="isotropic") == \
+        pytest.approx(case["expected"])
+
+
+def test_per_group_bound_arithmetic_golden():
+    case = CASES["per_group_bound_arithmetic"]
+    params = {"a": torch.tensor(1.0), "b": torch.tensor(1.0)}
+    pg = per_group(params, **case["patterns"])
+    sd = case["noise_multiplier"] * pg
+    assert isinstance(sd, PerGroup)
+    assert sd.values == {k: pytest.approx(v) for k, v in case["expected"].items()}
+
+
+def test_per_group_nested_assignment():
+    case = CASES["per_group_nested"]
+    tree = {k: {kk: torch.tensor(v) for kk, v in d.items()} for k, d in case["tree"].items()}
+    pg = per_group(tree, **case["patterns"])
+    assert pg.groups[("layer1", "attn")] == "attn"
+    assert pg.groups[("layer2", "mlp")] == "mlp"
+    assert pg.effective == pytest.approx(math.sqrt(2.0))
+
+
+def test_per_group_errors():
+    params = {"q_proj": torch.zeros(1), "mlp": torch.zeros(1)}
+    with pytest.raises(ValueError, match="At least one pattern"):
+        per_group(params)
+    with pytest.raises(ValueError, match="must be positive"):
+        per_group(params, q_proj=0.0, mlp=1.0)
+    with pytest.raises(ValueError, match="did not match any pattern"):
+        per_group(params, q_proj=1.0)
+    with pytest.raises(ValueError, match="matched multiple patterns"):
+        per_group(params, q=1.0, q_proj=1.0, mlp=1.0)
+    pg = per_group(params, q_proj=1.0, fallback=2.0)
+    assert pg.values == {"q_proj": 1.0, "fallback": 2.0}
+    with pytest.raises(ValueError, match="Fallback value must be positive"):
+        per_group(params, q_proj=1.0, fallback=-1.0)
+
+
+def test_clipped_pytree_arithmetic():
+    c = clipped({"w": torch.ones(2)}, max_norm=2.0)
+    assert (c * 3).max_norm == 6.0
+    assert (0.5 * c).max_norm == 1.0
+    assert (c / 4).max_norm == 0.5
+    assert (-c).max_norm == 2.0
+    with pytest.raises(TypeError):
+        c + c
+    with pytest.raises(TypeError):
+        c * torch.tensor(2.0)
+    with pytest.raises(ZeroDivisionError):
+        c / 0
+    n = NoisedPytree(pytree={"w": torch.ones(2)}, max_norm=1.0, noise_stddev=0.5)
+    assert (2 * n).noise_stddev == 1.0
+
+
+def test_paired_noise_stddevs_scalar():
+    s1, s2 = paired_noise_stddevs(1.5, first=2.0, second=3.0)
+    total = 5.0
+    assert s1 == pytest.approx(1.5 * math.sqrt(2.0 * total))
+    assert s2 == pytest.approx(1.5 * math.sqrt(3.0 * total))
+
+
+# -- keys and pytree order -----------------------------------------------------
+
+
+def test_rng_keys_match_oracle():
+    k = key(123)
+    assert isinstance(k, RngKey)
+    for data in [(0,), (7, 3), ("noise",), (2**40, -5)]:
+        assert fold_in(k, *data).seed == dp_ref.fold_in_seed(dp_ref.key_seed(123), *data)
+    assert fold_in(fold_in(k, 7), 3).seed == fold_in(k, 7, 3).seed
+    a, b, c = split(k, 3)
+    assert len({a.seed, b.seed, c.seed}) == 3
+    assert key(-1).seed == 2**64 - 1
+
+
+def test_pytree_order_sorted_keys_and_roundtrip():
+    tree = {"b": torch.zeros(1), "a": [torch.ones(1), {"z": torch.ones(2), "y": None}], "c": (torch.ones(3),)}
+    paths, leaves, td = tree_flatten_with_paths(tree)
+    assert paths == [("a", 0), ("a", 1, "z"), ("b",), ("c", 0)]
+    back = tree_unflatten(td, leaves)
+    assert list(back.keys()) == ["b", "a", "c"]
+    assert back["a"][1]["y"] is None
+    assert param_path("x.y") == ("x.y",)
+    assert [p for p, _ in dp_ref.flatten(tree)] == [tuple(p) for p in paths]
+
+
+# -- guard constants: product host code vs the oracle restatement --------------
+
+
+@pytest.mark.parametrize("shapes", [[(3,)], [(4096,)], [(4097,), (7, 5)], [(8192, 16), (16, 4096), (1,)]])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+def test_guard_constants_match_oracle(shapes, dt):
+    leaves = [torch.zeros(s, dtype=dt) for s in shapes]
+    acc, rnd = guard.leaf_guards(shapes, [dt] * len(shapes))
+    assert acc == dp_ref.acc_dtype(leaves, None)
+    assert rnd == dp_ref.roundoff(acc, len(leaves), dp_ref.reduction_terms(leaves))
+    rel, ab = guard.guard_constants(dt, rnd)
+    ratio = torch.tensor([0.5, 1.7, 3e-5], dtype=torch.float64)
+    expect = dp_ref.finalize(ratio, dt, rnd, clamp_one=False)
+    got = torch.clamp(ratio * rel - ab, min=0.0)
+    assert torch.equal(got, expect)
+
+
+# -- validation messages (the reference's tests assert these substrings) --------
+
+
+def _loss(p, x):
+    return (p * x).sum()
+
+
+@pytest.mark.parametrize(
+    "kwargs,exc,match",
+    [
+        (dict(clipping_norm=1.0, normalize_by=0.0), ValueError, "normalize_by must be > 0"),
+        (dict(clipping_norm=1.0, batch_argnums=()), ValueError, "Batch argnums must not be empty"),
+        (dict(clipping_norm=1.0, argnums=1, batch_argnums=1), ValueError, "have a batch axis"),
+        (dict(clipping_norm=0.0), ValueError, "clipping_norm must be positive"),
+        (dict(clipping_norm=1.0, return_aux=True, return_stats=True), ValueError, "return_stats cannot be combined"),
+        (dict(clipping_norm=1.0, compute_dtype=torch.int32), TypeError, "compute_dtype"),
+    ],
+)
+def test_clipped_grad_validation(kwargs, exc, match):
+    with pytest.raises(exc, match=match):
+        clipped_grad(_loss, **kwargs)
+
+
+def test_clipped_grad_per_group_validation():
+    pg = PerGroup(groups={"a": "g"}, values={"g": -1.0})
+    with pytest.raises(ValueError, match="clipping_norm must be positive for all groups"):
+        clipped_grad(_loss, clipping_norm=pg)
+
+
+def test_auto_clipped_grad_validation():
+    with pytest.raises(ValueError, match="R must be positive"):
+        auto_clipped_grad(_loss, R=0.0)
+    with pytest.raises(ValueError, match="gamma must be positive"):
+        auto_clipped_grad(_loss, gamma=0.0)
+
+
+def test_product_refuses_cpu_parameters():
+    fn, st = clipped_grad(_loss, clipping_norm=1.0)
+    with pytest.raises(RuntimeError, match="GPU"):
+        fn(torch.ones(3), torch.ones(2, 3), state=st)
+
+
+def test_gaussian_noise_validation():
+    with pytest.raises(ValueError, match="non-negative"):
+        gaussian_noise(noise_multiplier=-1.0, key=key(0))
+    with pytest.raises(TypeError, match="RngKey"):
+        gaussian_noise(noise_multiplier=1.0, key=0)
+    fn, st = gaussian_noise(noise_multiplier=1.0, key=key(0))
+    with pytest.raises(TypeError, match="not NoisedPytree"):
+        fn(NoisedPytree(pytree=torch.zeros(1), max_norm=1.0, noise_stddev=1.0), st)
+    with pytest.raises(TypeError, match="expects ClippedPytree"):
+        fn(torch.zeros(1), st)
+
+
+def test_gaussian_noise_zero_multiplier_passthrough_on_cpu_tree():
+    # nm = 0 adds nothing and launches nothing: the same leaf objects come back.
+    fn, st = gaussian_noise(noise_multiplier=0.0, key=key(0))
+    leaf = torch.ones(8)
+    out, st2 = fn(ClippedPytree(leaf, max_norm=float("inf")), st)
+    assert out.pytree is leaf and out.noise_stddev == 0.0
+    assert st2._step_counter == 1
