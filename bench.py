@@ -45,7 +45,44 @@ def parse_args():
     ap.add_argument("--rank", type=int, default=16)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device-to-device copy of BYTES five times (the known-size "
+                         "kernel that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
     return ap.parse_args()
+
+
+def kernel_label(stage, key):
+    """Device symbol of a table launch, as rocprofv3 names it."""
+    if key is None:
+        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum"}[stage]
+    dt, nkb = key
+    base = {"project": "k_project", "factor": "k_factor"}[stage]
+    if dt == torch.bfloat16:
+        return f"{base}_bf16<{nkb}>"
+    return f"{base}_f32"
+
+
+def committed_traffic(label):
+    """HBM bytes per launch of `label` from the committed PMC summary, or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("kernels", {}).get(label)
+    return None if entry is None else entry.get("traffic_bytes")
+
+
+def copy_calibration(nbytes):
+    dev = torch.device("cuda", 0)
+    n = nbytes // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n * 4, "launches": 5}), flush=True)
 
 
 def build_workload(layers, B, T, r, seed, device):
@@ -69,20 +106,6 @@ def build_workload(layers, B, T, r, seed, device):
             Bm = (torch.randn(r, d_out, device=device, generator=gd) * 0.02).to(torch.bfloat16)
             sites.append((name, x, gt, A, Bm))
     return lengths, sites
-
-
-def algorithmic_bytes(sites, lengths, n_leaf_params):
-    """One read of the unique a and g rows that carry tokens, plus the per-example
-    factor gradients written (fp32) and the bf16 clipped sum; per step."""
-    valid = sum(lengths)
-    seen = set()
-    ab = 0
-    for name, x, gt, A, Bm in sites:
-        if x.data_ptr() not in seen:
-            seen.add(x.data_ptr())
-            ab += valid * x.shape[1] * 2
-        ab += valid * gt.shape[1] * 2
-    return ab
 
 
 def cpu_baseline(r, seed):
@@ -149,6 +172,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     from opaque_amd import _native as N
     from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments
@@ -177,8 +203,8 @@ def main():
     sigma = 1.0 * 1.0 / B  # noise_multiplier * max_norm, max_norm = R / normalize_by
     k0 = key(42)
 
-    def step(i, events=None):
-        res = plan.run(events)
+    def step(i, events=None, log=None):
+        res = plan.run(events, log)
         flat = res.flat[torch.bfloat16]
         if events and "noise" in events:
             events["noise"][0].record()
@@ -194,18 +220,26 @@ def main():
     stages = ("project", "factor", "clip", "scale_sum", "noise")
     ev = [{s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for s in stages}
           for _ in range(args.steps)]
+    logs = [[] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(args.warmup + i, ev[i])
+        step(args.warmup + i, ev[i], logs[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1000.0 / args.steps
     stage_ms = {s: sum(e[s][0].elapsed_time(e[s][1]) for e in ev) / args.steps for s in stages}
 
+    # Per-launch durations (HIP events on the launch stream) and algorithmic bytes.
+    launches = []
+    for j, (stage, key, wgs, nbytes) in enumerate(plan.launch_info):
+        avg = sum(lg[j][2].elapsed_time(lg[j][3]) for lg in logs) / args.steps
+        launches.append({"kernel": kernel_label(stage, key), "stage": stage, "workgroups": wgs,
+                         "algorithmic_bytes": nbytes, "avg_ms": avg,
+                         "gbs": nbytes / (avg * 1e-3) / 1e9 if avg > 0 else None})
+    dom = max(launches, key=lambda d: d["avg_ms"])
+
     valid = sum(lengths)
-    ab_factor = algorithmic_bytes(sites, lengths, n_params) + B * n_params * 4
-    factor_gbs = ab_factor / (stage_ms["factor"] * 1e-3) / 1e9
     flops = 3 * 2 * valid * r * sum(d_in + d_out for d_in, d_out in LAYER_SHAPES.values()) * args.layers
     res = plan.run()
     torch.cuda.synchronize()
@@ -231,14 +265,16 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "odp_seg_factor (k_factor_bf16)",
-            "achieved": factor_gbs,
+            "kernel": dom["kernel"],
+            "achieved": dom["gbs"],
             "peak": MI355X_HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": factor_gbs / MI355X_HBM_PEAK_GBS,
-            "traffic": None,
-            "algorithmic_bytes_per_launch": ab_factor,
+            "frac": dom["gbs"] / MI355X_HBM_PEAK_GBS,
+            "traffic": committed_traffic(dom["kernel"]),
+            "algorithmic_bytes_per_launch": dom["algorithmic_bytes"],
+            "avg_launch_ms": dom["avg_ms"],
         },
+        "launches": launches,
         "stage_ms": stage_ms,
         "mfma_frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
         "algorithmic_tflops": flops / (ms * 1e-3) / 1e12,

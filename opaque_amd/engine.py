@@ -205,10 +205,12 @@ class _Table:
         self.fields = fields
         self.rows: list[list[int]] = []
         self.blocks: list[int] = []
+        self.nbytes = 0  # algorithmic HBM bytes of the launch (one read/write of each operand)
 
-    def add(self, row: dict[int, int], blocks: int) -> None:
+    def add(self, row: dict[int, int], blocks: int, nbytes: int = 0) -> None:
         if blocks <= 0:
             return
+        self.nbytes += int(nbytes)
         r = [0] * self.fields
         for k, v in row.items():
             r[k] = int(v)
@@ -410,6 +412,7 @@ class GhostPlan:
             return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
 
         elem = {torch.bfloat16: 2, torch.float32: 4}
+        valid = int(sum(seg.lengths))
         for ch, (dt, rtot, rows_alloc, planes, vbase, ubase) in zip(chunks, chunk_layout):
             qb = self.qbuf[dt]
             es = elem[dt]
@@ -432,6 +435,7 @@ class GhostPlan:
                     N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: 0, N.PJ_NSEG: n_seg,
                 },
                 lib.odp_project_blocks(n_rows),
+                (valid * d_in + rtot * d_in + planes * rtot * valid) * es,
             )
             c0 = 0
             a_leaves = []
@@ -451,6 +455,7 @@ class GhostPlan:
                         N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: 0, N.PJ_NSEG: n_seg,
                     },
                     lib.odp_project_blocks(n_rows),
+                    (valid * d_out + r * d_out + planes * r * valid) * es,
                 )
                 if s.a_leaf is not None:
                     a_leaves.append((s.a_leaf, c0, r))
@@ -465,7 +470,8 @@ class GhostPlan:
                         N.FT_LEAF0 + 1: 0 | (r << 16),
                         N.FT_LEAF0 + 2: slot_base[s.b_leaf],
                     }
-                    tab(ft, dt, r, N.FT_FIELDS).add(row, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r))
+                    tab(ft, dt, r, N.FT_FIELDS).add(row, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
+                                                    (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * 4)
                 c0 += r
             if a_leaves:
                 scal = {s.scaling for s in ch if s.a_leaf is not None}
@@ -476,12 +482,15 @@ class GhostPlan:
                         tab(ft, dt, r, N.FT_FIELDS).add(
                             self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, n_seg, sc,
                                         [(s_leaf, col0, r)], pe_off, slot_base),
-                            n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r))
+                            n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
+                            (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * 4)
                 else:
                     tab(ft, dt, rtot, N.FT_FIELDS).add(
                         self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, n_seg, scal.pop(),
                                     a_leaves, pe_off, slot_base),
-                        n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot))
+                        n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot),
+                        (valid * d_in + planes * rtot * valid) * es
+                        + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * 4)
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
@@ -498,6 +507,7 @@ class GhostPlan:
                     N.SQ_SLOT: slot_base[m.leaf], N.SQ_DTYPE: dtype_code(pe_m.dtype),
                 },
                 n_seg * lib.odp_sqnorm_blocks(n),
+                n_seg * n * pe_m.element_size(),
             )
             mat_pe[m.leaf] = pe_m
 
@@ -519,6 +529,8 @@ class GhostPlan:
                     N.SS_NSEG: n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2,
                 },
                 lib.odp_scale_sum_blocks(rank * M),
+                n_seg * rank * M * (4 if i not in mat_pe else mat_pe[i].element_size())
+                + rank * M * out.element_size() * (2 if self.out2 is not None else 1),
             )
 
         # Upload everything in one copy.
@@ -538,7 +550,7 @@ class GhostPlan:
         tab_idx = []
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
-            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total))
+            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total, t.nbytes))
         idx["gstart"] = pack.add(gstart)
         idx["thr"] = pack.add(np.asarray(self.clip.thresholds, dtype=np.float64))
         guards = self.clip.guards or [(1.0, 0.0, torch.float32)]
@@ -550,7 +562,9 @@ class GhostPlan:
         self.seg_start, self.seg_len, self.seg_ex = (views[idx[k]] for k in ("seg_start", "seg_len", "seg_ex"))
         self.gstart, self.thr = views[idx["gstart"]], views[idx["thr"]]
         self.guard, self.cls_dt = views[idx["guard"]], views[idx["cls_dt"]]
-        self.tables = [(name, dt, views[pi], views[wi], n, total) for name, dt, pi, wi, n, total in tab_idx]
+        self.tables = [(name, dt, views[pi], views[wi], n, total) for name, dt, pi, wi, n, total, _ in tab_idx]
+        # Per launch: (stage, (dtype, rank blocks) or None, workgroups, algorithmic bytes).
+        self.launch_info = [(name, dt, total, nb) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
 
     def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
@@ -579,12 +593,14 @@ class GhostPlan:
         return [self.pe[o : o + n] for o, n in self._pe_slices]
 
     # -- execution -------------------------------------------------------------
-    def run(self, events: dict | None = None) -> GhostResult:
+    def run(self, events: dict | None = None, launch_log: list | None = None) -> GhostResult:
         """Launch the step on the current stream.
 
         ``events`` may map a stage name ("project", "factor", "sqnorm",
         "clip", "scale_sum") to a (start, end) pair of torch.cuda.Event that
-        are recorded around that stage's launch.
+        are recorded around that stage's launches.  ``launch_log``, when a
+        list, receives one (stage, key, start, end) entry per table launch
+        with freshly recorded timing events, in ``launch_info`` order.
         """
         lib = N.load()
         stream = _stream()
@@ -592,11 +608,21 @@ class GhostPlan:
         ev = events or {}
         self.part.zero_()
         live = [t for t in self.tables if t[5] > 0 and t[0] != "scale_sum"]
+
+        def mark(name, dt):
+            if launch_log is None:
+                return None
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch_log.append((name, dt, e0, e1))
+            return e1
+
         for idx, (name, dt, probs, ws, n, total) in enumerate(live):
             first = idx == 0 or live[idx - 1][0] != name
             last = idx == len(live) - 1 or live[idx + 1][0] != name
             if name in ev and first:
                 ev[name][0].record()
+            end_ev = mark(name, dt)
             if name == "project":
                 N.check(lib.odp_project(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                         self.seg_start.data_ptr(), self.seg_len.data_ptr(), dt[1]), name)
@@ -608,6 +634,8 @@ class GhostPlan:
             elif name == "sqnorm":
                 N.check(lib.odp_sqnorm(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                        self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
+            if end_ev is not None:
+                end_ev.record()
             if name in ev and last:
                 ev[name][1].record()
         if "clip" in ev:
@@ -628,9 +656,12 @@ class GhostPlan:
             if name == "scale_sum" and total:
                 if name in ev:
                     ev[name][0].record()
+                end_ev = mark(name, dt)
                 N.check(lib.odp_scale_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                           self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
                                           self.n_groups, float(self.clip.normalize_by)), name)
+                if end_ev is not None:
+                    end_ev.record()
                 if name in ev:
                     ev[name][1].record()
         return GhostResult(

@@ -202,3 +202,23 @@ def test_gaussian_noise_zero_multiplier_passthrough_on_cpu_tree():
     out, st2 = fn(ClippedPytree(leaf, max_norm=float("inf")), st)
     assert out.pytree is leaf and out.noise_stddev == 0.0
     assert st2._step_counter == 1
+
+
+def test_alias_installs_reference_import_paths():
+    import subprocess
+    import sys
+
+    code = (
+        "import opaque_amd.alias as a; assert a.install();"
+        "from opaque.dpsgd.clipping import clipped_grad, auto_clipped_grad, per_group;"
+        "from opaque.dpsgd.noise import gaussian_noise;"
+        "from opaque.types import ClippedPytree, NoisedPytree, PerGroup;"
+        "from opaque.random import key, fold_in;"
+        "from opaque.pytree import tree_map;"
+        "from opaque.dpsgd.clipping.types import ClippingStats;"
+        "import opaque_amd.clipping as c; assert clipped_grad is c.clipped_grad; print('ok')"
+    )
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         cwd=os.path.dirname(HERE))
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "ok"
