@@ -53,8 +53,10 @@ def parse_args():
 
 def kernel_label(stage, key):
     """Device symbol of a table launch, as rocprofv3 names it."""
+    if stage == "lin_norm":
+        return "k_lin_gram_norm" if key == 1 else "k_lin_outer_norm"
     if key is None:
-        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum"}[stage]
+        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "lin_sum": "k_lin_clip_sum"}[stage]
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]
     if dt == torch.bfloat16:
@@ -232,7 +234,7 @@ def main():
 
     # Per-launch durations (HIP events on the launch stream) and algorithmic bytes.
     launches = []
-    for j, (stage, key, wgs, nbytes) in enumerate(plan.launch_info):
+    for j, (stage, key, wgs, nbytes, _flops) in enumerate(plan.launch_info):
         avg = sum(lg[j][2].elapsed_time(lg[j][3]) for lg in logs) / args.steps
         launches.append({"kernel": kernel_label(stage, key), "stage": stage, "workgroups": wgs,
                          "algorithmic_bytes": nbytes, "avg_ms": avg,

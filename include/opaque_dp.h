@@ -22,8 +22,9 @@
  *       per-example squared norms of clip_pytree,
  *       opaque-engine/src/opaque/api/engine/clipping/_pytree.py:224-265,520-540
  *   odp_linear_sqnorm             -> per-example squared norm of a full
- *       weight gradient G[i]^T X[i] without materialising it (the reference
- *       materialises it under vmap(grad), clipping/_clipped_fun.py:756-762)
+ *       weight gradient G[i]^T X[i] without materialising it, outer or
+ *       token-Gram form (the reference materialises it under vmap(grad),
+ *       clipping/_clipped_fun.py:756-762)
  *   odp_clip_factors              -> clip_pytree / auto_scale_pytree ratio,
  *       guard and finalisation, clipping/_pytree.py:106-142,345-431,475-564
  *       and the clipped counts of clipping/_clipped_fun.py:472-523
@@ -185,6 +186,49 @@ int64_t odp_scale_sum_blocks(int64_t n_elems);
 int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                   int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
                   const float* scales, int32_t n_ex, int32_t n_groups, float normalize_by);
+
+/* ---- full-weight linears: per-example norms and the clipped sum ---------
+ * A linear y = x W^T over rows of X [n_rows][d_in] and output gradients
+ * G [n_rows][d_out] (bf16, row pitches and d_in, d_out multiples of 8) has
+ * per-example weight gradients M_s = sum_{t in s} g_t x_t^T ([d_out][d_in]).
+ *
+ * odp_linear_sqnorm writes fp64 partials of ||M_s||_F^2 to
+ * part[seg_example[s] * part_stride + ODP_LN_SLOT + tile], in one of two
+ * forms (f32 squares of M's entries, non-finite entries counted as 0, for
+ * OUTER; the token-Gram identity sum_{t,u}(x_t.x_u)(g_t.g_u) for GRAM);
+ * odp_linear_tiles(form, ...) is the number of slots (and workgroups per
+ * segment) a problem uses; GRAM needs ODP_LN_NB = ceil(max_len / 128) of
+ * the problem's longest segment.  Replaces the per-example weight
+ * gradients that the reference materialises under vmap(grad)
+ * (opaque-engine/src/opaque/api/engine/clipping/_clipped_fun.py:756-762)
+ * and their squared norms (clipping/_pytree.py:224-265).
+ *
+ * odp_linear_clipped_sum writes out[o][i] = round_out(sum_s c_s M_s[o][i])
+ * and then round_out(out / normalize_by) if normalize_by != 1, with
+ * c_s = scales[cls][group][seg_example[s]] and non-finite entries of M_s
+ * dropped; one workgroup per 128 x 128 output tile
+ * (odp_linear_sum_blocks).  Replaces clip_pytree's scale and the batch sum
+ * (clipping/_pytree.py:553, clipping/_clipped_fun.py:115-134,821-824).      */
+enum {
+  ODP_LN_X = 0, ODP_LN_LDX = 1, ODP_LN_G = 2, ODP_LN_LDG = 3,
+  ODP_LN_DIN = 4, ODP_LN_DOUT = 5, ODP_LN_SEG_FIRST = 6, ODP_LN_NSEG = 7,
+  ODP_LN_SLOT = 8,   /* sqnorm: first partial slot of the weight            */
+  ODP_LN_OUT = 9,    /* clipped sum: address of out [d_out][d_in]           */
+  ODP_LN_FLAGS = 10, /* clipped sum: out dtype | group << 8 | cls << 24     */
+  ODP_LN_NB = 11,    /* GRAM: 128-row blocks of the longest segment         */
+  ODP_LN_FIELDS = 16
+};
+int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len);
+int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* problems,
+                      const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                      const int32_t* seg_row_start, const int32_t* seg_row_len,
+                      const int32_t* seg_example, double* part, int64_t part_stride);
+int64_t odp_linear_sum_blocks(int64_t d_in, int64_t d_out);
+int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
+                           const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                           const int32_t* seg_row_start, const int32_t* seg_row_len,
+                           const int32_t* seg_example, const float* scales, int32_t n_ex,
+                           int32_t n_groups, float normalize_by);
 
 /* ---- odp_gaussian_noise --------------------------------------------------
  * out[i] = round_out(in[i] + f32(sigma * sqrt 2) * erfinv(2u - 1)) with

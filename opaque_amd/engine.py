@@ -129,6 +129,27 @@ class LoraSite:
 
 
 @dataclass
+class LinearSite:
+    """A full-weight linear y = x W^T over the batch rows (bf16).
+
+    ``w_leaf`` indexes the plan's leaf list; the leaf is W's gradient,
+    shaped [d_out, d_in].  ``form`` picks the per-example norm algorithm
+    (``N.FORM_OUTER`` / ``N.FORM_GRAM``); None chooses the one with fewer
+    MFMA flops for the longest segment.
+    """
+
+    x: torch.Tensor
+    g: torch.Tensor
+    w_leaf: int
+    form: int | None = None
+
+
+def choose_form(max_len: int, d_in: int, d_out: int) -> int:
+    """GRAM costs L^2 (d_in + d_out) flops per example (upper triangle), OUTER 2 L d_in d_out."""
+    return N.FORM_GRAM if max_len * (d_in + d_out) < 2 * d_in * d_out else N.FORM_OUTER
+
+
+@dataclass
 class MaterializedLeaf:
     """A leaf whose per-example gradients are already materialised: [n_seg, *shape]."""
 
@@ -206,11 +227,13 @@ class _Table:
         self.rows: list[list[int]] = []
         self.blocks: list[int] = []
         self.nbytes = 0  # algorithmic HBM bytes of the launch (one read/write of each operand)
+        self.nflops = 0  # algorithmic flops of the launch
 
-    def add(self, row: dict[int, int], blocks: int, nbytes: int = 0) -> None:
+    def add(self, row: dict[int, int], blocks: int, nbytes: int = 0, nflops: int = 0) -> None:
         if blocks <= 0:
             return
         self.nbytes += int(nbytes)
+        self.nflops += int(nflops)
         r = [0] * self.fields
         for k, v in row.items():
             r[k] = int(v)
@@ -251,6 +274,7 @@ class GhostPlan:
         clip: ClipSpec,
         lora_sites: list[LoraSite] = (),
         materialized: list[MaterializedLeaf] = (),
+        linear_sites: list[LinearSite] = (),
         device: torch.device | str = "cuda",
         second_moment: bool = False,
     ) -> None:
@@ -271,13 +295,28 @@ class GhostPlan:
             if not 0 <= lf.group < self.n_groups or not 0 <= lf.cls < self.n_cls:
                 raise ValueError("leaf group/class out of range")
         self._keep: list[torch.Tensor] = []
-        self._build(list(lora_sites), list(materialized))
+        self._build(list(lora_sites), list(materialized), list(linear_sites))
 
     # -- construction --------------------------------------------------------
-    def _build(self, sites: list[LoraSite], mats: list[MaterializedLeaf]) -> None:
+    def _build(self, sites: list[LoraSite], mats: list[MaterializedLeaf], lins: list[LinearSite]) -> None:
         seg = self.segments
         dev = self.device
         n_rows, n_seg = seg.n_rows, seg.n_seg
+        if len(set(seg.examples)) != len(seg.examples):
+            raise ValueError("each example may own at most one segment of a plan")
+        max_len = max(seg.lengths, default=0)
+        for ls in lins:
+            if ls.x.device != dev or ls.g.device != dev:
+                raise ValueError("linear site tensors must be on the plan device")
+            if ls.x.dtype != torch.bfloat16 or ls.g.dtype != torch.bfloat16:
+                raise TypeError("full-weight linear sites run in bfloat16")
+            if ls.x.reshape(-1, ls.x.shape[-1]).shape[0] != n_rows or \
+                    ls.g.reshape(-1, ls.g.shape[-1]).shape[0] != n_rows:
+                raise ValueError("linear site row count does not match the segments")
+            if not (supports_rows(ls.x) and supports_rows(ls.g)):
+                raise ValueError("linear site feature sizes must be multiples of 8")
+            if tuple(self.leaves[ls.w_leaf].shape) != (ls.g.shape[-1], ls.x.shape[-1]):
+                raise ValueError("a linear site's leaf must be shaped [d_out, d_in]")
         ldq = (n_rows + 32 + 7) // 8 * 8
 
         # Group sites by activation tensor, then chunk by rank/leaf budget.
@@ -338,6 +377,12 @@ class GhostPlan:
             if m.per_example.shape[0] != n_seg:
                 raise ValueError("materialised leaves need one row per segment")
             leaf_slots[m.leaf] = int(N.load().odp_sqnorm_blocks(n))
+        lin_form: dict[int, int] = {}
+        for ls in lins:
+            d_in, d_out = ls.x.shape[-1], ls.g.shape[-1]
+            form = ls.form if ls.form is not None else choose_form(max_len, d_in, d_out)
+            lin_form[ls.w_leaf] = form
+            leaf_slots[ls.w_leaf] = int(lib.odp_linear_tiles(form, d_in, d_out, max_len))
         covered = set(leaf_slots)
         if len(covered) != len(leaf_slots) or covered != set(range(len(self.leaves))):
             missing = sorted(set(range(len(self.leaves))) - covered)
@@ -511,8 +556,40 @@ class GhostPlan:
             )
             mat_pe[m.leaf] = pe_m
 
+        lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS)}
+        lsum = _Table(N.LN_FIELDS)
+        nb_max = (max_len + 127) // 128
+        for ls in lins:
+            x, g = _rows(ls.x), _rows(ls.g)
+            self._keep += [x, g]
+            d_in, d_out = x.shape[1], g.shape[1]
+            form = lin_form[ls.w_leaf]
+            common = {
+                N.LN_X: x.data_ptr(), N.LN_LDX: x.stride(0), N.LN_G: g.data_ptr(), N.LN_LDG: g.stride(0),
+                N.LN_DIN: d_in, N.LN_DOUT: d_out, N.LN_SEG_FIRST: 0, N.LN_NSEG: n_seg,
+            }
+            tiles = int(lib.odp_linear_tiles(form, d_in, d_out, max_len))
+            if form == N.FORM_GRAM:
+                fl = sum(ln * ln for ln in seg.lengths) * (d_in + d_out)
+            else:
+                fl = 2 * valid * d_in * d_out
+            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf], N.LN_NB: nb_max}, n_seg * tiles,
+                          valid * (d_in + d_out) * 2, fl)
+            lf = self.leaves[ls.w_leaf]
+            out = self.out[ls.w_leaf]
+            flags = dtype_code(lf.out_dtype) | (lf.group << 8) | (lf.cls << 24)
+            lsum.add({**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags},
+                     int(lib.odp_linear_sum_blocks(d_in, d_out)),
+                     valid * (d_in + d_out) * 2 + d_in * d_out * out.element_size(),
+                     2 * valid * d_in * d_out)
+        lin_leaves = set(lin_form)
+        if lin_leaves and self.second_moment:
+            raise ValueError("second moments of full-weight linear sites are not computed natively")
+
         ss = _Table(N.SS_FIELDS)
         for i, lf in enumerate(self.leaves):
+            if i in lin_leaves:
+                continue
             out = self.out[i]
             out2 = self.out2[i].data_ptr() if self.out2 is not None else 0
             if i in mat_pe:
@@ -546,11 +623,14 @@ class GhostPlan:
         for key in sorted(ft, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("factor", key, ft[key]))
         tabs.append(("sqnorm", None, sq))
+        tabs.append(("lin_norm", N.FORM_OUTER, lnt[N.FORM_OUTER]))
+        tabs.append(("lin_norm", N.FORM_GRAM, lnt[N.FORM_GRAM]))
         tabs.append(("scale_sum", None, ss))
+        tabs.append(("lin_sum", None, lsum))
         tab_idx = []
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
-            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total, t.nbytes))
+            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total, (t.nbytes, t.nflops)))
         idx["gstart"] = pack.add(gstart)
         idx["thr"] = pack.add(np.asarray(self.clip.thresholds, dtype=np.float64))
         guards = self.clip.guards or [(1.0, 0.0, torch.float32)]
@@ -563,8 +643,10 @@ class GhostPlan:
         self.gstart, self.thr = views[idx["gstart"]], views[idx["thr"]]
         self.guard, self.cls_dt = views[idx["guard"]], views[idx["cls_dt"]]
         self.tables = [(name, dt, views[pi], views[wi], n, total) for name, dt, pi, wi, n, total, _ in tab_idx]
-        # Per launch: (stage, (dtype, rank blocks) or None, workgroups, algorithmic bytes).
-        self.launch_info = [(name, dt, total, nb) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
+        # Per launch, in launch order: (stage, key, workgroups, algorithmic bytes, algorithmic flops).
+        info = [(name, dt, total, nb[0], nb[1]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
+        after_clip = ("scale_sum", "lin_sum")
+        self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
 
     def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
@@ -607,7 +689,7 @@ class GhostPlan:
         seg = self.segments
         ev = events or {}
         self.part.zero_()
-        live = [t for t in self.tables if t[5] > 0 and t[0] != "scale_sum"]
+        live = [t for t in self.tables if t[5] > 0 and t[0] not in ("scale_sum", "lin_sum")]
 
         def mark(name, dt):
             if launch_log is None:
@@ -634,6 +716,10 @@ class GhostPlan:
             elif name == "sqnorm":
                 N.check(lib.odp_sqnorm(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                        self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
+            elif name == "lin_norm":
+                N.check(lib.odp_linear_sqnorm(stream, dt, probs.data_ptr(), ws.data_ptr(), n, total,
+                                              self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                              self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
             if end_ev is not None:
                 end_ev.record()
             if name in ev and last:
@@ -660,6 +746,18 @@ class GhostPlan:
                 N.check(lib.odp_scale_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                           self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
                                           self.n_groups, float(self.clip.normalize_by)), name)
+                if end_ev is not None:
+                    end_ev.record()
+                if name in ev:
+                    ev[name][1].record()
+            elif name == "lin_sum" and total:
+                if name in ev:
+                    ev[name][0].record()
+                end_ev = mark(name, dt)
+                N.check(lib.odp_linear_clipped_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                                   self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                                   self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
+                                                   self.n_groups, float(self.clip.normalize_by)), name)
                 if end_ev is not None:
                     end_ev.record()
                 if name in ev:

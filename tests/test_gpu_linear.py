@@ -1,0 +1,141 @@
+"""GPU parity of the full-weight linear kernels (outer / Gram norms, clipped-sum GEMM).
+
+Per-example weight gradients M_i = G_i^T X_i are formed in fp64 on the CPU
+by the oracle; the device never materialises them.  bf16 inputs, tolerance
+rel 2e-2 against the oracle (the two device norm forms agree far closer).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from opaque_amd import _native as N
+from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LinearSite, MaterializedLeaf, Segments
+from opaque_amd.guard import guard_constants, leaf_guards
+from oracle import dp_ref, lora_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _case(n_ex, T, d_in, d_out, lengths, seed, scale_spread=True):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(n_ex * T, d_in, generator=g)
+    G = torch.randn(n_ex * T, d_out, generator=g)
+    if scale_spread:
+        s = torch.logspace(-0.7, 0.7, n_ex).repeat_interleave(T).view(-1, 1)
+        G = G * s
+    seg = Segments.padded(n_ex, T, lengths)
+    for i, ln in enumerate(seg.lengths):  # padding rows carry garbage that must be ignored
+        X[i * T + ln : (i + 1) * T] = 1e4
+        G[i * T + ln : (i + 1) * T] = -1e4
+    return X.to(torch.bfloat16), G.to(torch.bfloat16), seg
+
+
+def _plan(X, G, seg, *, C, mode, form, normalize_by=1.0, out_dtype=torch.bfloat16):
+    d_in, d_out = X.shape[1], G.shape[1]
+    _, rnd = leaf_guards([(d_out, d_in)], [torch.bfloat16])
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=mode, thresholds=[C], effective=C, normalize_by=normalize_by,
+                    guards=[(rel, ab, torch.bfloat16)])
+    plan = GhostPlan(segments=seg, leaves=[LeafOut((d_out, d_in), out_dtype)], clip=clip,
+                     linear_sites=[LinearSite(X.to(DEV), G.to(DEV), 0, form)], device=DEV)
+    res = plan.run()
+    torch.cuda.synchronize()
+    return plan, res, rnd
+
+
+def _ref_norms(X, G, seg):
+    pe = lora_ref.linear_per_example(X.float(), G.float(), seg.starts, seg.lengths)
+    return pe, pe.pow(2).sum((1, 2)).sqrt()
+
+
+SHAPES = [
+    # n_ex, T, d_in, d_out, lengths
+    (4, 64, 128, 128, None),
+    (5, 160, 200, 72, [160, 37, 0, 129, 64]),
+    (3, 300, 136, 264, [300, 1, 255]),
+    (2, 512, 384, 256, [512, 400]),
+]
+
+
+@pytest.mark.parametrize("n_ex,T,d_in,d_out,lengths", SHAPES)
+@pytest.mark.parametrize("form", [N.FORM_OUTER, N.FORM_GRAM])
+def test_linear_norms_match_oracle(n_ex, T, d_in, d_out, lengths, form):
+    X, G, seg = _case(n_ex, T, d_in, d_out, lengths, seed=d_in + d_out)
+    _, want = _ref_norms(X, G, seg)
+    _, res, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=form)
+    got = res.norms.double().cpu()
+    assert torch.allclose(got, want.float().double(), rtol=2e-3, atol=1e-6), (got, want)
+
+
+def test_outer_and_gram_forms_agree():
+    X, G, seg = _case(3, 256, 256, 192, [256, 100, 17], seed=9)
+    _, r_outer, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=N.FORM_OUTER)
+    a = r_outer.norms.double().cpu().clone()
+    _, r_gram, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=N.FORM_GRAM)
+    b = r_gram.norms.double().cpu()
+    assert torch.allclose(a, b, rtol=1e-5), (a, b)
+
+
+@pytest.mark.parametrize("mode", [N.CLIP_FIXED, N.CLIP_AUTOS])
+@pytest.mark.parametrize("form", [N.FORM_OUTER, N.FORM_GRAM])
+def test_linear_clipped_sum_matches_oracle(mode, form):
+    n_ex, T, d_in, d_out = 6, 96, 264, 136
+    lengths = [96, 50, 7, 96, 0, 81]
+    X, G, seg = _case(n_ex, T, d_in, d_out, lengths, seed=4)
+    pe, norms = _ref_norms(X, G, seg)
+    C = float(norms[norms > 0].median())
+    _, res, rnd = _plan(X, G, seg, C=C, mode=mode, form=form, normalize_by=6.0)
+    # Oracle: reference clip_pytree per example (the per-example gradient rounded
+    # to the bf16 parameter dtype, as vmap(grad) produces it), fp32 sum, cast, /6.
+    outs = []
+    for i in range(n_ex):
+        leaf = {"w": pe[i].to(torch.bfloat16)}
+        if mode == N.CLIP_FIXED:
+            c, _, _ = dp_ref.clip_pytree(leaf, C)
+        else:
+            c, _, _ = dp_ref.auto_scale_pytree(leaf, C, 0.01)
+        outs.append(c["w"])
+    want = (torch.stack(outs).sum(0, dtype=torch.float32).to(torch.bfloat16) / 6.0).double()
+    got = res.leaves[0].double().cpu()
+    assert (got - want).norm() <= 2e-2 * want.norm()
+    band = 1e-3
+    far = ((norms - C).abs() / C) > band
+    assert torch.equal(res.clipped_total.cpu().bool()[far], (norms.float() > C)[far])
+
+
+def test_linear_with_materialized_leaf_per_group():
+    """A linear weight and a materialised bias leaf in two clip groups."""
+    n_ex, T, d_in, d_out = 4, 64, 128, 64
+    X, G, seg = _case(n_ex, T, d_in, d_out, [64, 30, 64, 12], seed=2)
+    pe, _ = _ref_norms(X, G, seg)
+    bias_pe = torch.stack([G[s : s + ln].float().sum(0) for s, ln in zip(seg.starts, seg.lengths)])
+    shapes = [(d_out, d_in), (d_out,)]
+    _, rnd = leaf_guards(shapes, [torch.bfloat16, torch.float32])
+    g_w, g_b = 0.5, 0.25
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[g_w, g_b], effective=(g_w**2 + g_b**2) ** 0.5,
+                    guards=[(*guard_constants(torch.bfloat16, rnd), torch.bfloat16),
+                            (*guard_constants(torch.float32, rnd), torch.float32)])
+    plan = GhostPlan(segments=seg,
+                     leaves=[LeafOut((d_out, d_in), torch.float32, group=0, cls=0),
+                             LeafOut((d_out,), torch.float32, group=1, cls=1)],
+                     clip=clip, linear_sites=[LinearSite(X.to(DEV), G.to(DEV), 0)],
+                     materialized=[MaterializedLeaf(bias_pe.to(DEV), 1)], device=DEV)
+    res = plan.run()
+    torch.cuda.synchronize()
+
+    class _PG:
+        groups = {("w",): "w", ("b",): "b"}
+        values = {"w": g_w, "b": g_b}
+
+    outs_w, outs_b = [], []
+    for i in range(n_ex):
+        c, _, gn = dp_ref.clip_pytree({"w": pe[i].to(torch.bfloat16), "b": bias_pe[i]}, _PG)
+        outs_w.append(c["w"].float())
+        outs_b.append(c["b"])
+    want_w = torch.stack(outs_w).sum(0).double()
+    want_b = torch.stack(outs_b).sum(0).double()
+    assert (res.leaves[0].double().cpu() - want_w).norm() <= 2e-2 * want_w.norm()
+    assert (res.leaves[1].double().cpu() - want_b).norm() <= 1e-5 * want_b.norm()
