@@ -40,8 +40,10 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--batch", type=int, default=16)
-    ap.add_argument("--seq", type=int, default=1024)
+    ap.add_argument("--workload", choices=["c3", "c4"], default="c3",
+                    help="c3: LoRA r=16 (the headline metric); c4: full-weight linears")
+    ap.add_argument("--batch", type=int, default=None, help="default 16 (c3) / 8 (c4)")
+    ap.add_argument("--seq", type=int, default=None, help="default 1024 (c3) / 4096 (c4)")
     ap.add_argument("--rank", type=int, default=16)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
@@ -165,6 +167,81 @@ def cpu_baseline(r, seed):
     }
 
 
+def setup_c3(args, dev):
+    """C3: captured LoRA seams, AUTO-S, one clip group."""
+    from opaque_amd import _native as N
+    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments
+    from opaque_amd.guard import guard_constants, leaf_guards
+
+    B, T, r = args.batch, args.seq, args.rank
+    lengths, sites = build_workload(args.layers, B, T, r, args.seed, dev)
+    seg = Segments.padded(B, T, lengths)
+    leaves, lsites, shapes = [], [], []
+    for name, x, gt, A, Bm in sites:
+        ia, ib = len(leaves), len(leaves) + 1
+        leaves += [LeafOut(tuple(A.shape), torch.bfloat16), LeafOut(tuple(Bm.shape), torch.bfloat16)]
+        shapes += [tuple(A.shape), tuple(Bm.shape)]
+        lsites.append(LoraSite(x, gt, A, Bm, 2.0, a_leaf=ia, b_leaf=ib))
+    _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=N.CLIP_AUTOS, thresholds=[1.0], effective=1.0, gamma=0.01,
+                    normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
+    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev)
+    valid = sum(lengths)
+    flops = 3 * 2 * valid * r * sum(d_in + d_out for d_in, d_out in LAYER_SHAPES.values()) * args.layers
+    config = {
+        "workload": "C3: Llama-3-8B-shaped LoRA r=16, 32 layers x 7 linears, batch 16 x seq 1024, "
+                    "ragged lengths U[256,1024], AUTO-S R=1 gamma=0.01, noise multiplier 1.0",
+        "global_batch": B, "seq_len": T, "layers": args.layers, "rank": r,
+        "valid_tokens": valid, "parallelism": "single GPU",
+    }
+    metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16"
+    return plan, 1.0 / B, config, metric, flops, ("project", "factor", "clip", "scale_sum", "noise"), "hbm"
+
+
+C4_THRESHOLDS = {"q": 1.0, "k": 0.5, "v": 0.5, "o": 1.0, "gate": 2.0, "up": 2.0, "down": 2.0}
+
+
+def setup_c4(args, dev):
+    """C4: full-weight linears (outer / Gram norms, clipped-sum GEMM), PerGroup per layer type."""
+    from opaque_amd import _native as N
+    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LinearSite, Segments
+    from opaque_amd.guard import guard_constants, leaf_guards
+
+    B, T = args.batch, args.seq
+    N_rows = B * T
+    gd = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    names = list(LAYER_SHAPES)
+    leaves, lins, shapes = [], [], []
+    for _ in range(args.layers):
+        xs = {}
+        for name, (d_in, d_out) in LAYER_SHAPES.items():
+            key_ = SHARED_INPUT[name]
+            if key_ not in xs:
+                xs[key_] = torch.randn(N_rows, d_in, dtype=torch.bfloat16, device=dev, generator=gd)
+            g = torch.randn(N_rows, d_out, dtype=torch.bfloat16, device=dev, generator=gd)
+            lins.append(LinearSite(xs[key_], g, len(leaves)))
+            leaves.append(LeafOut((d_out, d_in), torch.bfloat16, group=names.index(name)))
+            shapes.append((d_out, d_in))
+    seg = Segments.padded(B, T)
+    _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    thr = [C4_THRESHOLDS[n] for n in names]
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=thr, effective=math.sqrt(sum(v * v for v in thr)),
+                    normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
+    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=dev)
+    flops = sum(f for *_, f in plan.launch_info)
+    config = {
+        "workload": "C4: Llama-3-8B-shaped full weights, 32 layers x 7 linears, batch 8 x seq 4096, "
+                    "PerGroup fixed clipping (one threshold per linear type), noise multiplier 1.0",
+        "global_batch": B, "seq_len": T, "layers": args.layers,
+        "thresholds": C4_THRESHOLDS, "parallelism": "single GPU",
+    }
+    metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B full-weight per-example clipping"
+    sigma = 1.0 * clip.effective / B
+    return plan, sigma, config, metric, flops, ("lin_norm", "clip", "lin_sum", "noise"), "mfma"
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -179,30 +256,21 @@ def main():
         return
 
     from opaque_amd import _native as N
-    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments
-    from opaque_amd.guard import guard_constants, leaf_guards
     from opaque_amd.noise import add_noise_tree
     from opaque_amd.random import fold_in, key
 
     N.load()
     dev = torch.device("cuda", 0)
-    B, T, r = args.batch, args.seq, args.rank
-    lengths, sites = build_workload(args.layers, B, T, r, args.seed, dev)
-    seg = Segments.padded(B, T, lengths)
-
-    leaves, lsites, shapes = [], [], []
-    for name, x, gt, A, Bm in sites:
-        ia, ib = len(leaves), len(leaves) + 1
-        leaves += [LeafOut(tuple(A.shape), torch.bfloat16), LeafOut(tuple(Bm.shape), torch.bfloat16)]
-        shapes += [tuple(A.shape), tuple(Bm.shape)]
-        lsites.append(LoraSite(x, gt, A, Bm, 2.0, a_leaf=ia, b_leaf=ib))
-    _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
-    rel, ab = guard_constants(torch.bfloat16, rnd)
-    clip = ClipSpec(mode=N.CLIP_AUTOS, thresholds=[1.0], effective=1.0, gamma=0.01,
-                    normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
-    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev)
-    n_params = sum(math.prod(lf.shape) for lf in leaves)
-    sigma = 1.0 * 1.0 / B  # noise_multiplier * max_norm, max_norm = R / normalize_by
+    if args.workload == "c4":
+        args.batch = 8 if args.batch is None else args.batch
+        args.seq = 4096 if args.seq is None else args.seq
+        plan, sigma, config, metric, flops, stages, bound = setup_c4(args, dev)
+    else:
+        args.batch = 16 if args.batch is None else args.batch
+        args.seq = 1024 if args.seq is None else args.seq
+        plan, sigma, config, metric, flops, stages, bound = setup_c3(args, dev)
+    B = args.batch
+    n_params = sum(math.prod(lf.shape) for lf in plan.leaves)
     k0 = key(42)
 
     def step(i, events=None, log=None):
@@ -219,7 +287,6 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    stages = ("project", "factor", "clip", "scale_sum", "noise")
     ev = [{s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for s in stages}
           for _ in range(args.steps)]
     logs = [[] for _ in range(args.steps)]
@@ -232,22 +299,31 @@ def main():
     ms = elapsed * 1000.0 / args.steps
     stage_ms = {s: sum(e[s][0].elapsed_time(e[s][1]) for e in ev) / args.steps for s in stages}
 
-    # Per-launch durations (HIP events on the launch stream) and algorithmic bytes.
+    # Per-launch durations (HIP events on the launch stream), algorithmic bytes and flops.
     launches = []
-    for j, (stage, key, wgs, nbytes, _flops) in enumerate(plan.launch_info):
+    for j, (stage, key_, wgs, nbytes, nflops) in enumerate(plan.launch_info):
         avg = sum(lg[j][2].elapsed_time(lg[j][3]) for lg in logs) / args.steps
-        launches.append({"kernel": kernel_label(stage, key), "stage": stage, "workgroups": wgs,
-                         "algorithmic_bytes": nbytes, "avg_ms": avg,
-                         "gbs": nbytes / (avg * 1e-3) / 1e9 if avg > 0 else None})
+        launches.append({"kernel": kernel_label(stage, key_), "stage": stage, "workgroups": wgs,
+                         "algorithmic_bytes": nbytes, "algorithmic_flops": nflops, "avg_ms": avg,
+                         "gbs": nbytes / (avg * 1e-3) / 1e9 if avg > 0 else None,
+                         "tflops": nflops / (avg * 1e-3) / 1e12 if avg > 0 else None})
     dom = max(launches, key=lambda d: d["avg_ms"])
-
-    valid = sum(lengths)
-    flops = 3 * 2 * valid * r * sum(d_in + d_out for d_in, d_out in LAYER_SHAPES.values()) * args.layers
     res = plan.run()
     torch.cuda.synchronize()
 
+    if bound == "hbm":
+        roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["gbs"],
+                    "peak": MI355X_HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["gbs"] / MI355X_HBM_PEAK_GBS,
+                    "traffic": committed_traffic(dom["kernel"]),
+                    "algorithmic_bytes_per_launch": dom["algorithmic_bytes"], "avg_launch_ms": dom["avg_ms"]}
+    else:
+        roofline = {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["tflops"],
+                    "peak": MI355X_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": dom["tflops"] / MI355X_BF16_PEAK_TFLOPS,
+                    "traffic": committed_traffic(dom["kernel"]),
+                    "algorithmic_flops_per_launch": dom["algorithmic_flops"], "avg_launch_ms": dom["avg_ms"]}
     out = {
-        "metric": "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16",
+        "metric": metric,
         "value": B / (ms * 1e-3),
         "unit": "examples/sec",
         "n_gpus": 1,
@@ -259,31 +335,16 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {
-            "workload": "C3: Llama-3-8B-shaped LoRA r=16, 32 layers x 7 linears, batch 16 x seq 1024, "
-                        "ragged lengths U[256,1024], AUTO-S R=1 gamma=0.01, noise multiplier 1.0",
-            "global_batch": B, "seq_len": T, "layers": args.layers, "rank": r,
-            "valid_tokens": valid, "parallelism": "single GPU",
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom["kernel"],
-            "achieved": dom["gbs"],
-            "peak": MI355X_HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": dom["gbs"] / MI355X_HBM_PEAK_GBS,
-            "traffic": committed_traffic(dom["kernel"]),
-            "algorithmic_bytes_per_launch": dom["algorithmic_bytes"],
-            "avg_launch_ms": dom["avg_ms"],
-        },
+        "config": config,
+        "roofline": roofline,
         "launches": launches,
         "stage_ms": stage_ms,
         "mfma_frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
         "algorithmic_tflops": flops / (ms * 1e-3) / 1e12,
         "clipped_fraction": float(res.clipped_total.float().mean().item()),
     }
-    if args.cpu_baseline == "on":
-        out["cpu_baseline"] = cpu_baseline(r, args.seed)
+    if args.cpu_baseline == "on" and args.workload == "c3":
+        out["cpu_baseline"] = cpu_baseline(args.rank, args.seed)
     print(json.dumps(out), flush=True)
 
 

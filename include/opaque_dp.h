@@ -203,11 +203,12 @@ int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* w
  * (opaque-engine/src/opaque/api/engine/clipping/_clipped_fun.py:756-762)
  * and their squared norms (clipping/_pytree.py:224-265).
  *
- * odp_linear_clipped_sum writes out[o][i] = round_out(sum_s c_s M_s[o][i])
- * and then round_out(out / normalize_by) if normalize_by != 1, with
- * c_s = scales[cls][group][seg_example[s]] and non-finite entries of M_s
- * dropped; one workgroup per 128 x 128 output tile
- * (odp_linear_sum_blocks).  Replaces clip_pytree's scale and the batch sum
+ * odp_linear_clipped_sum writes out[o][i] = round_out(sum_s sum_{t in s}
+ * g_t[o] bf16(c_s x_t[i])) and then round_out(out / normalize_by) if
+ * normalize_by != 1, with c_s = scales[cls][group][seg_example[s]] (the
+ * clip factor folded into X's rows; non-finite inputs propagate); one
+ * workgroup per 256 x 128 output tile (odp_linear_sum_blocks, padded to a
+ * multiple of 8).  Replaces clip_pytree's scale and the batch sum
  * (clipping/_pytree.py:553, clipping/_clipped_fun.py:115-134,821-824).      */
 enum {
   ODP_LN_X = 0, ODP_LN_LDX = 1, ODP_LN_G = 2, ODP_LN_LDG = 3,
@@ -219,6 +220,10 @@ enum {
   ODP_LN_FIELDS = 16
 };
 int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len);
+/* Workgroups of one sqnorm problem (n_seg segments; padded to a multiple of
+ * 8 so that work maps onto the 8 XCDs predictably).                        */
+int64_t odp_linear_norm_blocks(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len,
+                               int64_t n_seg);
 int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* problems,
                       const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                       const int32_t* seg_row_start, const int32_t* seg_row_len,

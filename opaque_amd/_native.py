@@ -73,6 +73,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_gaussian_noise": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _c_u64, _c_u32]),
     "odp_philox_words": (_c_int, [_ptr, _c_u64, _c_u32, _c_u32, _c_u64, _c_i64, _ptr]),
     "odp_linear_tiles": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "odp_linear_norm_blocks": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64]),
     "odp_linear_sqnorm": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
     "odp_linear_sum_blocks": (_c_i64, [_c_i64, _c_i64]),
     "odp_linear_clipped_sum": (

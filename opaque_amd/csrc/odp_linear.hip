@@ -6,24 +6,24 @@
 // M_i under vmap(grad) (opaque-engine/.../clipping/_clipped_fun.py:756-762)
 // and then squares, scales and sums them.  Here:
 //
-//   k_lin_outer_norm : ||M_i||_F^2 tile by tile (128 x 128 output tiles,
+//   k_lin_outer_norm : ||M_i||_F^2 tile by tile (256 x 128 output tiles,
 //                      contraction over the example's tokens), squares
 //                      summed in fp64 into one partial slot per tile;
 //   k_lin_gram_norm  : sum_{t,s} (x_t . x_s)(g_t . g_s) over 128 x 128 token
 //                      tiles of the upper triangle (off-diagonal tiles
 //                      counted twice), the cheaper form when the example is
 //                      short relative to the weight;
-//   k_lin_clip_sum   : out = sum_i c_i M_i as one GEMM over all rows,
-//                      accumulating each example in its own fp32 registers
-//                      and folding it in with its clip factor (non-finite
-//                      entries dropped, as nan_to_num does in the reference).
+//   k_lin_clip_sum   : out = sum_i c_i M_i as one GEMM over all rows, the
+//                      clip factor applied to each example's X rows as they
+//                      are staged (c_i x_t rounded to bf16).
 //
-// All three are bf16 MFMA (16x16x32, fp32 accumulate) on 128 x 128
-// workgroup tiles with 4 waves of 64 x 64, operands staged through LDS with
-// one pipeline step of global loads in flight.  Rows are token-major in HBM,
-// so the outer-product forms read their operands K-major and take them from
-// LDS with the gfx950 transposing read; the Gram form's operands are
-// K-contiguous rows.
+// All three are bf16 MFMA (16x16x32, fp32 accumulate) with 4 waves per
+// workgroup (256 x 128 output tiles for the outer forms, 128 x 128 token
+// tiles for the Gram form), operands staged through LDS with one pipeline
+// step of global loads in flight.
+// Rows are token-major in HBM, so the outer-product forms read their
+// operands K-major and take them from LDS with the gfx950 transposing read;
+// the Gram form's operands are K-contiguous rows.
 #include "odp_internal.h"
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -32,10 +32,12 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
+#ifndef ODP_LIN_OCC
+#define ODP_LIN_OCC 2  // waves per SIMD the outer-product kernels are compiled for
+#endif
 constexpr int LT = 128;      // output tile edge (rows and columns)
 constexpr int LK = 64;       // tokens (outer forms) or features (Gram) per pipeline step
-constexpr int OP = LT + 8;   // LDS pitch of a [LK][LT] token-major tile (elements)
-constexpr int GP = LK + 8;   // LDS pitch of a [LT][LK] feature-major tile (elements)
+constexpr int OP = LT;       // LDS pitch of a [LK][LT] token-major tile (elements, swizzled)
 
 #define ODP_GLOBAL __attribute__((address_space(1)))
 #define ODP_LDS __attribute__((address_space(3)))
@@ -67,86 +69,203 @@ __device__ __forceinline__ LinProblem read_problem(const int64_t* f) {
 }
 
 // ---------------------------------------------------------------------------
-// Outer-product main loop.  acc[i][j] (wave tile 64 x 64 as 4 x 4 MFMA
-// blocks) += sum over tokens t in [t_begin, t_end) of G[t][o] X[t][n] for
-// o in [o0, o0 + 128), n in [n0, n0 + 128).  Each step stages 64 tokens of
-// both operands as token-major [64][128] LDS tiles; token rows outside the
-// range and columns past the matrix are zeroed at the LDS store.
+// Outer-product main loop.  The workgroup's tile covers OM output rows (o,
+// columns of G) by ON output columns (n, columns of X); four waves in a
+// 2 x 2 arrangement each own a WM x WN block as BI x BJ MFMA 16 x 16 blocks.
+// A pipeline step stages OK tokens of both operands as token-major LDS tiles
+// (token rows outside the step's segment and columns past the matrix are
+// zeroed at the LDS store); one step of global loads is in flight while the
+// previous one is computed.
 // ---------------------------------------------------------------------------
+#ifndef ODP_LIN_OM
+#define ODP_LIN_OM 256
+#endif
+#ifndef ODP_LIN_ON
+#define ODP_LIN_ON 128
+#endif
+constexpr int OM = ODP_LIN_OM, ON = ODP_LIN_ON, OK = 32;
+constexpr int WM = OM / 2, WN = ON / 2, BI = WM / 16, BJ = WN / 16;
+constexpr int A_PIECES = OK * OM / 8 / 256;  // 16-byte pieces per thread per step
+constexpr int B_PIECES = OK * ON / 8 / 256;
+constexpr int A_TILE = OK * OM, B_TILE = OK * ON;  // elements
+constexpr int OUTER_STAGE = A_TILE + B_TILE;
+constexpr int OUTER_LDS = 2 * OUTER_STAGE;
+
 struct OuterStage {
-  u32x4_t a[4];  // G pieces
-  u32x4_t b[4];  // X pieces
+  u32x4_t a[A_PIECES];  // G pieces
+  u32x4_t b[B_PIECES];  // X pieces
 };
+
+// Row and column arithmetic in 32 bits (the host keeps row counts and
+// pitches below 2^31); one 32 x 32 -> 64-bit multiply per piece.
+__device__ __forceinline__ const uint16_t* row_ptr(const uint16_t* base, int32_t t, int64_t ld,
+                                                   int32_t col) {
+  return base + ((uint64_t)(uint32_t)t * (uint32_t)ld + (uint32_t)col);
+}
 
 __device__ __forceinline__ void outer_load(const LinProblem& P, int64_t o0, int64_t n0, int64_t t0,
                                            int64_t t_begin, int64_t t_end, OuterStage& S) {
   const int tid = threadIdx.x;
+  const int32_t tb = (int32_t)t_begin, tl = (int32_t)t_end - 1, ts = (int32_t)t0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int id = tid + 256 * q;          // 1024 pieces: 64 rows x 16 pieces of 8
-    int64_t t = t0 + (id >> 4);
-    t = t < t_begin ? t_begin : (t >= t_end ? t_end - 1 : t);
-    const int64_t c = 8 * (id & 15);
-    const int64_t co = o0 + c, cn = n0 + c;
-    S.a[q] = ldg16(P.G + t * P.ldg + (co < P.d_out ? co : P.d_out - 8));
-    S.b[q] = ldg16(P.X + t * P.ldx + (cn < P.d_in ? cn : P.d_in - 8));
+  for (int q = 0; q < A_PIECES; ++q) {
+    const int id = tid + 256 * q;
+    int32_t t = ts + id / (OM / 8);
+    t = t < tb ? tb : (t > tl ? tl : t);
+    const int32_t co = (int32_t)o0 + 8 * (id % (OM / 8));
+    S.a[q] = ldg16(row_ptr(P.G, t, P.ldg, co < (int32_t)P.d_out ? co : (int32_t)P.d_out - 8));
+  }
+#pragma unroll
+  for (int q = 0; q < B_PIECES; ++q) {
+    const int id = tid + 256 * q;
+    int32_t t = ts + id / (ON / 8);
+    t = t < tb ? tb : (t > tl ? tl : t);
+    const int32_t cn = (int32_t)n0 + 8 * (id % (ON / 8));
+    S.b[q] = ldg16(row_ptr(P.X, t, P.ldx, cn < (int32_t)P.d_in ? cn : (int32_t)P.d_in - 8));
   }
 }
+
+// Token-major tiles are unpadded and XOR-swizzled in 4-element (8-byte)
+// chunks: chunk k of row r lives at chunk k ^ swz(r).  The 16 rows x 4
+// chunks that one transposing operand read touches (rows 8g + j, j < 4,
+// g < 4) then land on every LDS bank exactly twice, and a 16-byte piece
+// (an aligned chunk pair) stays contiguous.
+__device__ __forceinline__ int swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 2; }
 
 __device__ __forceinline__ void outer_store(const LinProblem& P, int64_t o0, int64_t n0, int64_t t0,
                                             int64_t t_begin, int64_t t_end, const OuterStage& S,
                                             uint16_t* ta, uint16_t* tb) {
   const int tid = threadIdx.x;
+  const u32x4_t z = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < A_PIECES; ++q) {
     const int id = tid + 256 * q;
-    const int row = id >> 4, c = 8 * (id & 15);
+    const int row = id / (OM / 8), c = 8 * (id % (OM / 8));
     const int64_t t = t0 + row;
-    const bool tok = t >= t_begin && t < t_end;
-    const u32x4_t z = {0u, 0u, 0u, 0u};
-    *(u32x4_t*)&ta[row * OP + c] = (tok && o0 + c < P.d_out) ? S.a[q] : z;
-    *(u32x4_t*)&tb[row * OP + c] = (tok && n0 + c < P.d_in) ? S.b[q] : z;
+    const bool ok = t >= t_begin && t < t_end && o0 + c < P.d_out;
+    *(u32x4_t*)&ta[row * OM + 4 * ((c >> 2) ^ swz(row))] = ok ? S.a[q] : z;
+  }
+#pragma unroll
+  for (int q = 0; q < B_PIECES; ++q) {
+    const int id = tid + 256 * q;
+    const int row = id / (ON / 8), c = 8 * (id % (ON / 8));
+    const int64_t t = t0 + row;
+    const bool ok = t >= t_begin && t < t_end && n0 + c < P.d_in;
+    *(u32x4_t*)&tb[row * ON + 4 * ((c >> 2) ^ swz(row))] = ok ? S.b[q] : z;
   }
 }
 
-// 16 columns col0.. of a token-major tile, tokens 32u + 8 (lane >> 4) + 0..7:
-// the MFMA operand layout (lane & 15 = row of A / column of B).
-__device__ __forceinline__ bf16x8_t outer_frag(const uint16_t* tile, int u, int col0) {
+// 16 columns col0.. of a token-major tile of row pitch `pitch`, tokens
+// 8 (lane >> 4) + 0..7: the MFMA operand layout (lane & 15 = row of A /
+// column of B).  Rows r and r + 4 share swz(), so the second read is
+// 4 rows further on.
+__device__ __forceinline__ bf16x8_t outer_frag(const uint16_t* tile, int pitch, int col0) {
   const int lane = threadIdx.x & 63, c = lane & 15;
-  const uint16_t* src = tile + (32 * u + 8 * (lane >> 4) + (c >> 2)) * OP + col0 + 4 * (c & 3);
-  const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * OP);
+  const int row = 8 * (lane >> 4) + (c >> 2);
+  const int k = (col0 >> 2) + (c & 3);
+  const uint16_t* src = tile + row * pitch + 4 * (k ^ swz(row));
+  const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * pitch);
   const v4i16_t tt[2] = {t0, t1};
   return __builtin_bit_cast(bf16x8_t, tt);
 }
 
-__device__ __forceinline__ void outer_compute(const uint16_t* ta, const uint16_t* tb,
-                                              f32x4_t (&acc)[4][4]) {
+typedef f32x4_t OuterAcc[BI][BJ];
+
+__device__ __forceinline__ void outer_compute(const uint16_t* ta, const uint16_t* tb, OuterAcc& acc) {
   const int wave = threadIdx.x >> 6;
-  const int wm = 64 * (wave & 1), wn = 64 * (wave >> 1);
+  const int wm = WM * (wave & 1), wn = WN * (wave >> 1);
+  // Operand reads run two A fragments ahead of the MFMAs that consume them.
+  bf16x8_t b[BJ], a[3];
 #pragma unroll
-  for (int u = 0; u < LK / 32; ++u) {
-    bf16x8_t a[4], b[4];
+  for (int j = 0; j < BJ; ++j) b[j] = outer_frag(tb, ON, wn + 16 * j);
+  a[0] = outer_frag(ta, OM, wm);
+  a[1] = outer_frag(ta, OM, wm + 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = outer_frag(ta, u, wm + 16 * i);
+  for (int i = 0; i < BI; ++i) {
+    if (i + 2 < BI) a[(i + 2) % 3] = outer_frag(ta, OM, wm + 16 * (i + 2));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = outer_frag(tb, u, wn + 16 * j);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < BJ; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i % 3], b[j], acc[i][j], 0, 0, 0);
   }
 }
 
-// LDS: two stages of (G tile, X tile), each [LK][OP] bf16.
-constexpr int OUTER_TILE = LK * OP;
-constexpr int OUTER_LDS = 2 * 2 * OUTER_TILE;
+// One pipeline step: rows [t0, t0 + OK) clipped to its segment [tb, te).
+struct Step {
+  int64_t t0, tb, te;
+  int seg;
+  bool live;
+};
 
-__device__ __forceinline__ void zero_acc(f32x4_t (&acc)[4][4]) {
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
+// c * v for 8 bf16 values: widened exactly, multiplied in fp32 and rounded
+// to nearest-even bf16 (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ u32x4_t scale_bf16x8(u32x4_t v, float c) {
+  f32x8_t f = __builtin_convertvector(__builtin_bit_cast(bf16x8_t, v), f32x8_t);
+  f = f * c;
+  return __builtin_bit_cast(u32x4_t, __builtin_convertvector(f, bf16x8_t));
+}
+
+// acc += sum over the steps first, next(first), ... of G^T X on the
+// workgroup's tile; `scale(step)` multiplies X's rows of a step as they are
+// staged (SCALE only; X's tile is the narrower one).
+template <bool SCALE, typename Next, typename Scale>
+__device__ __forceinline__ void outer_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step cur,
+                                               Next next, Scale scale, uint16_t* lds, OuterAcc& acc) {
+  OuterStage S;
+  auto stage = [&](const Step& st, int buf) {
+    if (SCALE) {
+      const float c = scale(st);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+      for (int q = 0; q < B_PIECES; ++q) S.b[q] = scale_bf16x8(S.b[q], c);
+    }
+    outer_store(P, o0, n0, st.t0, st.tb, st.te, S, lds + buf * OUTER_STAGE,
+                lds + buf * OUTER_STAGE + A_TILE);
+  };
+  if (cur.live) {
+    outer_load(P, o0, n0, cur.t0, cur.tb, cur.te, S);
+    stage(cur, 0);
+  }
+  __syncthreads();
+  int buf = 0;
+  while (cur.live) {
+    const Step nx = next(cur);
+    if (nx.live) outer_load(P, o0, n0, nx.t0, nx.tb, nx.te, S);
+    outer_compute(lds + buf * OUTER_STAGE, lds + buf * OUTER_STAGE + A_TILE, acc);
+    if (nx.live) stage(nx, buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    cur = nx;
+  }
+}
+
+template <int I, int J>
+__device__ __forceinline__ void zero_acc(f32x4_t (&acc)[I][J]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+}
+
+// Work decoding.  Workgroups are dispatched round-robin over the 8 XCDs
+// (blockIdx % 8), each with its own L2, and every problem's block count is
+// a multiple of 8 so that blockIdx % 8 == local % 8.  With BY_XCD and 8 or
+// more segments, XCD j works through segments j, j + 8, ... so that an
+// example's rows are cached by one L2 only (this pays for the Gram form,
+// whose workgroups drift apart in the feature loop; the outer forms keep
+// consecutive items on different XCDs, which measured faster).  Returns
+// false for padding blocks.
+template <bool BY_XCD>
+__device__ __forceinline__ bool seg_item(int local, int n_seg, int per_seg, int& seg, int& item) {
+  if (BY_XCD && n_seg >= 8) {
+    const int k = local >> 3;
+    seg = (local & 7) + 8 * (k / per_seg);
+    item = k % per_seg;
+  } else {
+    seg = local / per_seg;
+    item = local % per_seg;
+  }
+  return seg < n_seg;
 }
 
 // Block-wide fp64 sum; the result is valid in thread 0.
@@ -162,12 +281,13 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 }
 
 // fp32 squares of the finite entries, summed in fp64.
-__device__ __forceinline__ double acc_sq(const f32x4_t (&acc)[4][4]) {
+template <int I, int J>
+__device__ __forceinline__ double acc_sq(const f32x4_t (&acc)[I][J]) {
   double s = 0.0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < I; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < J; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float v = acc[i][j][e];
@@ -180,7 +300,7 @@ __device__ __forceinline__ double acc_sq(const f32x4_t (&acc)[4][4]) {
 // ---------------------------------------------------------------------------
 // ||M_i||^2 partials, outer form.  Workgroup = (segment, o-tile, n-tile).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_lin_outer_norm(const int64_t* __restrict__ probs,
+__global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64_t* __restrict__ probs,
                                                         const int32_t* __restrict__ ws, int n_prob,
                                                         const int32_t* __restrict__ sstart,
                                                         const int32_t* __restrict__ slen,
@@ -193,35 +313,26 @@ __global__ __launch_bounds__(256) void k_lin_outer_norm(const int64_t* __restric
   const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
   const LinProblem P = read_problem(f);
   const int64_t slot = f[ODP_LN_SLOT];
-  const int tn_count = (int)((P.d_in + LT - 1) / LT);
-  const int tm_count = (int)((P.d_out + LT - 1) / LT);
+  const int tn_count = (int)((P.d_in + ON - 1) / ON);
+  const int tm_count = (int)((P.d_out + OM - 1) / OM);
   const int tiles = tn_count * tm_count;
-  const int local = bid - ws[p];
-  const int seg = local / tiles, tile = local % tiles;
-  const int64_t o0 = (int64_t)(tile / tn_count) * LT, n0 = (int64_t)(tile % tn_count) * LT;
+  int seg, tile;
+  if (!seg_item<false>(bid - ws[p], P.n_seg, tiles, seg, tile)) return;
+  const int64_t o0 = (int64_t)(tile / tn_count) * OM, n0 = (int64_t)(tile % tn_count) * ON;
   const int gs = P.seg_first + seg;
   const int64_t t_begin = sstart[gs], t_end = t_begin + slen[gs];
   const int ex = sex[gs];
 
-  f32x4_t acc[4][4];
+  OuterAcc acc;
   zero_acc(acc);
-  const int64_t nsteps = t_end > t_begin ? (t_end - t_begin + LK - 1) / LK : 0;
-  OuterStage S;
-  if (nsteps > 0) {
-    outer_load(P, o0, n0, t_begin, t_begin, t_end, S);
-    outer_store(P, o0, n0, t_begin, t_begin, t_end, S, lds, lds + OUTER_TILE);
-  }
-  __syncthreads();
-  for (int64_t s = 0; s < nsteps; ++s) {
-    const int b = (int)(s & 1);
-    const bool more = s + 1 < nsteps;
-    const int64_t tn = t_begin + (s + 1) * LK;
-    if (more) outer_load(P, o0, n0, tn, t_begin, t_end, S);
-    outer_compute(lds + b * 2 * OUTER_TILE, lds + b * 2 * OUTER_TILE + OUTER_TILE, acc);
-    if (more) outer_store(P, o0, n0, tn, t_begin, t_end, S, lds + (b ^ 1) * 2 * OUTER_TILE,
-                          lds + (b ^ 1) * 2 * OUTER_TILE + OUTER_TILE);
-    __syncthreads();
-  }
+  const Step first = {t_begin, t_begin, t_end, seg, t_end > t_begin};
+  auto next = [&](const Step& st) {
+    Step n = st;
+    n.t0 = st.t0 + OK;
+    n.live = n.t0 < st.te;
+    return n;
+  };
+  outer_mainloop<false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, lds, acc);
   // Columns/rows past the matrix were zero operands, so they add nothing.
   const double tot = block_sum(acc_sq(acc), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
@@ -232,8 +343,12 @@ __global__ __launch_bounds__(256) void k_lin_outer_norm(const int64_t* __restric
 // tb <= sb).  Sx = X_tb X_sb^T over d_in and Sg = G_tb G_sb^T over d_out
 // (operands are K-contiguous rows), then sum Sx * Sg.
 // ---------------------------------------------------------------------------
-constexpr int GRAM_TILE = LT * GP;          // [128 rows][LK + 8]
+// Feature-major tiles [128 rows][LK] are unpadded; the 16-byte chunk q of
+// row r lives at chunk q ^ (r & 7).
+constexpr int GRAM_TILE = LT * LK;
 constexpr int GRAM_LDS = 2 * 2 * GRAM_TILE;  // two stages x (t rows, s rows)
+
+__device__ __forceinline__ int gram_at(int row, int k) { return row * LK + 8 * ((k >> 3) ^ (row & 7)); }
 
 struct GramStage {
   u32x4_t a[4];
@@ -243,17 +358,18 @@ struct GramStage {
 __device__ __forceinline__ void gram_load(const uint16_t* M, int64_t ld, int64_t d, int64_t ta0,
                                           int64_t sb0, int64_t t_end, int64_t k0, GramStage& S) {
   const int tid = threadIdx.x;
+  const int32_t tl = (int32_t)t_end - 1, d8 = (int32_t)d - 8;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int id = tid + 256 * q;  // 1024 pieces: 128 rows x 8 pieces of 8
     const int row = id >> 3;
-    const int64_t k = k0 + 8 * (id & 7);
-    const int64_t kc = k < d ? k : d - 8;
-    int64_t ra = ta0 + row, rb = sb0 + row;
-    ra = ra < t_end ? ra : t_end - 1;
-    rb = rb < t_end ? rb : t_end - 1;
-    S.a[q] = ldg16(M + ra * ld + kc);
-    S.b[q] = ldg16(M + rb * ld + kc);
+    const int32_t k = (int32_t)k0 + 8 * (id & 7);
+    const int32_t kc = k < (int32_t)d ? k : d8;
+    int32_t ra = (int32_t)ta0 + row, rb = (int32_t)sb0 + row;
+    ra = ra < tl ? ra : tl;
+    rb = rb < tl ? rb : tl;
+    S.a[q] = ldg16(row_ptr(M, ra, ld, kc));
+    S.b[q] = ldg16(row_ptr(M, rb, ld, kc));
   }
 }
 
@@ -267,8 +383,8 @@ __device__ __forceinline__ void gram_store(int64_t d, int64_t ta0, int64_t sb0, 
     const int id = tid + 256 * q;
     const int row = id >> 3, c = 8 * (id & 7);
     const bool kin = k0 + c < d;
-    *(u32x4_t*)&la[row * GP + c] = (kin && ta0 + row < t_end) ? S.a[q] : z;
-    *(u32x4_t*)&lb[row * GP + c] = (kin && sb0 + row < t_end) ? S.b[q] : z;
+    *(u32x4_t*)&la[gram_at(row, c)] = (kin && ta0 + row < t_end) ? S.a[q] : z;
+    *(u32x4_t*)&lb[gram_at(row, c)] = (kin && sb0 + row < t_end) ? S.b[q] : z;
   }
 }
 
@@ -282,10 +398,10 @@ __device__ __forceinline__ void gram_compute(const uint16_t* la, const uint16_t*
     bf16x8_t a[4], b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      a[i] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&la[(wm + 16 * i + r) * GP + 32 * u + kq]);
+      a[i] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&la[gram_at(wm + 16 * i + r, 32 * u + kq)]);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&lb[(wn + 16 * j + r) * GP + 32 * u + kq]);
+      b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&lb[gram_at(wn + 16 * j + r, 32 * u + kq)]);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -330,8 +446,8 @@ __global__ __launch_bounds__(256) void k_lin_gram_norm(const int64_t* __restrict
   const int64_t slot = f[ODP_LN_SLOT];
   const int nb = (int)f[ODP_LN_NB];
   const int pairs = nb * (nb + 1) / 2;
-  const int local = bid - ws[p];
-  const int seg = local / pairs, pair = local % pairs;
+  int seg, pair;
+  if (!seg_item<true>(bid - ws[p], P.n_seg, pairs, seg, pair)) return;
   // pair -> (tb, sb), tb <= sb, row-major over the upper triangle.
   int tb = 0, rem = pair;
   while (rem >= nb - tb) {
@@ -367,11 +483,12 @@ __global__ __launch_bounds__(256) void k_lin_gram_norm(const int64_t* __restrict
 
 // ---------------------------------------------------------------------------
 // Clipped sum.  Workgroup = (o-tile, n-tile) of one weight; the contraction
-// runs over every segment's rows in order.  Each segment accumulates into
-// its own registers (M_i exactly as fp32), which are folded in with the
-// example's clip factor when the next segment starts.
+// runs over every segment's rows in order, and a pipeline step never spans
+// two segments.  The G rows of a step are multiplied by their example's clip
+// factor (in fp32, rounded back to bf16) when the step is written to LDS,
+// so one accumulator holds sum_i c_i M_i.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_lin_clip_sum(const int64_t* __restrict__ probs,
+__global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t* __restrict__ probs,
                                                       const int32_t* __restrict__ ws, int n_prob,
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen,
@@ -389,91 +506,50 @@ __global__ __launch_bounds__(256) void k_lin_clip_sum(const int64_t* __restrict_
   const int grp = (int)((flags >> 8) & 0xffff);
   const int cls = (int)((flags >> 24) & 0xffff);
   const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
-  const int tn_count = (int)((P.d_in + LT - 1) / LT);
+  const int tn_count = (int)((P.d_in + ON - 1) / ON);
+  const int tm_count = (int)((P.d_out + OM - 1) / OM);
   const int tile = bid - ws[p];
-  const int64_t o0 = (int64_t)(tile / tn_count) * LT, n0 = (int64_t)(tile % tn_count) * LT;
+  if (tile >= tm_count * tn_count) return;  // padding block
+  const int64_t o0 = (int64_t)(tile / tn_count) * OM, n0 = (int64_t)(tile % tn_count) * ON;
 
-  f32x4_t acc[4][4], tot[4][4];
+  OuterAcc acc;
   zero_acc(acc);
-  zero_acc(tot);
 
-  // Step cursor over (segment, first token) pairs; empty segments are skipped.
-  int cs = 0;
-  int64_t ct = 0;
-  auto seek = [&](int s) {
-    while (s < P.n_seg && slen[P.seg_first + s] <= 0) ++s;
-    cs = s;
-    ct = s < P.n_seg ? (int64_t)sstart[P.seg_first + s] : 0;
+  // Steps walk every live segment in order, OK rows at a time.
+  auto at_segment = [&](int sg) {
+    while (sg < P.n_seg && slen[P.seg_first + sg] <= 0) ++sg;
+    Step st;
+    st.seg = sg;
+    st.live = sg < P.n_seg;
+    st.tb = st.live ? (int64_t)sstart[P.seg_first + sg] : 0;
+    st.te = st.live ? st.tb + slen[P.seg_first + sg] : 0;
+    st.t0 = st.tb;
+    return st;
   };
-  auto seg_end = [&](int s) {
-    return (int64_t)sstart[P.seg_first + s] + slen[P.seg_first + s];
+  auto next = [&](const Step& st) {
+    if (st.t0 + OK < st.te) {
+      Step n = st;
+      n.t0 = st.t0 + OK;
+      return n;
+    }
+    return at_segment(st.seg + 1);
   };
-  seek(0);
-  if (cs >= P.n_seg) {  // no rows at all: the sum is zero
-    // fall through with zero accumulators
-  }
-  OuterStage S;
-  int cur_s = cs;
-  int64_t cur_t = ct;
-  if (cs < P.n_seg) {
-    const int64_t tb = sstart[P.seg_first + cs], te = seg_end(cs);
-    outer_load(P, o0, n0, ct, tb, te, S);
-    outer_store(P, o0, n0, ct, tb, te, S, lds, lds + OUTER_TILE);
-  }
-  __syncthreads();
-  int b = 0;
-  while (cur_s < P.n_seg) {
-    // Cursor of the following step.
-    int nx_s = cur_s;
-    int64_t nx_t = cur_t + LK;
-    if (nx_t >= seg_end(cur_s)) {
-      seek(cur_s + 1);
-      nx_s = cs;
-      nx_t = ct;
-    }
-    const bool more = nx_s < P.n_seg;
-    int64_t ntb = 0, nte = 0;
-    if (more) {
-      ntb = sstart[P.seg_first + nx_s];
-      nte = seg_end(nx_s);
-      outer_load(P, o0, n0, nx_t, ntb, nte, S);
-    }
-    outer_compute(lds + b * 2 * OUTER_TILE, lds + b * 2 * OUTER_TILE + OUTER_TILE, acc);
-    if (nx_s != cur_s) {
-      // Segment cur_s is complete: fold it in with its clip factor.
-      const float c = sc[sex[P.seg_first + cur_s]];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float v = acc[i][j][e];
-            tot[i][j][e] = __fadd_rn(tot[i][j][e], __fmul_rn(c, isfinite(v) ? v : 0.f));
-          }
-      zero_acc(acc);
-    }
-    if (more) outer_store(P, o0, n0, nx_t, ntb, nte, S, lds + (b ^ 1) * 2 * OUTER_TILE,
-                          lds + (b ^ 1) * 2 * OUTER_TILE + OUTER_TILE);
-    __syncthreads();
-    b ^= 1;
-    cur_s = nx_s;
-    cur_t = nx_t;
-  }
+  auto scale = [&](const Step& st) { return sc[sex[P.seg_first + st.seg]]; };
+  outer_mainloop<true>(P, o0, n0, at_segment(0), next, scale, lds, acc);
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = 64 * (wave & 1), wn = 64 * (wave >> 1);
+  const int wm = WM * (wave & 1), wn = WN * (wave >> 1);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < BI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < BJ; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int64_t o = o0 + wm + 16 * i + 4 * (lane >> 4) + e;
         const int64_t n = n0 + wn + 16 * j + (lane & 15);
         if (o < P.d_out && n < P.d_in) {
-          float x = odp_round_to(tot[i][j][e], odt);
+          float x = odp_round_to(acc[i][j][e], odt);
           if (normalize_by != 1.0f) x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
           odp_store_from_float(out, o * P.d_in + n, odt, x);
         }
@@ -492,12 +568,21 @@ extern "C" int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64
     const int64_t nb = max_seg_len > 0 ? (max_seg_len + LT - 1) / LT : 0;
     return nb * (nb + 1) / 2;
   }
-  return ((d_out + LT - 1) / LT) * ((d_in + LT - 1) / LT);
+  return ((d_out + OM - 1) / OM) * ((d_in + ON - 1) / ON);
+}
+
+extern "C" int64_t odp_linear_norm_blocks(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len,
+                                          int64_t n_seg) {
+  const int64_t per = odp_linear_tiles(form, d_in, d_out, max_seg_len);
+  if (per <= 0 || n_seg <= 0) return 0;
+  if (form == ODP_FORM_GRAM && n_seg >= 8) return 8 * ((n_seg + 7) / 8) * per;
+  return (n_seg * per + 7) / 8 * 8;
 }
 
 extern "C" int64_t odp_linear_sum_blocks(int64_t d_in, int64_t d_out) {
   if (d_in <= 0 || d_out <= 0) return 0;
-  return ((d_out + LT - 1) / LT) * ((d_in + LT - 1) / LT);
+  const int64_t tiles = ((d_out + OM - 1) / OM) * ((d_in + ON - 1) / ON);
+  return (tiles + 7) / 8 * 8;
 }
 
 extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* problems,

@@ -573,7 +573,8 @@ class GhostPlan:
                 fl = sum(ln * ln for ln in seg.lengths) * (d_in + d_out)
             else:
                 fl = 2 * valid * d_in * d_out
-            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf], N.LN_NB: nb_max}, n_seg * tiles,
+            blocks = int(lib.odp_linear_norm_blocks(form, d_in, d_out, max_len, n_seg))
+            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf], N.LN_NB: nb_max}, blocks,
                           valid * (d_in + d_out) * 2, fl)
             lf = self.leaves[ls.w_leaf]
             out = self.out[ls.w_leaf]
