@@ -26,17 +26,22 @@ _STATE = threading.local()
 
 @dataclass
 class SiteRecord:
-    """One LoRA application seen during a capture pass."""
+    """One LoRA (or full-weight linear) application seen during a capture pass."""
 
     x: torch.Tensor  # physical activations [B, *, d_in]
-    A: torch.Tensor  # kernel-layout [d_in, r] values
-    B: torch.Tensor  # kernel-layout [r, d_out] values
+    A: torch.Tensor | None  # kernel-layout [d_in, r] values (LoRA)
+    B: torch.Tensor | None  # kernel-layout [r, d_out] values (LoRA)
     scaling: float
     a_obj: torch.Tensor | None  # the tensor the model passed (identity used for leaf lookup)
     b_obj: torch.Tensor | None
     a_transposed: bool
     b_transposed: bool
     g: torch.Tensor | None = None  # physical output gradients, filled by backward
+    w_obj: torch.Tensor | None = None  # full-weight linear: the weight passed ([d_out, d_in])
+
+    @property
+    def kind(self) -> str:
+        return "linear" if self.w_obj is not None else "lora"
 
 
 @dataclass
@@ -52,6 +57,7 @@ class CaptureSession:
     sites: list[SiteRecord] = field(default_factory=list)
     uses: dict[int, int] = field(default_factory=dict)  # id(tensor) -> number of seam uses
     pairs: list[tuple[int, int, int, int]] = field(default_factory=list)  # ids of (A, B, W, bias) per call
+    linear_ws: list[int] = field(default_factory=list)  # ids of weights of full-weight linear seams
     eligible: set[int] = field(default_factory=set)  # ids allowed to be captured
 
     def __enter__(self) -> CaptureSession:
@@ -179,6 +185,101 @@ def _lora(x, W, A, B, scaling, bias, a_obj, b_obj, a_t, b_t):
     return _SeamLoRA.apply(x, W, A, B, scaling, bias, a_obj, b_obj, a_t, b_t)
 
 
+class _TapLinear(torch.autograd.Function):
+    """Physical full-weight linear that records x now and g in backward."""
+
+    @staticmethod
+    def forward(x, W, bias, anchor, record):
+        return F.linear(x, W) if bias is None else F.linear(x, W) + bias
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        x, W, bias, anchor, record = inputs
+        ctx.save_for_backward(W)
+        ctx.record = record
+        ctx.has_bias = bias is not None
+        ctx.bias_batched = bias is not None and bias.dim() > 1
+
+    @staticmethod
+    def backward(ctx, g):
+        (W,) = ctx.saved_tensors
+        ctx.record.g = g.detach()
+        dx = g @ W if ctx.needs_input_grad[0] else None
+        dbias = None
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            if ctx.bias_batched:
+                red = tuple(range(1, g.dim() - 1))
+                dbias = g.sum(dim=red, keepdim=True) if red else g
+            else:
+                dbias = g.reshape(-1, g.shape[-1]).sum(0)
+        danchor = torch.zeros((), dtype=g.dtype, device=g.device) if ctx.needs_input_grad[3] else None
+        return dx, None, dbias, danchor, None
+
+
+class _SeamLinear(torch.autograd.Function):
+    """Per-example linear whose vmap rule merges the batch and taps the seam."""
+
+    generate_vmap_rule = False
+
+    @staticmethod
+    def forward(x, W, bias):
+        return F.linear(x, W) if bias is None else F.linear(x, W) + bias
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        pass
+
+    @staticmethod
+    def backward(ctx, g):
+        raise RuntimeError("the capture seam is differentiated through its vmap rule only")
+
+    @staticmethod
+    def vmap(info, in_dims, x, W, bias):
+        sess = active_session()
+        xd, wd, bias_d = in_dims
+        if xd is None:
+            x = x.unsqueeze(0).expand(info.batch_size, *x.shape)
+        elif xd != 0:
+            x = x.movedim(xd, 0)
+        if bias is not None and bias_d is not None:
+            bias = bias.movedim(bias_d, 0)
+            bias = bias.view(bias.shape[0], *([1] * (x.dim() - 2)), bias.shape[-1])
+        if wd is not None or sess is None or sess.mode != "capture" or id(W) not in sess.eligible:
+            if wd is not None:
+                out = torch.einsum("b...i,boi->b...o", x, W.movedim(wd, 0))
+            else:
+                out = F.linear(x, W)
+            return (out if bias is None else out + bias), 0
+        rec = SiteRecord(x=x, A=None, B=None, scaling=1.0, a_obj=None, b_obj=None,
+                         a_transposed=False, b_transposed=False, w_obj=W)
+        sess.sites.append(rec)
+        return _TapLinear.apply(x, W, bias, sess.anchor, rec), 0
+
+
+def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``x W^T + bias`` whose weight gradient the DP engine clips without materialising it.
+
+    Outside ``clipped_grad`` this is ``torch.nn.functional.linear``.
+    """
+    sess = active_session()
+    if sess is None:
+        return F.linear(x, W, bias)
+    if sess.mode == "discover":
+        sess.uses[id(W)] = sess.uses.get(id(W), 0) + 1
+        sess.linear_ws.append(id(W))
+        return F.linear(x, W.detach(), bias)
+    if id(W) not in sess.eligible:
+        return F.linear(x, W, bias)
+    return _SeamLinear.apply(x, W, bias)
+
+
+class Linear(torch.nn.Linear):
+    """``torch.nn.Linear`` routed through the full-weight seam."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return linear(x, self.weight, self.bias)
+
+
 def lora_linear(x: torch.Tensor, W: torch.Tensor, A: torch.Tensor, B: torch.Tensor,
                 scaling: float, bias: torch.Tensor | None = None) -> torch.Tensor:
     """``x W^T + bias + scaling (x A) B`` with A [d_in, r], B [r, d_out].
@@ -224,9 +325,11 @@ class LoRALinear(torch.nn.Module):
 
 __all__ = [
     "CaptureSession",
+    "Linear",
     "LoRALinear",
     "SiteRecord",
     "active_session",
+    "linear",
     "lora_linear",
     "peft_lora_linear",
 ]

@@ -40,6 +40,7 @@ from opaque_amd.engine import (
     ClipSpec,
     GhostPlan,
     LeafOut,
+    LinearSite,
     LoraSite,
     MaterializedLeaf,
     Segments,
@@ -474,13 +475,15 @@ class _ClipEngine:
 
     def _finish(self, n: int, paths: list, treedef, shapes: list, dtypes: list, device,
                 sites: list[LoraSite], mats: list[MaterializedLeaf], segments: Segments,
-                normalize_by: float, out_dtype_of, values, loss_aux, all_finite) -> tuple:
+                normalize_by: float, out_dtype_of, values, loss_aux, all_finite,
+                lins: list[LinearSite] = ()) -> tuple:
         leaf_group, names, thresholds = self._groups(paths)
         spec, leaf_cls = self._clip_spec(shapes, dtypes, thresholds, normalize_by)
         outs = [LeafOut(tuple(s), out_dtype_of(dt), leaf_group[k], leaf_cls[k])
                 for k, (s, dt) in enumerate(zip(shapes, dtypes))]
         plan = GhostPlan(segments=segments, leaves=outs, clip=spec, lora_sites=sites,
-                         materialized=mats, device=device, second_moment=self.second_moment)
+                         materialized=mats, linear_sites=list(lins), device=device,
+                         second_moment=self.second_moment)
         res = plan.run()
         if all_finite is not None and plan.pe.numel() > 1:
             all_finite = all_finite & _pe_finite(plan)
@@ -555,7 +558,7 @@ class _ClipEngine:
         recs = sess.sites
         seen: dict[int, int] = {}
         for r in recs:
-            for o in (r.a_obj, r.b_obj):
+            for o in (r.a_obj, r.b_obj, r.w_obj):
                 if o is not None and id(o) in obj_leaf:
                     seen[obj_leaf[id(o)]] = seen.get(obj_leaf[id(o)], 0) + 1
         if any(seen.get(k, 0) != 1 for k in disc.eligible):
@@ -573,11 +576,24 @@ class _ClipEngine:
         rows_per_ex: dict[int, int] = {}
         for r in recs:
             if r.g is None:
-                r.g = torch.zeros(*r.x.shape[:-1], r.B.shape[1], dtype=r.x.dtype, device=r.x.device)
+                d_out = r.w_obj.shape[0] if r.w_obj is not None else r.B.shape[1]
+                r.g = torch.zeros(*r.x.shape[:-1], d_out, dtype=r.x.dtype, device=r.x.device)
             t_rows = r.x[0].numel() // r.x.shape[-1] if r.x.dim() > 1 else 1
             rows_per_ex[t_rows] = rows_per_ex.get(t_rows, 0) + 1
         seq = max(rows_per_ex, key=rows_per_ex.get) if rows_per_ex else 1
+        lins: list[LinearSite] = []
         for r in recs:
+            if r.w_obj is not None:
+                kw = obj_leaf[id(r.w_obj)]
+                t_rows = r.x[0].numel() // r.x.shape[-1]
+                if (t_rows == seq and r.x.shape[0] == n and not self.second_moment
+                        and r.x.dtype == r.g.dtype == leaves[kw].dtype == torch.bfloat16
+                        and supports_rows(r.x) and supports_rows(r.g)):
+                    lins.append(LinearSite(x=r.x, g=r.g, w_leaf=kw))
+                else:
+                    for k, pe in _site_per_example(r, None, None, leaves, kw):
+                        mats.append(MaterializedLeaf(per_example=pe.reshape(n, -1), leaf=k))
+                continue
             ka = obj_leaf.get(id(r.a_obj)) if r.a_obj is not None else None
             kb = obj_leaf.get(id(r.b_obj)) if r.b_obj is not None else None
             t_rows = r.x[0].numel() // r.x.shape[-1]
@@ -607,7 +623,7 @@ class _ClipEngine:
         dtypes = [t.dtype for t in leaves]
         seg = Segments.padded(n, seq)
         return self._finish(n, paths, treedef, shapes, dtypes, device, sites, mats, seg,
-                            normalize_by, out_dtype_of, values.detach(), loss_aux, all_finite)
+                            normalize_by, out_dtype_of, values.detach(), loss_aux, all_finite, lins)
 
     # -- the call ----------------------------------------------------------------
     def __call__(self, args: tuple, kwargs: dict) -> Any:
@@ -731,15 +747,20 @@ def _pe_finite(plan: GhostPlan) -> torch.Tensor:
 
 
 def _site_per_example(r: SiteRecord, ka: int | None, kb: int | None,
-                      leaves: list[torch.Tensor]) -> list[tuple[int, torch.Tensor]]:
-    """Per-example factor gradients of a seam the kernels cannot take, in the leaf dtype.
+                      leaves: list[torch.Tensor], kw: int | None = None) -> list[tuple[int, torch.Tensor]]:
+    """Per-example gradients of a seam the kernels cannot take, in the leaf dtype.
 
-    dA_i = s X_i^T (G_i B^T), dB_i = s (X_i A)^T G_i over each example's rows.
+    dA_i = s X_i^T (G_i B^T), dB_i = s (X_i A)^T G_i (LoRA) and dW_i = G_i^T X_i
+    (full-weight linear) over each example's rows.
     """
     n = r.x.shape[0]
     x = r.x.reshape(n, -1, r.x.shape[-1])
     g = r.g.reshape(n, -1, r.g.shape[-1])
     out = []
+    if kw is not None:
+        dt = leaves[kw].dtype
+        out.append((kw, torch.matmul(g.to(dt).transpose(1, 2).contiguous(), x.to(dt))))
+        return out
     if ka is not None:
         dt = leaves[ka].dtype
         u = torch.matmul(g.to(dt), r.B.to(dt).t().contiguous())  # [n, T, r]

@@ -62,8 +62,12 @@ def _capture_per_example(eng, args, n):
                                 allow_unused=True)
     got = {paths[k]: g for k, g in zip(sorted(expanded), grads[1:])}
     for r in sess.sites:
-        ka, kb = obj_leaf.get(id(r.a_obj)), obj_leaf.get(id(r.b_obj))
-        for k, pe in C._site_per_example(r, ka, kb, leaves):
+        if r.w_obj is not None:
+            found = C._site_per_example(r, None, None, leaves, obj_leaf[id(r.w_obj)])
+        else:
+            ka, kb = obj_leaf.get(id(r.a_obj)), obj_leaf.get(id(r.b_obj))
+            found = C._site_per_example(r, ka, kb, leaves)
+        for k, pe in found:
             got[paths[k]] = pe
     return disc, sess, got, paths
 
@@ -159,3 +163,34 @@ def test_nested_sessions_rejected():
             with capture.CaptureSession(mode="discover"):
                 pass
     assert capture.active_session() is None
+
+
+def test_full_weight_linear_seams():
+    torch.manual_seed(4)
+
+    class Net(torch.nn.Module):
+        def __init__(self) -> None:
+            super().__init__()
+            self.a = capture.Linear(12, 20, bias=True)
+            self.b = capture.Linear(20, 12, bias=False)
+            self.shared = capture.Linear(12, 12, bias=False)
+
+        def forward(self, x):
+            h = torch.relu(self.a(x))
+            y = self.b(h)
+            # `shared` is applied twice: two seam uses, so it is not captured.
+            return self.shared(self.shared(y))
+
+    net = Net()
+    params = dict(net.named_parameters())
+
+    def loss_fn(p, x, y):
+        return ((torch.func.functional_call(net, p, (x,)) - y) ** 2).mean()
+
+    n = 3
+    x, y = torch.randn(n, 4, 12), torch.randn(n, 4, 12)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0, 0))(params, x, y)
+    disc, sess, got, paths = _capture_per_example(_engine(loss_fn), (params, x, y), n)
+    assert {paths[k][0] for k in disc.eligible} == {"a.weight", "b.weight"}
+    assert sorted(r.kind for r in sess.sites) == ["linear", "linear"]
+    _check(ref, got)
