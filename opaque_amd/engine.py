@@ -102,6 +102,60 @@ class Segments:
         return cls([i * seq_len for i in range(n_ex)], lens, list(range(n_ex)), n_ex, n_ex * seq_len)
 
 
+@dataclass
+class _SegView:
+    """A segment list as laid out in the plan's device segment arrays."""
+
+    segs: Segments
+    first: int
+
+    @property
+    def n_seg(self) -> int:
+        return self.segs.n_seg
+
+    @property
+    def n_rows(self) -> int:
+        return self.segs.n_rows
+
+    @property
+    def valid(self) -> int:
+        return int(sum(self.segs.lengths))
+
+    @property
+    def max_len(self) -> int:
+        return max(self.segs.lengths, default=0)
+
+
+class _SegRegistry:
+    """The plan's segments followed by every other segment list a site brings (MoE experts)."""
+
+    def __init__(self, default: Segments) -> None:
+        self.views: list[_SegView] = []
+        self._by_id: dict[int, _SegView] = {}
+        self.default = self.view(default)
+
+    def view(self, segs: Segments | None) -> _SegView:
+        if segs is None:
+            return self.default
+        v = self._by_id.get(id(segs))
+        if v is None:
+            if self.views and segs.n_ex != self.views[0].segs.n_ex:
+                raise ValueError("all segment lists of a plan must count the same examples")
+            if len(set(segs.examples)) != len(segs.examples):
+                raise ValueError("each example may own at most one segment of a segment list")
+            first = sum(w.n_seg for w in self.views)
+            v = _SegView(segs, first)
+            self.views.append(v)
+            self._by_id[id(segs)] = v
+        return v
+
+    def arrays(self) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        st = np.asarray([x for v in self.views for x in v.segs.starts], dtype=np.int32)
+        ln = np.asarray([x for v in self.views for x in v.segs.lengths], dtype=np.int32)
+        ex = np.asarray([x for v in self.views for x in v.segs.examples], dtype=np.int32)
+        return st.reshape(-1), ln.reshape(-1), ex.reshape(-1)
+
+
 # ---------------------------------------------------------------------------
 # Inputs and outputs of a plan
 # ---------------------------------------------------------------------------
@@ -126,6 +180,7 @@ class LoraSite:
     b_leaf: int | None
     a_transposed: bool = False
     b_transposed: bool = False
+    segments: Segments | None = None  # rows of x / g; None: the plan's segments
 
 
 @dataclass
@@ -142,6 +197,7 @@ class LinearSite:
     g: torch.Tensor
     w_leaf: int
     form: int | None = None
+    segments: Segments | None = None  # rows of x / g; None: the plan's segments
 
 
 def choose_form(max_len: int, d_in: int, d_out: int) -> int:
@@ -155,6 +211,7 @@ class MaterializedLeaf:
 
     per_example: torch.Tensor
     leaf: int
+    segments: Segments | None = None  # one row of per_example per segment; None: the plan's
 
 
 @dataclass
@@ -301,15 +358,14 @@ class GhostPlan:
     def _build(self, sites: list[LoraSite], mats: list[MaterializedLeaf], lins: list[LinearSite]) -> None:
         seg = self.segments
         dev = self.device
-        n_rows, n_seg = seg.n_rows, seg.n_seg
-        if len(set(seg.examples)) != len(seg.examples):
-            raise ValueError("each example may own at most one segment of a plan")
-        max_len = max(seg.lengths, default=0)
+        reg = _SegRegistry(seg)
+        self._segreg = reg
         for ls in lins:
             if ls.x.device != dev or ls.g.device != dev:
                 raise ValueError("linear site tensors must be on the plan device")
             if ls.x.dtype != torch.bfloat16 or ls.g.dtype != torch.bfloat16:
                 raise TypeError("full-weight linear sites run in bfloat16")
+            n_rows = reg.view(ls.segments).n_rows
             if ls.x.reshape(-1, ls.x.shape[-1]).shape[0] != n_rows or \
                     ls.g.reshape(-1, ls.g.shape[-1]).shape[0] != n_rows:
                 raise ValueError("linear site row count does not match the segments")
@@ -317,14 +373,13 @@ class GhostPlan:
                 raise ValueError("linear site feature sizes must be multiples of 8")
             if tuple(self.leaves[ls.w_leaf].shape) != (ls.g.shape[-1], ls.x.shape[-1]):
                 raise ValueError("a linear site's leaf must be shaped [d_out, d_in]")
-        ldq = (n_rows + 32 + 7) // 8 * 8
-
         # Group sites by activation tensor, then chunk by rank/leaf budget.
         for s in sites:
             if s.x.device != dev or s.g.device != dev:
                 raise ValueError("LoRA site tensors must be on the plan device")
             if s.x.dtype != s.g.dtype:
                 raise TypeError("x and g of a LoRA site must share a dtype")
+            n_rows = reg.view(s.segments).n_rows
             if s.x.reshape(-1, s.x.shape[-1]).shape[0] != n_rows or s.g.reshape(-1, s.g.shape[-1]).shape[0] != n_rows:
                 raise ValueError("LoRA site row count does not match the segments")
             if not (supports_rows(s.x) and supports_rows(s.g)):
@@ -333,7 +388,7 @@ class GhostPlan:
         for s in sites:
             if s.a_leaf is None and s.b_leaf is None:
                 continue
-            k = (s.x.data_ptr(), tuple(s.x.shape), tuple(s.x.stride()), s.x.dtype)
+            k = (s.x.data_ptr(), tuple(s.x.shape), tuple(s.x.stride()), s.x.dtype, reg.view(s.segments).first)
             groups.setdefault(k, []).append(s)
         chunks: list[list[LoraSite]] = []
         for members in groups.values():
@@ -356,11 +411,16 @@ class GhostPlan:
         pe_elems: dict[int, int] = {}
         leaf_rank_m: dict[int, tuple[int, int]] = {}
         lib = N.load()
+        leaf_view: dict[int, _SegView] = {}
         for ch in chunks:
             dcode = dtype_code(ch[0].x.dtype)
             rtot = sum(s.A.shape[1] for s in ch)
             fused = len({s.scaling for s in ch if s.a_leaf is not None}) <= 1
+            n_seg = reg.view(ch[0].segments).n_seg
             for s in ch:
+                for lf in (s.a_leaf, s.b_leaf):
+                    if lf is not None:
+                        leaf_view[lf] = reg.view(s.segments)
                 d_in, r = s.A.shape
                 d_out = s.B.shape[1]
                 if s.a_leaf is not None:
@@ -374,15 +434,18 @@ class GhostPlan:
                     pe_elems[s.b_leaf] = n_seg * r * d_out
         for m in mats:
             n = int(math.prod(m.per_example.shape[1:]))
-            if m.per_example.shape[0] != n_seg:
+            leaf_view[m.leaf] = reg.view(m.segments)
+            if m.per_example.shape[0] != leaf_view[m.leaf].n_seg:
                 raise ValueError("materialised leaves need one row per segment")
             leaf_slots[m.leaf] = int(N.load().odp_sqnorm_blocks(n))
         lin_form: dict[int, int] = {}
         for ls in lins:
             d_in, d_out = ls.x.shape[-1], ls.g.shape[-1]
-            form = ls.form if ls.form is not None else choose_form(max_len, d_in, d_out)
+            v = reg.view(ls.segments)
+            leaf_view[ls.w_leaf] = v
+            form = ls.form if ls.form is not None else choose_form(v.max_len, d_in, d_out)
             lin_form[ls.w_leaf] = form
-            leaf_slots[ls.w_leaf] = int(lib.odp_linear_tiles(form, d_in, d_out, max_len))
+            leaf_slots[ls.w_leaf] = int(lib.odp_linear_tiles(form, d_in, d_out, v.max_len))
         covered = set(leaf_slots)
         if len(covered) != len(leaf_slots) or covered != set(range(len(self.leaves))):
             missing = sorted(set(range(len(self.leaves))) - covered)
@@ -442,9 +505,10 @@ class GhostPlan:
             rtot = sum(s.A.shape[1] for s in ch)
             rows_alloc = (rtot + 15) // 16 * 16 + 16
             planes = 2 if dt == torch.bfloat16 else 1
+            ldq = (reg.view(ch[0].segments).n_rows + 32 + 7) // 8 * 8
             per = planes * rows_alloc * ldq
             base = q_need.get(dt, 0)
-            chunk_layout.append((dt, rtot, rows_alloc, planes, base, base + per))
+            chunk_layout.append((dt, rtot, rows_alloc, planes, base, base + per, ldq))
             q_need[dt] = base + 2 * per
         self.qbuf = {dt: torch.empty(max(n, 1), dtype=dt, device=dev) for dt, n in q_need.items()}
 
@@ -457,13 +521,14 @@ class GhostPlan:
             return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
 
         elem = {torch.bfloat16: 2, torch.float32: 4}
-        valid = int(sum(seg.lengths))
-        for ch, (dt, rtot, rows_alloc, planes, vbase, ubase) in zip(chunks, chunk_layout):
+        for ch, (dt, rtot, rows_alloc, planes, vbase, ubase, ldq) in zip(chunks, chunk_layout):
             qb = self.qbuf[dt]
             es = elem[dt]
             plane = rows_alloc * ldq
+            v = reg.view(ch[0].segments)
+            n_rows, n_seg, valid, sf = v.n_rows, v.n_seg, v.valid, v.first
 
-            def qaddr(base: int, row: int, lo: bool) -> int:
+            def qaddr(base: int, row: int, lo: bool, qb=qb, plane=plane, ldq=ldq, es=es) -> int:
                 return qb.data_ptr() + (base + (plane if lo else 0) + row * ldq) * es
 
             x = _rows(ch[0].x)
@@ -477,7 +542,7 @@ class GhostPlan:
                     N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
                     N.PJ_W: wx.data_ptr(), N.PJ_R: rtot,
                     N.PJ_Q: qaddr(vbase, 0, False), N.PJ_QLO: qaddr(vbase, 0, True),
-                    N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: 0, N.PJ_NSEG: n_seg,
+                    N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                 },
                 lib.odp_project_blocks(n_rows),
                 (valid * d_in + rtot * d_in + planes * rtot * valid) * es,
@@ -497,7 +562,7 @@ class GhostPlan:
                         N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
                         N.PJ_W: wb.data_ptr(), N.PJ_R: r,
                         N.PJ_Q: qaddr(ubase, c0, False), N.PJ_QLO: qaddr(ubase, c0, True),
-                        N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: 0, N.PJ_NSEG: n_seg,
+                        N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                     },
                     lib.odp_project_blocks(n_rows),
                     (valid * d_out + r * d_out + planes * r * valid) * es,
@@ -509,7 +574,7 @@ class GhostPlan:
                     row = {
                         N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
                         N.FT_Q: qaddr(vbase, c0, False), N.FT_QLO: qaddr(vbase, c0, True),
-                        N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: 0, N.FT_NSEG: n_seg,
+                        N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
                         N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
                         N.FT_LEAF0: self.pe.data_ptr() + pe_off[s.b_leaf] * 4,
                         N.FT_LEAF0 + 1: 0 | (r << 16),
@@ -525,13 +590,13 @@ class GhostPlan:
                     for s_leaf, col0, r in a_leaves:
                         sc = next(s.scaling for s in ch if s.a_leaf == s_leaf)
                         tab(ft, dt, r, N.FT_FIELDS).add(
-                            self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, n_seg, sc,
+                            self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, sf, n_seg, sc,
                                         [(s_leaf, col0, r)], pe_off, slot_base),
                             n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
                             (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * 4)
                 else:
                     tab(ft, dt, rtot, N.FT_FIELDS).add(
-                        self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, n_seg, scal.pop(),
+                        self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
                                     a_leaves, pe_off, slot_base),
                         n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot),
                         (valid * d_in + planes * rtot * valid) * es
@@ -543,12 +608,14 @@ class GhostPlan:
             pe_m = m.per_example.detach()
             if pe_m.dtype not in _DTYPE_CODE:
                 pe_m = pe_m.float()
+            v = leaf_view[m.leaf]
+            n_seg = v.n_seg
             pe_m = pe_m.reshape(n_seg, -1).contiguous()
             self._keep.append(pe_m)
             n = pe_m.shape[1]
             sq.add(
                 {
-                    N.SQ_X: pe_m.data_ptr(), N.SQ_N: n, N.SQ_NSEG: n_seg, N.SQ_SEG_FIRST: 0,
+                    N.SQ_X: pe_m.data_ptr(), N.SQ_N: n, N.SQ_NSEG: n_seg, N.SQ_SEG_FIRST: v.first,
                     N.SQ_SLOT: slot_base[m.leaf], N.SQ_DTYPE: dtype_code(pe_m.dtype),
                 },
                 n_seg * lib.odp_sqnorm_blocks(n),
@@ -558,22 +625,23 @@ class GhostPlan:
 
         lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS)}
         lsum = _Table(N.LN_FIELDS)
-        nb_max = (max_len + 127) // 128
         for ls in lins:
             x, g = _rows(ls.x), _rows(ls.g)
             self._keep += [x, g]
             d_in, d_out = x.shape[1], g.shape[1]
             form = lin_form[ls.w_leaf]
+            v = leaf_view[ls.w_leaf]
+            n_seg, valid = v.n_seg, v.valid
             common = {
                 N.LN_X: x.data_ptr(), N.LN_LDX: x.stride(0), N.LN_G: g.data_ptr(), N.LN_LDG: g.stride(0),
-                N.LN_DIN: d_in, N.LN_DOUT: d_out, N.LN_SEG_FIRST: 0, N.LN_NSEG: n_seg,
+                N.LN_DIN: d_in, N.LN_DOUT: d_out, N.LN_SEG_FIRST: v.first, N.LN_NSEG: n_seg,
             }
-            tiles = int(lib.odp_linear_tiles(form, d_in, d_out, max_len))
             if form == N.FORM_GRAM:
-                fl = sum(ln * ln for ln in seg.lengths) * (d_in + d_out)
+                fl = sum(ln * ln for ln in v.segs.lengths) * (d_in + d_out)
             else:
                 fl = 2 * valid * d_in * d_out
-            blocks = int(lib.odp_linear_norm_blocks(form, d_in, d_out, max_len, n_seg))
+            blocks = int(lib.odp_linear_norm_blocks(form, d_in, d_out, v.max_len, n_seg))
+            nb_max = (v.max_len + 127) // 128
             lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf], N.LN_NB: nb_max}, blocks,
                           valid * (d_in + d_out) * 2, fl)
             lf = self.leaves[ls.w_leaf]
@@ -593,6 +661,8 @@ class GhostPlan:
                 continue
             out = self.out[i]
             out2 = self.out2[i].data_ptr() if self.out2 is not None else 0
+            v = leaf_view[i]
+            n_seg = v.n_seg
             if i in mat_pe:
                 pe_m = mat_pe[i]
                 rank, M, transpose, pdt, pe_addr = 1, pe_m.shape[1], 0, dtype_code(pe_m.dtype), pe_m.data_ptr()
@@ -603,7 +673,7 @@ class GhostPlan:
             flags = dtype_code(lf.out_dtype) | (transpose << 8) | (lf.group << 16) | (lf.cls << 40) | (pdt << 56)
             ss.add(
                 {
-                    N.SS_PE: pe_addr, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: 0,
+                    N.SS_PE: pe_addr, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: v.first,
                     N.SS_NSEG: n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2,
                 },
                 lib.odp_scale_sum_blocks(rank * M),
@@ -614,9 +684,10 @@ class GhostPlan:
         # Upload everything in one copy.
         pack = _Pack()
         idx = {}
-        idx["seg_start"] = pack.add(np.asarray(seg.starts, dtype=np.int32).reshape(-1))
-        idx["seg_len"] = pack.add(np.asarray(seg.lengths, dtype=np.int32).reshape(-1))
-        idx["seg_ex"] = pack.add(np.asarray(seg.examples, dtype=np.int32).reshape(-1))
+        seg_st, seg_ln, seg_ex = reg.arrays()
+        idx["seg_start"] = pack.add(seg_st)
+        idx["seg_len"] = pack.add(seg_ln)
+        idx["seg_ex"] = pack.add(seg_ex)
         self._launch: list[tuple] = []
         tabs = []
         for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
@@ -649,11 +720,11 @@ class GhostPlan:
         after_clip = ("scale_sum", "lin_sum")
         self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
 
-    def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, n_seg, scaling, leaves, pe_off, slot_base):
+    def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, seg_first, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
             N.FT_P: x.data_ptr(), N.FT_LDP: x.stride(0), N.FT_M: d_in,
             N.FT_Q: qaddr(ubase, col0, False), N.FT_QLO: qaddr(ubase, col0, True),
-            N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: 0, N.FT_NSEG: n_seg,
+            N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: seg_first, N.FT_NSEG: n_seg,
             N.FT_SCALING: _f64_bits(scaling), N.FT_NLEAF: len(leaves),
         }
         for li, (leaf, c, rk) in enumerate(sorted(leaves, key=lambda t: t[1])):

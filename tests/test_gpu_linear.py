@@ -139,3 +139,71 @@ def test_linear_with_materialized_leaf_per_group():
     want_b = torch.stack(outs_b).sum(0).double()
     assert (res.leaves[0].double().cpu() - want_w).norm() <= 2e-2 * want_w.norm()
     assert (res.leaves[1].double().cpu() - want_b).norm() <= 1e-5 * want_b.norm()
+
+
+# ---------------------------------------------------------------------------
+# MoE: per-(example, expert) segments, each expert with its own rows
+# (virtual groups b * E + e of opaque-patches/.../kernels/_grouped_moe.py:255)
+# ---------------------------------------------------------------------------
+
+
+def _moe_case(n_ex, T, E, k, d, h, r, dtype, seed):
+    from opaque_amd.engine import LoraSite
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n_ex, T, d, generator=g)
+    logits = torch.randn(n_ex, T, E, generator=g)
+    top = logits.topk(k, dim=-1).indices  # [n_ex, T, k]
+    sites, oracle = [], []
+    for e in range(E):
+        rows, starts, lengths, exs = [], [], [], []
+        for b in range(n_ex):
+            tok = [t for t in range(T) if bool((top[b, t] == e).any())]
+            if not tok and b % 2 == 0:
+                continue  # examples without tokens for e may omit their segment ...
+            starts.append(len(rows))
+            lengths.append(len(tok))  # ... or keep an empty one
+            exs.append(b)
+            rows += [(b, t) for t in tok]
+        xe = torch.stack([x[b, t] for b, t in rows]) if rows else torch.zeros(0, d)
+        ge = torch.randn(len(rows), h, generator=g) * (1.0 + e)
+        A = torch.randn(d, r, generator=g) / d**0.5
+        B = torch.randn(r, h, generator=g) * 0.1
+        seg = Segments(starts, lengths, exs, n_ex, len(rows))
+        xe, ge, A, B = (t.to(dtype) for t in (xe, ge, A, B))
+        sites.append(LoraSite(xe.to(DEV), ge.to(DEV), A.to(DEV), B.to(DEV), 2.0, a_leaf=2 * e, b_leaf=2 * e + 1,
+                              segments=seg))
+        dA, dB = lora_ref.lora_per_example(xe, ge, A, B, 2.0, seg.starts, seg.lengths)
+        oracle.append((seg, dA, dB))
+    return sites, oracle
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_moe_expert_segments(dtype, tol):
+    n_ex, T, E, k, d, h, r = 6, 40, 4, 2, 64, 96, 16
+    sites, oracle = _moe_case(n_ex, T, E, k, d, h, r, dtype, seed=7)
+    # Oracle: per example, squared norms summed over every expert's two leaves.
+    sq = torch.zeros(n_ex, dtype=torch.float64)
+    for seg, dA, dB in oracle:
+        for i, b in enumerate(seg.examples):
+            sq[b] += dA[i].pow(2).sum() + dB[i].pow(2).sum()
+    norms = sq.sqrt()
+    C = float(norms.median())
+    shapes = [(d, r), (r, h)] * E
+    _, rnd = leaf_guards(shapes, [dtype] * len(shapes))
+    rel_, ab = guard_constants(dtype, rnd)
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[C], effective=C, normalize_by=3.0, guards=[(rel_, ab, dtype)])
+    plan = GhostPlan(segments=Segments.padded(n_ex, 1), leaves=[LeafOut(s, dtype) for s in shapes], clip=clip,
+                     lora_sites=sites, device=DEV)
+    res = plan.run()
+    torch.cuda.synchronize()
+    got = res.norms.double().cpu()
+    assert torch.allclose(got, norms, rtol=tol, atol=0), (got, norms)
+    fac = torch.clamp(C / norms, max=1.0)
+    for e, (seg, dA, dB) in enumerate(oracle):
+        ex = torch.tensor(seg.examples, dtype=torch.long)
+        wa = (fac[ex][:, None, None] * dA).sum(0) / 3.0
+        wb = (fac[ex][:, None, None] * dB).sum(0) / 3.0
+        ga, gb = res.leaves[2 * e].double().cpu(), res.leaves[2 * e + 1].double().cpu()
+        assert (ga - wa).norm() <= tol * wa.norm(), e
+        assert (gb - wb).norm() <= tol * wb.norm(), e
