@@ -16,7 +16,7 @@ import importlib.util
 import sys
 import types
 
-from opaque_amd import clipping, noise, pytree, random, types as dp_types
+from opaque_amd import adaptive, clipping, noise, pytree, random, types as dp_types
 
 _MODULES = {
     "opaque.types": (dp_types, ["PerGroup", "ClippedPytree", "NoisedPytree", "ClipState", "NoiseState",
@@ -27,6 +27,8 @@ _MODULES = {
                                "tree_flatten_with_paths", "tree_unflatten", "tree_map", "tree_map_with_path",
                                "tree_leaves", "tree_structure", "global_norm"]),
     "opaque.dpsgd.clipping": (clipping, ["clipped_grad", "auto_clipped_grad", "per_group"]),
+    "opaque.dpsgd.clipping.adaptive": (adaptive, ["adaptive_clipped_grad", "AdaptiveClipState",
+                                                  "AdaptiveClippedGradAux"]),
     "opaque.dpsgd.clipping.types": (clipping, ["FixedClipState", "AutoClipState", "ClippedGradAux",
                                                "AutoClippedGradAux", "ClippingStats"]),
     "opaque.dpsgd.noise": (noise, ["gaussian_noise"]),
@@ -57,7 +59,12 @@ def install(force: bool = False) -> bool:
         for attr in names:
             setattr(mod, attr, getattr(src, attr))
         mod.__all__ = list(names)
+    module("opaque.dpsgd.clipping").adaptive_clipped_grad = adaptive.adaptive_clipped_grad
+    types_mod = module("opaque.dpsgd.clipping.types")
+    types_mod.AdaptiveClipState = adaptive.AdaptiveClipState
+    types_mod.AdaptiveClippedGradAux = adaptive.AdaptiveClippedGradAux
     dpsgd = module("opaque.dpsgd")
+    dpsgd.adaptive_clipped_grad = adaptive.adaptive_clipped_grad
     for attr in ("clipped_grad", "auto_clipped_grad", "per_group"):
         setattr(dpsgd, attr, getattr(clipping, attr))
     dpsgd.gaussian_noise = noise.gaussian_noise

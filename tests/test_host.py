@@ -222,3 +222,48 @@ def test_alias_installs_reference_import_paths():
                          cwd=os.path.dirname(HERE))
     assert out.returncode == 0, out.stderr
     assert out.stdout.strip() == "ok"
+
+
+# -- adaptive clipping: update rule and validation (reference test_adaptive.py:145-218) --
+
+
+def test_adaptive_update_rule_known_answers():
+    from opaque_amd.adaptive import _adaptive_clipping_norm_update as upd
+
+    kw = dict(base_clipping_norm=1.0, target_quantile=0.5, learning_rate=0.2,
+              clipping_norm_min=0.01, clipping_norm_max=100.0)
+    assert abs(upd(noisy_clipping_rate=0.8, **kw) - math.exp(0.2 * 0.3)) < 1e-6
+    assert abs(upd(noisy_clipping_rate=0.2, **kw) - math.exp(-0.2 * 0.3)) < 1e-6
+    assert abs(upd(noisy_clipping_rate=0.5, **kw) - 1.0) < 1e-6
+    assert upd(noisy_clipping_rate=1e6, **kw) == 100.0
+    assert upd(noisy_clipping_rate=-1e6, **kw) == 0.01
+
+
+def test_adaptive_noisy_rate_is_keyed():
+    from opaque_amd.adaptive import _sample_noisy_clipping_rate as noisy
+
+    a = noisy(0.3, key=key(5), step=2, fraction_noise_std=0.05)
+    b = noisy(0.3, key=key(5), step=2, fraction_noise_std=0.05)
+    c = noisy(0.3, key=key(5), step=3, fraction_noise_std=0.05)
+    assert a == b and a != c
+    g = torch.Generator().manual_seed(dp_ref.fold_in_seed(dp_ref.key_seed(5), 2) % (2**63 - 1))
+    assert a == pytest.approx(0.3 + torch.randn(1, generator=g).item() * 0.05, abs=0)
+
+
+@pytest.mark.parametrize(
+    "kwargs,match",
+    [
+        (dict(initial_clipping_norm=0.0), "initial_clipping_norm must be positive"),
+        (dict(target_quantile=1.0), "target_quantile must be in"),
+        (dict(learning_rate=0.0), "learning_rate must be positive"),
+        (dict(clipping_norm_min=0.0), "clipping_norm_min must be positive"),
+        (dict(clipping_norm_min=1.0, clipping_norm_max=1.0), "must be > clipping_norm_min"),
+        (dict(fraction_noise_std=0.0), "fraction_noise_std must be positive"),
+        (dict(return_aux=True, return_stats=True), "return_stats cannot be combined"),
+    ],
+)
+def test_adaptive_validation(kwargs, match):
+    from opaque_amd.adaptive import adaptive_clipped_grad
+
+    with pytest.raises(ValueError, match=match):
+        adaptive_clipped_grad(_loss, key=key(0), **kwargs)
