@@ -38,8 +38,15 @@ constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 // bf16 project: contraction elements per pipeline step, by rank blocks.
 __host__ __device__ constexpr int pj_ks(int nkb) { return nkb <= 2 ? 256 : 128; }
 __host__ __device__ constexpr int pj_pitch(int nkb) { return pj_ks(nkb) + 8; }
-// bf16 factor: 16-wide m blocks per wave (M-tile = 64 * NJ), by rank blocks.
-__host__ __device__ constexpr int ft_nj(int nkb) { return nkb > 0 ? 2 : 2; }  // 128-wide M-tile
+// bf16 factor: 16-wide m blocks per wave (M-tile = 64 NJ).  256-wide tiles
+// (512-byte contiguous runs of each P row) measured fastest.
+#ifndef ODP_FT_NJ
+#define ODP_FT_NJ 4
+#endif
+#ifndef ODP_FT_NJ_WIDE
+#define ODP_FT_NJ_WIDE 2  // rank blocks 3 and 4
+#endif
+__host__ __device__ constexpr int ft_nj(int nkb) { return nkb <= 2 ? ODP_FT_NJ : ODP_FT_NJ_WIDE; }
 
 // Table pointers arrive as integers (generic address space); loads through
 // them are issued as global (not flat) loads so that they only count in
@@ -396,6 +403,12 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
 // ahead of the compute; the token mask is applied when a stage is written to
 // LDS (never right after its load, which would stall the prefetch).
 // ---------------------------------------------------------------------------
+// P tiles of the factor kernel are unpadded [token][MT] rows, XOR-swizzled
+// in 4-element chunks (chunk k of row r at k ^ ft_swz(r)): the 16 rows x 4
+// chunks of one transposing operand read then hit every LDS bank twice and
+// a stage is written with 16-byte stores.
+__device__ __forceinline__ int ft_swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 2; }
+
 template <int NKB>
 __global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__ probs,
                                                      const int32_t* __restrict__ ws, int n_prob,
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__
                                                      const int32_t* __restrict__ slen,
                                                      const int32_t* __restrict__ sex,
                                                      double* __restrict__ part, int64_t part_stride) {
-  constexpr int NJ = ft_nj(NKB), MT = 64 * NJ, PP = MT + 4;
+  constexpr int NJ = ft_nj(NKB), MT = 64 * NJ, PP = MT;  // unpadded, XOR-swizzled rows
   constexpr int QP = FT_T + 8, QROWS = 16 * NKB;
   constexpr int PTILE = FT_T * PP, STAGE = PTILE + 2 * QROWS * QP;
   constexpr int NPP = NJ * FT_T / 32;                 // P pieces per thread per step
@@ -466,9 +479,8 @@ __global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__
       const int64_t t = t0 + id / (MT / 8);
       const bool ok = t >= rs && t < t_hi && m_base + (id % (MT / 8)) * 8 < M;
       const u32x4_t v = ok ? S.p[ps] : u32x4_t{0u, 0u, 0u, 0u};
-      u32x2_t* dst = (u32x2_t*)&st[(id / (MT / 8)) * PP + (id % (MT / 8)) * 8];
-      dst[0] = u32x2_t{v[0], v[1]};
-      dst[1] = u32x2_t{v[2], v[3]};
+      const int row = id / (MT / 8), chunk = 2 * (id % (MT / 8));
+      *(u32x4_t*)&st[row * PP + 4 * (chunk ^ ft_swz(row))] = v;
     }
 #pragma unroll
     for (int ps = 0; ps < NQP; ++ps) {
@@ -505,7 +517,9 @@ __global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__
       // B operand: lane gets tokens 32u + 8*(lane>>4) + 0..7 of column m0 + (lane&15),
       // as two transposing reads of 4 tokens each.
       const int m0 = (NJ * wave + j) * 16, c = lane & 15;
-      const uint16_t* src = st + (32 * u + 8 * (lane >> 4) + (c >> 2)) * PP + m0 + 4 * (c & 3);
+      const int row = 32 * u + 8 * (lane >> 4) + (c >> 2);
+      // Rows r and r + 4 share ft_swz(), so the second read is 4 rows on.
+      const uint16_t* src = st + row * PP + 4 * (((m0 >> 2) + (c & 3)) ^ ft_swz(row));
       const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
       const v4i16_t tt[2] = {t0, t1};
       const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
