@@ -31,13 +31,15 @@ namespace {
 #ifndef ODP_FT_T
 #define ODP_FT_T 32  // tokens per bf16 factor step (a multiple of the MFMA K, 32)
 #endif
-constexpr int PJ_ROWS = 64;   // rows per project workgroup (4 waves x 16)
+#ifndef ODP_PJ_RPW
+#define ODP_PJ_RPW 1  // 16-row MFMA blocks per wave in the bf16 projection (2 measured slower)
+#endif
+constexpr int PJ_ROWS = 64;   // rows per fp32 project workgroup (4 waves x 16)
+constexpr int PJ_RPW = ODP_PJ_RPW;
+constexpr int PJ_ROWS_BF16 = 64 * PJ_RPW;  // rows per bf16 project workgroup
 constexpr int FT_T = ODP_FT_T;
 constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 
-// bf16 project: contraction elements per pipeline step, by rank blocks.
-__host__ __device__ constexpr int pj_ks(int nkb) { return nkb <= 2 ? 256 : 128; }
-__host__ __device__ constexpr int pj_pitch(int nkb) { return pj_ks(nkb) + 8; }
 // bf16 factor: 16-wide m blocks per wave (M-tile = 64 NJ).  256-wide tiles
 // (512-byte contiguous runs of each P row) measured fastest.
 #ifndef ODP_FT_NJ
@@ -82,10 +84,11 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen) {
   constexpr int KS = ODP_PJ_KS, WPITCH = KS + 8, PPITCH = KS + 8, RP = 16 * NKB;
-  constexpr int NPR = KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
+  constexpr int RB = PJ_RPW, WR = 16 * RB;  // row blocks and rows per wave
+  constexpr int NPR = RB * KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
   constexpr int NW = (RP * (KS / 8) + 255) / 256;  // W pieces per thread per step
   __shared__ __attribute__((aligned(16))) uint16_t wlds[2 * RP * WPITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t plds[4 * 16 * PPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t plds[4 * WR * PPITCH];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_PJ_FIELDS;
@@ -99,46 +102,49 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
   const int seg_first = (int)f[ODP_PJ_SEG_FIRST], n_seg = (int)f[ODP_PJ_NSEG];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row0 = (int64_t)(bid - ws[p]) * PJ_ROWS + 16 * wave;
-  // Lane i < 16 tests row row0 + i; the wave shares the answers as a bit mask.
-  const int64_t test_row = row0 + (lane & 15);
+  const int64_t row0 = (int64_t)(bid - ws[p]) * PJ_ROWS_BF16 + WR * wave;
+  // Lane i < WR tests row row0 + i; the wave shares the answers as a bit mask.
+  const int64_t test_row = row0 + (lane % WR);
   const bool tvalid = test_row < n_rows &&
                       odp_row_in_segments(test_row, sstart + seg_first, slen + seg_first, n_seg);
-  const uint64_t vmask = __ballot(tvalid && lane < 16);
+  const uint64_t vmask = __ballot(tvalid && lane < WR);
   if (!__syncthreads_or(vmask != 0 ? 1 : 0)) return;  // the whole block is padding
 
-  // Load mapping: instruction i covers rows 4(i % 4) + (lane >> 4), 16 lanes x
-  // 16 B per row, at column block i / 4 of the step.
+  // Load mapping: instruction i covers rows 4(i % (4 RB)) + (lane >> 4),
+  // 16 lanes x 16 B per row, at column block i / (4 RB) of the step.
   const int lr = lane >> 4, piece = lane & 15;
-  const uint16_t* prow[4];
-  bool rowok[4];
+  constexpr int NRL = 4 * RB;  // row groups of 4 per wave
+  const uint16_t* prow[NRL];
+  bool rowok[NRL];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NRL; ++i) {
     const int rl = 4 * i + lr;
     rowok[i] = (vmask >> rl) & 1;
     prow[i] = P + (rowok[i] ? row0 + rl : 0) * ldp;
   }
-  uint16_t* pw = plds + wave * 16 * PPITCH;
+  uint16_t* pw = plds + wave * WR * PPITCH;
   const int kq = (lane >> 4) * 8;
   const int64_t nsteps = (d + KS - 1) / KS;
 
-  f32x4_t acc[NKB];
+  f32x4_t acc[RB][NKB];
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) acc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < RB; ++b)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc[b][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto load_p = [&](int64_t s, u32x4_t(&pr)[NPR]) {
 #pragma unroll
     for (int i = 0; i < NPR; ++i) {
-      const int64_t k = s * KS + 128 * (i / 4) + 8 * piece;
-      pr[i] = ld16(prow[i % 4] + (k < d ? k : d - 8));
+      const int64_t k = s * KS + 128 * (i / NRL) + 8 * piece;
+      pr[i] = ld16(prow[i % NRL] + (k < d ? k : d - 8));
     }
   };
   auto store_p = [&](int64_t s, const u32x4_t(&pr)[NPR]) {
 #pragma unroll
     for (int i = 0; i < NPR; ++i) {
-      const int c = 128 * (i / 4) + 8 * piece;
-      const bool ok = rowok[i % 4] && s * KS + c < d;
-      *(u32x4_t*)&pw[(4 * (i % 4) + lr) * PPITCH + c] = ok ? pr[i] : u32x4_t{0u, 0u, 0u, 0u};
+      const int c = 128 * (i / NRL) + 8 * piece;
+      const bool ok = rowok[i % NRL] && s * KS + c < d;
+      *(u32x4_t*)&pw[(4 * (i % NRL) + lr) * PPITCH + c] = ok ? pr[i] : u32x4_t{0u, 0u, 0u, 0u};
     }
   };
   auto load_w = [&](int64_t s, u32x4_t(&wr)[NW]) {
@@ -164,14 +170,16 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
   auto compute = [&](int b) {
 #pragma unroll
     for (int i = 0; i < KS / 32; ++i) {
-      const u32x4_t av = *(const u32x4_t*)&pw[(lane & 15) * PPITCH + 32 * i + kq];
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         const u32x4_t bv =
             *(const u32x4_t*)&wlds[(b * RP + kb * 16 + (lane & 15)) * WPITCH + 32 * i + kq];
-        acc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv),
-                                                          acc[kb], 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const u32x4_t av = *(const u32x4_t*)&pw[(16 * rb + (lane & 15)) * PPITCH + 32 * i + kq];
+          acc[rb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv), acc[rb][kb], 0, 0, 0);
+        }
       }
     }
   };
@@ -220,19 +228,22 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
 #endif
 
   // lane holds D[4*(lane>>4) + i][lane & 15] of each 16x16 block
-  const int64_t rb = row0 + 4 * (lane >> 4);
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    const int col = kb * 16 + (lane & 15);
-    if (col < r) {
-      uint16_t* qhi = Q + (int64_t)col * ldq;
-      uint16_t* qlo = Qlo + (int64_t)col * ldq;
+  for (int b = 0; b < RB; ++b) {
+    const int64_t rb = row0 + 16 * b + 4 * (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (rb + i < n_rows) {
-          const uint16_t h = odp_f2bf(acc[kb][i]);
-          qhi[rb + i] = h;
-          qlo[rb + i] = odp_f2bf(acc[kb][i] - odp_bf2f(h));
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int col = kb * 16 + (lane & 15);
+      if (col < r) {
+        uint16_t* qhi = Q + (int64_t)col * ldq;
+        uint16_t* qlo = Qlo + (int64_t)col * ldq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (rb + i < n_rows) {
+            const uint16_t h = odp_f2bf(acc[b][kb][i]);
+            qhi[rb + i] = h;
+            qlo[rb + i] = odp_f2bf(acc[b][kb][i] - odp_bf2f(h));
+          }
         }
       }
     }
@@ -643,8 +654,9 @@ __global__ __launch_bounds__(256) void k_factor_f32(const int64_t* __restrict__ 
 
 }  // namespace
 
-extern "C" int64_t odp_project_blocks(int64_t n_rows) {
-  return n_rows <= 0 ? 0 : (n_rows + PJ_ROWS - 1) / PJ_ROWS;
+extern "C" int64_t odp_project_blocks(int dtype, int64_t n_rows) {
+  const int64_t rows = dtype == ODP_DTYPE_BF16 ? PJ_ROWS_BF16 : PJ_ROWS;
+  return n_rows <= 0 ? 0 : (n_rows + rows - 1) / rows;
 }
 
 extern "C" int64_t odp_seg_factor_tiles(int dtype, int64_t M, int32_t r) {
