@@ -58,7 +58,8 @@ def kernel_label(stage, key):
     if stage == "lin_norm":
         return "k_lin_gram_norm" if key == 1 else "k_lin_outer_norm"
     if key is None:
-        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "lin_sum": "k_lin_clip_sum"}[stage]
+        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "lin_sum": "k_lin_clip_sum",
+                "factor_project": "k_factor_project_bf16"}[stage]
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]
     if dt == torch.bfloat16:
@@ -196,7 +197,7 @@ def setup_c3(args, dev):
         "valid_tokens": valid, "parallelism": "single GPU",
     }
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16"
-    return plan, 1.0 / B, config, metric, flops, ("project", "factor", "clip", "scale_sum", "noise"), "hbm"
+    return plan, 1.0 / B, config, metric, flops, ("project", "factor_project", "factor", "clip", "scale_sum", "noise"), "hbm"
 
 
 C4_THRESHOLDS = {"q": 1.0, "k": 0.5, "v": 0.5, "o": 1.0, "gate": 2.0, "up": 2.0, "down": 2.0}

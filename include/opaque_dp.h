@@ -132,6 +132,30 @@ int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
                    const int32_t* seg_row_start, const int32_t* seg_row_len,
                    const int32_t* seg_example, double* part, int64_t part_stride, int32_t nkb);
 
+/* ---- odp_seg_factor_project: the G side of a LoRA site in one pass ------
+ * Replaces the per-sample G-side products of _LoRAWBackward.vmap
+ * (opaque-patches/src/opaque/patches/kernels/lora.py:164-176):
+ * grad_out_Bt = grad_out @ B^T and dB[i] = s * (X[i] A)^T grad_out[i].
+ * One bf16 pass over P = G computes, per segment, what odp_project (U =
+ * G B^T into ODP_FP_U / ODP_FP_ULO) and odp_seg_factor (pe rows and norm
+ * partials of the dB leaf, Q = the V planes) would, reading G once.
+ * A problem is an odp_seg_factor row with NLEAF == 1 and r <= 16 plus the
+ * fields below; one workgroup per segment (total blocks = sum of n_seg).
+ * U is written for the rows of the segments only, as odp_project's planes
+ * (same ldq as Q).  Segments may be at most odp_factor_project_max_len()
+ * rows long (the caller checks; longer segments use odp_project +
+ * odp_seg_factor).  Partial slots and pe layout are odp_seg_factor's.    */
+enum {
+  ODP_FP_W = 13,    /* address of B [r][M] bf16 row-major                      */
+  ODP_FP_U = 14,    /* hi plane of U [k][ldq]                                  */
+  ODP_FP_ULO = 15   /* lo plane of U                                           */
+};
+int64_t odp_factor_project_max_len(void);
+int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
+                           const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                           const int32_t* seg_row_start, const int32_t* seg_row_len,
+                           const int32_t* seg_example, double* part, int64_t part_stride);
+
 /* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
  * For leaves that are not behind a captured linear op, the per-example
  * gradients X[n_seg][n] are materialised; each workgroup sums

@@ -37,7 +37,6 @@ namespace {
 #endif
 constexpr int LT = 128;      // output tile edge (rows and columns)
 constexpr int LK = 64;       // tokens (outer forms) or features (Gram) per pipeline step
-constexpr int OP = LT;       // LDS pitch of a [LK][LT] token-major tile (elements, swizzled)
 
 #define ODP_GLOBAL __attribute__((address_space(1)))
 #define ODP_LDS __attribute__((address_space(3)))

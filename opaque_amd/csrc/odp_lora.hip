@@ -312,9 +312,6 @@ __global__ __launch_bounds__(256) void k_project_f32(const int64_t* __restrict__
 }
 
 // Shared epilogue of the factor kernels: scale, store per-leaf rows, and
-// reduce the squared values per leaf in a fixed order.
-
-// Shared epilogue of the factor kernels: scale, store per-leaf rows, and
 // reduce the squared values per leaf in a fixed order.  Wave w owns the
 // 16-wide m blocks w*NJ .. w*NJ + NJ - 1 of the workgroup's M-tile.
 struct FactorLeaves {
@@ -577,6 +574,203 @@ __global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// G side of one LoRA site in a single pass over G, bf16, r <= 16.  For one
+// segment the workgroup walks G in 256-column chunks; within a chunk it
+// streams the segment's tokens 64 at a time and forms both
+//   pe[k][m]  = scaling * sum_t V[k][t] G[t][m]   (dB rows, as k_factor_bf16)
+//   U[t][k]  += sum_{m in chunk} G[t][m] B[k][m]  (the projection U = G B^T)
+// so that G is read from HBM once instead of once per stage.  U of every
+// token of the segment stays in registers across the chunks (wave w owns
+// tokens 16w .. 16w + 15 of each step), which bounds the segment to
+// FP_STEPS steps: lengths up to FP_STEPS * 64 - 7 tokens.  One step of
+// loads is in flight (the LDS stage parity then does not depend on the
+// step count); B's 256-column chunk is held in registers as MFMA operands.
+// ---------------------------------------------------------------------------
+constexpr int FP_T = 64, FP_MT = 256, FP_STEPS = 17;
+constexpr uint32_t ODP_BUFFER_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA buffer resource)
+
+__global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* __restrict__ probs,
+                                                                const int32_t* __restrict__ ws, int n_prob,
+                                                                const int32_t* __restrict__ sstart,
+                                                                const int32_t* __restrict__ slen,
+                                                                const int32_t* __restrict__ sex,
+                                                                double* __restrict__ part,
+                                                                int64_t part_stride) {
+  constexpr int NJ = FP_MT / 64, PP = FP_MT;  // unpadded, XOR-swizzled G rows
+  constexpr int QP = FP_T + 8, QROWS = 16;
+  constexpr int PTILE = FP_T * PP, STAGE = PTILE + 2 * QROWS * QP;
+  constexpr int NPP = FP_T * FP_MT / 8 / 256;  // G pieces per thread per step
+  constexpr int QPC = FP_T / 8;                // V pieces per row per step
+  static_assert(2 * QPC * QROWS == 256, "one V piece per thread");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_FT_FIELDS;
+  const uint16_t* P = (const uint16_t*)f[ODP_FT_P];
+  const int32_t ldp = (int32_t)f[ODP_FT_LDP], M = (int32_t)f[ODP_FT_M];
+  const int32_t ldq = (int32_t)f[ODP_FT_LDQ];
+  const int r = (int)f[ODP_FT_R];
+  const float scale = (float)__longlong_as_double(f[ODP_FT_SCALING]);
+  const uint16_t* W = (const uint16_t*)f[ODP_FP_W];
+
+  const int seg = bid - ws[p];
+  const int gs = (int)f[ODP_FT_SEG_FIRST] + seg;
+  const int32_t rs = sstart[gs], len = slen[gs], t_hi = rs + len;
+  const int ex = sex[gs];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t t_lo = rs & ~7;
+  int nsteps = len > 0 ? (t_hi - t_lo + FP_T - 1) / FP_T : 0;
+  nsteps = nsteps < FP_STEPS ? nsteps : FP_STEPS;  // the host keeps segments within bounds
+  const int nchunks = (M + FP_MT - 1) / FP_MT;
+
+  // G through a buffer resource over the segment's rows, loaded straight
+  // into LDS: rows outside the segment (offsets below it wrap past the end)
+  // and columns past M (given an offset past the end) arrive as zeros.
+  const __amdgpu_buffer_rsrc_t grsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(P + (int64_t)rs * ldp), (short)0, (int)((uint32_t)len * (uint32_t)ldp * 2u), ODP_BUFFER_DWORD3);
+  // Each wave fills tile rows 16 wave .. + 15, two rows (1 KB) per
+  // instruction; lane l lands in physical 16-byte slot l & 31 of row
+  // 16 wave + 2 i + (l >> 5), so it fetches the logical slot that the XOR
+  // swizzle maps there.
+  const int gh = lane >> 5, gslot = lane & 31;
+  // Thread's V piece: plane, rank row and 8 tokens of a step.
+  const int qplane = tid / (QPC * QROWS), qrow = (tid % (QPC * QROWS)) / QPC, qpc = tid % QPC;
+  const uint16_t* qsrc =
+      (const uint16_t*)f[qplane ? ODP_FT_QLO : ODP_FT_Q] + (int64_t)qrow * ldq;
+  uint16_t* const qdst_base = lds + PTILE + (qplane * QROWS + qrow) * QP + 8 * qpc;
+
+  auto load = [&](int b, int32_t t0, int32_t m_base, u32x4_t& qv) {
+    uint16_t* dst = lds + b * STAGE + 16 * wave * PP;
+#pragma unroll
+    for (int i = 0; i < FP_T / 4 / 2; ++i) {
+      const int row = 16 * wave + 2 * i + gh;
+      const int32_t col = m_base + 8 * (gslot ^ (ft_swz(row) >> 1));
+      const uint32_t off = col < M ? ((uint32_t)(t0 - rs + row) * (uint32_t)ldp + (uint32_t)col) * 2u
+                                   : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(grsrc, (ODP_LDS void*)(dst + 2 * i * PP), 16, off, 0, 0, 0);
+    }
+    const int32_t tq = t0 + 8 * qpc;
+    qv = ld16(qsrc + (tq < t_hi ? tq : t_lo));
+  };
+  // V's tokens outside [rs, t_hi) are zeroed when its piece is written.
+  auto store_q = [&](int b, int32_t t0, u32x4_t v) {
+    const int32_t tq = t0 + 8 * qpc;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int32_t ta = tq + 2 * w;
+      v[w] &= ((ta >= rs && ta < t_hi) ? 0x0000ffffu : 0u) |
+              ((ta + 1 >= rs && ta + 1 < t_hi) ? 0xffff0000u : 0u);
+    }
+    *(u32x4_t*)(qdst_base + b * STAGE) = v;
+  };
+
+  f32x4_t acc_u[FP_STEPS];
+#pragma unroll
+  for (int st = 0; st < FP_STEPS; ++st) acc_u[st] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const FactorLeaves L = read_leaves(f);
+
+  u32x4_t qv;
+  int buf = 0;
+  if (nsteps > 0 && nchunks > 0) load(0, t_lo, 0, qv);
+  for (int c = 0; c < nchunks; ++c) {
+    const int32_t m_base = c * FP_MT;
+    // The first token of the steps, re-read per chunk: address arithmetic
+    // of the unrolled steps then stays inside the loop instead of being
+    // hoisted out of it for every step (which exhausts registers).
+    int32_t tc0 = t_lo;
+    __asm__ volatile("" : "+s"(tc0));
+    // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
+    // lane holds B[lane & 15][32 ks + 8 (lane >> 4) .. + 7].
+    bf16x8_t wf[FP_MT / 32];
+    {
+      const int n = lane & 15;
+      const uint16_t* wrow = W + (int64_t)(n < r ? n : 0) * M;
+#pragma unroll
+      for (int ks = 0; ks < FP_MT / 32; ++ks) {
+        const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
+        const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
+        wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
+      }
+    }
+    f32x4_t acc[NJ][1];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int st = 0; st < FP_STEPS; ++st) {
+      if (st < nsteps) {
+        store_q(buf, tc0 + st * FP_T, qv);
+        __syncthreads();  // also waits for this wave's loads into the stage
+        if (st + 1 < nsteps)
+          load(buf ^ 1, tc0 + (st + 1) * FP_T, m_base, qv);
+        else if (c + 1 < nchunks)
+          load(buf ^ 1, tc0, m_base + FP_MT, qv);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+        const uint16_t* sp = lds + buf * STAGE;
+        // dB rows: B operand = G columns by transposing reads, A = V hi / lo.
+#pragma unroll
+        for (int u = 0; u < FP_T / 32; ++u) {
+          const int tc = 32 * u + 8 * (lane >> 4);
+          const u32x4_t hv = *(const u32x4_t*)&sp[PTILE + (lane & 15) * QP + tc];
+          const u32x4_t lv = *(const u32x4_t*)&sp[PTILE + (QROWS + (lane & 15)) * QP + tc];
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const int m0 = (NJ * wave + j) * 16, cc = lane & 15;
+            const int row = 32 * u + 8 * (lane >> 4) + (cc >> 2);
+            const uint16_t* src = sp + row * PP + 4 * (((m0 >> 2) + (cc & 3)) ^ ft_swz(row));
+            const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
+            const v4i16_t tt[2] = {t0, t1};
+            const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
+            acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hv), bop,
+                                                                acc[j][0], 0, 0, 0);
+            acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lv), bop,
+                                                                acc[j][0], 0, 0, 0);
+          }
+        }
+        // U rows 16 wave .. + 15 of the step: A = G rows (8 consecutive
+        // columns per lane; a swizzled chunk pair stays contiguous).
+        {
+          const int row = 16 * wave + (lane & 15);
+#pragma unroll
+          for (int ks = 0; ks < FP_MT / 32; ++ks) {
+            const int chunk = 8 * ks + 2 * (lane >> 4);
+            const u32x4_t av = *(const u32x4_t*)&sp[row * PP + 4 * (chunk ^ ft_swz(row))];
+            acc_u[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), wf[ks],
+                                                                acc_u[st], 0, 0, 0);
+          }
+        }
+        buf ^= 1;
+      }
+    }
+    factor_epilogue<NJ, 1>(acc, r, scale, M, m_base, seg, c, ex, part_stride, L, part);
+    __syncthreads();  // the partial-sum scratch of the epilogue is reused by the next chunk
+  }
+
+  // U: lane holds rows 4 (lane >> 4) + i, column lane & 15 of each step's
+  // 16 x 16 block; tokens outside the segment belong to other workgroups.
+  const int col = lane & 15;
+  if (col < r) {
+    uint16_t* uh = (uint16_t*)f[ODP_FP_U] + (int64_t)col * ldq;
+    uint16_t* ul = (uint16_t*)f[ODP_FP_ULO] + (int64_t)col * ldq;
+#pragma unroll
+    for (int st = 0; st < FP_STEPS; ++st) {
+      if (st < nsteps) {
+        const int32_t tb = t_lo + st * FP_T + 16 * wave + 4 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t t = tb + i;
+          if (t >= rs && t < t_hi) {
+            const uint16_t h = odp_f2bf(acc_u[st][i]);
+            uh[t] = h;
+            ul[t] = odp_f2bf(acc_u[st][i] - odp_bf2f(h));
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Factor gradients, fp32 P: MFMA 16x16x4 f32 with K = 16 tokens per step in
 // four MFMAs; operands come straight from global memory (P rows are read
 // 64 bytes per 16 lanes, which coalesces).
@@ -697,6 +891,27 @@ extern "C" int odp_project(odp_stream_t stream, int dtype, const int64_t* proble
                        seg_row_start, seg_row_len);
   }
   return odp_check_launch("odp_project");
+}
+
+extern "C" int64_t odp_factor_project_max_len(void) { return (int64_t)FP_STEPS * FP_T - 7; }
+
+extern "C" int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
+                                      const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                                      const int32_t* seg_row_start, const int32_t* seg_row_len,
+                                      const int32_t* seg_example, double* part, int64_t part_stride) {
+  int rc = odp_check_table("odp_seg_factor_project", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_row_start == nullptr || seg_row_len == nullptr || seg_example == nullptr ||
+      part == nullptr || part_stride <= 0) {
+    odp_set_error("odp_seg_factor_project: null segment/partial arrays or part_stride <= 0");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  static_assert(FP_MT == 64 * ODP_FT_NJ, "chunks must match the bf16 factor tiles (partial slots)");
+  hipLaunchKernelGGL(k_factor_project_bf16, dim3(total_blocks), dim3(256), 0, odp_hip_stream(stream),
+                     problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part,
+                     part_stride);
+  return odp_check_launch("odp_seg_factor_project");
 }
 
 extern "C" int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,

@@ -334,6 +334,7 @@ class GhostPlan:
         linear_sites: list[LinearSite] = (),
         device: torch.device | str = "cuda",
         second_moment: bool = False,
+        fuse_g_side: bool = True,
     ) -> None:
         N.load()
         dev = torch.device(device)
@@ -344,6 +345,7 @@ class GhostPlan:
         self.leaves = leaves
         self.clip = clip
         self.second_moment = second_moment
+        self.fuse_g_side = fuse_g_side
         self.n_groups = len(clip.thresholds)
         self.n_cls = max(1, len(clip.guards))
         if self.n_groups < 1:
@@ -516,6 +518,7 @@ class GhostPlan:
         # Tables are keyed by (dtype, rank blocks): one launch per key.
         pj: dict[tuple, _Table] = {}
         ft: dict[tuple, _Table] = {}
+        fused_rows: list[tuple] = []
 
         def tab(tables: dict, dt: torch.dtype, r: int, fields: int) -> _Table:
             return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
@@ -556,6 +559,29 @@ class GhostPlan:
                 wb = s.B.detach().to(dt).contiguous()
                 self._keep.append(wb)
                 d_out = g.shape[1]
+                if s.a_leaf is not None:
+                    a_leaves.append((s.a_leaf, c0, r))
+                # dB_i^T rows: pe[s][k][m] = scaling * sum_t V[k][t] G[t][m]
+                frow = None
+                if s.b_leaf is not None:
+                    frow = {
+                        N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
+                        N.FT_Q: qaddr(vbase, c0, False), N.FT_QLO: qaddr(vbase, c0, True),
+                        N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
+                        N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
+                        N.FT_LEAF0: self.pe.data_ptr() + pe_off[s.b_leaf] * 4,
+                        N.FT_LEAF0 + 1: 0 | (r << 16),
+                        N.FT_LEAF0 + 2: slot_base[s.b_leaf],
+                    }
+                if frow is not None and self._fusable(dt, r, v, g):
+                    # U and the dB rows in one pass over G.
+                    frow.update({N.FP_W: wb.data_ptr(), N.FP_U: qaddr(ubase, c0, False),
+                                 N.FP_ULO: qaddr(ubase, c0, True)})
+                    fused_rows.append((-d_out, len(fused_rows), frow, n_seg,
+                                       (valid * d_out + r * d_out + 2 * planes * r * valid) * es
+                                       + n_seg * r * d_out * 4))
+                    c0 += r
+                    continue
                 # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
                 tab(pj, dt, r, N.PJ_FIELDS).add(
                     {
@@ -567,20 +593,8 @@ class GhostPlan:
                     lib.odp_project_blocks(dtype_code(dt), n_rows),
                     (valid * d_out + r * d_out + planes * r * valid) * es,
                 )
-                if s.a_leaf is not None:
-                    a_leaves.append((s.a_leaf, c0, r))
-                if s.b_leaf is not None:
-                    # dB_i^T rows: pe[s][k][m] = scaling * sum_t V[k][t] G[t][m]
-                    row = {
-                        N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
-                        N.FT_Q: qaddr(vbase, c0, False), N.FT_QLO: qaddr(vbase, c0, True),
-                        N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
-                        N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
-                        N.FT_LEAF0: self.pe.data_ptr() + pe_off[s.b_leaf] * 4,
-                        N.FT_LEAF0 + 1: 0 | (r << 16),
-                        N.FT_LEAF0 + 2: slot_base[s.b_leaf],
-                    }
-                    tab(ft, dt, r, N.FT_FIELDS).add(row, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
+                if frow is not None:
+                    tab(ft, dt, r, N.FT_FIELDS).add(frow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
                                                     (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * 4)
                 c0 += r
             if a_leaves:
@@ -601,6 +615,11 @@ class GhostPlan:
                         n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot),
                         (valid * d_in + planes * rtot * valid) * es
                         + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * 4)
+
+        # Longest G first: the fused launch has one workgroup per segment.
+        fp = _Table(N.FT_FIELDS)
+        for _, _, row, blocks, nbytes in sorted(fused_rows, key=lambda t: (t[0], t[1])):
+            fp.add(row, blocks, nbytes)
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
@@ -692,6 +711,7 @@ class GhostPlan:
         tabs = []
         for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("project", key, pj[key]))
+        tabs.append(("factor_project", None, fp))
         for key in sorted(ft, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("factor", key, ft[key]))
         tabs.append(("sqnorm", None, sq))
@@ -719,6 +739,13 @@ class GhostPlan:
         info = [(name, dt, total, nb[0], nb[1]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
         after_clip = ("scale_sum", "lin_sum")
         self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
+
+    def _fusable(self, dt: torch.dtype, r: int, v: _SegView, g: torch.Tensor) -> bool:
+        """Whether a site's G side runs as one odp_seg_factor_project pass."""
+        if not self.fuse_g_side or dt != torch.bfloat16 or r > 16:
+            return False
+        lib = N.load()
+        return v.max_len <= lib.odp_factor_project_max_len() and v.max_len * g.stride(0) * 2 < 2**31
 
     def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, seg_first, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
@@ -750,8 +777,8 @@ class GhostPlan:
     def run(self, events: dict | None = None, launch_log: list | None = None) -> GhostResult:
         """Launch the step on the current stream.
 
-        ``events`` may map a stage name ("project", "factor", "sqnorm",
-        "clip", "scale_sum") to a (start, end) pair of torch.cuda.Event that
+        ``events`` may map a stage name ("project", "factor_project",
+        "factor", "sqnorm", "lin_norm", "clip", "scale_sum", "lin_sum") to a (start, end) pair of torch.cuda.Event that
         are recorded around that stage's launches.  ``launch_log``, when a
         list, receives one (stage, key, start, end) entry per table launch
         with freshly recorded timing events, in ``launch_info`` order.
@@ -780,6 +807,11 @@ class GhostPlan:
             if name == "project":
                 N.check(lib.odp_project(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                         self.seg_start.data_ptr(), self.seg_len.data_ptr(), dt[1]), name)
+            elif name == "factor_project":
+                N.check(lib.odp_seg_factor_project(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                                   self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                                   self.seg_ex.data_ptr(), self.part.data_ptr(),
+                                                   self.n_slots), name)
             elif name == "factor":
                 N.check(lib.odp_seg_factor(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                            self.seg_start.data_ptr(), self.seg_len.data_ptr(),
