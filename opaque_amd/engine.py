@@ -574,12 +574,19 @@ class GhostPlan:
                         N.FT_LEAF0 + 2: slot_base[s.b_leaf],
                     }
                 if frow is not None and self._fusable(dt, r, v, g):
-                    # U and the dB rows in one pass over G.
+                    # U and the dB rows in one pass over G, one workgroup per
+                    # segment: a row per segment, so that the launch can run
+                    # the longest first (the segment's pe rows start at its
+                    # own offset).
                     frow.update({N.FP_W: wb.data_ptr(), N.FP_U: qaddr(ubase, c0, False),
-                                 N.FP_ULO: qaddr(ubase, c0, True)})
-                    fused_rows.append((-d_out, len(fused_rows), frow, n_seg,
-                                       (valid * d_out + r * d_out + 2 * planes * r * valid) * es
-                                       + n_seg * r * d_out * 4))
+                                 N.FP_ULO: qaddr(ubase, c0, True), N.FT_NSEG: 1})
+                    pe0 = self.pe.data_ptr() + pe_off[s.b_leaf] * 4
+                    for j, ln in enumerate(v.segs.lengths):
+                        row = dict(frow)
+                        row[N.FT_SEG_FIRST] = sf + j
+                        row[N.FT_LEAF0] = pe0 + j * r * d_out * 4
+                        fused_rows.append((-ln * d_out, len(fused_rows), row, 1,
+                                           (ln * d_out + r * d_out + 2 * planes * r * ln) * es + r * d_out * 4))
                     c0 += r
                     continue
                 # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
@@ -616,7 +623,8 @@ class GhostPlan:
                         (valid * d_in + planes * rtot * valid) * es
                         + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * 4)
 
-        # Longest G first: the fused launch has one workgroup per segment.
+        # Most work first (the fused launch has one workgroup per segment, of
+        # very different lengths).
         fp = _Table(N.FT_FIELDS)
         for _, _, row, blocks, nbytes in sorted(fused_rows, key=lambda t: (t[0], t[1])):
             fp.add(row, blocks, nbytes)
