@@ -8,7 +8,8 @@
  *
  * Work is described by "problem tables": device arrays of int64_t rows whose
  * field indices are listed below.  One launch processes every problem of its
- * table, so a whole model's DP step is five launches regardless of depth.
+ * table, so a whole model's DP step is a handful of launches regardless of
+ * depth.
  * Each table comes with a device int32 array work_start[n_prob + 1] holding
  * the cumulative number of workgroups per problem (work_start[0] == 0);
  * the *_blocks() helpers give the per-problem workgroup counts.
@@ -16,7 +17,8 @@
  * The reference (JetBrains-Research/opaque) is Python; these entry points
  * replace the following internals of its DP-SGD hot path
  * (paths relative to packages/):
- *   odp_project + odp_seg_factor  -> per-sample LoRA factor gradients,
+ *   odp_project + odp_seg_factor_project + odp_seg_factor
+ *                                 -> per-sample LoRA factor gradients,
  *       opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176
  *       (dA[i] = s X[i]^T (G[i] B^T), dB[i] = s (X[i] A)^T G[i]) and the
  *       per-example squared norms of clip_pytree,
