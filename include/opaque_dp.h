@@ -136,7 +136,7 @@ int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
 
 /* ---- odp_seg_factor_project: the G side of a LoRA site in one pass ------
  * Replaces the per-sample G-side products of _LoRAWBackward.vmap
- * (opaque-patches/src/opaque/patches/kernels/lora.py:164-176):
+ * (opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176):
  * grad_out_Bt = grad_out @ B^T and dB[i] = s * (X[i] A)^T grad_out[i].
  * One bf16 pass over P = G computes, per segment, what odp_project (U =
  * G B^T into ODP_FP_U / ODP_FP_ULO) and odp_seg_factor (pe rows and norm
