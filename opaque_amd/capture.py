@@ -322,6 +322,62 @@ class LoRALinear(torch.nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return peft_lora_linear(x, self.weight, self.lora_A, self.lora_B, self.scaling, self.bias)
 
+    @classmethod
+    def from_linear(cls, base: torch.nn.Linear, r: int, alpha: float = 16.0) -> LoRALinear:
+        """Wrap an existing ``Linear``: its weight and bias become the frozen base (shared, not copied)."""
+        m = cls.__new__(cls)
+        torch.nn.Module.__init__(m)
+        w = base.weight
+        m.weight = torch.nn.Parameter(w.data, requires_grad=False)
+        m.bias = None if base.bias is None else torch.nn.Parameter(base.bias.data, requires_grad=False)
+        m.lora_A = torch.nn.Parameter(torch.empty(r, base.in_features, device=w.device, dtype=w.dtype))
+        m.lora_B = torch.nn.Parameter(torch.zeros(base.out_features, r, device=w.device, dtype=w.dtype))
+        m.scaling = alpha / r
+        torch.nn.init.kaiming_uniform_(m.lora_A, a=5**0.5)
+        return m
+
+
+def _replace_linears(model: torch.nn.Module, targets, make) -> list[str]:
+    names = []
+    for name, mod in list(model.named_modules()):
+        for child_name, child in list(mod.named_children()):
+            if type(child) is torch.nn.Linear and child_name in targets:
+                setattr(mod, child_name, make(child))
+                names.append(f"{name}.{child_name}" if name else child_name)
+    return names
+
+
+def inject_lora(model: torch.nn.Module, target_modules=("q_proj", "k_proj", "v_proj", "o_proj",
+                                                        "gate_proj", "up_proj", "down_proj"),
+                r: int = 8, alpha: float = 16.0, freeze_base: bool = True) -> list[str]:
+    """Give every ``nn.Linear`` child named in ``target_modules`` a LoRA adapter routed through the seam.
+
+    The counterpart of building a PEFT LoRA model and installing the
+    reference's patched forward (``apply_peft_model_patches``,
+    PAT/peft/_router.py:158-198, which routes ``lora_A``/``lora_B`` into
+    ``Opaque_LoRA_W``): each matching ``Linear`` becomes a ``LoRALinear``
+    sharing its weight and bias, ``lora_A`` Kaiming-initialised and
+    ``lora_B`` zero as in PEFT.  With ``freeze_base`` every parameter of the
+    model other than the adapters stops requiring grad.  Returns the
+    replaced modules' names.
+    """
+    if freeze_base:
+        for p in model.parameters():
+            p.requires_grad_(False)
+    return _replace_linears(model, set(target_modules), lambda lin: LoRALinear.from_linear(lin, r, alpha))
+
+
+def route_linears(model: torch.nn.Module, target_modules) -> list[str]:
+    """Route the named ``nn.Linear`` children through the full-weight seam (parameters shared)."""
+    def make(lin: torch.nn.Linear) -> Linear:
+        m = Linear.__new__(Linear)
+        torch.nn.Module.__init__(m)
+        m.in_features, m.out_features = lin.in_features, lin.out_features
+        m.weight, m.bias = lin.weight, lin.bias
+        return m
+
+    return _replace_linears(model, set(target_modules), make)
+
 
 __all__ = [
     "CaptureSession",
@@ -329,7 +385,9 @@ __all__ = [
     "LoRALinear",
     "SiteRecord",
     "active_session",
+    "inject_lora",
     "linear",
     "lora_linear",
     "peft_lora_linear",
+    "route_linears",
 ]

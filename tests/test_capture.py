@@ -194,3 +194,70 @@ def test_full_weight_linear_seams():
     assert {paths[k][0] for k in disc.eligible} == {"a.weight", "b.weight"}
     assert sorted(r.kind for r in sess.sites) == ["linear", "linear"]
     _check(ref, got)
+
+
+def _tiny_llama(seed=0, dtype=torch.float32):
+    """A random-init two-layer Llama (GQA attention, RMSNorm, SwiGLU) with LoRA on all seven projections."""
+    transformers = __import__("pytest").importorskip("transformers")
+    torch.manual_seed(seed)
+    cfg = transformers.LlamaConfig(vocab_size=64, hidden_size=32, intermediate_size=48, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+                                   attn_implementation="eager")
+    m = transformers.LlamaForCausalLM(cfg).to(dtype).eval()
+    names = capture.inject_lora(m, r=4, alpha=8)
+    for mod in m.modules():
+        if isinstance(mod, capture.LoRALinear):
+            torch.nn.init.normal_(mod.lora_B, std=0.1)
+    return m, names
+
+
+def test_inject_lora_on_hf_llama_reproduces_vmap_grad():
+    m, names = _tiny_llama()
+    assert len(names) == 14
+    train = {k: v for k, v in m.named_parameters() if v.requires_grad}
+    assert set(train) == {f"{n}.{f}" for n in names for f in ("lora_A", "lora_B")}
+    frozen = {k: v for k, v in m.named_parameters() if k not in train}
+
+    def loss_fn(params, ids, labels):
+        out = torch.func.functional_call(m, {**frozen, **params}, (ids.unsqueeze(0),),
+                                         {"labels": labels.unsqueeze(0)})
+        return out.loss
+
+    n, T = 3, 8
+    g = torch.Generator().manual_seed(1)
+    ids, labels = torch.randint(0, 64, (n, T), generator=g), torch.randint(0, 64, (n, T), generator=g)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0, 0), randomness="same")(train, ids, labels)
+    eng = _engine(loss_fn)
+    disc, sess, got, paths = _capture_per_example(eng, (train, ids, labels), n)
+    assert len(disc.eligible) == 28 and len(sess.sites) == 14
+    _check(ref, got)
+
+
+def test_route_linears_reproduces_vmap_grad():
+    m, _ = _tiny_llama(seed=2)
+    for p in m.parameters():
+        p.requires_grad_(False)
+    for mod in m.modules():  # drop the adapters' trainability; train two full weights instead
+        if isinstance(mod, capture.LoRALinear):
+            mod.lora_A.requires_grad_(False)
+            mod.lora_B.requires_grad_(False)
+    lm = m.lm_head
+    routed = capture.route_linears(m, ("lm_head",))
+    assert routed == ["lm_head"] and m.lm_head.weight is lm.weight
+    m.lm_head.weight.requires_grad_(True)
+    train = {k: v for k, v in m.named_parameters() if v.requires_grad}
+    frozen = {k: v for k, v in m.named_parameters() if k not in train}
+
+    def loss_fn(params, ids, labels):
+        out = torch.func.functional_call(m, {**frozen, **params}, (ids.unsqueeze(0),),
+                                         {"labels": labels.unsqueeze(0)})
+        return out.loss
+
+    n, T = 2, 6
+    g = torch.Generator().manual_seed(3)
+    ids, labels = torch.randint(0, 64, (n, T), generator=g), torch.randint(0, 64, (n, T), generator=g)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0, 0), randomness="same")(train, ids, labels)
+    eng = _engine(loss_fn)
+    disc, sess, got, paths = _capture_per_example(eng, (train, ids, labels), n)
+    assert len(disc.eligible) == 1
+    _check(ref, got)
