@@ -38,6 +38,8 @@ class SiteRecord:
     b_transposed: bool
     g: torch.Tensor | None = None  # physical output gradients, filled by backward
     w_obj: torch.Tensor | None = None  # full-weight linear: the weight passed ([d_out, d_in])
+    w_index: int | None = None  # MoE expert: slice of the stacked weight w_obj ([E, d_out, d_in])
+    segments: Any = None  # MoE expert: engine Segments of x's rows (x is then [rows, d_in])
 
     @property
     def kind(self) -> str:
@@ -256,6 +258,160 @@ class _SeamLinear(torch.autograd.Function):
         return _TapLinear.apply(x, W, bias, sess.anchor, rec), 0
 
 
+# ---------------------------------------------------------------------------
+# Mixture-of-experts expert FFN (full expert weights)
+# ---------------------------------------------------------------------------
+
+
+def _dense_routing(top_k_index: torch.Tensor, top_k_weights: torch.Tensor, n_experts: int) -> torch.Tensor:
+    """Per-expert routing weights [..., E]: a token's weight for each expert, 0 where not routed."""
+    if top_k_weights.shape[-1] == n_experts and top_k_index.shape != top_k_weights.shape:
+        return top_k_weights  # already dense
+    hit = top_k_index.unsqueeze(-1) == torch.arange(n_experts, device=top_k_index.device)
+    return (hit.to(top_k_weights.dtype) * top_k_weights.unsqueeze(-1)).sum(-2)
+
+
+def _expert_ffn(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, batched: bool) -> torch.Tensor:
+    """down(silu(gate(x)) * up(x)) for one expert; with ``batched`` the weights carry the batch axis."""
+    inter = w1.shape[-2] // 2
+    gu = torch.einsum("b...h,bjh->b...j", x, w1) if batched else F.linear(x, w1)
+    h = F.silu(gu[..., :inter].float()).to(x.dtype) * gu[..., inter:]
+    return torch.einsum("b...i,bhi->b...h", h, w2) if batched else F.linear(h, w2)
+
+
+def _moe_dense(x, gate_up_proj, down_proj, top_k_index, top_k_weights, batched: bool = False):
+    """Every token through every expert, weighted by its routing weight; fp32 sum over experts."""
+    n_exp = gate_up_proj.shape[-3]
+    w_te = _dense_routing(top_k_index, top_k_weights, n_exp)
+    out = torch.zeros(x.shape, dtype=torch.float32, device=x.device)
+    for e in range(n_exp):
+        w1 = gate_up_proj[:, e] if batched else gate_up_proj[e]
+        w2 = down_proj[:, e] if batched else down_proj[e]
+        out = out + (_expert_ffn(x, w1, w2, batched) * w_te[..., e : e + 1]).float()
+    return out.to(x.dtype)
+
+
+def _moe_tapped(sess: CaptureSession, x, gate_up_proj, down_proj, top_k_index, top_k_weights):
+    """Batch-merged MoE over the routed rows only, recording each expert's two linears.
+
+    Rows are grouped by expert (stable, so each expert's rows stay in example
+    order); every expert's rows form one segment per example, the
+    per-(example, expert) groups of the reference's grouped backward
+    (PAT/kernels/_grouped_moe.py:255).
+    """
+    from opaque_amd.engine import Segments  # the engine imports this module
+
+    n_ex, hid = x.shape[0], x.shape[-1]
+    xf = x.reshape(-1, hid)
+    per = xf.shape[0] // n_ex
+    k = top_k_index.shape[-1]
+    idf = top_k_index.reshape(-1, k).long()
+    wf = top_k_weights.reshape(-1, k)
+    n_exp, two_i = gate_up_proj.shape[0], gate_up_proj.shape[1]
+    inter, dt = two_i // 2, x.dtype
+    hit = idf.unsqueeze(-1) == torch.arange(n_exp, device=x.device)  # [N, K, E]
+    routed = hit.any(1)  # [N, E]
+    counts = routed.view(n_ex, per, n_exp).sum(1).t().tolist()  # [E][n_ex], one host sync
+    w_te = (hit.to(wf.dtype) * wf.unsqueeze(-1)).sum(1)  # [N, E], differentiable in the weights
+    # Flat (expert, row) positions of the routed pairs, grouped by expert and
+    # ascending in row within each expert.
+    order = torch.argsort(routed.t().reshape(-1).logical_not().to(torch.int8), stable=True)
+    out = torch.zeros(xf.shape, dtype=torch.float32, device=x.device)
+    pos = 0
+    n_rows_all = xf.shape[0]
+    for e in range(n_exp):
+        lens = counts[e]
+        n_e = sum(lens)
+        starts = [sum(lens[:j]) for j in range(n_ex)]
+        segs = Segments(starts, list(lens), list(range(n_ex)), n_ex, max(n_e, 1))
+        r1 = SiteRecord(x=None, A=None, B=None, scaling=1.0, a_obj=None, b_obj=None, a_transposed=False,
+                        b_transposed=False, w_obj=gate_up_proj, w_index=e, segments=segs)
+        r2 = SiteRecord(x=None, A=None, B=None, scaling=1.0, a_obj=None, b_obj=None, a_transposed=False,
+                        b_transposed=False, w_obj=down_proj, w_index=e, segments=segs)
+        sess.sites += [r1, r2]
+        if n_e == 0:
+            # One zero row stands in for the empty group: it adds nothing.
+            r1.x, r1.g = xf.new_zeros(1, hid), xf.new_zeros(1, two_i)
+            r2.x, r2.g = xf.new_zeros(1, inter), xf.new_zeros(1, hid)
+            continue
+        rows = order[pos : pos + n_e] - e * n_rows_all
+        pos += n_e
+        xe = xf.index_select(0, rows)
+        r1.x = xe.detach()
+        gu = _TapLinear.apply(xe, gate_up_proj[e], None, sess.anchor, r1)
+        h = F.silu(gu[:, :inter].float()).to(dt) * gu[:, inter:]
+        r2.x = h.detach()
+        y = _TapLinear.apply(h, down_proj[e], None, sess.anchor, r2)
+        we = w_te[:, e].index_select(0, rows)
+        out = out.index_add(0, rows, (y * we.unsqueeze(-1).to(dt)).float())
+    return out.to(dt).reshape(x.shape)
+
+
+class _SeamMoE(torch.autograd.Function):
+    """Per-example MoE expert FFN whose vmap rule merges the batch and taps every expert."""
+
+    generate_vmap_rule = False
+
+    @staticmethod
+    def forward(x, gate_up_proj, down_proj, top_k_index, top_k_weights):
+        return _moe_dense(x, gate_up_proj, down_proj, top_k_index, top_k_weights)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        pass
+
+    @staticmethod
+    def backward(ctx, g):
+        raise RuntimeError("the capture seam is differentiated through its vmap rule only")
+
+    @staticmethod
+    def vmap(info, in_dims, x, gate_up_proj, down_proj, top_k_index, top_k_weights):
+        sess = active_session()
+        xd, w1d, w2d, id_d, wd = in_dims
+
+        def front(t, d):
+            return t.unsqueeze(0).expand(info.batch_size, *t.shape) if d is None else t.movedim(d, 0)
+
+        x, top_k_index, top_k_weights = front(x, xd), front(top_k_index, id_d), front(top_k_weights, wd)
+        if w1d is not None or w2d is not None:
+            # Per-example (expanded) expert weights: plain batched math.
+            w1, w2 = front(gate_up_proj, w1d), front(down_proj, w2d)
+            return _moe_dense(x, w1, w2, top_k_index, top_k_weights, batched=True), 0
+        if (sess is None or sess.mode != "capture" or id(gate_up_proj) not in sess.eligible
+                or id(down_proj) not in sess.eligible):
+            return _moe_dense(x, gate_up_proj, down_proj, top_k_index, top_k_weights), 0
+        return _moe_tapped(sess, x, gate_up_proj, down_proj, top_k_index, top_k_weights), 0
+
+
+def moe(x: torch.Tensor, gate_up_proj: torch.Tensor, down_proj: torch.Tensor,
+        top_k_index: torch.Tensor, top_k_weights: torch.Tensor) -> torch.Tensor:
+    """Mixture-of-experts expert FFN with stacked expert weights, clipped per (example, expert).
+
+    Same signature and layout as the reference's ``opaque_moe``
+    (PAT/kernels/moe.py:179-221; Hugging Face stacked experts):
+    ``x`` [..., H], ``gate_up_proj`` [E, 2I, H] (gate rows first),
+    ``down_proj`` [E, H, I], ``top_k_index`` / ``top_k_weights`` [..., K]
+    (or dense [..., E] weights); out = sum_k w_k down_e(silu(gate_e(x)) *
+    up_e(x)) over the routed experts e = top_k_index[k].  Outside
+    ``clipped_grad`` this is plain differentiable math.  Inside it the
+    expert weights' per-example gradients are never materialised: each
+    expert's two linears are full-weight sites over that expert's rows, one
+    segment per example, so an example's norm sums its share of every
+    expert it was routed to.
+    """
+    sess = active_session()
+    if sess is None:
+        return _moe_dense(x, gate_up_proj, down_proj, top_k_index, top_k_weights)
+    if sess.mode == "discover":
+        for t in (gate_up_proj, down_proj):
+            sess.uses[id(t)] = sess.uses.get(id(t), 0) + 1
+            sess.linear_ws.append(id(t))
+        return _moe_dense(x, gate_up_proj.detach(), down_proj.detach(), top_k_index, top_k_weights)
+    if id(gate_up_proj) not in sess.eligible and id(down_proj) not in sess.eligible:
+        return _moe_dense(x, gate_up_proj, down_proj, top_k_index, top_k_weights)
+    return _SeamMoE.apply(x, gate_up_proj, down_proj, top_k_index, top_k_weights)
+
+
 def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """``x W^T + bias`` whose weight gradient the DP engine clips without materialising it.
 
@@ -388,6 +544,7 @@ __all__ = [
     "inject_lora",
     "linear",
     "lora_linear",
+    "moe",
     "peft_lora_linear",
     "route_linears",
 ]

@@ -557,11 +557,15 @@ class _ClipEngine:
             values, loss_aux = torch.func.vmap(per_example, in_dims=in_dims, randomness="same")(*cargs)
         recs = sess.sites
         seen: dict[int, int] = {}
+        want = dict.fromkeys(disc.eligible, 1)
         for r in recs:
             for o in (r.a_obj, r.b_obj, r.w_obj):
                 if o is not None and id(o) in obj_leaf:
-                    seen[obj_leaf[id(o)]] = seen.get(obj_leaf[id(o)], 0) + 1
-        if any(seen.get(k, 0) != 1 for k in disc.eligible):
+                    k = obj_leaf[id(o)]
+                    seen[k] = seen.get(k, 0) + 1
+                    if r.w_index is not None:  # a stacked (MoE) weight: one record per expert
+                        want[k] = leaves[k].shape[0]
+        if any(seen.get(k, 0) != want[k] for k in disc.eligible):
             # The batched pass took a different route than discovery: redo it materialised.
             self._discovery = None
             return None
@@ -576,13 +580,25 @@ class _ClipEngine:
         rows_per_ex: dict[int, int] = {}
         for r in recs:
             if r.g is None:
-                d_out = r.w_obj.shape[0] if r.w_obj is not None else r.B.shape[1]
+                d_out = r.w_obj.shape[-2] if r.w_obj is not None else r.B.shape[1]
                 r.g = torch.zeros(*r.x.shape[:-1], d_out, dtype=r.x.dtype, device=r.x.device)
+            if r.segments is not None:
+                continue  # MoE experts bring their own rows
             t_rows = r.x[0].numel() // r.x.shape[-1] if r.x.dim() > 1 else 1
             rows_per_ex[t_rows] = rows_per_ex.get(t_rows, 0) + 1
         seq = max(rows_per_ex, key=rows_per_ex.get) if rows_per_ex else 1
         lins: list[LinearSite] = []
+        stacked: dict[int, torch.Tensor] = {}
         for r in recs:
+            if r.w_obj is not None and r.segments is not None:
+                kw = obj_leaf[id(r.w_obj)]
+                if (not self.second_moment and r.x.dtype == r.g.dtype == leaves[kw].dtype == torch.bfloat16
+                        and supports_rows(r.x) and supports_rows(r.g)):
+                    lins.append(LinearSite(x=r.x, g=r.g, w_leaf=kw, segments=r.segments, index=r.w_index))
+                else:
+                    pe = _expert_per_example(r, leaves[kw], n)
+                    stacked[kw] = pe if kw not in stacked else stacked[kw] + pe
+                continue
             if r.w_obj is not None:
                 kw = obj_leaf[id(r.w_obj)]
                 t_rows = r.x[0].numel() // r.x.shape[-1]
@@ -610,6 +626,8 @@ class _ClipEngine:
             else:
                 for k, pe in _site_per_example(r, ka, kb, leaves):
                     mats.append(MaterializedLeaf(per_example=pe.reshape(n, -1), leaf=k))
+        for k, pe in stacked.items():
+            mats.append(MaterializedLeaf(per_example=pe.reshape(n, -1), leaf=k))
         for k, g in ex_grads.items():
             if g is None:
                 g = torch.zeros((n, *leaves[k].shape), dtype=leaves[k].dtype, device=device)
@@ -772,6 +790,18 @@ def _site_per_example(r: SiteRecord, ka: int | None, kb: int | None,
         db = r.scaling * torch.matmul(v.transpose(1, 2).contiguous(), g.to(dt))  # [n, r, d_out]
         out.append((kb, db.transpose(1, 2) if r.b_transposed else db))
     return out
+
+
+def _expert_per_example(r: SiteRecord, leaf: torch.Tensor, n: int) -> torch.Tensor:
+    """Per-example gradients [n, E, d_out, d_in] of one MoE expert's weight slice (others zero),
+    for experts the kernels cannot take: dW_i = G_i^T X_i over example i's rows of the expert."""
+    dt = leaf.dtype
+    full = torch.zeros((n, *leaf.shape), dtype=dt, device=leaf.device)
+    seg = r.segments
+    for s, ln, ex in zip(seg.starts, seg.lengths, seg.examples):
+        if ln:
+            full[ex, r.w_index] = r.g[s : s + ln].to(dt).t().contiguous() @ r.x[s : s + ln].to(dt)
+    return full
 
 
 # ---------------------------------------------------------------------------

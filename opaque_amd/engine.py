@@ -188,7 +188,8 @@ class LinearSite:
     """A full-weight linear y = x W^T over the batch rows (bf16).
 
     ``w_leaf`` indexes the plan's leaf list; the leaf is W's gradient,
-    shaped [d_out, d_in].  ``form`` picks the per-example norm algorithm
+    shaped [d_out, d_in], or with ``index`` one slice of a stacked
+    [E, d_out, d_in] leaf (each slice produced by one site).  ``form`` picks the per-example norm algorithm
     (``N.FORM_OUTER`` / ``N.FORM_GRAM``); None chooses the one with fewer
     MFMA flops for the longest segment.
     """
@@ -198,6 +199,7 @@ class LinearSite:
     w_leaf: int
     form: int | None = None
     segments: Segments | None = None  # rows of x / g; None: the plan's segments
+    index: int | None = None  # slice of a stacked [E, d_out, d_in] leaf (an MoE expert); None: the whole leaf
 
 
 def choose_form(max_len: int, d_in: int, d_out: int) -> int:
@@ -373,8 +375,12 @@ class GhostPlan:
                 raise ValueError("linear site row count does not match the segments")
             if not (supports_rows(ls.x) and supports_rows(ls.g)):
                 raise ValueError("linear site feature sizes must be multiples of 8")
-            if tuple(self.leaves[ls.w_leaf].shape) != (ls.g.shape[-1], ls.x.shape[-1]):
+            shape = tuple(self.leaves[ls.w_leaf].shape)
+            want = (ls.g.shape[-1], ls.x.shape[-1])
+            if ls.index is None and shape != want:
                 raise ValueError("a linear site's leaf must be shaped [d_out, d_in]")
+            if ls.index is not None and (len(shape) != 3 or shape[1:] != want or not 0 <= ls.index < shape[0]):
+                raise ValueError("a stacked linear site's leaf must be shaped [E, d_out, d_in] with index < E")
         # Group sites by activation tensor, then chunk by rank/leaf budget.
         for s in sites:
             if s.x.device != dev or s.g.device != dev:
@@ -440,17 +446,32 @@ class GhostPlan:
             if m.per_example.shape[0] != leaf_view[m.leaf].n_seg:
                 raise ValueError("materialised leaves need one row per segment")
             leaf_slots[m.leaf] = int(N.load().odp_sqnorm_blocks(n))
-        lin_form: dict[int, int] = {}
+        # Linear sites: per site its norm form, segment view and first partial
+        # slot within its leaf (the slices of a stacked leaf follow each other).
+        lin_form: list[int] = []
+        lin_view: list[_SegView] = []
+        lin_off: list[int] = []
+        others = set(leaf_slots)
+        slices: dict[int, set[int]] = {}
         for ls in lins:
             d_in, d_out = ls.x.shape[-1], ls.g.shape[-1]
             v = reg.view(ls.segments)
-            leaf_view[ls.w_leaf] = v
             form = ls.form if ls.form is not None else choose_form(v.max_len, d_in, d_out)
-            lin_form[ls.w_leaf] = form
-            leaf_slots[ls.w_leaf] = int(lib.odp_linear_tiles(form, d_in, d_out, v.max_len))
-        covered = set(leaf_slots)
-        if len(covered) != len(leaf_slots) or covered != set(range(len(self.leaves))):
-            missing = sorted(set(range(len(self.leaves))) - covered)
+            tiles = int(lib.odp_linear_tiles(form, d_in, d_out, v.max_len))
+            lin_form.append(form)
+            lin_view.append(v)
+            taken = slices.setdefault(ls.w_leaf, set())
+            key = -1 if ls.index is None else ls.index
+            if ls.w_leaf in others or key in taken or (taken and (key == -1) != (-1 in taken)):
+                raise ValueError(f"leaf {ls.w_leaf} (slice {ls.index}) has more than one producer")
+            taken.add(key)
+            lin_off.append(leaf_slots.get(ls.w_leaf, 0))
+            leaf_slots[ls.w_leaf] = leaf_slots.get(ls.w_leaf, 0) + tiles
+        for k, taken in slices.items():
+            if -1 not in taken and taken != set(range(self.leaves[k].shape[0])):
+                raise ValueError(f"stacked leaf {k} needs a linear site for every slice")
+        if set(leaf_slots) != set(range(len(self.leaves))):
+            missing = sorted(set(range(len(self.leaves))) - set(leaf_slots))
             raise ValueError(f"every output leaf needs exactly one producer; missing {missing}")
         order = sorted(leaf_slots, key=lambda i: (self.leaves[i].group, i))
         slot_base: dict[int, int] = {}
@@ -652,12 +673,12 @@ class GhostPlan:
 
         lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS)}
         lsum = _Table(N.LN_FIELDS)
-        for ls in lins:
+        for i, ls in enumerate(lins):
             x, g = _rows(ls.x), _rows(ls.g)
             self._keep += [x, g]
             d_in, d_out = x.shape[1], g.shape[1]
-            form = lin_form[ls.w_leaf]
-            v = leaf_view[ls.w_leaf]
+            form = lin_form[i]
+            v = lin_view[i]
             n_seg, valid = v.n_seg, v.valid
             common = {
                 N.LN_X: x.data_ptr(), N.LN_LDX: x.stride(0), N.LN_G: g.data_ptr(), N.LN_LDG: g.stride(0),
@@ -669,16 +690,16 @@ class GhostPlan:
                 fl = 2 * valid * d_in * d_out
             blocks = int(lib.odp_linear_norm_blocks(form, d_in, d_out, v.max_len, n_seg))
             nb_max = (v.max_len + 127) // 128
-            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf], N.LN_NB: nb_max}, blocks,
+            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_off[i], N.LN_NB: nb_max}, blocks,
                           valid * (d_in + d_out) * 2, fl)
             lf = self.leaves[ls.w_leaf]
-            out = self.out[ls.w_leaf]
+            out = self.out[ls.w_leaf] if ls.index is None else self.out[ls.w_leaf][ls.index]
             flags = dtype_code(lf.out_dtype) | (lf.group << 8) | (lf.cls << 24)
             lsum.add({**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags},
                      int(lib.odp_linear_sum_blocks(d_in, d_out)),
                      valid * (d_in + d_out) * 2 + d_in * d_out * out.element_size(),
                      2 * valid * d_in * d_out)
-        lin_leaves = set(lin_form)
+        lin_leaves = {ls.w_leaf for ls in lins}
         if lin_leaves and self.second_moment:
             raise ValueError("second moments of full-weight linear sites are not computed natively")
 

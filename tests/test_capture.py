@@ -62,6 +62,11 @@ def _capture_per_example(eng, args, n):
                                 allow_unused=True)
     got = {paths[k]: g for k, g in zip(sorted(expanded), grads[1:])}
     for r in sess.sites:
+        if r.segments is not None:  # an MoE expert's slice of a stacked weight
+            k = obj_leaf[id(r.w_obj)]
+            pe = C._expert_per_example(r, leaves[k], n)
+            got[paths[k]] = got[paths[k]] + pe if paths[k] in got else pe
+            continue
         if r.w_obj is not None:
             found = C._site_per_example(r, None, None, leaves, obj_leaf[id(r.w_obj)])
         else:
@@ -260,4 +265,42 @@ def test_route_linears_reproduces_vmap_grad():
     eng = _engine(loss_fn)
     disc, sess, got, paths = _capture_per_example(eng, (train, ids, labels), n)
     assert len(disc.eligible) == 1
+    _check(ref, got)
+
+
+class _MoEBlock(torch.nn.Module):
+    """Pre-norm residual MoE block: softmax top-k router, stacked expert weights."""
+
+    def __init__(self, H=16, inter=8, E=4, K=2):
+        super().__init__()
+        self.k = K
+        self.norm = torch.nn.LayerNorm(H)
+        self.router = torch.nn.Linear(H, E, bias=False)
+        self.gate_up_proj = torch.nn.Parameter(torch.randn(E, 2 * inter, H) * H**-0.5)
+        self.down_proj = torch.nn.Parameter(torch.randn(E, H, inter) * inter**-0.5)
+
+    def forward(self, x):
+        h = self.norm(x)
+        w, idx = torch.topk(self.router(h).softmax(-1), self.k, dim=-1)
+        w = w / w.sum(-1, keepdim=True)
+        return x + capture.moe(h, self.gate_up_proj, self.down_proj, idx, w)
+
+
+def test_moe_experts_reproduce_vmap_grad():
+    torch.manual_seed(4)
+    m = _MoEBlock()
+    train = dict(m.named_parameters())  # experts captured; router and norm per-example by autograd
+
+    def loss_fn(params, x, y):
+        return ((torch.func.functional_call(m, params, (x,)) - y) ** 2).mean()
+
+    n, T = 3, 7
+    x, y = torch.randn(n, T, 16), torch.randn(n, T, 16)
+    ref = torch.func.vmap(torch.func.grad(loss_fn), in_dims=(None, 0, 0))(train, x, y)
+    eng = _engine(loss_fn)
+    disc, sess, got, paths = _capture_per_example(eng, (train, x, y), n)
+    assert {paths[k][0] for k in disc.eligible} == {"gate_up_proj", "down_proj"}
+    assert len(sess.sites) == 2 * 4 and all(r.segments is not None for r in sess.sites)
+    # Each expert's rows: one segment per example, lengths summing to the routed tokens.
+    assert sum(sum(r.segments.lengths) for r in sess.sites[::2]) == n * T * 2
     _check(ref, got)

@@ -90,3 +90,55 @@ def test_hf_llama_lora_matches_oracle(dtype, tol, autos):
         assert rel(got, ref) <= tol, (k, rel(got, ref))
     assert rel(gaux.grad_norms, aux["norms"]) <= tol
     assert rel(gaux.loss_values, aux["loss_values"]) <= tol
+
+
+class _MoEBlock(torch.nn.Module):
+    """Pre-norm residual MoE block (softmax top-2 router, stacked expert weights)."""
+
+    def __init__(self, H=64, inter=32, E=4, K=2):
+        super().__init__()
+        self.k = K
+        self.norm = torch.nn.LayerNorm(H)
+        self.router = torch.nn.Linear(H, E, bias=False)
+        self.gate_up_proj = torch.nn.Parameter(torch.randn(E, 2 * inter, H) * H**-0.5)
+        self.down_proj = torch.nn.Parameter(torch.randn(E, H, inter) * inter**-0.5)
+
+    def forward(self, x):
+        h = self.norm(x)
+        w, idx = torch.topk(self.router(h).float().softmax(-1), self.k, dim=-1)
+        w = (w / w.sum(-1, keepdim=True)).to(x.dtype)
+        return x + capture.moe(h, self.gate_up_proj, self.down_proj, idx, w)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_moe_block_matches_oracle(dtype, tol):
+    """Expert weights clipped per (example, expert) segment; router and norm by per-example autograd."""
+    print(f"moe block: dtype={dtype}", flush=True)
+    torch.manual_seed(3)
+    m_cpu = _MoEBlock().to(dtype)
+    m_gpu = copy.deepcopy(m_cpu).to(DEV)
+    train_cpu = dict(m_cpu.named_parameters())
+    train_gpu = dict(m_gpu.named_parameters())
+    n, T = 6, 24
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(n, T, 64, generator=g) * torch.logspace(-0.5, 0.5, n).view(n, 1, 1)).to(dtype)
+    y = torch.randn(n, T, 64, generator=g).to(dtype)
+
+    def loss_of(m):
+        def loss_fn(params, xb, yb):
+            return ((torch.func.functional_call(m, params, (xb,)).float() - yb.float()) ** 2).mean()
+        return loss_fn
+
+    _, aux0 = dp_ref.clipped_grad(loss_of(m_cpu), train_cpu, (x, y), clipping_norm=float("inf"))
+    C = float(aux0["norms"].detach().median())
+    fn, st = clipped_grad(loss_of(m_gpu), clipping_norm=C, batch_argnums=(1, 2), return_aux=True)
+    (grads, gaux), _ = fn(train_gpu, x.to(DEV), y.to(DEV), state=st)
+    torch.cuda.synchronize()
+    disc = fn.engine._discovery[1]
+    assert len(disc.eligible) == 2  # the two stacked expert weights went through the seam
+    summed, aux = dp_ref.clipped_grad(loss_of(m_cpu), train_cpu, (x, y), clipping_norm=C)
+    for k, ref in summed.items():
+        got = grads.pytree[k]
+        assert got.dtype == dtype and got.shape == ref.shape, k
+        assert rel(got, ref) <= tol, (k, rel(got, ref))
+    assert rel(gaux.grad_norms, aux["norms"]) <= tol
