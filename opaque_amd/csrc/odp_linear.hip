@@ -40,6 +40,7 @@ constexpr int LK = 64;       // tokens (outer forms) or features (Gram) per pipe
 
 #define ODP_GLOBAL __attribute__((address_space(1)))
 #define ODP_LDS __attribute__((address_space(3)))
+#define ODP_CONST __attribute__((address_space(4)))
 __device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) {
   return *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)p;
 }
@@ -189,10 +190,11 @@ __device__ __forceinline__ void outer_compute(const uint16_t* ta, const uint16_t
 }
 
 // One pipeline step: rows [t0, t0 + OK) clipped to its segment [tb, te).
+// Plain 32-bit fields (row counts stay below 2^31): a struct of mixed
+// widths and a bool was kept in memory by the compiler when copied
+// conditionally.
 struct Step {
-  int64_t t0, tb, te;
-  int seg;
-  bool live;
+  int32_t t0, tb, te, seg, live;
 };
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
@@ -236,6 +238,130 @@ __device__ __forceinline__ void outer_mainloop(const LinProblem& P, int64_t o0, 
     buf ^= 1;
     cur = nx;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Outer-product main loop, buffer loads straight into LDS.  The step's G and
+// X tiles (token-major rows, the XOR swizzle above) are fetched by
+// buffer_load ... lds into a ring of three LDS stages, two steps ahead of the
+// compute, with no staging registers; each step waits for its own loads
+// with an explicit vmcnt and an LDS-only barrier.  The buffer resources
+// cover only the rows of the step's segment, so rows outside it (and
+// columns past the matrix, sent past the end) arrive as zeros.  A step never
+// crosses a segment, so the clip factor is one scalar per step; it scales
+// X's fragments after the LDS read (c * x rounded to bf16, as staged
+// scaling would).
+// ---------------------------------------------------------------------------
+#ifndef ODP_LIN_DMA
+#define ODP_LIN_DMA 1
+#endif
+constexpr uint32_t LIN_BUF_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA buffer resource)
+constexpr uint32_t LIN_OOB = 0x80000000u;        // an offset past every buffer's end
+constexpr int A_DMA = A_TILE * 2 / 1024 / 4;      // 1 KB loads per wave per step (G tile)
+constexpr int B_DMA = B_TILE * 2 / 1024 / 4;      // (X tile)
+constexpr int DMA_PER_STEP = A_DMA + B_DMA;
+static_assert(OM * 2 == 512 && ON * 2 == 256, "ring loads assume 2 G rows / 4 X rows per 1 KB");
+static_assert(DMA_PER_STEP < 16, "the step wait encodes vmcnt in 4 bits");
+
+// Column-major over the wave's blocks: X fragment j + 1 is scaled (VALU)
+// while the MFMAs of fragment j run, instead of all scaling up front.
+__device__ __forceinline__ void outer_compute_scaled(const uint16_t* ta, const uint16_t* tb, float c,
+                                                     OuterAcc& acc) {
+  const int wave = threadIdx.x >> 6;
+  const int wm = WM * (wave & 1), wn = WN * (wave >> 1);
+  bf16x8_t a[BI], b[BJ];
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) b[j] = outer_frag(tb, ON, wn + 16 * j);
+#pragma unroll
+  for (int i = 0; i < BI; ++i) a[i] = outer_frag(ta, OM, wm + 16 * i);
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    const bf16x8_t bs = __builtin_bit_cast(bf16x8_t, scale_bf16x8(__builtin_bit_cast(u32x4_t, b[j]), c));
+#pragma unroll
+    for (int i = 0; i < BI; ++i)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bs, acc[i][j], 0, 0, 0);
+  }
+}
+
+template <bool SCALE, typename Next, typename Scale>
+__device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step first,
+                                             Next next, Scale scale, OuterAcc& acc) {
+  // One array per ring stage, so that reads of one stage are not made to
+  // wait for the loads into the others.
+  __shared__ __attribute__((aligned(16))) uint16_t ring0[OUTER_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t ring1[OUTER_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t ring2[OUTER_STAGE];
+  auto stage = [&](int k) -> uint16_t* { return k == 0 ? ring0 : k == 1 ? ring1 : ring2; };
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Per lane: tile row and column of each of its loads (row within the
+  // step, column within the tile after undoing the swizzle).
+  int arow[A_DMA], acol[A_DMA], brow[B_DMA], bcol[B_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    arow[i] = 8 * wave + 2 * i + (lane >> 5);
+    acol[i] = 8 * ((lane & 31) ^ (swz(arow[i]) >> 1));
+  }
+#pragma unroll
+  for (int i = 0; i < B_DMA; ++i) {
+    brow[i] = 8 * wave + 4 * i + (lane >> 4);
+    bcol[i] = 8 * ((lane & 15) ^ (swz(brow[i]) >> 1));
+  }
+  const int32_t dout = (int32_t)P.d_out, din = (int32_t)P.d_in;
+  const uint32_t ldg = (uint32_t)P.ldg, ldx = (uint32_t)P.ldx;
+
+  auto issue = [&](uint16_t* st, const Step& x) {
+    const uint32_t rows = x.live ? (uint32_t)(x.te - x.tb) : 0u;
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.G + x.tb * P.ldg), (short)0, (int)(rows * ldg * 2u), LIN_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.X + x.tb * P.ldx), (short)0, (int)(rows * ldx * 2u), LIN_BUF_DWORD3);
+    const uint32_t r0 = (uint32_t)(x.t0 - x.tb);
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      const int32_t col = (int32_t)o0 + acol[i];
+      const uint32_t off = col < dout ? ((r0 + arow[i]) * ldg + (uint32_t)col) * 2u : LIN_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (ODP_LDS void*)(st + (8 * wave + 2 * i) * OM), 16, off, 0,
+                                               0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const int32_t col = (int32_t)n0 + bcol[i];
+      const uint32_t off = col < din ? ((r0 + brow[i]) * ldx + (uint32_t)col) * 2u : LIN_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (ODP_LDS void*)(st + A_TILE + (8 * wave + 4 * i) * ON),
+                                               16, off, 0, 0, 0);
+    }
+  };
+
+  // Prologue: steps 0 and 1 in flight.  Steps past the last one still
+  // issue (zero rows, so out of range) to keep the wait counts constant.
+  Step cur = first;
+  Step ld = next(first);
+  float cs[3];
+  issue(ring0, cur);
+  cs[0] = SCALE && cur.live ? scale(cur) : 1.0f;
+  issue(ring1, ld);
+  cs[1] = SCALE && ld.live ? scale(ld) : 1.0f;
+  ld = next(ld);
+  while (cur.live) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      if (!cur.live) break;
+      __builtin_amdgcn_s_waitcnt(0x0F70 | DMA_PER_STEP);  // this step's loads; the next one may fly
+      __asm__ volatile("s_barrier" ::: "memory");
+      issue(stage((k + 2) % 3), ld);  // into the stage computed at the previous step
+      cs[(k + 2) % 3] = SCALE && ld.live ? scale(ld) : 1.0f;
+      ld = next(ld);
+      const uint16_t* st = stage(k);
+      if (SCALE)
+        outer_compute_scaled(st, st + A_TILE, cs[k], acc);
+      else
+        outer_compute(st, st + A_TILE, acc);
+      cur = next(cur);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
+  __asm__ volatile("s_barrier" ::: "memory");
 }
 
 template <int I, int J>
@@ -305,7 +431,9 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64
                                                         const int32_t* __restrict__ slen,
                                                         const int32_t* __restrict__ sex,
                                                         double* __restrict__ part, int64_t part_stride) {
+#if !ODP_LIN_DMA
   __shared__ __attribute__((aligned(16))) uint16_t lds[OUTER_LDS];
+#endif
   __shared__ double red[4];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -324,14 +452,18 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64
 
   OuterAcc acc;
   zero_acc(acc);
-  const Step first = {t_begin, t_begin, t_end, seg, t_end > t_begin};
+  const Step first = {(int32_t)t_begin, (int32_t)t_begin, (int32_t)t_end, seg, t_end > t_begin ? 1 : 0};
   auto next = [&](const Step& st) {
     Step n = st;
     n.t0 = st.t0 + OK;
-    n.live = n.t0 < st.te;
+    n.live = n.t0 < st.te ? 1 : 0;
     return n;
   };
+#if ODP_LIN_DMA
+  dma_mainloop<false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, acc);
+#else
   outer_mainloop<false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, lds, acc);
+#endif
   // Columns/rows past the matrix were zero operands, so they add nothing.
   const double tot = block_sum(acc_sq(acc), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
@@ -494,7 +626,9 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
                                                       const int32_t* __restrict__ sex,
                                                       const float* __restrict__ scales, int n_ex,
                                                       int n_groups, float normalize_by) {
+#if !ODP_LIN_DMA
   __shared__ __attribute__((aligned(16))) uint16_t lds[OUTER_LDS];
+#endif
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
@@ -515,26 +649,37 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
   zero_acc(acc);
 
   // Steps walk every live segment in order, OK rows at a time.
+  // Segment bounds through the scalar (constant) path: uniform loads that
+  // must not wait behind the vector loads in flight.
+  const ODP_CONST int32_t* cstart = (const ODP_CONST int32_t*)(sstart + P.seg_first);
+  const ODP_CONST int32_t* clen = (const ODP_CONST int32_t*)(slen + P.seg_first);
   auto at_segment = [&](int sg) {
-    while (sg < P.n_seg && slen[P.seg_first + sg] <= 0) ++sg;
+    while (sg < P.n_seg && clen[sg] <= 0) ++sg;
     Step st;
     st.seg = sg;
-    st.live = sg < P.n_seg;
-    st.tb = st.live ? (int64_t)sstart[P.seg_first + sg] : 0;
-    st.te = st.live ? st.tb + slen[P.seg_first + sg] : 0;
+    st.live = sg < P.n_seg ? 1 : 0;
+    st.tb = st.live ? cstart[sg] : 0;
+    st.te = st.live ? st.tb + clen[sg] : 0;
     st.t0 = st.tb;
     return st;
   };
+  // Also valid on a finished step (which stays finished).
   auto next = [&](const Step& st) {
     if (st.t0 + OK < st.te) {
       Step n = st;
       n.t0 = st.t0 + OK;
       return n;
     }
-    return at_segment(st.seg + 1);
+    return at_segment(st.seg + 1 < P.n_seg ? st.seg + 1 : P.n_seg);
   };
-  auto scale = [&](const Step& st) { return sc[sex[P.seg_first + st.seg]]; };
+  const ODP_CONST int32_t* cex = (const ODP_CONST int32_t*)(sex + P.seg_first);
+  const ODP_CONST float* csc = (const ODP_CONST float*)sc;
+  auto scale = [&](const Step& st) { return csc[cex[st.seg]]; };
+#if ODP_LIN_DMA
+  dma_mainloop<true>(P, o0, n0, at_segment(0), next, scale, acc);
+#else
   outer_mainloop<true>(P, o0, n0, at_segment(0), next, scale, lds, acc);
+#endif
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
