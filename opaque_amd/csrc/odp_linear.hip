@@ -9,21 +9,23 @@
 //   k_lin_outer_norm : ||M_i||_F^2 tile by tile (256 x 128 output tiles,
 //                      contraction over the example's tokens), squares
 //                      summed in fp64 into one partial slot per tile;
-//   k_lin_gram_norm  : sum_{t,s} (x_t . x_s)(g_t . g_s) over 128 x 128 token
-//                      tiles of the upper triangle (off-diagonal tiles
-//                      counted twice), the cheaper form when the example is
-//                      short relative to the weight;
+//   k_lin_gram_norm  : sum_{t,s} (x_t . x_s)(g_t . g_s) over the upper
+//                      triangle of 128-token blocks (off-diagonal blocks
+//                      counted twice), one block against two per workgroup,
+//                      the cheaper form when the example is short relative
+//                      to the weight;
 //   k_lin_clip_sum   : out = sum_i c_i M_i as one GEMM over all rows, the
-//                      clip factor applied to each example's X rows as they
-//                      are staged (c_i x_t rounded to bf16).
+//                      clip factor applied to each example's X fragments
+//                      (c_i x_t rounded to bf16).
 //
-// All three are bf16 MFMA (16x16x32, fp32 accumulate) with 4 waves per
-// workgroup (256 x 128 output tiles for the outer forms, 128 x 128 token
-// tiles for the Gram form), operands staged through LDS with one pipeline
-// step of global loads in flight.
-// Rows are token-major in HBM, so the outer-product forms read their
-// operands K-major and take them from LDS with the gfx950 transposing read;
-// the Gram form's operands are K-contiguous rows.
+// All three are bf16 MFMA (16x16x32, fp32 accumulate).  Operand tiles move
+// from HBM to LDS by buffer loads straight into LDS (no staging registers)
+// through rings of LDS stages, several steps ahead of the compute, with
+// explicit vmcnt waits and LDS-only barriers; buffer resources bounded to
+// the current segment's rows turn rows outside it into zeros.  Rows are
+// token-major in HBM, so the outer-product forms read their operands K-major
+// and take them from LDS with the gfx950 transposing read; the Gram form's
+// operands are K-contiguous rows.
 #include "odp_internal.h"
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -35,15 +37,11 @@ namespace {
 #ifndef ODP_LIN_OCC
 #define ODP_LIN_OCC 2  // waves per SIMD the outer-product kernels are compiled for
 #endif
-constexpr int LT = 128;      // output tile edge (rows and columns)
-constexpr int LK = 64;       // tokens (outer forms) or features (Gram) per pipeline step
+constexpr int LT = 128;      // token block of the Gram form
 
 #define ODP_GLOBAL __attribute__((address_space(1)))
 #define ODP_LDS __attribute__((address_space(3)))
 #define ODP_CONST __attribute__((address_space(4)))
-__device__ __forceinline__ u32x4_t ldg16(const uint16_t* p) {
-  return *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)p;
-}
 __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((ODP_LDS v4i16_t*)(ODP_LDS void*)p);
 }
@@ -85,45 +83,9 @@ __device__ __forceinline__ LinProblem read_problem(const int64_t* f) {
 #endif
 constexpr int OM = ODP_LIN_OM, ON = ODP_LIN_ON, OK = 32;
 constexpr int WM = OM / 2, WN = ON / 2, BI = WM / 16, BJ = WN / 16;
-constexpr int A_PIECES = OK * OM / 8 / 256;  // 16-byte pieces per thread per step
-constexpr int B_PIECES = OK * ON / 8 / 256;
 constexpr int A_TILE = OK * OM, B_TILE = OK * ON;  // elements
 constexpr int OUTER_STAGE = A_TILE + B_TILE;
-constexpr int OUTER_LDS = 2 * OUTER_STAGE;
 
-struct OuterStage {
-  u32x4_t a[A_PIECES];  // G pieces
-  u32x4_t b[B_PIECES];  // X pieces
-};
-
-// Row and column arithmetic in 32 bits (the host keeps row counts and
-// pitches below 2^31); one 32 x 32 -> 64-bit multiply per piece.
-__device__ __forceinline__ const uint16_t* row_ptr(const uint16_t* base, int32_t t, int64_t ld,
-                                                   int32_t col) {
-  return base + ((uint64_t)(uint32_t)t * (uint32_t)ld + (uint32_t)col);
-}
-
-__device__ __forceinline__ void outer_load(const LinProblem& P, int64_t o0, int64_t n0, int64_t t0,
-                                           int64_t t_begin, int64_t t_end, OuterStage& S) {
-  const int tid = threadIdx.x;
-  const int32_t tb = (int32_t)t_begin, tl = (int32_t)t_end - 1, ts = (int32_t)t0;
-#pragma unroll
-  for (int q = 0; q < A_PIECES; ++q) {
-    const int id = tid + 256 * q;
-    int32_t t = ts + id / (OM / 8);
-    t = t < tb ? tb : (t > tl ? tl : t);
-    const int32_t co = (int32_t)o0 + 8 * (id % (OM / 8));
-    S.a[q] = ldg16(row_ptr(P.G, t, P.ldg, co < (int32_t)P.d_out ? co : (int32_t)P.d_out - 8));
-  }
-#pragma unroll
-  for (int q = 0; q < B_PIECES; ++q) {
-    const int id = tid + 256 * q;
-    int32_t t = ts + id / (ON / 8);
-    t = t < tb ? tb : (t > tl ? tl : t);
-    const int32_t cn = (int32_t)n0 + 8 * (id % (ON / 8));
-    S.b[q] = ldg16(row_ptr(P.X, t, P.ldx, cn < (int32_t)P.d_in ? cn : (int32_t)P.d_in - 8));
-  }
-}
 
 // Token-major tiles are unpadded and XOR-swizzled in 4-element (8-byte)
 // chunks: chunk k of row r lives at chunk k ^ swz(r).  The 16 rows x 4
@@ -132,28 +94,6 @@ __device__ __forceinline__ void outer_load(const LinProblem& P, int64_t o0, int6
 // (an aligned chunk pair) stays contiguous.
 __device__ __forceinline__ int swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 2; }
 
-__device__ __forceinline__ void outer_store(const LinProblem& P, int64_t o0, int64_t n0, int64_t t0,
-                                            int64_t t_begin, int64_t t_end, const OuterStage& S,
-                                            uint16_t* ta, uint16_t* tb) {
-  const int tid = threadIdx.x;
-  const u32x4_t z = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int q = 0; q < A_PIECES; ++q) {
-    const int id = tid + 256 * q;
-    const int row = id / (OM / 8), c = 8 * (id % (OM / 8));
-    const int64_t t = t0 + row;
-    const bool ok = t >= t_begin && t < t_end && o0 + c < P.d_out;
-    *(u32x4_t*)&ta[row * OM + 4 * ((c >> 2) ^ swz(row))] = ok ? S.a[q] : z;
-  }
-#pragma unroll
-  for (int q = 0; q < B_PIECES; ++q) {
-    const int id = tid + 256 * q;
-    const int row = id / (ON / 8), c = 8 * (id % (ON / 8));
-    const int64_t t = t0 + row;
-    const bool ok = t >= t_begin && t < t_end && n0 + c < P.d_in;
-    *(u32x4_t*)&tb[row * ON + 4 * ((c >> 2) ^ swz(row))] = ok ? S.b[q] : z;
-  }
-}
 
 // 16 columns col0.. of a token-major tile of row pitch `pitch`, tokens
 // 8 (lane >> 4) + 0..7: the MFMA operand layout (lane & 15 = row of A /
@@ -207,38 +147,6 @@ __device__ __forceinline__ u32x4_t scale_bf16x8(u32x4_t v, float c) {
   return __builtin_bit_cast(u32x4_t, __builtin_convertvector(f, bf16x8_t));
 }
 
-// acc += sum over the steps first, next(first), ... of G^T X on the
-// workgroup's tile; `scale(step)` multiplies X's rows of a step as they are
-// staged (SCALE only; X's tile is the narrower one).
-template <bool SCALE, typename Next, typename Scale>
-__device__ __forceinline__ void outer_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step cur,
-                                               Next next, Scale scale, uint16_t* lds, OuterAcc& acc) {
-  OuterStage S;
-  auto stage = [&](const Step& st, int buf) {
-    if (SCALE) {
-      const float c = scale(st);
-#pragma unroll
-      for (int q = 0; q < B_PIECES; ++q) S.b[q] = scale_bf16x8(S.b[q], c);
-    }
-    outer_store(P, o0, n0, st.t0, st.tb, st.te, S, lds + buf * OUTER_STAGE,
-                lds + buf * OUTER_STAGE + A_TILE);
-  };
-  if (cur.live) {
-    outer_load(P, o0, n0, cur.t0, cur.tb, cur.te, S);
-    stage(cur, 0);
-  }
-  __syncthreads();
-  int buf = 0;
-  while (cur.live) {
-    const Step nx = next(cur);
-    if (nx.live) outer_load(P, o0, n0, nx.t0, nx.tb, nx.te, S);
-    outer_compute(lds + buf * OUTER_STAGE, lds + buf * OUTER_STAGE + A_TILE, acc);
-    if (nx.live) stage(nx, buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    cur = nx;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Outer-product main loop, buffer loads straight into LDS.  The step's G and
@@ -252,9 +160,6 @@ __device__ __forceinline__ void outer_mainloop(const LinProblem& P, int64_t o0, 
 // X's fragments after the LDS read (c * x rounded to bf16, as staged
 // scaling would).
 // ---------------------------------------------------------------------------
-#ifndef ODP_LIN_DMA
-#define ODP_LIN_DMA 1
-#endif
 constexpr uint32_t LIN_BUF_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA buffer resource)
 constexpr uint32_t LIN_OOB = 0x80000000u;        // an offset past every buffer's end
 constexpr int A_DMA = A_TILE * 2 / 1024 / 4;      // 1 KB loads per wave per step (G tile)
@@ -431,9 +336,6 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64
                                                         const int32_t* __restrict__ slen,
                                                         const int32_t* __restrict__ sex,
                                                         double* __restrict__ part, int64_t part_stride) {
-#if !ODP_LIN_DMA
-  __shared__ __attribute__((aligned(16))) uint16_t lds[OUTER_LDS];
-#endif
   __shared__ double red[4];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -459,148 +361,178 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64
     n.live = n.t0 < st.te ? 1 : 0;
     return n;
   };
-#if ODP_LIN_DMA
   dma_mainloop<false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, acc);
-#else
-  outer_mainloop<false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, lds, acc);
-#endif
   // Columns/rows past the matrix were zero operands, so they add nothing.
   const double tot = block_sum(acc_sq(acc), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
 }
 
 // ---------------------------------------------------------------------------
-// ||M_i||^2 partials, Gram form.  Workgroup = (segment, token-tile pair
-// tb <= sb).  Sx = X_tb X_sb^T over d_in and Sg = G_tb G_sb^T over d_out
-// (operands are K-contiguous rows), then sum Sx * Sg.
+// ||M_i||^2 partials, token-Gram form, wide tiles.  A workgroup of 8 waves
+// covers token block tb (128 rows) against blocks sb0 and sb0 + 1 (256
+// rows) of one segment, with both Gram products in registers: waves 0-3
+// own (tb, sb0), waves 4-7 (tb, sb0 + 1), each a 64 x 64 block of
+// sum_f x_t,f x_s,f (features of X) and of sum_f g_t,f g_s,f (features of
+// G).  The 384 rows x 32 features of a step arrive by buffer loads straight
+// into a ring of GR_RING LDS stages (GR_RING - 1 steps in flight), the X
+// steps then the G steps as one sequence.  Rows past the segment and
+// features past d arrive as zeros.  Rows are 64 bytes; the 16-byte slot k
+// of row r sits at k ^ ((r >> 2) & 3), so a fragment read (16 rows, one
+// slot) touches every LDS bank once.
 // ---------------------------------------------------------------------------
-// Feature-major tiles [128 rows][LK] are unpadded; the 16-byte chunk q of
-// row r lives at chunk q ^ (r & 7).
-constexpr int GRAM_TILE = LT * LK;
-constexpr int GRAM_LDS = 2 * 2 * GRAM_TILE;  // two stages x (t rows, s rows)
+constexpr int GR_K = 32;                   // features per step
+constexpr int GR_ROWS = 3 * LT;            // t block + two s blocks
+constexpr int GR_STAGE = GR_ROWS * GR_K;   // elements
+constexpr int GR_RING = 6;
+constexpr int GR_LOADS = GR_ROWS * GR_K * 2 / 1024 / 8;  // 1 KB loads per wave per step
+static_assert(GR_LOADS == 3, "three loads per wave per step");
 
-__device__ __forceinline__ int gram_at(int row, int k) { return row * LK + 8 * ((k >> 3) ^ (row & 7)); }
-
-struct GramStage {
-  u32x4_t a[4];
-  u32x4_t b[4];
-};
-
-__device__ __forceinline__ void gram_load(const uint16_t* M, int64_t ld, int64_t d, int64_t ta0,
-                                          int64_t sb0, int64_t t_end, int64_t k0, GramStage& S) {
-  const int tid = threadIdx.x;
-  const int32_t tl = (int32_t)t_end - 1, d8 = (int32_t)d - 8;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int id = tid + 256 * q;  // 1024 pieces: 128 rows x 8 pieces of 8
-    const int row = id >> 3;
-    const int32_t k = (int32_t)k0 + 8 * (id & 7);
-    const int32_t kc = k < (int32_t)d ? k : d8;
-    int32_t ra = (int32_t)ta0 + row, rb = (int32_t)sb0 + row;
-    ra = ra < tl ? ra : tl;
-    rb = rb < tl ? rb : tl;
-    S.a[q] = ldg16(row_ptr(M, ra, ld, kc));
-    S.b[q] = ldg16(row_ptr(M, rb, ld, kc));
-  }
+// Work items of a segment with nb blocks: for each tb, s-block pairs
+// sb0 = tb, tb + 2, ... (the second block may lie past the segment).
+__host__ __device__ constexpr int64_t gram_items(int64_t nb) {
+  return (nb & 1) ? ((nb + 1) / 2) * ((nb + 1) / 2) : (nb / 2) * (nb / 2 + 1);
 }
 
-__device__ __forceinline__ void gram_store(int64_t d, int64_t ta0, int64_t sb0, int64_t t_end,
-                                           int64_t k0, const GramStage& S, uint16_t* la,
-                                           uint16_t* lb) {
-  const int tid = threadIdx.x;
-  const u32x4_t z = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int id = tid + 256 * q;
-    const int row = id >> 3, c = 8 * (id & 7);
-    const bool kin = k0 + c < d;
-    *(u32x4_t*)&la[gram_at(row, c)] = (kin && ta0 + row < t_end) ? S.a[q] : z;
-    *(u32x4_t*)&lb[gram_at(row, c)] = (kin && sb0 + row < t_end) ? S.b[q] : z;
-  }
+__device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ ((row >> 2) & 3)); }
+
+__host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
+  return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
 }
 
-__device__ __forceinline__ void gram_compute(const uint16_t* la, const uint16_t* lb,
-                                             f32x4_t (&acc)[4][4]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = 64 * (wave & 1), wn = 64 * (wave >> 1);
-  const int r = lane & 15, kq = 8 * (lane >> 4);
-#pragma unroll
-  for (int u = 0; u < LK / 32; ++u) {
-    bf16x8_t a[4], b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      a[i] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&la[gram_at(wm + 16 * i + r, 32 * u + kq)]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&lb[gram_at(wn + 16 * j + r, 32 * u + kq)]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-  }
-}
-
-// acc += (rows ta0.. of M)(rows sb0.. of M)^T over the d features of M.
-__device__ __forceinline__ void gram_pass(const uint16_t* M, int64_t ld, int64_t d, int64_t ta0,
-                                          int64_t sb0, int64_t t_end, uint16_t* lds,
-                                          f32x4_t (&acc)[4][4]) {
-  const int64_t nsteps = (d + LK - 1) / LK;
-  GramStage S;
-  gram_load(M, ld, d, ta0, sb0, t_end, 0, S);
-  gram_store(d, ta0, sb0, t_end, 0, S, lds, lds + GRAM_TILE);
-  __syncthreads();
-  for (int64_t s = 0; s < nsteps; ++s) {
-    const int b = (int)(s & 1);
-    const bool more = s + 1 < nsteps;
-    const int64_t k1 = (s + 1) * LK;
-    if (more) gram_load(M, ld, d, ta0, sb0, t_end, k1, S);
-    gram_compute(lds + b * 2 * GRAM_TILE, lds + b * 2 * GRAM_TILE + GRAM_TILE, acc);
-    if (more) gram_store(d, ta0, sb0, t_end, k1, S, lds + (b ^ 1) * 2 * GRAM_TILE,
-                         lds + (b ^ 1) * 2 * GRAM_TILE + GRAM_TILE);
-    __syncthreads();
-  }
-}
-
-__global__ __launch_bounds__(256) void k_lin_gram_norm(const int64_t* __restrict__ probs,
-                                                       const int32_t* __restrict__ ws, int n_prob,
-                                                       const int32_t* __restrict__ sstart,
-                                                       const int32_t* __restrict__ slen,
-                                                       const int32_t* __restrict__ sex,
-                                                       double* __restrict__ part, int64_t part_stride) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[GRAM_LDS];
-  __shared__ double red[4];
+__global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restrict__ probs,
+                                                             const int32_t* __restrict__ ws, int n_prob,
+                                                             const int32_t* __restrict__ sstart,
+                                                             const int32_t* __restrict__ slen,
+                                                             const int32_t* __restrict__ sex,
+                                                             double* __restrict__ part, int64_t part_stride) {
+  __shared__ __attribute__((aligned(16))) uint16_t st0[GR_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st1[GR_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st2[GR_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st3[GR_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st4[GR_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st5[GR_STAGE];
+  __shared__ double red[8];
+  auto stage = [&](int k) -> uint16_t* {
+    return k == 0 ? st0 : k == 1 ? st1 : k == 2 ? st2 : k == 3 ? st3 : k == 4 ? st4 : st5;
+  };
+  static_assert(GR_RING == 6, "six ring stages");
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
   const LinProblem P = read_problem(f);
   const int64_t slot = f[ODP_LN_SLOT];
   const int nb = (int)f[ODP_LN_NB];
-  const int pairs = nb * (nb + 1) / 2;
-  int seg, pair;
-  if (!seg_item<true>(bid - ws[p], P.n_seg, pairs, seg, pair)) return;
-  // pair -> (tb, sb), tb <= sb, row-major over the upper triangle.
-  int tb = 0, rem = pair;
-  while (rem >= nb - tb) {
-    rem -= nb - tb;
+  const int items = (int)gram_items(nb);
+  int seg, item;
+  if (!seg_item<true>(bid - ws[p], P.n_seg, items, seg, item)) return;
+  int tb = 0, rem = item;
+  while (rem >= (nb - tb + 1) / 2) {
+    rem -= (nb - tb + 1) / 2;
     ++tb;
   }
-  const int sb = tb + rem;
+  const int sb0 = tb + 2 * rem;
   const int gs = P.seg_first + seg;
-  const int64_t t_begin = sstart[gs], t_end = t_begin + slen[gs];
+  const int32_t t_begin = sstart[gs], len = slen[gs];
   const int ex = sex[gs];
-  const int64_t ta0 = t_begin + (int64_t)tb * LT, sb0 = t_begin + (int64_t)sb * LT;
-  double* dst = part + (int64_t)ex * part_stride + slot + pair;
-  if (sb0 >= t_end) {  // tile past this segment's length
+  double* dst = part + (int64_t)ex * part_stride + slot + item;
+  if ((int64_t)sb0 * LT >= len) {  // item past this segment's length
     if (threadIdx.x == 0) *dst = 0.0;
     return;
   }
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // Rows of the stage: 0..127 block tb, 128..255 block sb0, 256..383 sb0 + 1.
+  // Wave w loads stage rows 48 w .. + 47, 16 per load; lane l lands in row
+  // 16 i' + (l >> 2), physical slot l & 3, and fetches its logical slot.
+  int lrow[GR_LOADS];
+  uint32_t lbase[GR_LOADS];  // segment row of the loaded row, times the row pitch later
+  int lslot[GR_LOADS];
+#pragma unroll
+  for (int i = 0; i < GR_LOADS; ++i) {
+    const int row = 48 * wave + 16 * i + (lane >> 2);
+    lrow[i] = row;
+    const int blk = row < LT ? tb : (row < 2 * LT ? sb0 : sb0 + 1);
+    lbase[i] = (uint32_t)(blk * LT + (row & (LT - 1)));
+    lslot[i] = (lane & 3) ^ ((row >> 2) & 3);
+  }
+  const uint32_t nrow = (uint32_t)len;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(P.X + (int64_t)t_begin * P.ldx), (short)0, (int)(nrow * (uint32_t)P.ldx * 2u), LIN_BUF_DWORD3);
+  const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(P.G + (int64_t)t_begin * P.ldg), (short)0, (int)(nrow * (uint32_t)P.ldg * 2u), LIN_BUF_DWORD3);
+  // X steps then G steps, each phase padded to a multiple of the ring size
+  // (the padding steps load nothing) so that every step's stage is fixed.
+  const int nx = (int)((P.d_in + GR_K - 1) / GR_K), ng = (int)((P.d_out + GR_K - 1) / GR_K);
+  const int px = (nx + GR_RING - 1) / GR_RING * GR_RING;
+  const int total = px + (ng + GR_RING - 1) / GR_RING * GR_RING;
+  const uint32_t ldx = (uint32_t)P.ldx, ldg = (uint32_t)P.ldg;
+  const int32_t din = (int32_t)P.d_in, dout = (int32_t)P.d_out;
+
+  // Step x: features [GR_K x', + GR_K) of X (x' = x) or of G (x' = x - nx);
+  // steps past the end load nothing (out of range) but still issue.
+  auto issue = [&](uint16_t* st, int x) {
+    const bool isx = x < px;
+    const int32_t kx = isx ? x : x - px;
+    const int32_t k0 = kx * GR_K;
+    const int32_t d = isx ? din : dout;
+    const uint32_t ld = isx ? ldx : ldg;
+    const bool live = x < total && kx < (isx ? nx : ng);
+#pragma unroll
+    for (int i = 0; i < GR_LOADS; ++i) {
+      const int32_t col = k0 + 8 * lslot[i];
+      const uint32_t off = live && col < d ? (lbase[i] * ld + (uint32_t)col) * 2u : LIN_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isx ? xr : gr,
+                                               (ODP_LDS void*)(st + (48 * wave + 16 * i) * GR_K), 16, off, 0,
+                                               0, 0);
+    }
+  };
+
+  // Wave w: t rows 64 (w & 1) .., s rows 128 + 64 (w >> 1) .. of the stage.
+  const int wt = 64 * (wave & 1), wsr = LT + 64 * (wave >> 1);
   f32x4_t sx[4][4], sg[4][4];
   zero_acc(sx);
   zero_acc(sg);
-  gram_pass(P.X, P.ldx, P.d_in, ta0, sb0, t_end, lds, sx);
-  gram_pass(P.G, P.ldg, P.d_out, ta0, sb0, t_end, lds, sg);
-  // Rows past the segment were zero operands, so their products vanish.
+  auto compute = [&](const uint16_t* st, f32x4_t (&acc)[4][4]) {
+    const int r = lane & 15, kq = lane >> 4;
+    bf16x8_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      a[i] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wt + 16 * i + r, kq)]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wsr + 16 * j + r, kq)]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
+
+  // One phase: steps [lo, hi) (a multiple of GR_RING), the first `live`
+  // of them holding features.
+  auto phase = [&](int lo, int hi, int live, f32x4_t (&acc)[4][4]) {
+    for (int g0 = lo; g0 < hi; g0 += GR_RING) {
+#pragma unroll
+      for (int k = 0; k < GR_RING; ++k) {
+        const int g = g0 + k;
+        // This step's loads have landed; the later GR_RING - 2 steps' may fly.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((GR_RING - 2) * GR_LOADS));
+        __asm__ volatile("s_barrier" ::: "memory");
+        issue(stage((k + GR_RING - 1) % GR_RING), g + GR_RING - 1);
+        if (g - lo < live) compute(stage(k), acc);
+      }
+    }
+  };
+#pragma unroll
+  for (int x = 0; x < GR_RING - 1; ++x) issue(stage(x), x);
+  phase(0, px, nx, sx);
+  phase(px, total, ng, sg);
+  __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
+
+  // Off-diagonal blocks count twice (the (s, t) block is not computed);
+  // a block past the segment holds zeros.
+  const int sb = sb0 + (wave >> 2);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -608,8 +540,17 @@ __global__ __launch_bounds__(256) void k_lin_gram_norm(const int64_t* __restrict
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) s += (double)sx[i][j][e] * (double)sg[i][j][e];
-  const double tot = block_sum(s, red);
-  if (threadIdx.x == 0) *dst = tb == sb ? tot : 2.0 * tot;
+  if (sb != tb) s *= 2.0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) t += red[w];
+    *dst = t;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -626,9 +567,6 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
                                                       const int32_t* __restrict__ sex,
                                                       const float* __restrict__ scales, int n_ex,
                                                       int n_groups, float normalize_by) {
-#if !ODP_LIN_DMA
-  __shared__ __attribute__((aligned(16))) uint16_t lds[OUTER_LDS];
-#endif
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
@@ -675,11 +613,7 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
   const ODP_CONST int32_t* cex = (const ODP_CONST int32_t*)(sex + P.seg_first);
   const ODP_CONST float* csc = (const ODP_CONST float*)sc;
   auto scale = [&](const Step& st) { return csc[cex[st.seg]]; };
-#if ODP_LIN_DMA
   dma_mainloop<true>(P, o0, n0, at_segment(0), next, scale, acc);
-#else
-  outer_mainloop<true>(P, o0, n0, at_segment(0), next, scale, lds, acc);
-#endif
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -710,7 +644,7 @@ extern "C" int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64
   if (d_in <= 0 || d_out <= 0) return 0;
   if (form == ODP_FORM_GRAM) {
     const int64_t nb = max_seg_len > 0 ? (max_seg_len + LT - 1) / LT : 0;
-    return nb * (nb + 1) / 2;
+    return gram_items(nb);
   }
   return ((d_out + OM - 1) / OM) * ((d_in + ON - 1) / ON);
 }
@@ -748,7 +682,7 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
   hipStream_t s = odp_hip_stream(stream);
   const dim3 grid(total_blocks), block(256);
   if (form == ODP_FORM_GRAM)
-    hipLaunchKernelGGL(k_lin_gram_norm, grid, block, 0, s, problems, work_start, n_prob,
+    hipLaunchKernelGGL(k_lin_gram_norm, grid, dim3(512), 0, s, problems, work_start, n_prob,
                        seg_row_start, seg_row_len, seg_example, part, part_stride);
   else
     hipLaunchKernelGGL(k_lin_outer_norm, grid, block, 0, s, problems, work_start, n_prob,

@@ -599,7 +599,6 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   constexpr int NJ = FP_MT / 64, PP = FP_MT;  // unpadded, XOR-swizzled G rows
   constexpr int QP = FP_T + 8, QROWS = 16;
   constexpr int PTILE = FP_T * PP, STAGE = PTILE + 2 * QROWS * QP;
-  constexpr int NPP = FP_T * FP_MT / 8 / 256;  // G pieces per thread per step
   constexpr int QPC = FP_T / 8;                // V pieces per row per step
   static_assert(2 * QPC * QROWS == 256, "one V piece per thread");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
