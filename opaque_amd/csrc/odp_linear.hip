@@ -188,6 +188,21 @@ __device__ __forceinline__ void outer_compute_scaled(const uint16_t* ta, const u
   }
 }
 
+// One ring step: loads into stage `nxt`, then the MFMAs from stage `cur`.
+// Both pointers are restrict parameters of one inlined call, which gives
+// the compiler the alias scopes that keep the reads of `cur` from waiting
+// for the loads into `nxt` (without them every LDS read waits for all
+// loads into LDS in flight).
+template <bool SCALE, typename Issue>
+__device__ __forceinline__ void ring_step(uint16_t* __restrict__ nxt, const uint16_t* __restrict__ cur,
+                                          Issue issue, float c, OuterAcc& acc) {
+  issue(nxt);
+  if (SCALE)
+    outer_compute_scaled(cur, cur + A_TILE, c, acc);
+  else
+    outer_compute(cur, cur + A_TILE, acc);
+}
+
 template <bool SCALE, typename Next, typename Scale>
 __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step first,
                                              Next next, Scale scale, OuterAcc& acc) {
@@ -254,14 +269,11 @@ __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, in
       if (!cur.live) break;
       __builtin_amdgcn_s_waitcnt(0x0F70 | DMA_PER_STEP);  // this step's loads; the next one may fly
       __asm__ volatile("s_barrier" ::: "memory");
-      issue(stage((k + 2) % 3), ld);  // into the stage computed at the previous step
+      // Loads of step ld go into the stage computed at the previous step.
+      const Step x = ld;
+      ring_step<SCALE>(stage((k + 2) % 3), stage(k), [&](uint16_t* st) { issue(st, x); }, cs[k], acc);
       cs[(k + 2) % 3] = SCALE && ld.live ? scale(ld) : 1.0f;
       ld = next(ld);
-      const uint16_t* st = stage(k);
-      if (SCALE)
-        outer_compute_scaled(st, st + A_TILE, cs[k], acc);
-      else
-        outer_compute(st, st + A_TILE, acc);
       cur = next(cur);
     }
   }
@@ -377,8 +389,8 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64
 // into a ring of GR_RING LDS stages (GR_RING - 1 steps in flight), the X
 // steps then the G steps as one sequence.  Rows past the segment and
 // features past d arrive as zeros.  Rows are 64 bytes; the 16-byte slot k
-// of row r sits at k ^ ((r >> 2) & 3), so a fragment read (16 rows, one
-// slot) touches every LDS bank once.
+// of row r sits at k ^ ((r >> 2) & 3), which spreads the 16 rows of a
+// fragment read over the LDS banks.
 // ---------------------------------------------------------------------------
 constexpr int GR_K = 32;                   // features per step
 constexpr int GR_ROWS = 3 * LT;            // t block + two s blocks
@@ -393,7 +405,8 @@ __host__ __device__ constexpr int64_t gram_items(int64_t nb) {
   return (nb & 1) ? ((nb + 1) / 2) * ((nb + 1) / 2) : (nb / 2) * (nb / 2 + 1);
 }
 
-__device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ ((row >> 2) & 3)); }
+__device__ __forceinline__ int gr_swz(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ gr_swz(row)); }
 
 __host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
   return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
@@ -454,7 +467,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
     lrow[i] = row;
     const int blk = row < LT ? tb : (row < 2 * LT ? sb0 : sb0 + 1);
     lbase[i] = (uint32_t)(blk * LT + (row & (LT - 1)));
-    lslot[i] = (lane & 3) ^ ((row >> 2) & 3);
+    lslot[i] = (lane & 3) ^ gr_swz(row);
   }
   const uint32_t nrow = (uint32_t)len;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -475,15 +488,16 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
     const bool isx = x < px;
     const int32_t kx = isx ? x : x - px;
     const int32_t k0 = kx * GR_K;
-    const int32_t d = isx ? din : dout;
+    // A finished phase (or step) gets d = 0: every column is then past the end.
+    const int32_t d = x < total && kx < (isx ? nx : ng) ? (isx ? din : dout) : 0;
     const uint32_t ld = isx ? ldx : ldg;
-    const bool live = x < total && kx < (isx ? nx : ng);
+    const __amdgpu_buffer_rsrc_t rs = isx ? xr : gr;
 #pragma unroll
     for (int i = 0; i < GR_LOADS; ++i) {
       const int32_t col = k0 + 8 * lslot[i];
-      const uint32_t off = live && col < d ? (lbase[i] * ld + (uint32_t)col) * 2u : LIN_OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(isx ? xr : gr,
-                                               (ODP_LDS void*)(st + (48 * wave + 16 * i) * GR_K), 16, off, 0,
+      const uint32_t o = (lbase[i] * ld + (uint32_t)col) * 2u;
+      const uint32_t off = col < d ? o : LIN_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (ODP_LDS void*)(st + (48 * wave + 16 * i) * GR_K), 16, off, 0,
                                                0, 0);
     }
   };
@@ -511,6 +525,14 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
 
   // One phase: steps [lo, hi) (a multiple of GR_RING), the first `live`
   // of them holding features.
+  // Loads into `nxt` and reads of `cur` as restrict parameters of one
+  // inlined call: the alias scopes keep the reads from waiting for the
+  // loads in flight.
+  auto step = [&](uint16_t* __restrict__ nxt, const uint16_t* __restrict__ cur, int x, bool live,
+                  f32x4_t (&acc)[4][4]) {
+    issue(nxt, x);
+    if (live) compute(cur, acc);
+  };
   auto phase = [&](int lo, int hi, int live, f32x4_t (&acc)[4][4]) {
     for (int g0 = lo; g0 < hi; g0 += GR_RING) {
 #pragma unroll
@@ -519,8 +541,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
         // This step's loads have landed; the later GR_RING - 2 steps' may fly.
         __builtin_amdgcn_s_waitcnt(vmcnt_imm((GR_RING - 2) * GR_LOADS));
         __asm__ volatile("s_barrier" ::: "memory");
-        issue(stage((k + GR_RING - 1) % GR_RING), g + GR_RING - 1);
-        if (g - lo < live) compute(stage(k), acc);
+        step(stage((k + GR_RING - 1) % GR_RING), stage(k), g + GR_RING - 1, g - lo < live, acc);
       }
     }
   };
