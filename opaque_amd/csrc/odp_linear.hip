@@ -203,7 +203,13 @@ __device__ __forceinline__ void ring_step(uint16_t* __restrict__ nxt, const uint
     outer_compute(cur, cur + A_TILE, acc);
 }
 
-template <bool SCALE, typename Next, typename Scale>
+// DEEP: the step's reads carry alias scopes (ring_step), so they do not
+// wait for the next stage's loads and two steps stay in flight.  Without
+// it the compiler makes the reads wait for all but the newest loads, about
+// one step ahead; the clipped sum, whose workgroups stream 32768 tokens
+// against operands shared with many other tiles, measured faster that way
+// (less cache pressure), the per-example norms slower.
+template <bool SCALE, bool DEEP, typename Next, typename Scale>
 __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step first,
                                              Next next, Scale scale, OuterAcc& acc) {
   // One array per ring stage, so that reads of one stage are not made to
@@ -271,7 +277,15 @@ __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, in
       __asm__ volatile("s_barrier" ::: "memory");
       // Loads of step ld go into the stage computed at the previous step.
       const Step x = ld;
-      ring_step<SCALE>(stage((k + 2) % 3), stage(k), [&](uint16_t* st) { issue(st, x); }, cs[k], acc);
+      if (DEEP) {
+        ring_step<SCALE>(stage((k + 2) % 3), stage(k), [&](uint16_t* st) { issue(st, x); }, cs[k], acc);
+      } else {
+        issue(stage((k + 2) % 3), x);
+        if (SCALE)
+          outer_compute_scaled(stage(k), stage(k) + A_TILE, cs[k], acc);
+        else
+          outer_compute(stage(k), stage(k) + A_TILE, acc);
+      }
       cs[(k + 2) % 3] = SCALE && ld.live ? scale(ld) : 1.0f;
       ld = next(ld);
       cur = next(cur);
@@ -373,7 +387,7 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64
     n.live = n.t0 < st.te ? 1 : 0;
     return n;
   };
-  dma_mainloop<false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, acc);
+  dma_mainloop<false, true>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, acc);
   // Columns/rows past the matrix were zero operands, so they add nothing.
   const double tot = block_sum(acc_sq(acc), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
@@ -634,7 +648,7 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
   const ODP_CONST int32_t* cex = (const ODP_CONST int32_t*)(sex + P.seg_first);
   const ODP_CONST float* csc = (const ODP_CONST float*)sc;
   auto scale = [&](const Step& st) { return csc[cex[st.seg]]; };
-  dma_mainloop<true>(P, o0, n0, at_segment(0), next, scale, acc);
+  dma_mainloop<true, false>(P, o0, n0, at_segment(0), next, scale, acc);
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
