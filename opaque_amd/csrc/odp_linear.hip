@@ -157,8 +157,7 @@ __device__ __forceinline__ u32x4_t scale_bf16x8(u32x4_t v, float c) {
 // cover only the rows of the step's segment, so rows outside it (and
 // columns past the matrix, sent past the end) arrive as zeros.  A step never
 // crosses a segment, so the clip factor is one scalar per step; it scales
-// X's fragments after the LDS read (c * x rounded to bf16, as staged
-// scaling would).
+// X's fragments after the LDS read (c * x rounded to bf16).
 // ---------------------------------------------------------------------------
 constexpr uint32_t LIN_BUF_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA buffer resource)
 constexpr uint32_t LIN_OOB = 0x80000000u;        // an offset past every buffer's end
@@ -591,8 +590,8 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
 // ---------------------------------------------------------------------------
 // Clipped sum.  Workgroup = (o-tile, n-tile) of one weight; the contraction
 // runs over every segment's rows in order, and a pipeline step never spans
-// two segments.  The G rows of a step are multiplied by their example's clip
-// factor (in fp32, rounded back to bf16) when the step is written to LDS,
+// two segments.  The X fragments of a step are multiplied by their
+// example's clip factor (in fp32, rounded back to bf16) after the LDS read,
 // so one accumulator holds sum_i c_i M_i.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t* __restrict__ probs,
