@@ -375,6 +375,10 @@ class GhostPlan:
                 raise ValueError("linear site row count does not match the segments")
             if not (supports_rows(ls.x) and supports_rows(ls.g)):
                 raise ValueError("linear site feature sizes must be multiples of 8")
+            # The kernels address one segment's rows through 32-bit buffer ranges.
+            ld = max(_rows(ls.x).stride(0), _rows(ls.g).stride(0))
+            if reg.view(ls.segments).max_len * ld * 2 >= 2**31:
+                raise ValueError("a linear site's longest segment spans 2 GiB or more of x or g")
             shape = tuple(self.leaves[ls.w_leaf].shape)
             want = (ls.g.shape[-1], ls.x.shape[-1])
             if ls.index is None and shape != want:
