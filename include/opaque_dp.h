@@ -119,8 +119,10 @@ enum {
   ODP_FT_SEG_FIRST = 6, ODP_FT_NSEG = 7,
   ODP_FT_SCALING = 8, /* double bit pattern                                  */
   ODP_FT_NLEAF = 9,   /* 1..4                                                */
-  ODP_FT_LEAF0 = 10,  /* per leaf l: [10+3l] pe address (f32 [n_seg][rank][M]),
-                         [11+3l] col0 | rank << 16, [12+3l] slot_base;
+  ODP_FT_LEAF0 = 10,  /* per leaf l: [10+3l] pe address ([n_seg][rank][M], f32,
+                         or bf16 when bit 32 of [11+3l] is set; norms always
+                         use the fp32 values), [11+3l] col0 | rank << 16 |
+                         pe_bf16 << 32, [12+3l] slot_base;
                          leaves sorted by col0                               */
   ODP_FT_QLO = 22,    /* lo plane of Q (bf16 only)                           */
   ODP_FT_FIELDS = 24

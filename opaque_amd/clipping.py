@@ -485,7 +485,7 @@ class _ClipEngine:
                          materialized=mats, linear_sites=list(lins), device=device,
                          second_moment=self.second_moment)
         res = plan.run()
-        if all_finite is not None and plan.pe.numel() > 1:
+        if all_finite is not None and plan.pe_views():
             all_finite = all_finite & _pe_finite(plan)
         # ||scaled gradient||: per group, scale * group norm (class 0 scale).
         cn2 = (res.scales[0] * res.group_norms).square().sum(0).sqrt()
@@ -758,7 +758,7 @@ class _ClipEngine:
 
 def _pe_finite(plan: GhostPlan) -> torch.Tensor:
     """Whether the stored per-example factor gradients are all finite."""
-    ok = torch.ones((), dtype=torch.bool, device=plan.pe.device)
+    ok = torch.ones((), dtype=torch.bool, device=plan.device)
     for view in plan.pe_views():
         ok = ok & torch.isfinite(view).all()
     return ok

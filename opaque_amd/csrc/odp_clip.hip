@@ -107,6 +107,7 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
   if (e0 >= E) return;
   const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
   const bool vec = pdt == ODP_DTYPE_F32 && (E & 3) == 0;
+  const bool vec16 = pdt == ODP_DTYPE_BF16 && (E & 3) == 0;
 
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   f32x4_t acc2 = {0.f, 0.f, 0.f, 0.f};
@@ -115,6 +116,12 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
     f32x4_t v;
     if (vec) {
       v = *(const f32x4_t*)(pe + (int64_t)s * E + e0);
+    } else if (vec16) {
+      const uint2 w = *(const uint2*)((const uint16_t*)pe + (int64_t)s * E + e0);
+      v[0] = __uint_as_float(w.x << 16);
+      v[1] = __uint_as_float(w.x & 0xffff0000u);
+      v[2] = __uint_as_float(w.y << 16);
+      v[3] = __uint_as_float(w.y & 0xffff0000u);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)

@@ -316,9 +316,10 @@ __global__ __launch_bounds__(256) void k_project_f32(const int64_t* __restrict__
 // 16-wide m blocks w*NJ .. w*NJ + NJ - 1 of the workgroup's M-tile.
 struct FactorLeaves {
   int n;
-  float* pe[4];
+  float* pe[4];  // f32 rows, or bf16 rows where pe16 is set
   int col0[4];
   int rank[4];
+  int pe16[4];
   int64_t slot[4];
 };
 
@@ -332,6 +333,7 @@ __device__ __forceinline__ FactorLeaves read_leaves(const int64_t* f) {
     L.pe[l] = on ? (float*)g[0] : nullptr;
     L.col0[l] = on ? (int)(g[1] & 0xffff) : 1 << 20;
     L.rank[l] = on ? (int)((g[1] >> 16) & 0xffff) : 0;
+    L.pe16[l] = on ? (int)((g[1] >> 32) & 1) : 0;
     L.slot[l] = on ? g[2] : 0;
   }
   return L;
@@ -355,23 +357,30 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
       // Leaf owning column k (leaves are sorted by col0); selected without
       // dynamic indexing so the descriptor stays in registers.
       float* lpe = L.pe[0];
-      int lc0 = L.col0[0], lrk = L.rank[0];
+      int lc0 = L.col0[0], lrk = L.rank[0], l16 = L.pe16[0];
 #pragma unroll
       for (int q = 1; q < 4; ++q)
         if (q < L.n && k >= L.col0[q]) {
           lpe = L.pe[q];
           lc0 = L.col0[q];
           lrk = L.rank[q];
+          l16 = L.pe16[q];
         }
       // Columns of frozen factors between leaves belong to no leaf.
       if (k < lc0 || k - lc0 >= lrk) continue;
-      float* dst = lpe + ((int64_t)seg * lrk + (k - lc0)) * M;
+      const int64_t row = ((int64_t)seg * lrk + (k - lc0)) * M;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int64_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
         if (m < M) {
           const float v = scale * acc[j][kb][i];
-          dst[m] = v;
+          // The stored copy (summed after clipping) is in the leaf's dtype,
+          // as the reference's per-example gradients are; the norm below
+          // uses the fp32 value.
+          if (l16)
+            ((uint16_t*)lpe)[row + m] = odp_f2bf(v);
+          else
+            lpe[row + m] = v;
           // Non-finite entries count as 0 (nan_to_num); squares are taken
           // in fp32 like the reference's float32 accumulation dtype.
           const float vf = isfinite(v) ? v : 0.f;

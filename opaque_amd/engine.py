@@ -424,6 +424,7 @@ class GhostPlan:
         leaf_rank_m: dict[int, tuple[int, int]] = {}
         lib = N.load()
         leaf_view: dict[int, _SegView] = {}
+        pe_dt: dict[int, torch.dtype] = {}
         for ch in chunks:
             dcode = dtype_code(ch[0].x.dtype)
             rtot = sum(s.A.shape[1] for s in ch)
@@ -433,6 +434,8 @@ class GhostPlan:
                 for lf in (s.a_leaf, s.b_leaf):
                     if lf is not None:
                         leaf_view[lf] = reg.view(s.segments)
+                        # Stored per-example factor gradients in the parameter dtype.
+                        pe_dt[lf] = ch[0].x.dtype
                 d_in, r = s.A.shape
                 d_out = s.B.shape[1]
                 if s.a_leaf is not None:
@@ -489,14 +492,23 @@ class GhostPlan:
             gstart[g] = max(gstart[g], gstart[g - 1])
         self.n_slots = max(pos, 1)
 
-        # Device buffers.
+        # Device buffers.  Per-example factor gradients: one buffer per dtype.
         pe_off: dict[int, int] = {}
-        off = 0
+        pe_size: dict[torch.dtype, int] = {}
         for i in sorted(pe_elems):
-            pe_off[i] = off
-            off += (pe_elems[i] + 63) // 64 * 64
-        self.pe = torch.empty(max(off, 1), dtype=torch.float32, device=dev)
-        self._pe_slices = [(pe_off[i], pe_elems[i]) for i in sorted(pe_elems)]
+            pe_off[i] = pe_size.get(pe_dt[i], 0)
+            pe_size[pe_dt[i]] = pe_off[i] + (pe_elems[i] + 63) // 64 * 64
+        self.pe = {dt: torch.empty(n, dtype=dt, device=dev) for dt, n in pe_size.items()}
+        self._pe_slices = [(pe_dt[i], pe_off[i], pe_elems[i]) for i in sorted(pe_elems)]
+
+        def pe_addr(i: int) -> int:
+            buf = self.pe[pe_dt[i]]
+            return buf.data_ptr() + pe_off[i] * buf.element_size()
+
+        def pe_bits(i: int) -> int:  # the leaf descriptor's dtype bit
+            return (1 << 32) if pe_dt[i] == torch.bfloat16 else 0
+
+        self._pe_addr, self._pe_bits = pe_addr, pe_bits
         self.part = torch.zeros((seg.n_ex, self.n_slots), dtype=torch.float64, device=dev)
 
         # Output leaves: one flat buffer per output dtype, views in leaf order.
@@ -594,8 +606,8 @@ class GhostPlan:
                         N.FT_Q: qaddr(vbase, c0, False), N.FT_QLO: qaddr(vbase, c0, True),
                         N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
                         N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
-                        N.FT_LEAF0: self.pe.data_ptr() + pe_off[s.b_leaf] * 4,
-                        N.FT_LEAF0 + 1: 0 | (r << 16),
+                        N.FT_LEAF0: pe_addr(s.b_leaf),
+                        N.FT_LEAF0 + 1: 0 | (r << 16) | pe_bits(s.b_leaf),
                         N.FT_LEAF0 + 2: slot_base[s.b_leaf],
                     }
                 if frow is not None and self._fusable(dt, r, v, g):
@@ -605,13 +617,14 @@ class GhostPlan:
                     # own offset).
                     frow.update({N.FP_W: wb.data_ptr(), N.FP_U: qaddr(ubase, c0, False),
                                  N.FP_ULO: qaddr(ubase, c0, True), N.FT_NSEG: 1})
-                    pe0 = self.pe.data_ptr() + pe_off[s.b_leaf] * 4
+                    pe0 = pe_addr(s.b_leaf)
+                    pe_es = self.pe[pe_dt[s.b_leaf]].element_size()
                     for j, ln in enumerate(v.segs.lengths):
                         row = dict(frow)
                         row[N.FT_SEG_FIRST] = sf + j
-                        row[N.FT_LEAF0] = pe0 + j * r * d_out * 4
+                        row[N.FT_LEAF0] = pe0 + j * r * d_out * pe_es
                         fused_rows.append((-ln * d_out, len(fused_rows), row, 1,
-                                           (ln * d_out + r * d_out + 2 * planes * r * ln) * es + r * d_out * 4))
+                                           (ln * d_out + r * d_out + 2 * planes * r * ln) * es + r * d_out * es))
                     c0 += r
                     continue
                 # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
@@ -627,7 +640,7 @@ class GhostPlan:
                 )
                 if frow is not None:
                     tab(ft, dt, r, N.FT_FIELDS).add(frow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
-                                                    (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * 4)
+                                                    (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es)
                 c0 += r
             if a_leaves:
                 scal = {s.scaling for s in ch if s.a_leaf is not None}
@@ -639,14 +652,14 @@ class GhostPlan:
                             self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, sf, n_seg, sc,
                                         [(s_leaf, col0, r)], pe_off, slot_base),
                             n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
-                            (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * 4)
+                            (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * es)
                 else:
                     tab(ft, dt, rtot, N.FT_FIELDS).add(
                         self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
                                     a_leaves, pe_off, slot_base),
                         n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot),
                         (valid * d_in + planes * rtot * valid) * es
-                        + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * 4)
+                        + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * es)
 
         # Most work first (the fused launch has one workgroup per segment, of
         # very different lengths).
@@ -717,19 +730,19 @@ class GhostPlan:
             n_seg = v.n_seg
             if i in mat_pe:
                 pe_m = mat_pe[i]
-                rank, M, transpose, pdt, pe_addr = 1, pe_m.shape[1], 0, dtype_code(pe_m.dtype), pe_m.data_ptr()
+                rank, M, transpose, pdt, pe_a = 1, pe_m.shape[1], 0, dtype_code(pe_m.dtype), pe_m.data_ptr()
             else:
                 rank, M = leaf_rank_m[i]
                 transpose = 1 if self._leaf_transposed(i, sites) else 0
-                pdt, pe_addr = N.DTYPE_F32, self.pe.data_ptr() + pe_off[i] * 4
+                pdt, pe_a = dtype_code(pe_dt[i]), pe_addr(i)
             flags = dtype_code(lf.out_dtype) | (transpose << 8) | (lf.group << 16) | (lf.cls << 40) | (pdt << 56)
             ss.add(
                 {
-                    N.SS_PE: pe_addr, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: v.first,
+                    N.SS_PE: pe_a, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: v.first,
                     N.SS_NSEG: n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2,
                 },
                 lib.odp_scale_sum_blocks(rank * M),
-                n_seg * rank * M * (4 if i not in mat_pe else mat_pe[i].element_size())
+                n_seg * rank * M * (self.pe[pe_dt[i]].element_size() if i not in mat_pe else mat_pe[i].element_size())
                 + rank * M * out.element_size() * (2 if self.out2 is not None else 1),
             )
 
@@ -788,8 +801,8 @@ class GhostPlan:
             N.FT_SCALING: _f64_bits(scaling), N.FT_NLEAF: len(leaves),
         }
         for li, (leaf, c, rk) in enumerate(sorted(leaves, key=lambda t: t[1])):
-            row[N.FT_LEAF0 + 3 * li] = self.pe.data_ptr() + pe_off[leaf] * 4
-            row[N.FT_LEAF0 + 3 * li + 1] = (c - col0) | (rk << 16)
+            row[N.FT_LEAF0 + 3 * li] = self._pe_addr(leaf)
+            row[N.FT_LEAF0 + 3 * li + 1] = (c - col0) | (rk << 16) | self._pe_bits(leaf)
             row[N.FT_LEAF0 + 3 * li + 2] = slot_base[leaf]
         return row
 
@@ -803,8 +816,8 @@ class GhostPlan:
         return False
 
     def pe_views(self) -> list[torch.Tensor]:
-        """The per-example factor gradients each LoRA leaf stored ([n_seg * r * M] fp32)."""
-        return [self.pe[o : o + n] for o, n in self._pe_slices]
+        """The per-example factor gradients each LoRA leaf stored ([n_seg * r * M], parameter dtype)."""
+        return [self.pe[dt][o : o + n] for dt, o, n in self._pe_slices]
 
     # -- execution -------------------------------------------------------------
     def run(self, events: dict | None = None, launch_log: list | None = None) -> GhostResult:
