@@ -98,7 +98,7 @@ enum {
   ODP_PJ_QLO = 10,   /* address of the lo plane (bf16 only)                   */
   ODP_PJ_FIELDS = 12
 };
-int64_t odp_project_blocks(int dtype, int64_t n_rows);
+int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r);
 /* Every problem of one table must have ceil(ODP_PJ_R / 16) == nkb (1..4). */
 int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
                 const int32_t* work_start, int32_t n_prob, int32_t total_blocks,

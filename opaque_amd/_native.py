@@ -49,7 +49,7 @@ _ptr = ctypes.c_void_p
 _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_abi_version": (_c_int, []),
     "odp_last_error": (ctypes.c_char_p, []),
-    "odp_project_blocks": (_c_i64, [_c_int, _c_i64]),
+    "odp_project_blocks": (_c_i64, [_c_int, _c_i64, _c_i32]),
     "odp_project": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i32]),
     "odp_seg_factor_tiles": (_c_i64, [_c_int, _c_i64, _c_i32]),
     "odp_seg_factor": (

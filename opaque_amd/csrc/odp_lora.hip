@@ -31,12 +31,14 @@ namespace {
 #ifndef ODP_FT_T
 #define ODP_FT_T 32  // tokens per bf16 factor step (a multiple of the MFMA K, 32)
 #endif
-#ifndef ODP_PJ_RPW
-#define ODP_PJ_RPW 1  // 16-row MFMA blocks per wave in the bf16 projection (2 measured slower)
+#ifndef ODP_PJ_RPW_WIDE
+#define ODP_PJ_RPW_WIDE 2  // 16-row blocks per wave for rank blocks >= 2 (W re-read per workgroup)
 #endif
 constexpr int PJ_ROWS = 64;   // rows per fp32 project workgroup (4 waves x 16)
-constexpr int PJ_RPW = ODP_PJ_RPW;
-constexpr int PJ_ROWS_BF16 = 64 * PJ_RPW;  // rows per bf16 project workgroup
+// bf16 projection: 16-row MFMA blocks per wave.  One block for rank <= 16
+// (two measured slower there); wider ranks re-read a larger W tile per
+// workgroup, so they take more rows per workgroup.
+__host__ __device__ constexpr int pj_rpw(int nkb) { return nkb >= 2 ? ODP_PJ_RPW_WIDE : 1; }
 constexpr int FT_T = ODP_FT_T;
 constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen) {
   constexpr int KS = ODP_PJ_KS, WPITCH = KS + 8, PPITCH = KS + 8, RP = 16 * NKB;
-  constexpr int RB = PJ_RPW, WR = 16 * RB;  // row blocks and rows per wave
+  constexpr int RB = pj_rpw(NKB), WR = 16 * RB;  // row blocks and rows per wave
   constexpr int NPR = RB * KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
   constexpr int NW = (RP * (KS / 8) + 255) / 256;  // W pieces per thread per step
   __shared__ __attribute__((aligned(16))) uint16_t wlds[2 * RP * WPITCH];
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
   const int seg_first = (int)f[ODP_PJ_SEG_FIRST], n_seg = (int)f[ODP_PJ_NSEG];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row0 = (int64_t)(bid - ws[p]) * PJ_ROWS_BF16 + WR * wave;
+  const int64_t row0 = (int64_t)(bid - ws[p]) * (4 * WR) + WR * wave;
   // Lane i < WR tests row row0 + i; the wave shares the answers as a bit mask.
   const int64_t test_row = row0 + (lane % WR);
   const bool tvalid = test_row < n_rows &&
@@ -856,8 +858,8 @@ __global__ __launch_bounds__(256) void k_factor_f32(const int64_t* __restrict__ 
 
 }  // namespace
 
-extern "C" int64_t odp_project_blocks(int dtype, int64_t n_rows) {
-  const int64_t rows = dtype == ODP_DTYPE_BF16 ? PJ_ROWS_BF16 : PJ_ROWS;
+extern "C" int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r) {
+  const int64_t rows = dtype == ODP_DTYPE_BF16 ? 64 * pj_rpw((r + 15) / 16) : PJ_ROWS;
   return n_rows <= 0 ? 0 : (n_rows + rows - 1) / rows;
 }
 

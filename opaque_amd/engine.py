@@ -584,7 +584,7 @@ class GhostPlan:
                     N.PJ_Q: qaddr(vbase, 0, False), N.PJ_QLO: qaddr(vbase, 0, True),
                     N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                 },
-                lib.odp_project_blocks(dtype_code(dt), n_rows),
+                lib.odp_project_blocks(dtype_code(dt), n_rows, rtot),
                 (valid * d_in + rtot * d_in + planes * rtot * valid) * es,
             )
             c0 = 0
@@ -635,7 +635,7 @@ class GhostPlan:
                         N.PJ_Q: qaddr(ubase, c0, False), N.PJ_QLO: qaddr(ubase, c0, True),
                         N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                     },
-                    lib.odp_project_blocks(dtype_code(dt), n_rows),
+                    lib.odp_project_blocks(dtype_code(dt), n_rows, r),
                     (valid * d_out + r * d_out + planes * r * valid) * es,
                 )
                 if frow is not None:

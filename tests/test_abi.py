@@ -71,11 +71,12 @@ def test_field_indices_match_header():
 
 def test_block_helpers_are_pure_host_code(lib):
     # The *_blocks helpers compute launch sizes on the host (no device needed).
-    assert lib.odp_project_blocks(N.DTYPE_F32, 0) == 0
-    assert lib.odp_project_blocks(N.DTYPE_F32, 64) == 1
-    assert lib.odp_project_blocks(N.DTYPE_F32, 65) == 2
-    per = lib.odp_project_blocks(N.DTYPE_BF16, 1 << 20)
-    assert per > 0 and lib.odp_project_blocks(N.DTYPE_BF16, ((1 << 20) // per) + 1) == 2
+    assert lib.odp_project_blocks(N.DTYPE_F32, 0, 16) == 0
+    assert lib.odp_project_blocks(N.DTYPE_F32, 64, 16) == 1
+    assert lib.odp_project_blocks(N.DTYPE_F32, 65, 16) == 2
+    for r in (16, 48):
+        per = (1 << 20) // lib.odp_project_blocks(N.DTYPE_BF16, 1 << 20, r)  # rows per workgroup
+        assert per >= 64 and lib.odp_project_blocks(N.DTYPE_BF16, per + 1, r) == 2
     assert lib.odp_sqnorm_blocks(1) >= 1
     assert lib.odp_scale_sum_blocks(4096) >= 1
     assert lib.odp_seg_factor_tiles(N.DTYPE_BF16, 4096, 16) >= 1
