@@ -26,7 +26,6 @@ Two ways to obtain the per-example gradients feed the same kernels:
 
 from __future__ import annotations
 
-import math
 from collections.abc import Callable
 from dataclasses import dataclass
 from typing import Any
