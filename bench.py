@@ -57,8 +57,12 @@ def kernel_label(stage, key):
     """Device symbol of a table launch, as rocprofv3 names it."""
     if stage == "lin_norm":
         return "k_lin_gram_norm" if key == 1 else "k_lin_outer_norm"
+    if stage == "lin_prescale":
+        return "k_lin_prescale"
+    if stage == "lin_sum":  # keyed by prescale chunk, None for in-register scaling
+        return f"k_lin_clip_sum<{'false' if key is None else 'true'}>"
     if key is None:
-        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "lin_sum": "k_lin_clip_sum",
+        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum",
                 "factor_project": "k_factor_project_bf16"}[stage]
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]

@@ -234,7 +234,8 @@ int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* w
  * odp_linear_clipped_sum writes out[o][i] = round_out(sum_s sum_{t in s}
  * g_t[o] bf16(c_s x_t[i])) and then round_out(out / normalize_by) if
  * normalize_by != 1, with c_s = scales[cls][group][seg_example[s]] (the
- * clip factor folded into X's rows; non-finite inputs propagate); one
+ * clip factor folded into X's rows, in registers or, with prescaled != 0,
+ * by odp_linear_prescale beforehand; non-finite inputs propagate); one
  * workgroup per 256 x 128 output tile (odp_linear_sum_blocks, padded to a
  * multiple of 8).  Replaces clip_pytree's scale and the batch sum
  * (clipping/_pytree.py:553, clipping/_clipped_fun.py:115-134,821-824).      */
@@ -245,6 +246,7 @@ enum {
   ODP_LN_OUT = 9,    /* clipped sum: address of out [d_out][d_in]           */
   ODP_LN_FLAGS = 10, /* clipped sum: out dtype | group << 8 | cls << 24     */
   ODP_LN_NB = 11,    /* GRAM: 128-row blocks of the longest segment         */
+  ODP_LN_NROWS = 12, /* prescale: rows of X (the output X' is [n_rows][d_in]) */
   ODP_LN_FIELDS = 16
 };
 int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len);
@@ -257,11 +259,27 @@ int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* problems,
                       const int32_t* seg_row_start, const int32_t* seg_row_len,
                       const int32_t* seg_example, double* part, int64_t part_stride);
 int64_t odp_linear_sum_blocks(int64_t d_in, int64_t d_out);
+/* ---- odp_linear_prescale: X' = c_i x_t for the clipped sum ------------
+ * The per-example scaling of clip_pytree (scale * leaf, clipping/_pytree.py:
+ * 553) moved onto the activations: for every row t of a segment of example
+ * i, X'[t] = bf16(c_i * x_t) with c_i the clip factor of the problem's
+ * (class, group) (ODP_LN_FLAGS as for the clipped sum); rows in no segment
+ * get 0.  odp_linear_clipped_sum with prescaled != 0 reads such an X' in
+ * every problem (ODP_LN_X = X', ODP_LN_LDX = d_in) and skips its own
+ * scaling; the result is bit-identical.  Problem rows: ODP_LN_X, LDX, DIN,
+ * SEG_FIRST, NSEG, NROWS, FLAGS, OUT = X' (bf16); one workgroup per 16 rows
+ * (odp_linear_prescale_blocks).                                            */
+int64_t odp_linear_prescale_blocks(int64_t n_rows);
+int odp_linear_prescale(odp_stream_t stream, const int64_t* problems,
+                        const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                        const int32_t* seg_row_start, const int32_t* seg_row_len,
+                        const int32_t* seg_example, const float* scales, int32_t n_ex,
+                        int32_t n_groups);
 int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
                            const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                            const int32_t* seg_row_start, const int32_t* seg_row_len,
                            const int32_t* seg_example, const float* scales, int32_t n_ex,
-                           int32_t n_groups, float normalize_by);
+                           int32_t n_groups, float normalize_by, int32_t prescaled);
 
 /* ---- odp_gaussian_noise --------------------------------------------------
  * out[i] = round_out(in[i] + f32(sigma * sqrt 2) * erfinv(2u - 1)) with

@@ -32,7 +32,7 @@ NZ_IN, NZ_OUT, NZ_N, NZ_FLAT_OFFSET, NZ_SIGMA, NZ_DTYPES = range(6)
 SQ_FIELDS = 8
 SQ_X, SQ_N, SQ_NSEG, SQ_SEG_FIRST, SQ_SLOT, SQ_DTYPE = range(6)
 LN_FIELDS = 16
-LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB = range(12)
+LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB, LN_NROWS = range(13)
 FORM_OUTER = 0
 FORM_GRAM = 1
 
@@ -76,12 +76,14 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_gaussian_noise": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _c_u64, _c_u32]),
     "odp_philox_words": (_c_int, [_ptr, _c_u64, _c_u32, _c_u32, _c_u64, _c_i64, _ptr]),
     "odp_linear_tiles": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "odp_linear_prescale_blocks": (_c_i64, [_c_i64]),
+    "odp_linear_prescale": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32]),
     "odp_linear_norm_blocks": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64]),
     "odp_linear_sqnorm": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
     "odp_linear_sum_blocks": (_c_i64, [_c_i64, _c_i64]),
     "odp_linear_clipped_sum": (
         _c_int,
-        [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32],
+        [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32, _c_i32],
     ),
 }
 

@@ -14,9 +14,10 @@
 //                      counted twice), one block against two per workgroup,
 //                      the cheaper form when the example is short relative
 //                      to the weight;
-//   k_lin_clip_sum   : out = sum_i c_i M_i as one GEMM over all rows, the
-//                      clip factor applied to each example's X fragments
-//                      (c_i x_t rounded to bf16).
+//   k_lin_prescale   : X' = c_i x_t rounded to bf16, per (X, group, class).
+//   k_lin_clip_sum   : out = sum_i c_i M_i as one GEMM over all rows, on X'
+//                      or with the clip factor applied to each example's X
+//                      fragments in registers (the same c_i x_t in bf16).
 //
 // All three are bf16 MFMA (16x16x32, fp32 accumulate).  Operand tiles move
 // from HBM to LDS by buffer loads straight into LDS (no staging registers)
@@ -588,12 +589,72 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
 }
 
 // ---------------------------------------------------------------------------
+// Prescale for the clipped sum: X'[t] = c_i x_t (fp32 product rounded to
+// bf16, as the clipped sum would form it in registers) for the rows t of
+// example i's segments, 0 for rows in no segment.  With X' the clipped sum
+// is a plain GEMM; the in-register scaling costs it more than this pass.
+// Workgroup = PS_ROWS rows of one problem; rows are found in the sorted
+// segment list by binary search.
+// ---------------------------------------------------------------------------
+constexpr int PS_ROWS = 16;
+
+__global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict__ probs,
+                                                      const int32_t* __restrict__ ws, int n_prob,
+                                                      const int32_t* __restrict__ sstart,
+                                                      const int32_t* __restrict__ slen,
+                                                      const int32_t* __restrict__ sex,
+                                                      const float* __restrict__ scales, int n_ex,
+                                                      int n_groups) {
+  __shared__ float rowc[PS_ROWS];
+  __shared__ int rowin[PS_ROWS];
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
+  const uint16_t* X = (const uint16_t*)f[ODP_LN_X];
+  const int64_t ldx = f[ODP_LN_LDX], d = f[ODP_LN_DIN], n_rows = f[ODP_LN_NROWS];
+  uint16_t* out = (uint16_t*)f[ODP_LN_OUT];
+  const int seg_first = (int)f[ODP_LN_SEG_FIRST], n_seg = (int)f[ODP_LN_NSEG];
+  const int64_t flags = f[ODP_LN_FLAGS];
+  const int grp = (int)((flags >> 8) & 0xffff), cls = (int)((flags >> 24) & 0xffff);
+  const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
+  const int64_t row0 = (int64_t)(bid - ws[p]) * PS_ROWS;
+  const int tid = threadIdx.x;
+  if (tid < PS_ROWS) {
+    const int64_t t = row0 + tid;
+    // Last segment starting at or before t.
+    int lo = 0, hi = n_seg;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sstart[seg_first + mid] <= t)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    const int s = lo - 1;
+    const bool in = t < n_rows && s >= 0 && t < (int64_t)sstart[seg_first + s] + slen[seg_first + s];
+    rowin[tid] = in ? 1 : 0;
+    rowc[tid] = in ? sc[sex[seg_first + s]] : 0.f;
+  }
+  __syncthreads();
+  const int64_t pieces = d / 8;
+  for (int64_t i = tid; i < PS_ROWS * pieces; i += 256) {
+    const int r = (int)(i / pieces);
+    const int64_t pc = i - (int64_t)r * pieces, t = row0 + r;
+    if (t >= n_rows) break;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (rowin[r]) v = scale_bf16x8(*(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(X + t * ldx + 8 * pc), rowc[r]);
+    *(u32x4_t*)(out + t * d + 8 * pc) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Clipped sum.  Workgroup = (o-tile, n-tile) of one weight; the contraction
 // runs over every segment's rows in order, and a pipeline step never spans
 // two segments.  The X fragments of a step are multiplied by their
 // example's clip factor (in fp32, rounded back to bf16) after the LDS read,
 // so one accumulator holds sum_i c_i M_i.
 // ---------------------------------------------------------------------------
+template <bool PRESCALED>
 __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t* __restrict__ probs,
                                                       const int32_t* __restrict__ ws, int n_prob,
                                                       const int32_t* __restrict__ sstart,
@@ -647,7 +708,8 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
   const ODP_CONST int32_t* cex = (const ODP_CONST int32_t*)(sex + P.seg_first);
   const ODP_CONST float* csc = (const ODP_CONST float*)sc;
   auto scale = [&](const Step& st) { return csc[cex[st.seg]]; };
-  dma_mainloop<true, false>(P, o0, n0, at_segment(0), next, scale, acc);
+  // PRESCALED: X already holds c_i x_t (odp_linear_prescale).
+  dma_mainloop<!PRESCALED, false>(P, o0, n0, at_segment(0), next, scale, acc);
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -724,12 +786,34 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
   return odp_check_launch("odp_linear_sqnorm");
 }
 
+extern "C" int64_t odp_linear_prescale_blocks(int64_t n_rows) {
+  return n_rows <= 0 ? 0 : (n_rows + PS_ROWS - 1) / PS_ROWS;
+}
+
+extern "C" int odp_linear_prescale(odp_stream_t stream, const int64_t* problems,
+                                   const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                                   const int32_t* seg_row_start, const int32_t* seg_row_len,
+                                   const int32_t* seg_example, const float* scales, int32_t n_ex,
+                                   int32_t n_groups) {
+  int rc = odp_check_table("odp_linear_prescale", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_row_start == nullptr || seg_row_len == nullptr || seg_example == nullptr ||
+      scales == nullptr || n_ex <= 0 || n_groups <= 0) {
+    odp_set_error("odp_linear_prescale: null segment/scale arrays or empty batch");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_lin_prescale, dim3(total_blocks), dim3(256), 0, odp_hip_stream(stream), problems,
+                     work_start, n_prob, seg_row_start, seg_row_len, seg_example, scales, n_ex, n_groups);
+  return odp_check_launch("odp_linear_prescale");
+}
+
 extern "C" int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
                                       const int32_t* work_start, int32_t n_prob,
                                       int32_t total_blocks, const int32_t* seg_row_start,
                                       const int32_t* seg_row_len, const int32_t* seg_example,
                                       const float* scales, int32_t n_ex, int32_t n_groups,
-                                      float normalize_by) {
+                                      float normalize_by, int32_t prescaled) {
   int rc = odp_check_table("odp_linear_clipped_sum", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
   if (!(normalize_by > 0.0f)) {
@@ -743,7 +827,7 @@ extern "C" int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* proble
     return ODP_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = odp_hip_stream(stream);
-  hipLaunchKernelGGL(k_lin_clip_sum, dim3(total_blocks), dim3(256), 0, s, problems, work_start,
+  hipLaunchKernelGGL(prescaled ? k_lin_clip_sum<true> : k_lin_clip_sum<false>, dim3(total_blocks), dim3(256), 0, s, problems, work_start,
                      n_prob, seg_row_start, seg_row_len, seg_example, scales, n_ex, n_groups,
                      normalize_by);
   return odp_check_launch("odp_linear_clipped_sum");

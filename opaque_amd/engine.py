@@ -318,6 +318,10 @@ def _stream() -> int:
 # ---------------------------------------------------------------------------
 
 
+# Stages launched after the clip factors, in table order.
+_AFTER_CLIP = ("scale_sum", "lin_prescale", "lin_sum")
+
+
 class GhostPlan:
     """Buffers and problem tables of one DP clip step.  Build, then ``run()``.
 
@@ -337,6 +341,7 @@ class GhostPlan:
         device: torch.device | str = "cuda",
         second_moment: bool = False,
         fuse_g_side: bool = True,
+        prescale_bytes: int = 8 << 30,
     ) -> None:
         N.load()
         dev = torch.device(device)
@@ -348,6 +353,7 @@ class GhostPlan:
         self.clip = clip
         self.second_moment = second_moment
         self.fuse_g_side = fuse_g_side
+        self.prescale_bytes = int(prescale_bytes)
         self.n_groups = len(clip.thresholds)
         self.n_cls = max(1, len(clip.guards))
         if self.n_groups < 1:
@@ -688,6 +694,41 @@ class GhostPlan:
             )
             mat_pe[m.leaf] = pe_m
 
+        # Clipped sums read X' = c_i x_t (odp_linear_prescale) from a scratch
+        # buffer, one X' per (activation, group, class), filled chunk by chunk
+        # so that a chunk's X' fit in prescale_bytes; a site whose X' alone
+        # does not fit scales its activations in registers instead.
+        site_chunk: list[tuple[int, tuple] | None] = []
+        xs_chunks: list[dict[tuple, tuple[int, int]]] = []
+        cur: dict[tuple, tuple[int, int]] = {}
+        cur_bytes = xs_bytes = 0
+        for i, ls in enumerate(lins):
+            x, lf = _rows(ls.x), self.leaves[ls.w_leaf]
+            nbytes = -(-x.shape[0] * x.shape[1] * 2 // 256) * 256
+            if nbytes > self.prescale_bytes:
+                site_chunk.append(None)
+                continue
+            k = (x.data_ptr(), tuple(x.shape), tuple(x.stride()), lin_view[i].first, lf.group, lf.cls)
+            if k not in cur:
+                if cur_bytes + nbytes > self.prescale_bytes:
+                    xs_chunks.append(cur)
+                    cur, cur_bytes = {}, 0
+                cur[k] = (cur_bytes // 2, i)
+                cur_bytes += nbytes
+                xs_bytes = max(xs_bytes, cur_bytes)
+            site_chunk.append((len(xs_chunks), k))
+        if cur:
+            xs_chunks.append(cur)
+        self.xs = torch.empty(xs_bytes // 2, dtype=torch.bfloat16, device=dev)
+        xs_pre = [_Table(N.LN_FIELDS) for _ in xs_chunks]
+        xs_sum = [_Table(N.LN_FIELDS) for _ in xs_chunks]
+        for c, members in enumerate(xs_chunks):
+            for off, i in members.values():
+                x, v, lf = _rows(lins[i].x), lin_view[i], self.leaves[lins[i].w_leaf]
+                xs_pre[c].add({N.LN_X: x.data_ptr(), N.LN_LDX: x.stride(0), N.LN_DIN: x.shape[1],
+                               N.LN_SEG_FIRST: v.first, N.LN_NSEG: v.n_seg, N.LN_NROWS: x.shape[0],
+                               N.LN_FLAGS: (lf.group << 8) | (lf.cls << 24), N.LN_OUT: self.xs[off:].data_ptr()},
+                              int(lib.odp_linear_prescale_blocks(x.shape[0])), 2 * v.valid * x.shape[1] * 2)
         lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS)}
         lsum = _Table(N.LN_FIELDS)
         for i, ls in enumerate(lins):
@@ -712,8 +753,13 @@ class GhostPlan:
             lf = self.leaves[ls.w_leaf]
             out = self.out[ls.w_leaf] if ls.index is None else self.out[ls.w_leaf][ls.index]
             flags = dtype_code(lf.out_dtype) | (lf.group << 8) | (lf.cls << 24)
-            lsum.add({**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags},
-                     int(lib.odp_linear_sum_blocks(d_in, d_out)),
+            row, into = {**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags}, lsum
+            if site_chunk[i] is not None:
+                c, k = site_chunk[i]
+                row[N.LN_X] = self.xs[xs_chunks[c][k][0]:].data_ptr()
+                row[N.LN_LDX] = d_in
+                into = xs_sum[c]
+            into.add(row, int(lib.odp_linear_sum_blocks(d_in, d_out)),
                      valid * (d_in + d_out) * 2 + d_in * d_out * out.element_size(),
                      2 * valid * d_in * d_out)
         lin_leaves = {ls.w_leaf for ls in lins}
@@ -764,6 +810,9 @@ class GhostPlan:
         tabs.append(("lin_norm", N.FORM_OUTER, lnt[N.FORM_OUTER]))
         tabs.append(("lin_norm", N.FORM_GRAM, lnt[N.FORM_GRAM]))
         tabs.append(("scale_sum", None, ss))
+        for c in range(len(xs_chunks)):
+            tabs.append(("lin_prescale", c, xs_pre[c]))
+            tabs.append(("lin_sum", c, xs_sum[c]))
         tabs.append(("lin_sum", None, lsum))
         tab_idx = []
         for name, dt, t in tabs:
@@ -783,7 +832,7 @@ class GhostPlan:
         self.tables = [(name, dt, views[pi], views[wi], n, total) for name, dt, pi, wi, n, total, _ in tab_idx]
         # Per launch, in launch order: (stage, key, workgroups, algorithmic bytes, algorithmic flops).
         info = [(name, dt, total, nb[0], nb[1]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
-        after_clip = ("scale_sum", "lin_sum")
+        after_clip = _AFTER_CLIP
         self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
 
     def _fusable(self, dt: torch.dtype, r: int, v: _SegView, g: torch.Tensor) -> bool:
@@ -824,8 +873,10 @@ class GhostPlan:
         """Launch the step on the current stream.
 
         ``events`` may map a stage name ("project", "factor_project",
-        "factor", "sqnorm", "lin_norm", "clip", "scale_sum", "lin_sum") to a (start, end) pair of torch.cuda.Event that
-        are recorded around that stage's launches.  ``launch_log``, when a
+        "factor", "sqnorm", "lin_norm", "clip", "scale_sum", "lin_sum") to a
+        (start, end) pair of torch.cuda.Event that are recorded around that
+        stage's launches ("lin_sum" spans the clipped sums and their
+        prescale launches).  ``launch_log``, when a
         list, receives one (stage, key, start, end) entry per table launch
         with freshly recorded timing events, in ``launch_info`` order.
         """
@@ -834,7 +885,7 @@ class GhostPlan:
         seg = self.segments
         ev = events or {}
         self.part.zero_()
-        live = [t for t in self.tables if t[5] > 0 and t[0] not in ("scale_sum", "lin_sum")]
+        live = [t for t in self.tables if t[5] > 0 and t[0] not in _AFTER_CLIP]
 
         def mark(name, dt):
             if launch_log is None:
@@ -888,30 +939,32 @@ class GhostPlan:
         )
         if "clip" in ev:
             ev["clip"][1].record()
-        for name, dt, probs, ws, n, total in self.tables:
-            if name == "scale_sum" and total:
-                if name in ev:
-                    ev[name][0].record()
-                end_ev = mark(name, dt)
+        post = [t for t in self.tables if t[5] > 0 and t[0] in _AFTER_CLIP]
+        stage = [("lin_sum" if t[0] == "lin_prescale" else t[0]) for t in post]
+        for idx, (name, dt, probs, ws, n, total) in enumerate(post):
+            st = stage[idx]
+            if st in ev and st not in stage[:idx]:
+                ev[st][0].record()
+            end_ev = mark(name, dt)
+            if name == "scale_sum":
                 N.check(lib.odp_scale_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                           self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
                                           self.n_groups, float(self.clip.normalize_by)), name)
-                if end_ev is not None:
-                    end_ev.record()
-                if name in ev:
-                    ev[name][1].record()
-            elif name == "lin_sum" and total:
-                if name in ev:
-                    ev[name][0].record()
-                end_ev = mark(name, dt)
+            elif name == "lin_prescale":
+                N.check(lib.odp_linear_prescale(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                                self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                                self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
+                                                self.n_groups), name)
+            elif name == "lin_sum":
                 N.check(lib.odp_linear_clipped_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                                    self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                                    self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
-                                                   self.n_groups, float(self.clip.normalize_by)), name)
-                if end_ev is not None:
-                    end_ev.record()
-                if name in ev:
-                    ev[name][1].record()
+                                                   self.n_groups, float(self.clip.normalize_by),
+                                                   0 if dt is None else 1), name)
+            if end_ev is not None:
+                end_ev.record()
+            if st in ev and st not in stage[idx + 1:]:
+                ev[st][1].record()
         return GhostResult(
             leaves=self.out,
             norms=self.norms,

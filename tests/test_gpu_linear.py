@@ -207,3 +207,49 @@ def test_moe_expert_segments(dtype, tol):
         ga, gb = res.leaves[2 * e].double().cpu(), res.leaves[2 * e + 1].double().cpu()
         assert (ga - wa).norm() <= tol * wa.norm(), e
         assert (gb - wb).norm() <= tol * wb.norm(), e
+
+
+@pytest.mark.parametrize("budget", [1 << 30, 100_000])
+def test_prescaled_clipped_sum_equals_in_register(budget):
+    """X' = c_i x_t staged by odp_linear_prescale gives the in-register result bit for bit.
+
+    Packed segments with gaps (rows in no segment hold garbage), three sites
+    on one X in two clip groups, a second X; the small budget splits the
+    sites into several prescale chunks and leaves the widest X' in registers.
+    """
+    print(f"prescale: budget={budget}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    n_rows = 300
+    starts, lengths = [3, 40, 41, 150, 151], [37, 0, 100, 1, 140]
+    seg = Segments(starts, lengths, [0, 1, 2, 3, 4], 5, n_rows)
+    X1 = torch.randn(n_rows, 136, generator=g)
+    X2 = torch.randn(n_rows, 520, generator=g) * 3
+    for X in (X1, X2):
+        X[:3] = 1e4
+        X[291:] = -1e4
+    X1, X2 = X1.to(torch.bfloat16).to(DEV), X2.to(torch.bfloat16).to(DEV)
+    outs = [(X1, 72, 0), (X1, 200, 1), (X1, 64, 0), (X2, 96, 1)]
+    leaves, lins, shapes = [], [], []
+    for i, (X, d_out, grp) in enumerate(outs):
+        G = (torch.randn(n_rows, d_out, generator=g) * (i + 1)).to(torch.bfloat16).to(DEV)
+        lins.append(LinearSite(X, G, i))
+        leaves.append(LeafOut((d_out, X.shape[1]), torch.bfloat16, group=grp))
+        shapes.append((d_out, X.shape[1]))
+    _, rnd = leaf_guards(shapes, [torch.bfloat16] * 4)
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[3.0, 20.0], effective=20.0, normalize_by=3.0,
+                    guards=[(rel, ab, torch.bfloat16)])
+    res = {}
+    for b in (budget, 0):
+        plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
+                         prescale_bytes=b)
+        r = plan.run()
+        torch.cuda.synchronize()
+        res[b] = ([t.clone() for t in r.leaves], r.scales.clone(), plan)
+    pre = [t for t in res[budget][2].tables if t[0] == "lin_prescale" and t[5] > 0]
+    assert len(pre) == (1 if budget == 1 << 30 else 3)
+    assert not any(t[0] == "lin_prescale" and t[5] > 0 for t in res[0][2].tables)
+    assert torch.equal(res[budget][1], res[0][1])
+    assert (res[0][1] < 1).any()  # some examples clip
+    for a, b in zip(res[budget][0], res[0][0]):
+        assert torch.equal(a, b)
