@@ -236,7 +236,7 @@ int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* w
  * normalize_by != 1, with c_s = scales[cls][group][seg_example[s]] (the
  * clip factor folded into X's rows, in registers or, with prescaled != 0,
  * by odp_linear_prescale beforehand; non-finite inputs propagate); one
- * workgroup per 256 x 128 output tile (odp_linear_sum_blocks, padded to a
+ * workgroup per 256 x 256 output tile (odp_linear_sum_blocks, padded to a
  * multiple of 8).  Replaces clip_pytree's scale and the batch sum
  * (clipping/_pytree.py:553, clipping/_clipped_fun.py:115-134,821-824).      */
 enum {

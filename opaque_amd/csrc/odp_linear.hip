@@ -6,7 +6,7 @@
 // M_i under vmap(grad) (opaque-engine/.../clipping/_clipped_fun.py:756-762)
 // and then squares, scales and sums them.  Here:
 //
-//   k_lin_outer_norm : ||M_i||_F^2 tile by tile (256 x 128 output tiles,
+//   k_lin_outer_norm : ||M_i||_F^2 tile by tile (256 x 256 output tiles,
 //                      contraction over the example's tokens), squares
 //                      summed in fp64 into one partial slot per tile;
 //   k_lin_gram_norm  : sum_{t,s} (x_t . x_s)(g_t . g_s) over the upper
@@ -47,6 +47,11 @@ __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((ODP_LDS v4i16_t*)(ODP_LDS void*)p);
 }
 
+// s_waitcnt immediate: vmcnt <= n (0..63), lgkmcnt and expcnt not waited on.
+__host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
+  return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
+}
+
 struct LinProblem {
   const uint16_t* X;
   const uint16_t* G;
@@ -69,21 +74,25 @@ __device__ __forceinline__ LinProblem read_problem(const int64_t* f) {
 
 // ---------------------------------------------------------------------------
 // Outer-product main loop.  The workgroup's tile covers OM output rows (o,
-// columns of G) by ON output columns (n, columns of X); four waves in a
-// 2 x 2 arrangement each own a WM x WN block as BI x BJ MFMA 16 x 16 blocks.
-// A pipeline step stages OK tokens of both operands as token-major LDS tiles
-// (token rows outside the step's segment and columns past the matrix are
-// zeroed at the LDS store); one step of global loads is in flight while the
-// previous one is computed.
+// columns of G) by ON output columns (n, columns of X); NW waves in a
+// 2 x (NW / 2) arrangement each own a WM x WN block as BI x BJ MFMA 16 x 16
+// blocks.  A pipeline step stages OK tokens of both operands as token-major
+// LDS tiles.  256 x 256 tiles of eight 128 x 64 waves (one workgroup and two
+// waves per SIMD per CU) move a third less data from L2 into LDS per flop
+// than 256 x 128 tiles of four, at the same registers per wave; the loads
+// into LDS, not the MFMAs or the LDS reads, bound these kernels.
 // ---------------------------------------------------------------------------
 #ifndef ODP_LIN_OM
 #define ODP_LIN_OM 256
 #endif
 #ifndef ODP_LIN_ON
-#define ODP_LIN_ON 128
+#define ODP_LIN_ON 256
 #endif
-constexpr int OM = ODP_LIN_OM, ON = ODP_LIN_ON, OK = 32;
-constexpr int WM = OM / 2, WN = ON / 2, BI = WM / 16, BJ = WN / 16;
+#ifndef ODP_LIN_WAVES
+#define ODP_LIN_WAVES 8  // waves per workgroup, 2 x (NW / 2) over the tile
+#endif
+constexpr int OM = ODP_LIN_OM, ON = ODP_LIN_ON, OK = 32, NW = ODP_LIN_WAVES, OUTER_THREADS = 64 * NW;
+constexpr int WM = OM / 2, WN = ON / (NW / 2), BI = WM / 16, BJ = WN / 16;
 constexpr int A_TILE = OK * OM, B_TILE = OK * ON;  // elements
 constexpr int OUTER_STAGE = A_TILE + B_TILE;
 
@@ -152,8 +161,8 @@ __device__ __forceinline__ u32x4_t scale_bf16x8(u32x4_t v, float c) {
 // ---------------------------------------------------------------------------
 // Outer-product main loop, buffer loads straight into LDS.  The step's G and
 // X tiles (token-major rows, the XOR swizzle above) are fetched by
-// buffer_load ... lds into a ring of three LDS stages, two steps ahead of the
-// compute, with no staging registers; each step waits for its own loads
+// buffer_load ... lds into a ring of RING LDS stages, RING - 1 steps ahead of
+// the compute, with no staging registers; each step waits for its own loads
 // with an explicit vmcnt and an LDS-only barrier.  The buffer resources
 // cover only the rows of the step's segment, so rows outside it (and
 // columns past the matrix, sent past the end) arrive as zeros.  A step never
@@ -162,10 +171,19 @@ __device__ __forceinline__ u32x4_t scale_bf16x8(u32x4_t v, float c) {
 // ---------------------------------------------------------------------------
 constexpr uint32_t LIN_BUF_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA buffer resource)
 constexpr uint32_t LIN_OOB = 0x80000000u;        // an offset past every buffer's end
-constexpr int A_DMA = A_TILE * 2 / 1024 / 4;      // 1 KB loads per wave per step (G tile)
-constexpr int B_DMA = B_TILE * 2 / 1024 / 4;      // (X tile)
+constexpr int A_DMA = A_TILE * 2 / 1024 / NW;     // 1 KB loads per wave per step (G tile)
+constexpr int B_DMA = B_TILE * 2 / 1024 / NW;     // (X tile)
+constexpr int RPW = OK / NW;                      // tile rows each wave loads per step
+#ifndef ODP_LIN_RING
+#define ODP_LIN_RING 4  // LDS stages of the outer-form ring (RING - 1 steps in flight)
+#endif
+constexpr int RING = ODP_LIN_RING;
+static_assert((RING == 3 || RING == 4) && (RING - 2) * (A_DMA + B_DMA) < 64, "ring depth");
 constexpr int DMA_PER_STEP = A_DMA + B_DMA;
-static_assert(OM * 2 == 512 && ON * 2 == 256, "ring loads assume 2 G rows / 4 X rows per 1 KB");
+constexpr int B_LPR = ON / 8, B_RPI = 64 / B_LPR;  // X tile: lanes per row, rows per load
+static_assert(OM == 256 && (ON == 128 || ON == 256), "G tile rows take 32 lanes; X tile rows 16 or 32");
+static_assert((NW == 4 || NW == 8) && A_DMA * 2 == RPW && B_DMA * B_RPI == RPW && WN % 16 == 0,
+              "each wave loads whole rows of both tiles");
 static_assert(DMA_PER_STEP < 16, "the step wait encodes vmcnt in 4 bits");
 
 // Column-major over the wave's blocks: X fragment j + 1 is scaled (VALU)
@@ -204,9 +222,9 @@ __device__ __forceinline__ void ring_step(uint16_t* __restrict__ nxt, const uint
 }
 
 // DEEP: the step's reads carry alias scopes (ring_step), so they do not
-// wait for the next stage's loads and two steps stay in flight.  Without
-// it the compiler makes the reads wait for all but the newest loads, about
-// one step ahead; the clipped sum, whose workgroups stream 32768 tokens
+// wait for the next stage's loads and RING - 1 steps stay in flight.
+// Without it the compiler makes the reads wait for all but the newest
+// loads, one step fewer; the clipped sum, whose workgroups stream 32768 tokens
 // against operands shared with many other tiles, measured faster that way
 // (less cache pressure), the per-example norms slower.
 template <bool SCALE, bool DEEP, typename Next, typename Scale>
@@ -217,7 +235,8 @@ __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, in
   __shared__ __attribute__((aligned(16))) uint16_t ring0[OUTER_STAGE];
   __shared__ __attribute__((aligned(16))) uint16_t ring1[OUTER_STAGE];
   __shared__ __attribute__((aligned(16))) uint16_t ring2[OUTER_STAGE];
-  auto stage = [&](int k) -> uint16_t* { return k == 0 ? ring0 : k == 1 ? ring1 : ring2; };
+  __shared__ __attribute__((aligned(16))) uint16_t ring3[RING > 3 ? OUTER_STAGE : 8];
+  auto stage = [&](int k) -> uint16_t* { return k == 0 ? ring0 : k == 1 ? ring1 : k == 2 ? ring2 : ring3; };
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Per lane: tile row and column of each of its loads (row within the
@@ -225,13 +244,13 @@ __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, in
   int arow[A_DMA], acol[A_DMA], brow[B_DMA], bcol[B_DMA];
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
-    arow[i] = 8 * wave + 2 * i + (lane >> 5);
+    arow[i] = RPW * wave + 2 * i + (lane >> 5);
     acol[i] = 8 * ((lane & 31) ^ (swz(arow[i]) >> 1));
   }
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) {
-    brow[i] = 8 * wave + 4 * i + (lane >> 4);
-    bcol[i] = 8 * ((lane & 15) ^ (swz(brow[i]) >> 1));
+    brow[i] = RPW * wave + B_RPI * i + (lane / B_LPR);
+    bcol[i] = 8 * ((lane % B_LPR) ^ (swz(brow[i]) >> 1));
   }
   const int32_t dout = (int32_t)P.d_out, din = (int32_t)P.d_in;
   const uint32_t ldg = (uint32_t)P.ldg, ldx = (uint32_t)P.ldx;
@@ -247,52 +266,71 @@ __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, in
     for (int i = 0; i < A_DMA; ++i) {
       const int32_t col = (int32_t)o0 + acol[i];
       const uint32_t off = col < dout ? ((r0 + arow[i]) * ldg + (uint32_t)col) * 2u : LIN_OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (ODP_LDS void*)(st + (8 * wave + 2 * i) * OM), 16, off, 0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (ODP_LDS void*)(st + (RPW * wave + 2 * i) * OM), 16, off, 0,
                                                0, 0);
     }
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) {
       const int32_t col = (int32_t)n0 + bcol[i];
       const uint32_t off = col < din ? ((r0 + brow[i]) * ldx + (uint32_t)col) * 2u : LIN_OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (ODP_LDS void*)(st + A_TILE + (8 * wave + 4 * i) * ON),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (ODP_LDS void*)(st + A_TILE + (RPW * wave + B_RPI * i) * ON),
                                                16, off, 0, 0, 0);
     }
   };
 
-  // Prologue: steps 0 and 1 in flight.  Steps past the last one still
-  // issue (zero rows, so out of range) to keep the wait counts constant.
+  // Prologue: steps 0 .. RING - 2 in flight.  Steps past the last one
+  // still issue (zero rows, so out of range) to keep the wait counts
+  // constant.
   Step cur = first;
-  Step ld = next(first);
-  float cs[3];
-  issue(ring0, cur);
-  cs[0] = SCALE && cur.live ? scale(cur) : 1.0f;
-  issue(ring1, ld);
-  cs[1] = SCALE && ld.live ? scale(ld) : 1.0f;
-  ld = next(ld);
+  Step ld = first;
+  float cs[RING];
+#pragma unroll
+  for (int q = 0; q < RING - 1; ++q) {
+    issue(stage(q), ld);
+    cs[q] = SCALE && ld.live ? scale(ld) : 1.0f;
+    ld = next(ld);
+  }
   while (cur.live) {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
+    for (int k = 0; k < RING; ++k) {
       if (!cur.live) break;
-      __builtin_amdgcn_s_waitcnt(0x0F70 | DMA_PER_STEP);  // this step's loads; the next one may fly
+      // This step's loads have landed; the later RING - 2 steps' may fly.
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((RING - 2) * DMA_PER_STEP));
       __asm__ volatile("s_barrier" ::: "memory");
       // Loads of step ld go into the stage computed at the previous step.
       const Step x = ld;
+      const int kn = (k + RING - 1) % RING;
       if (DEEP) {
-        ring_step<SCALE>(stage((k + 2) % 3), stage(k), [&](uint16_t* st) { issue(st, x); }, cs[k], acc);
+        ring_step<SCALE>(stage(kn), stage(k), [&](uint16_t* st) { issue(st, x); }, cs[k], acc);
       } else {
-        issue(stage((k + 2) % 3), x);
+        issue(stage(kn), x);
         if (SCALE)
           outer_compute_scaled(stage(k), stage(k) + A_TILE, cs[k], acc);
         else
           outer_compute(stage(k), stage(k) + A_TILE, acc);
       }
-      cs[(k + 2) % 3] = SCALE && ld.live ? scale(ld) : 1.0f;
+      cs[kn] = SCALE && ld.live ? scale(ld) : 1.0f;
       ld = next(ld);
       cur = next(cur);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
   __asm__ volatile("s_barrier" ::: "memory");
+}
+
+// Compile-time loop: f(Idx<0>{}), ..., f(Idx<N - 1>{}).  Accumulator
+// arrays indexed only through it stay in registers whatever their size
+// (a plain loop the unroller declines leaves them in scratch memory).
+template <int V>
+struct Idx {
+  static constexpr int value = V;
+};
+template <int N, int K = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (K < N) {
+    f(Idx<K>{});
+    static_for<N, K + 1>(f);
+  }
 }
 
 template <int I, int J>
@@ -332,7 +370,10 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
   if (lane == 0) red[wave] = v;
   __syncthreads();
   double t = 0.0;
-  if (threadIdx.x == 0) t = (red[0] + red[1]) + (red[2] + red[3]);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < NW; w += 4) t += (red[w] + red[w + 1]) + (red[w + 2] + red[w + 3]);
+  }
   return t;
 }
 
@@ -340,29 +381,30 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 template <int I, int J>
 __device__ __forceinline__ double acc_sq(const f32x4_t (&acc)[I][J]) {
   double s = 0.0;
+  static_for<I * J>([&](auto q) {
+    constexpr int i = decltype(q)::value / J, j = decltype(q)::value % J;
 #pragma unroll
-  for (int i = 0; i < I; ++i)
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v = acc[i][j][e];
-        const float vf = isfinite(v) ? v : 0.f;
-        s += (double)__fmul_rn(vf, vf);
-      }
+    for (int e = 0; e < 4; ++e) {
+      const float v = acc[i][j][e];
+      const float vf = isfinite(v) ? v : 0.f;
+      s += (double)__fmul_rn(vf, vf);
+    }
+    // One tile's accumulators at a time in VGPRs.
+    __builtin_amdgcn_sched_barrier(0);
+  });
   return s;
 }
 
 // ---------------------------------------------------------------------------
 // ||M_i||^2 partials, outer form.  Workgroup = (segment, o-tile, n-tile).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_outer_norm(const int64_t* __restrict__ probs,
+__global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(const int64_t* __restrict__ probs,
                                                         const int32_t* __restrict__ ws, int n_prob,
                                                         const int32_t* __restrict__ sstart,
                                                         const int32_t* __restrict__ slen,
                                                         const int32_t* __restrict__ sex,
                                                         double* __restrict__ part, int64_t part_stride) {
-  __shared__ double red[4];
+  __shared__ double red[NW];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
@@ -421,10 +463,6 @@ __host__ __device__ constexpr int64_t gram_items(int64_t nb) {
 
 __device__ __forceinline__ int gr_swz(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ gr_swz(row)); }
-
-__host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
-  return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
-}
 
 __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restrict__ probs,
                                                              const int32_t* __restrict__ ws, int n_prob,
@@ -655,7 +693,7 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
 // so one accumulator holds sum_i c_i M_i.
 // ---------------------------------------------------------------------------
 template <bool PRESCALED>
-__global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t* __restrict__ probs,
+__global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t* __restrict__ probs,
                                                       const int32_t* __restrict__ ws, int n_prob,
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen,
@@ -714,20 +752,21 @@ __global__ __launch_bounds__(256, ODP_LIN_OCC) void k_lin_clip_sum(const int64_t
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = WM * (wave & 1), wn = WN * (wave >> 1);
+  static_for<BI * BJ>([&](auto q) {
+    constexpr int i = decltype(q)::value / BJ, j = decltype(q)::value % BJ;
 #pragma unroll
-  for (int i = 0; i < BI; ++i)
-#pragma unroll
-    for (int j = 0; j < BJ; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t o = o0 + wm + 16 * i + 4 * (lane >> 4) + e;
-        const int64_t n = n0 + wn + 16 * j + (lane & 15);
-        if (o < P.d_out && n < P.d_in) {
-          float x = odp_round_to(acc[i][j][e], odt);
-          if (normalize_by != 1.0f) x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
-          odp_store_from_float(out, o * P.d_in + n, odt, x);
-        }
+    for (int e = 0; e < 4; ++e) {
+      const int64_t o = o0 + wm + 16 * i + 4 * (lane >> 4) + e;
+      const int64_t n = n0 + wn + 16 * j + (lane & 15);
+      if (o < P.d_out && n < P.d_in) {
+        float x = odp_round_to(acc[i][j][e], odt);
+        if (normalize_by != 1.0f) x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
+        odp_store_from_float(out, o * P.d_in + n, odt, x);
       }
+    }
+    // One tile's accumulators at a time in VGPRs.
+    __builtin_amdgcn_sched_barrier(0);
+  });
 }
 
 }  // namespace
@@ -776,7 +815,7 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
     return ODP_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = odp_hip_stream(stream);
-  const dim3 grid(total_blocks), block(256);
+  const dim3 grid(total_blocks), block(OUTER_THREADS);
   if (form == ODP_FORM_GRAM)
     hipLaunchKernelGGL(k_lin_gram_norm, grid, dim3(512), 0, s, problems, work_start, n_prob,
                        seg_row_start, seg_row_len, seg_example, part, part_stride);
@@ -827,7 +866,7 @@ extern "C" int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* proble
     return ODP_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = odp_hip_stream(stream);
-  hipLaunchKernelGGL(prescaled ? k_lin_clip_sum<true> : k_lin_clip_sum<false>, dim3(total_blocks), dim3(256), 0, s, problems, work_start,
+  hipLaunchKernelGGL(prescaled ? k_lin_clip_sum<true> : k_lin_clip_sum<false>, dim3(total_blocks), dim3(OUTER_THREADS), 0, s, problems, work_start,
                      n_prob, seg_row_start, seg_row_len, seg_example, scales, n_ex, n_groups,
                      normalize_by);
   return odp_check_launch("odp_linear_clipped_sum");
