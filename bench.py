@@ -46,6 +46,9 @@ def parse_args():
     ap.add_argument("--seq", type=int, default=None, help="default 1024 (c3) / 4096 (c4)")
     ap.add_argument("--rank", type=int, default=16)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--linear-pe-gb", type=float, default=None,
+                    help="c4: HBM for stored per-example weight gradients (default: free memory after "
+                         "the inputs less 32 GiB; 0: clipped-sum GEMM for every site)")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES five times (the known-size "
@@ -232,19 +235,25 @@ def setup_c4(args, dev):
     _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
     rel, ab = guard_constants(torch.bfloat16, rnd)
     thr = [C4_THRESHOLDS[n] for n in names]
+    if args.linear_pe_gb is None:  # leave room for the noised copy of the gradients and the allocator
+        pe_bytes = max(0, torch.cuda.mem_get_info(dev)[0] - (32 << 30))
+    else:
+        pe_bytes = int(args.linear_pe_gb * 2**30)
     clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=thr, effective=math.sqrt(sum(v * v for v in thr)),
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
-    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=dev)
+    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=dev,
+                     linear_pe_bytes=pe_bytes)
     flops = sum(f for *_, f in plan.launch_info)
     config = {
         "workload": "C4: Llama-3-8B-shaped full weights, 32 layers x 7 linears, batch 8 x seq 4096, "
                     "PerGroup fixed clipping (one threshold per linear type), noise multiplier 1.0",
         "global_batch": B, "seq_len": T, "layers": args.layers,
         "thresholds": C4_THRESHOLDS, "parallelism": "single GPU",
+        "stored_per_example_gb": round(plan.lin_pe.numel() * 2 / 2**30, 1),
     }
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B full-weight per-example clipping"
     sigma = 1.0 * clip.effective / B
-    return plan, sigma, config, metric, flops, ("lin_norm", "clip", "lin_sum", "noise"), "mfma"
+    return plan, sigma, config, metric, flops, ("lin_norm", "clip", "scale_sum", "lin_sum", "noise"), "mfma"
 
 
 def main():
@@ -275,6 +284,9 @@ def main():
         args.seq = 1024 if args.seq is None else args.seq
         plan, sigma, config, metric, flops, stages, bound = setup_c3(args, dev)
     B = args.batch
+    # Stages with no launch in this plan record no events.
+    present = {("lin_sum" if i[0] == "lin_prescale" else i[0]) for i in plan.launch_info} | {"clip", "noise"}
+    stages = tuple(s for s in stages if s in present)
     n_params = sum(math.prod(lf.shape) for lf in plan.leaves)
     k0 = key(42)
 

@@ -247,6 +247,8 @@ enum {
   ODP_LN_FLAGS = 10, /* clipped sum: out dtype | group << 8 | cls << 24     */
   ODP_LN_NB = 11,    /* GRAM: 128-row blocks of the longest segment         */
   ODP_LN_NROWS = 12, /* prescale: rows of X (the output X' is [n_rows][d_in]) */
+  ODP_LN_PE = 13,    /* OUTER sqnorm: address of bf16 [n_seg][d_out][d_in]
+                        that receives each M_s (RNE), or 0                  */
   ODP_LN_FIELDS = 16
 };
 int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len);

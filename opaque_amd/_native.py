@@ -32,7 +32,7 @@ NZ_IN, NZ_OUT, NZ_N, NZ_FLAT_OFFSET, NZ_SIGMA, NZ_DTYPES = range(6)
 SQ_FIELDS = 8
 SQ_X, SQ_N, SQ_NSEG, SQ_SEG_FIRST, SQ_SLOT, SQ_DTYPE = range(6)
 LN_FIELDS = 16
-LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB, LN_NROWS = range(13)
+LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB, LN_NROWS, LN_PE = range(14)
 FORM_OUTER = 0
 FORM_GRAM = 1
 

@@ -433,6 +433,24 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
   // Columns/rows past the matrix were zero operands, so they add nothing.
   const double tot = block_sum(acc_sq(acc), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
+  // Optionally keep the tile of M_s itself, rounded to bf16, for a later
+  // clipped sum over stored per-example gradients.
+  uint16_t* pe = (uint16_t*)f[ODP_LN_PE];
+  if (pe != nullptr) {
+    uint16_t* dst = pe + (int64_t)seg * P.d_out * P.d_in;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = WM * (wave & 1), wn = WN * (wave >> 1);
+    static_for<BI * BJ>([&](auto q) {
+      constexpr int i = decltype(q)::value / BJ, j = decltype(q)::value % BJ;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t o = o0 + wm + 16 * i + 4 * (lane >> 4) + e;
+        const int64_t n = n0 + wn + 16 * j + (lane & 15);
+        if (o < P.d_out && n < P.d_in) dst[o * P.d_in + n] = odp_f2bf(acc[i][j][e]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -349,6 +349,7 @@ class GhostPlan:
         second_moment: bool = False,
         fuse_g_side: bool = True,
         prescale_bytes: int = 8 << 30,
+        linear_pe_bytes: int | None = None,
     ) -> None:
         N.load()
         dev = torch.device(device)
@@ -361,6 +362,7 @@ class GhostPlan:
         self.second_moment = second_moment
         self.fuse_g_side = fuse_g_side
         self.prescale_bytes = int(prescale_bytes)
+        self.linear_pe_bytes = linear_pe_bytes
         self.n_groups = len(clip.thresholds)
         self.n_cls = max(1, len(clip.guards))
         if self.n_groups < 1:
@@ -701,6 +703,25 @@ class GhostPlan:
             )
             mat_pe[m.leaf] = pe_m
 
+        # Outer-form sites whose per-example gradients fit in linear_pe_bytes
+        # keep them (bf16, written by the norm kernel) and are clipped and
+        # summed like stored per-example gradients; the rest go through the
+        # clipped-sum GEMM.
+        budget = self.linear_pe_bytes
+        if budget is None:
+            budget = torch.cuda.mem_get_info(dev)[0] // 2 if dev.type == "cuda" and lins else 0
+        lin_pe: dict[int, int] = {}  # site -> element offset in self.lin_pe
+        pe_total = 0
+        for i, ls in enumerate(lins):
+            n = lin_view[i].n_seg * ls.x.shape[-1] * ls.g.shape[-1]
+            if lin_form[i] == N.FORM_OUTER and (pe_total + n) * 2 <= budget:
+                lin_pe[i] = pe_total
+                pe_total += (n + 127) // 128 * 128
+        self.lin_pe = torch.empty(pe_total, dtype=torch.bfloat16, device=dev)
+        if self.second_moment and len(lin_pe) < len(lins):
+            raise ValueError("second moments of full-weight linear sites need their per-example "
+                             "gradients stored (outer form, within linear_pe_bytes)")
+
         # Clipped sums read X' = c_i x_t (odp_linear_prescale) from a scratch
         # buffer, one X' per (activation, group, class), filled chunk by chunk
         # so that a chunk's X' fit in prescale_bytes; a site whose X' alone
@@ -710,6 +731,9 @@ class GhostPlan:
         cur: dict[tuple, tuple[int, int]] = {}
         cur_bytes = xs_bytes = 0
         for i, ls in enumerate(lins):
+            if i in lin_pe:
+                site_chunk.append(None)
+                continue
             x, lf = _rows(ls.x), self.leaves[ls.w_leaf]
             nbytes = -(-x.shape[0] * x.shape[1] * 2 // 256) * 256
             if nbytes > self.prescale_bytes:
@@ -755,8 +779,12 @@ class GhostPlan:
                 fl = 2 * valid * d_in * d_out
             blocks = int(lib.odp_linear_norm_blocks(form, d_in, d_out, v.max_len, n_seg))
             nb_max = (v.max_len + 127) // 128
-            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_off[i], N.LN_NB: nb_max}, blocks,
-                          valid * (d_in + d_out) * 2, fl)
+            pe_at = self.lin_pe[lin_pe[i]:].data_ptr() if i in lin_pe else 0
+            lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_off[i], N.LN_NB: nb_max,
+                           N.LN_PE: pe_at}, blocks,
+                          valid * (d_in + d_out) * 2 + (n_seg * d_in * d_out * 2 if pe_at else 0), fl)
+            if i in lin_pe:
+                continue
             lf = self.leaves[ls.w_leaf]
             out = self.out[ls.w_leaf] if ls.index is None else self.out[ls.w_leaf][ls.index]
             flags = dtype_code(lf.out_dtype) | (lf.group << 8) | (lf.cls << 24)
@@ -770,10 +798,22 @@ class GhostPlan:
                      valid * (d_in + d_out) * 2 + d_in * d_out * out.element_size(),
                      2 * valid * d_in * d_out)
         lin_leaves = {ls.w_leaf for ls in lins}
-        if lin_leaves and self.second_moment:
-            raise ValueError("second moments of full-weight linear sites are not computed natively")
 
         ss = _Table(N.SS_FIELDS)
+        for i, off in lin_pe.items():
+            ls, v = lins[i], lin_view[i]
+            lf = self.leaves[ls.w_leaf]
+            out = self.out[ls.w_leaf] if ls.index is None else self.out[ls.w_leaf][ls.index]
+            out2 = 0
+            if self.out2 is not None:
+                o2 = self.out2[ls.w_leaf]
+                out2 = (o2 if ls.index is None else o2[ls.index]).data_ptr()
+            M = ls.x.shape[-1] * ls.g.shape[-1]
+            flags = dtype_code(lf.out_dtype) | (lf.group << 16) | (lf.cls << 40) | (N.DTYPE_BF16 << 56)
+            ss.add({N.SS_PE: self.lin_pe[off:].data_ptr(), N.SS_M: M, N.SS_RANK: 1, N.SS_SEG_FIRST: v.first,
+                    N.SS_NSEG: v.n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2},
+                   lib.odp_scale_sum_blocks(M),
+                   v.n_seg * M * 2 + M * out.element_size() * (2 if self.out2 is not None else 1))
         for i, lf in enumerate(self.leaves):
             if i in lin_leaves:
                 continue

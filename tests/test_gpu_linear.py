@@ -33,14 +33,15 @@ def _case(n_ex, T, d_in, d_out, lengths, seed, scale_spread=True):
     return X.to(torch.bfloat16), G.to(torch.bfloat16), seg
 
 
-def _plan(X, G, seg, *, C, mode, form, normalize_by=1.0, out_dtype=torch.bfloat16):
+def _plan(X, G, seg, *, C, mode, form, normalize_by=1.0, out_dtype=torch.bfloat16, pe_bytes=None):
     d_in, d_out = X.shape[1], G.shape[1]
     _, rnd = leaf_guards([(d_out, d_in)], [torch.bfloat16])
     rel, ab = guard_constants(torch.bfloat16, rnd)
     clip = ClipSpec(mode=mode, thresholds=[C], effective=C, normalize_by=normalize_by,
                     guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=seg, leaves=[LeafOut((d_out, d_in), out_dtype)], clip=clip,
-                     linear_sites=[LinearSite(X.to(DEV), G.to(DEV), 0, form)], device=DEV)
+                     linear_sites=[LinearSite(X.to(DEV), G.to(DEV), 0, form)], device=DEV,
+                     linear_pe_bytes=pe_bytes)
     res = plan.run()
     torch.cuda.synchronize()
     return plan, res, rnd
@@ -80,14 +81,16 @@ def test_outer_and_gram_forms_agree():
 
 
 @pytest.mark.parametrize("mode", [N.CLIP_FIXED, N.CLIP_AUTOS])
-@pytest.mark.parametrize("form", [N.FORM_OUTER, N.FORM_GRAM])
-def test_linear_clipped_sum_matches_oracle(mode, form):
+@pytest.mark.parametrize("form,pe_bytes", [(N.FORM_OUTER, None), (N.FORM_OUTER, 0), (N.FORM_GRAM, None)])
+def test_linear_clipped_sum_matches_oracle(mode, form, pe_bytes):
+    """pe_bytes None: the outer form keeps each M_s (bf16) for odp_scale_sum; 0: the clipped-sum GEMM."""
     n_ex, T, d_in, d_out = 6, 96, 264, 136
     lengths = [96, 50, 7, 96, 0, 81]
     X, G, seg = _case(n_ex, T, d_in, d_out, lengths, seed=4)
     pe, norms = _ref_norms(X, G, seg)
     C = float(norms[norms > 0].median())
-    _, res, rnd = _plan(X, G, seg, C=C, mode=mode, form=form, normalize_by=6.0)
+    plan, res, rnd = _plan(X, G, seg, C=C, mode=mode, form=form, normalize_by=6.0, pe_bytes=pe_bytes)
+    assert plan.lin_pe.numel() == (n_ex * d_in * d_out if form == N.FORM_OUTER and pe_bytes is None else 0)
     # Oracle: reference clip_pytree per example (the per-example gradient rounded
     # to the bf16 parameter dtype, as vmap(grad) produces it), fp32 sum, cast, /6.
     outs = []
@@ -242,7 +245,7 @@ def test_prescaled_clipped_sum_equals_in_register(budget):
     res = {}
     for b in (budget, 0):
         plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
-                         prescale_bytes=b)
+                         prescale_bytes=b, linear_pe_bytes=0)
         r = plan.run()
         torch.cuda.synchronize()
         res[b] = ([t.clone() for t in r.leaves], r.scales.clone(), plan)
@@ -253,3 +256,69 @@ def test_prescaled_clipped_sum_equals_in_register(budget):
     assert (res[0][1] < 1).any()  # some examples clip
     for a, b in zip(res[budget][0], res[0][0]):
         assert torch.equal(a, b)
+
+
+def _multi_site(seed=23):
+    g = torch.Generator().manual_seed(seed)
+    n_rows = 200
+    seg = Segments([0, 60, 61, 130], [60, 1, 69, 70], [0, 1, 2, 3], 4, n_rows)
+    X = (torch.randn(n_rows, 136, generator=g)).to(torch.bfloat16).to(DEV)
+    outs = [72, 264, 40, 128]
+    leaves, lins, shapes = [], [], []
+    for i, d_out in enumerate(outs):
+        G = (torch.randn(n_rows, d_out, generator=g) * (0.5 + i)).to(torch.bfloat16).to(DEV)
+        lins.append(LinearSite(X, G, i, N.FORM_OUTER))
+        leaves.append(LeafOut((d_out, 136), torch.float32, group=i % 2))
+        shapes.append((d_out, 136))
+    _, rnd = leaf_guards(shapes, [torch.bfloat16] * 4)
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[4.0, 30.0], effective=30.0, normalize_by=2.0,
+                    guards=[(rel, ab, torch.bfloat16)])
+    return seg, leaves, lins, clip
+
+
+def test_stored_linear_gradients_within_a_budget():
+    """A budget that holds two of four sites' per-example gradients: those two are
+    summed from storage, the other two by the GEMM; norms are identical either way."""
+    print("stored linear gradients: partial budget", flush=True)
+    seg, leaves, lins, clip = _multi_site()
+    res = {}
+    for name, b in (("all", None), ("none", 0), ("part", 4 * 136 * (72 + 264) * 2)):
+        plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
+                         linear_pe_bytes=b)
+        r = plan.run()
+        torch.cuda.synchronize()
+        res[name] = ([t.clone() for t in r.leaves], r.norms.clone(), plan.lin_pe.numel())
+    assert res["part"][2] == 4 * 136 * (72 + 264) and res["none"][2] == 0
+    assert torch.equal(res["all"][1], res["none"][1]) and torch.equal(res["part"][1], res["none"][1])
+    for k in range(4):
+        ref = res["none"][0][k].double()
+        for name in ("all", "part"):
+            got = res[name][0][k].double()
+            assert (got - ref).norm() <= 1e-2 * ref.norm(), (name, k)
+    # Sites 0 and 1 of the partial plan come from storage, 2 and 3 from the GEMM.
+    for k in (2, 3):
+        assert torch.equal(res["part"][0][k], res["none"][0][k])
+    for k in (0, 1):
+        assert torch.equal(res["part"][0][k], res["all"][0][k])
+
+
+def test_stored_linear_gradients_second_moment():
+    print("stored linear gradients: second moment", flush=True)
+    seg, leaves, lins, clip = _multi_site(seed=29)
+    with pytest.raises(ValueError, match="second moments"):
+        GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
+                  second_moment=True, linear_pe_bytes=0)
+    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
+                     second_moment=True)
+    r = plan.run()
+    torch.cuda.synchronize()
+    scales = r.scales.cpu()
+    for k, ls in enumerate(lins):
+        X, G = ls.x.cpu(), ls.g.cpu()
+        pe = lora_ref.linear_per_example(X.float(), G.float(), seg.starts, seg.lengths).to(torch.bfloat16)
+        c = scales[0, leaves[k].group].double().view(-1, 1, 1)
+        y = c * pe.double()
+        want, want2 = y.sum(0) / 2.0, (y * y).sum(0) / 2.0
+        assert (r.leaves[k].double().cpu() - want).norm() <= 2e-4 * want.norm(), k
+        assert (r.second_moment[k].double().cpu() - want2).norm() <= 2e-4 * want2.norm(), k
