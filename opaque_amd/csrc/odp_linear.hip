@@ -178,6 +178,8 @@ constexpr int RPW = OK / NW;                      // tile rows each wave loads p
 #define ODP_LIN_RING 4  // LDS stages of the outer-form ring (RING - 1 steps in flight)
 #endif
 constexpr int RING = ODP_LIN_RING;
+static_assert(WN == 64 && 2 * WM * WN <= OUTER_STAGE && NW <= 2 * RING,
+              "two waves' bf16 blocks fit in each ring stage (outer-norm store)");
 static_assert((RING == 3 || RING == 4) && (RING - 2) * (A_DMA + B_DMA) < 64, "ring depth");
 constexpr int DMA_PER_STEP = A_DMA + B_DMA;
 constexpr int B_LPR = ON / 8, B_RPI = 64 / B_LPR;  // X tile: lanes per row, rows per load
@@ -221,6 +223,17 @@ __device__ __forceinline__ void ring_step(uint16_t* __restrict__ nxt, const uint
     outer_compute(cur, cur + A_TILE, acc);
 }
 
+// The ring: one array per stage, so that reads of one stage are not made to
+// wait for the loads into the others.  Kernels may reuse it once the main
+// loop has returned.
+__shared__ __attribute__((aligned(16))) uint16_t lin_ring0[OUTER_STAGE];
+__shared__ __attribute__((aligned(16))) uint16_t lin_ring1[OUTER_STAGE];
+__shared__ __attribute__((aligned(16))) uint16_t lin_ring2[OUTER_STAGE];
+__shared__ __attribute__((aligned(16))) uint16_t lin_ring3[RING > 3 ? OUTER_STAGE : 8];
+__device__ __forceinline__ uint16_t* lin_stage(int k) {
+  return k == 0 ? lin_ring0 : k == 1 ? lin_ring1 : k == 2 ? lin_ring2 : lin_ring3;
+}
+
 // DEEP: the step's reads carry alias scopes (ring_step), so they do not
 // wait for the next stage's loads and RING - 1 steps stay in flight.
 // Without it the compiler makes the reads wait for all but the newest
@@ -230,13 +243,7 @@ __device__ __forceinline__ void ring_step(uint16_t* __restrict__ nxt, const uint
 template <bool SCALE, bool DEEP, typename Next, typename Scale>
 __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step first,
                                              Next next, Scale scale, OuterAcc& acc) {
-  // One array per ring stage, so that reads of one stage are not made to
-  // wait for the loads into the others.
-  __shared__ __attribute__((aligned(16))) uint16_t ring0[OUTER_STAGE];
-  __shared__ __attribute__((aligned(16))) uint16_t ring1[OUTER_STAGE];
-  __shared__ __attribute__((aligned(16))) uint16_t ring2[OUTER_STAGE];
-  __shared__ __attribute__((aligned(16))) uint16_t ring3[RING > 3 ? OUTER_STAGE : 8];
-  auto stage = [&](int k) -> uint16_t* { return k == 0 ? ring0 : k == 1 ? ring1 : k == 2 ? ring2 : ring3; };
+  auto stage = [&](int k) -> uint16_t* { return lin_stage(k); };
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Per lane: tile row and column of each of its loads (row within the
@@ -434,22 +441,33 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
   const double tot = block_sum(acc_sq(acc), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
   // Optionally keep the tile of M_s itself, rounded to bf16, for a later
-  // clipped sum over stored per-example gradients.
+  // clipped sum over stored per-example gradients.  Each wave's WM x WN
+  // block goes through its own part of the (now idle) LDS ring so that rows
+  // leave in 16-byte pieces: 8-column chunk q of block row r sits at chunk
+  // q ^ ((r >> 2) & 7), which keeps both the 2-byte writes of the MFMA
+  // layout and the 16-byte reads free of bank conflicts.
   uint16_t* pe = (uint16_t*)f[ODP_LN_PE];
   if (pe != nullptr) {
-    uint16_t* dst = pe + (int64_t)seg * P.d_out * P.d_in;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = WM * (wave & 1), wn = WN * (wave >> 1);
+    uint16_t* stg = lin_stage(wave >> 1) + (wave & 1) * (WM * WN);
     static_for<BI * BJ>([&](auto q) {
       constexpr int i = decltype(q)::value / BJ, j = decltype(q)::value % BJ;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t o = o0 + wm + 16 * i + 4 * (lane >> 4) + e;
-        const int64_t n = n0 + wn + 16 * j + (lane & 15);
-        if (o < P.d_out && n < P.d_in) dst[o * P.d_in + n] = odp_f2bf(acc[i][j][e]);
+        const int r = 16 * i + 4 * (lane >> 4) + e, c = 16 * j + (lane & 15);
+        stg[r * WN + 8 * ((c >> 3) ^ ((r >> 2) & 7)) + (c & 7)] = odp_f2bf(acc[i][j][e]);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
+    uint16_t* dst = pe + (int64_t)seg * P.d_out * P.d_in;
+    const int64_t ob = o0 + WM * (wave & 1), nb = n0 + WN * (wave >> 1);
+#pragma unroll
+    for (int k = 0; k < WM / 8; ++k) {
+      const int r = 8 * k + (lane >> 3), qq = lane & 7;
+      const u32x4_t v = *(const u32x4_t*)&stg[r * WN + 8 * (qq ^ ((r >> 2) & 7))];
+      const int64_t o = ob + r, n = nb + 8 * qq;
+      if (o < P.d_out && n < P.d_in) *(ODP_GLOBAL u32x4_t*)(ODP_GLOBAL void*)(dst + o * P.d_in + n) = v;
+    }
   }
 }
 
