@@ -592,6 +592,10 @@ class GhostPlan:
             # V = X [A_1 .. A_k]
             wx = torch.cat([s.A.detach().to(dt).t() for s in ch], dim=0).contiguous()
             self._keep.append(wx)
+            if self._mirrored(ch, dt, v):
+                self._mirror_rows(ch[0], x, wx, dt, v, qaddr, vbase, ubase, ldq, planes, es, pj, ft, tab,
+                                  fused_rows, slot_base)
+                continue
             tab(pj, dt, rtot, N.PJ_FIELDS).add(
                 {
                     N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
@@ -881,6 +885,72 @@ class GhostPlan:
         info = [(name, dt, total, nb[0], nb[1]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
         after_clip = _AFTER_CLIP
         self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
+
+    def _mirrored(self, ch: list[LoraSite], dt: torch.dtype, v: _SegView) -> bool:
+        """Whether a one-site chunk reads its activation once and its output
+        gradient twice (U = G B^T first, then V and dA in one fused pass over
+        X, then dB): fewer bytes when d_in > d_out, e.g. a down projection."""
+        if len(ch) != 1 or ch[0].a_leaf is None:
+            return False
+        s = ch[0]
+        x = _rows(s.x)
+        return x.shape[1] > s.g.shape[-1] and self._fusable(dt, s.A.shape[1], v, x)
+
+    def _mirror_rows(self, s, x, wx, dt, v, qaddr, vbase, ubase, ldq, planes, es, pj, ft, tab, fused_rows,
+                     slot_base) -> None:
+        lib = N.load()
+        r = s.A.shape[1]
+        d_in = x.shape[1]
+        g = _rows(s.g)
+        wb = s.B.detach().to(dt).contiguous()
+        self._keep += [g, wb]
+        d_out = g.shape[1]
+        n_rows, n_seg, valid, sf = v.n_rows, v.n_seg, v.valid, v.first
+        # U = G B^T (the projection kernel on G).
+        tab(pj, dt, r, N.PJ_FIELDS).add(
+            {
+                N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
+                N.PJ_W: wb.data_ptr(), N.PJ_R: r,
+                N.PJ_Q: qaddr(ubase, 0, False), N.PJ_QLO: qaddr(ubase, 0, True),
+                N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
+            },
+            lib.odp_project_blocks(dtype_code(dt), n_rows, r),
+            (valid * d_out + r * d_out + planes * r * valid) * es,
+        )
+        # V = X A and the dA^T rows (scaling * sum_t U[k][t] X[t][m]) in one
+        # pass over X: the fused kernel with X, A^T and U in the places of G,
+        # B and V.  One row per segment, most work first.
+        pe0 = self._pe_addr(s.a_leaf)
+        pe_es = self.pe[dt].element_size()
+        row = {
+            N.FT_P: x.data_ptr(), N.FT_LDP: x.stride(0), N.FT_M: d_in,
+            N.FT_Q: qaddr(ubase, 0, False), N.FT_QLO: qaddr(ubase, 0, True),
+            N.FT_LDQ: ldq, N.FT_R: r, N.FT_NSEG: 1,
+            N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
+            N.FT_LEAF0 + 1: 0 | (r << 16) | self._pe_bits(s.a_leaf),
+            N.FT_LEAF0 + 2: slot_base[s.a_leaf],
+            N.FP_W: wx.data_ptr(), N.FP_U: qaddr(vbase, 0, False), N.FP_ULO: qaddr(vbase, 0, True),
+        }
+        for j, ln in enumerate(v.segs.lengths):
+            rj = dict(row)
+            rj[N.FT_SEG_FIRST] = sf + j
+            rj[N.FT_LEAF0] = pe0 + j * r * d_in * pe_es
+            fused_rows.append((-ln * d_in, len(fused_rows), rj, 1,
+                               (ln * d_in + r * d_in + 2 * planes * r * ln) * es + r * d_in * es))
+        # dB^T rows from G and V.
+        if s.b_leaf is not None:
+            tab(ft, dt, r, N.FT_FIELDS).add(
+                {
+                    N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
+                    N.FT_Q: qaddr(vbase, 0, False), N.FT_QLO: qaddr(vbase, 0, True),
+                    N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
+                    N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
+                    N.FT_LEAF0: self._pe_addr(s.b_leaf),
+                    N.FT_LEAF0 + 1: 0 | (r << 16) | self._pe_bits(s.b_leaf),
+                    N.FT_LEAF0 + 2: slot_base[s.b_leaf],
+                },
+                n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
+                (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es)
 
     def _fusable(self, dt: torch.dtype, r: int, v: _SegView, g: torch.Tensor) -> bool:
         """Whether a site's G side runs as one odp_seg_factor_project pass."""

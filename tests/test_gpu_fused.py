@@ -1,5 +1,8 @@
 """The single-pass G side of LoRA sites (odp_seg_factor_project) against the
-two-kernel path (odp_project + odp_seg_factor) and the CPU oracle.
+two-kernel path (odp_project + odp_seg_factor) and the CPU oracle.  A
+one-site activation wider than its output gradient takes the mirrored
+order instead (U from G first, then V and dA in one fused pass over X,
+then dB), also compared bit for bit with the two-kernel path.
 
 Both paths accumulate U = G B^T over G's columns and the dB rows over the
 segment's tokens in the same order of 32-wide MFMA blocks, so their results
@@ -65,6 +68,9 @@ CASES = [
     (3, 1081, [1081, 0, 517], 64, [512], [16], ()),               # longest segment, empty segment
     (4, 40, [40, 39, 17, 25], 96, [1000, 200], [12, 4], ()),      # ranks below 16, two sites share X
     (3, 64, [64, 50, 9], 128, [256, 136], [8, 8], ((0, "B"), (1, "A"))),  # frozen factors
+    (4, 80, [80, 33, 1, 64], 520, [136], [16], ()),               # mirrored: d_in > d_out
+    (3, 64, [64, 0, 40], 392, [128], [8], ((0, "B"),)),           # mirrored, frozen B
+    (3, 1081, [1081, 5, 300], 264, [64], [16], ()),               # mirrored, longest segment
 ]
 
 
@@ -84,13 +90,15 @@ def test_fused_g_side_equals_two_pass(n_ex, T, lengths, d_in, d_outs, ranks, fro
         assert torch.equal(a, b)
 
 
-def test_fused_g_side_unaligned_segments_match_oracle():
+@pytest.mark.parametrize("d_in,d_out", [(72, 328), (520, 72)])
+def test_fused_g_side_unaligned_segments_match_oracle(d_in, d_out):
     # Packed rows: segment starts are not multiples of 8.
+    print(f"fused, unaligned segments: d_in={d_in} d_out={d_out}", flush=True)
     lengths = [13, 37, 77, 0, 100]
     starts = [0, 13, 50, 127, 127]
     n_rows = 240
     seg = Segments(starts, lengths, list(range(5)), 5, n_rows)
-    X, sites, leaves, shapes = _sites(n_rows, 72, [328], [16], seed=5)
+    X, sites, leaves, shapes = _sites(n_rows, d_in, [d_out], [16], seed=5)
     p1, r1 = _plan(X, sites, leaves, shapes, seg, fuse=True, C=1e30)
     p0, r0 = _plan(X, sites, leaves, shapes, seg, fuse=False, C=1e30)
     assert torch.equal(r1.norms, r0.norms)
@@ -101,3 +109,5 @@ def test_fused_g_side_unaligned_segments_match_oracle():
     assert torch.allclose(got, want, rtol=2e-2, atol=1e-30), (got, want)
     gb = r1.leaves[1].double().cpu()
     assert (gb - dB.sum(0)).norm() <= 2e-2 * dB.sum(0).norm()
+    ga = r1.leaves[0].double().cpu()
+    assert (ga - dA.sum(0)).norm() <= 2e-2 * dA.sum(0).norm()
