@@ -470,15 +470,32 @@ class GhostPlan:
             leaf_slots[m.leaf] = int(N.load().odp_sqnorm_blocks(n))
         # Linear sites: per site its norm form, segment view and first partial
         # slot within its leaf (the slices of a stacked leaf follow each other).
+        # Sites whose per-example gradients fit in linear_pe_bytes keep them:
+        # the outer form stores them (bf16) as it computes the norms, and
+        # the clipped sum becomes a pass over storage.  That beats the Gram
+        # form, which would still need the clipped-sum GEMM, whatever the
+        # sequence length.  The other sites take the faster norm form and
+        # the GEMM.
+        budget = self.linear_pe_bytes
+        if budget is None:
+            budget = torch.cuda.mem_get_info(dev)[0] // 2 if dev.type == "cuda" and lins else 0
+        lin_pe: dict[int, int] = {}  # site -> element offset in self.lin_pe
+        pe_total = 0
         lin_form: list[int] = []
         lin_view: list[_SegView] = []
         lin_off: list[int] = []
         others = set(leaf_slots)
         slices: dict[int, set[int]] = {}
-        for ls in lins:
+        for i, ls in enumerate(lins):
             d_in, d_out = ls.x.shape[-1], ls.g.shape[-1]
             v = reg.view(ls.segments)
-            form = ls.form if ls.form is not None else choose_form(v.max_len, d_in, d_out)
+            n = v.n_seg * d_in * d_out
+            if ls.form in (None, N.FORM_OUTER) and (pe_total + n) * 2 <= budget:
+                lin_pe[i] = pe_total
+                pe_total += (n + 127) // 128 * 128
+                form = N.FORM_OUTER
+            else:
+                form = ls.form if ls.form is not None else choose_form(v.max_len, d_in, d_out)
             tiles = int(lib.odp_linear_tiles(form, d_in, d_out, v.max_len))
             lin_form.append(form)
             lin_view.append(v)
@@ -707,20 +724,6 @@ class GhostPlan:
             )
             mat_pe[m.leaf] = pe_m
 
-        # Outer-form sites whose per-example gradients fit in linear_pe_bytes
-        # keep them (bf16, written by the norm kernel) and are clipped and
-        # summed like stored per-example gradients; the rest go through the
-        # clipped-sum GEMM.
-        budget = self.linear_pe_bytes
-        if budget is None:
-            budget = torch.cuda.mem_get_info(dev)[0] // 2 if dev.type == "cuda" and lins else 0
-        lin_pe: dict[int, int] = {}  # site -> element offset in self.lin_pe
-        pe_total = 0
-        for i, ls in enumerate(lins):
-            n = lin_view[i].n_seg * ls.x.shape[-1] * ls.g.shape[-1]
-            if lin_form[i] == N.FORM_OUTER and (pe_total + n) * 2 <= budget:
-                lin_pe[i] = pe_total
-                pe_total += (n + 127) // 128 * 128
         self.lin_pe = torch.empty(pe_total, dtype=torch.bfloat16, device=dev)
         if self.second_moment and len(lin_pe) < len(lins):
             raise ValueError("second moments of full-weight linear sites need their per-example "

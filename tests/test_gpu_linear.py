@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from opaque_amd import _native as N
-from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LinearSite, MaterializedLeaf, Segments
+from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LinearSite, MaterializedLeaf, Segments, choose_form
 from opaque_amd.guard import guard_constants, leaf_guards
 from oracle import dp_ref, lora_ref
 
@@ -322,3 +322,20 @@ def test_stored_linear_gradients_second_moment():
         want, want2 = y.sum(0) / 2.0, (y * y).sum(0) / 2.0
         assert (r.leaves[k].double().cpu() - want).norm() <= 2e-4 * want.norm(), k
         assert (r.second_moment[k].double().cpu() - want2).norm() <= 2e-4 * want2.norm(), k
+
+
+def test_storage_takes_the_outer_form():
+    """Short examples favour the Gram form for the norms alone; with room to
+    store the per-example gradients the outer form (which stores them) is
+    taken instead, and both plans agree."""
+    print("form choice with storage", flush=True)
+    X, G, seg = _case(4, 64, 512, 512, [64, 40, 64, 9], seed=31)
+    assert choose_form(64, 512, 512) == N.FORM_GRAM
+    res = {}
+    for b in (None, 0):
+        plan, r, _ = _plan(X, G, seg, C=5.0, mode=N.CLIP_FIXED, form=None, pe_bytes=b)
+        kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
+        assert kinds == ({N.FORM_OUTER} if b is None else {N.FORM_GRAM}), (b, kinds)
+        res[b] = (r.leaves[0].double().cpu(), r.norms.double().cpu())
+    assert torch.allclose(res[None][1], res[0][1], rtol=1e-4)
+    assert (res[None][0] - res[0][0]).norm() <= 1e-2 * res[0][0].norm()
