@@ -243,7 +243,14 @@ def setup_c4(args, dev):
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=dev,
                      linear_pe_bytes=pe_bytes)
-    flops = sum(f for *_, f in plan.launch_info)
+    # Algorithmic flops of the C4 step: per example and weight the cheaper
+    # norm form, min(2 L d_in d_out, 2 L^2 (d_in + d_out)), plus the clipped
+    # sum's 2 L d_in d_out, whichever kernels run.
+    flops = 0
+    for L in seg.lengths:
+        for d_in, d_out in LAYER_SHAPES.values():
+            flops += min(2 * L * d_in * d_out, 2 * L * L * (d_in + d_out)) + 2 * L * d_in * d_out
+    flops *= args.layers
     config = {
         "workload": "C4: Llama-3-8B-shaped full weights, 32 layers x 7 linears, batch 8 x seq 4096, "
                     "PerGroup fixed clipping (one threshold per linear type), noise multiplier 1.0",
@@ -358,6 +365,8 @@ def main():
         "stage_ms": stage_ms,
         "mfma_frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
         "algorithmic_tflops": flops / (ms * 1e-3) / 1e12,
+        "executed_mfma_tflops": (sum(f for *_, f in plan.launch_info) / (ms * 1e-3) / 1e12
+                                 if args.workload == "c4" else None),
         "clipped_fraction": float(res.clipped_total.float().mean().item()),
     }
     if args.cpu_baseline == "on" and args.workload == "c3":
