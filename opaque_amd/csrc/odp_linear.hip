@@ -178,6 +178,7 @@ constexpr int RPW = OK / NW;                      // tile rows each wave loads p
 #define ODP_LIN_RING 4  // LDS stages of the outer-form ring (RING - 1 steps in flight)
 #endif
 constexpr int RING = ODP_LIN_RING;
+constexpr int OUTER_GROUP = 8;  // tile rows per group in the outer-norm work order
 static_assert(WN == 64 && 2 * WM * WN <= OUTER_STAGE && NW <= 2 * RING,
               "two waves' bf16 blocks fit in each ring stage (outer-norm store)");
 static_assert((RING == 3 || RING == 4) && (RING - 2) * (A_DMA + B_DMA) < 64, "ring depth");
@@ -353,9 +354,8 @@ __device__ __forceinline__ void zero_acc(f32x4_t (&acc)[I][J]) {
 // a multiple of 8 so that blockIdx % 8 == local % 8.  With BY_XCD and 8 or
 // more segments, XCD j works through segments j, j + 8, ... so that an
 // example's rows are cached by one L2 only (this pays for the Gram form,
-// whose workgroups drift apart in the feature loop; the outer forms keep
-// consecutive items on different XCDs, which measured faster).  Returns
-// false for padding blocks.
+// whose workgroups drift apart in the feature loop).  Returns false for
+// padding blocks.
 template <bool BY_XCD>
 __device__ __forceinline__ bool seg_item(int local, int n_seg, int per_seg, int& seg, int& item) {
   if (BY_XCD && n_seg >= 8) {
@@ -420,8 +420,22 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
   const int tn_count = (int)((P.d_in + ON - 1) / ON);
   const int tm_count = (int)((P.d_out + OM - 1) / OM);
   const int tiles = tn_count * tm_count;
-  int seg, tile;
-  if (!seg_item<false>(bid - ws[p], P.n_seg, tiles, seg, tile)) return;
+  // Work order: XCD j (blockIdx % 8) takes the j-th eighth of the problem's
+  // (segment, tile) items, so that the workgroups on one L2 share a
+  // segment, and walks its tiles in groups of OUTER_GROUP tile rows, so that
+  // the concurrent ones share operand columns (+1.5 % on C4 shapes).
+  const int local = bid - ws[p];
+  const int nblk = (P.n_seg * tiles + 7) / 8 * 8;  // odp_linear_norm_blocks
+  const int pid = (local & 7) * (nblk >> 3) + (local >> 3);
+  if (pid >= P.n_seg * tiles) return;
+  const int seg = pid / tiles;
+  int tile;
+  {
+    const int t = pid - seg * tiles;
+    const int per_group = OUTER_GROUP * tn_count, g = t / per_group, first_m = g * OUTER_GROUP;
+    const int gm = min(tm_count - first_m, OUTER_GROUP), rr = t - g * per_group;
+    tile = (first_m + rr % gm) * tn_count + rr / gm;
+  }
   const int64_t o0 = (int64_t)(tile / tn_count) * OM, n0 = (int64_t)(tile % tn_count) * ON;
   const int gs = P.seg_first + seg;
   const int64_t t_begin = sstart[gs], t_end = t_begin + slen[gs];
