@@ -402,14 +402,19 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
     }
   }
   __syncthreads();
-  const int t = threadIdx.x;
+  // Per leaf, wave 0 sums its rank x 4 column partials: lane l takes
+  // entries l, l + 64, ... in order, then a butterfly over the lanes (a
+  // fixed order, so runs stay bitwise reproducible).
+  if (wave == 0) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    if (t == q && q < L.n) {
-      double total = 0.0;
-      for (int k = L.col0[q]; k < L.col0[q] + L.rank[q]; ++k)
-        for (int w = 0; w < 4; ++w) total += colsq[w][k];
-      part[(int64_t)ex * part_stride + L.slot[q] + tile] = total;
+    for (int q = 0; q < 4; ++q) {
+      if (q < L.n) {
+        double v = 0.0;
+        for (int e = lane; e < 4 * L.rank[q]; e += 64) v += colsq[e & 3][L.col0[q] + (e >> 2)];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) part[(int64_t)ex * part_stride + L.slot[q] + tile] = v;
+      }
     }
   }
 }
@@ -753,7 +758,9 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       }
     }
     factor_epilogue<NJ, 1>(acc, r, scale, M, m_base, seg, c, ex, part_stride, L, part);
-    __syncthreads();  // the partial-sum scratch of the epilogue is reused by the next chunk
+    // The epilogue's partial-sum scratch is reused by the next chunk's; the
+    // next chunk's step barriers order that, except for an empty segment.
+    if (nsteps == 0) __syncthreads();
   }
 
   // U: lane holds rows 4 (lane >> 4) + i, column lane & 15 of each step's
