@@ -108,8 +108,10 @@ int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
  * For every segment s and column k < r of Q (up to 4 leaves laid side by
  * side in Q's columns):  pe_leaf[s][k - col0][m] = scaling * sum_{t in s}
  * Q[k][t] * P[t][m],  m < M.  Each workgroup covers FACTOR_MTILE values of
- * m and writes, per leaf, its fp64 sum of squares to
- * part[seg_example[s] * part_stride + slot_base + tile].  Requirements: M
+ * m and writes, per leaf, the fp64 sum of squares of each of its four
+ * waves to part[seg_example[s] * part_stride + slot_base +
+ * ODP_FT_WAVE_SLOTS * tile + wave] (a leaf uses ODP_FT_WAVE_SLOTS slots per
+ * tile, so no workgroup barrier is needed).  Requirements: M
  * and the P row pitch are multiples of 8 (bf16) or 4 (f32); Q is the output
  * of odp_project (ldq a multiple of 8 and >= n_rows + 32), readable for
  * 16*ceil(r/16) rows; rows k >= r may hold anything (they are discarded). */
@@ -125,9 +127,11 @@ enum {
                          pe_bf16 << 32, [12+3l] slot_base;
                          leaves sorted by col0                               */
   ODP_FT_QLO = 22,    /* lo plane of Q (bf16 only)                           */
-  ODP_FT_FIELDS = 24
+  ODP_FT_FIELDS = 24,
+  ODP_FT_WAVE_SLOTS = 4 /* partial slots per leaf and tile                   */
 };
-/* M-tiles (and partial slots per leaf) of a problem; the bf16 tile width
+/* M-tiles of a problem (a leaf uses ODP_FT_WAVE_SLOTS partial slots per
+ * tile); the bf16 tile width
  * depends on the rank.  Every problem of one table must have
  * ceil(ODP_FT_R / 16) == nkb (1..4).                                       */
 int64_t odp_seg_factor_tiles(int dtype, int64_t M, int32_t r);

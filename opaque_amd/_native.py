@@ -24,6 +24,7 @@ FT_FIELDS = 24
 FT_P, FT_LDP, FT_M, FT_Q, FT_LDQ, FT_R, FT_SEG_FIRST, FT_NSEG, FT_SCALING, FT_NLEAF = range(10)
 FT_LEAF0 = 10
 FT_QLO = 22
+FT_WAVE_SLOTS = 4  # partial slots per LoRA leaf and M-tile
 FP_W, FP_U, FP_ULO = 13, 14, 15
 SS_FIELDS = 8
 SS_PE, SS_M, SS_RANK, SS_SEG_FIRST, SS_NSEG, SS_OUT, SS_FLAGS, SS_OUT2 = range(8)

@@ -347,7 +347,7 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
                                                 int ex, int64_t part_stride,
                                                 const FactorLeaves& L, double* __restrict__ part) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __shared__ double colsq[4][64];
+  double wsum[4] = {0.0, 0.0, 0.0, 0.0};  // this wave's sum of squares per leaf
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
     double cs[4];
@@ -390,7 +390,8 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
         }
       }
     }
-    // Sum over the 16 lanes that share a column (same lane >> 4).
+    // Sum over the 16 lanes that share a column (same lane >> 4), then add
+    // the column to its leaf's sum.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       double v = cs[i];
@@ -398,23 +399,21 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
       v += __shfl_xor(v, 2);
       v += __shfl_xor(v, 4);
       v += __shfl_xor(v, 8);
-      if ((lane & 15) == 0) colsq[wave][kb * 16 + 4 * (lane >> 4) + i] = v;
+      const int k = kb * 16 + 4 * (lane >> 4) + i;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q < L.n && k >= L.col0[q] && k < L.col0[q] + L.rank[q]) wsum[q] += v;
     }
   }
-  __syncthreads();
-  // Per leaf, wave 0 sums its rank x 4 column partials: lane l takes
-  // entries l, l + 64, ... in order, then a butterfly over the lanes (a
-  // fixed order, so runs stay bitwise reproducible).
-  if (wave == 0) {
+  // The four column groups of the wave, then one slot per (tile, wave): no
+  // workgroup barrier, and a fixed order, so runs stay bitwise reproducible.
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q < L.n) {
-        double v = 0.0;
-        for (int e = lane; e < 4 * L.rank[q]; e += 64) v += colsq[e & 3][L.col0[q] + (e >> 2)];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) part[(int64_t)ex * part_stride + L.slot[q] + tile] = v;
-      }
+  for (int q = 0; q < 4; ++q) {
+    if (q < L.n) {
+      double v = wsum[q];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (lane == 0) part[(int64_t)ex * part_stride + L.slot[q] + ODP_FT_WAVE_SLOTS * tile + wave] = v;
     }
   }
 }
@@ -758,9 +757,6 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       }
     }
     factor_epilogue<NJ, 1>(acc, r, scale, M, m_base, seg, c, ex, part_stride, L, part);
-    // The epilogue's partial-sum scratch is reused by the next chunk's; the
-    // next chunk's step barriers order that, except for an empty segment.
-    if (nsteps == 0) __syncthreads();
   }
 
   // U: lane holds rows 4 (lane >> 4) + i, column lane & 15 of each step's

@@ -461,11 +461,12 @@ class GhostPlan:
                 d_out = s.B.shape[1]
                 if s.a_leaf is not None:
                     # dA leaves of one activation share a pass of width rtot.
-                    leaf_slots[s.a_leaf] = int(lib.odp_seg_factor_tiles(dcode, d_in, rtot if fused else r))
+                    leaf_slots[s.a_leaf] = N.FT_WAVE_SLOTS * int(
+                        lib.odp_seg_factor_tiles(dcode, d_in, rtot if fused else r))
                     leaf_rank_m[s.a_leaf] = (r, d_in)
                     pe_elems[s.a_leaf] = n_seg * r * d_in
                 if s.b_leaf is not None:
-                    leaf_slots[s.b_leaf] = int(lib.odp_seg_factor_tiles(dcode, d_out, r))
+                    leaf_slots[s.b_leaf] = N.FT_WAVE_SLOTS * int(lib.odp_seg_factor_tiles(dcode, d_out, r))
                     leaf_rank_m[s.b_leaf] = (r, d_out)
                     pe_elems[s.b_leaf] = n_seg * r * d_out
         for m in mats:

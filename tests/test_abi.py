@@ -62,6 +62,7 @@ def test_field_indices_match_header():
     assert value("ODP_FT_FIELDS") == N.FT_FIELDS
     assert value("ODP_FT_LEAF0") == N.FT_LEAF0
     assert value("ODP_FT_QLO") == N.FT_QLO
+    assert value("ODP_FT_WAVE_SLOTS") == N.FT_WAVE_SLOTS
     assert value("ODP_SS_FIELDS") == N.SS_FIELDS
     assert value("ODP_SQ_FIELDS") == N.SQ_FIELDS
     assert value("ODP_NZ_FIELDS") == N.NZ_FIELDS
