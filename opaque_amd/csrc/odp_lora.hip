@@ -681,7 +681,88 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   f32x4_t acc_u[FP_STEPS];
 #pragma unroll
   for (int st = 0; st < FP_STEPS; ++st) acc_u[st] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const FactorLeaves L = read_leaves(f);
+  const FactorLeaves L = read_leaves(f);  // one leaf at column 0, rank r, bf16 rows
+
+  // A chunk's dB rows (bf16) and this wave's norm partial wait in registers
+  // and are stored after the next step's barrier: a barrier waits for every
+  // memory operation in flight, so stores issued just before one would
+  // stall it for their whole latency.  The arithmetic is factor_epilogue's
+  // for one leaf, in the same order.
+  uint32_t pend[NJ * 2];
+  double pend_sq = 0.0;
+  int32_t pend_m0 = -1, pend_tile = 0;  // pend_m0 < 0: nothing pending
+  auto hold = [&](const f32x4_t (&acc)[NJ][1], int32_t m_base, int tile) {
+    double wsum = 0.0, cs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      cs[i] = 0.0;
+      const int k = 4 * (lane >> 4) + i;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int32_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
+        const float v = scale * acc[j][0][i];
+        const uint32_t h = odp_f2bf(v);
+        if (i & 1)
+          pend[2 * j + (i >> 1)] |= h << 16;
+        else
+          pend[2 * j + (i >> 1)] = h;
+        if (k < r && m < M) {
+          const float vf = isfinite(v) ? v : 0.f;
+          cs[i] += (double)__fmul_rn(vf, vf);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      double v = cs[i];
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      if (4 * (lane >> 4) + i < r) wsum += v;
+    }
+    wsum += __shfl_xor(wsum, 16);
+    wsum += __shfl_xor(wsum, 32);
+    pend_sq = wsum;
+    pend_m0 = m_base;
+    pend_tile = tile;
+  };
+  // Each 16 x 16 block of dB rows leaves as 8-byte pieces: a 4 x 4
+  // transpose within each quad of lanes (two exchanges) turns lane
+  // (g, 4q + t)'s column of rows 4g .. 4g + 3 into row 4g + t, columns
+  // 4q .. 4q + 3.
+  auto flush = [&]() {
+    if (pend_m0 < 0) return;
+    uint16_t* pe0 = (uint16_t*)L.pe[0];
+    const int t = lane & 3, tl = t & 1, th = t >> 1;
+    const int k = 4 * (lane >> 4) + t;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t h0 = pend[2 * j] & 0xffffu, h1 = pend[2 * j] >> 16;
+      const uint32_t h2 = pend[2 * j + 1] & 0xffffu, h3 = pend[2 * j + 1] >> 16;
+      // Rows of the other parity to the odd/even neighbour.
+      const uint32_t r1 = (uint32_t)__shfl_xor((int)(tl ? (h0 | (h2 << 16)) : (h1 | (h3 << 16))), 1);
+      // Rows 4g + 2a + tl, columns of this lane pair (low half: even column).
+      const uint32_t p0 = tl ? ((r1 & 0xffffu) | (h1 << 16)) : (h0 | (r1 << 16));
+      const uint32_t p1 = tl ? ((r1 >> 16) | (h3 << 16)) : (h2 | (r1 & 0xffff0000u));
+      // Row pairs across the two lane pairs of the quad.
+      const uint32_t r2 = (uint32_t)__shfl_xor((int)(th ? p0 : p1), 2);
+      const uint32_t keep = th ? p1 : p0;
+      const int32_t m = pend_m0 + (NJ * wave + j) * 16 + 4 * ((lane & 15) >> 2);
+      if (k < r && m < M) {
+        uint2 v;
+        v.x = th ? r2 : keep;
+        v.y = th ? keep : r2;
+        *(uint2*)(pe0 + ((int64_t)seg * r + k) * M + m) = v;
+      }
+    }
+    if (lane == 0) part[(int64_t)ex * part_stride + L.slot[0] + ODP_FT_WAVE_SLOTS * pend_tile + wave] = pend_sq;
+    pend_m0 = -1;
+  };
+  // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
+  // lane holds B[lane & 15][32 ks + 8 (lane >> 4) .. + 7].  Loaded after the
+  // chunk's first barrier, like the stores above.
+  const uint16_t* wrow = W + (int64_t)((lane & 15) < r ? (lane & 15) : 0) * M;
 
   u32x4_t qv;
   int buf = 0;
@@ -693,19 +774,7 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
     // hoisted out of it for every step (which exhausts registers).
     int32_t tc0 = t_lo;
     __asm__ volatile("" : "+s"(tc0));
-    // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
-    // lane holds B[lane & 15][32 ks + 8 (lane >> 4) .. + 7].
     bf16x8_t wf[FP_MT / 32];
-    {
-      const int n = lane & 15;
-      const uint16_t* wrow = W + (int64_t)(n < r ? n : 0) * M;
-#pragma unroll
-      for (int ks = 0; ks < FP_MT / 32; ++ks) {
-        const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
-        const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
-        wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
-      }
-    }
     f32x4_t acc[NJ][1];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -719,6 +788,15 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
           load(buf ^ 1, tc0 + (st + 1) * FP_T, m_base, qv);
         else if (c + 1 < nchunks)
           load(buf ^ 1, tc0, m_base + FP_MT, qv);
+        if (st == 0) {
+          flush();
+#pragma unroll
+          for (int ks = 0; ks < FP_MT / 32; ++ks) {
+            const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
+            const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
+            wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
         const uint16_t* sp = lds + buf * STAGE;
         // dB rows: B operand = G columns by transposing reads, A = V hi / lo.
@@ -756,8 +834,10 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
         buf ^= 1;
       }
     }
-    factor_epilogue<NJ, 1>(acc, r, scale, M, m_base, seg, c, ex, part_stride, L, part);
+    hold(acc, m_base, c);
+    if (nsteps == 0) flush();  // no step of the next chunk will
   }
+  flush();
 
   // U: lane holds rows 4 (lane >> 4) + i, column lane & 15 of each step's
   // 16 x 16 block; tokens outside the segment belong to other workgroups.
