@@ -341,6 +341,24 @@ __device__ __forceinline__ FactorLeaves read_leaves(const int64_t* f) {
   return L;
 }
 
+// 4 x 4 transpose within each quad of lanes: lane t of the quad holds
+// x[i] = B[i][t] on entry and x[c] = B[t][c] on return (two exchanges).
+__device__ __forceinline__ void quad_transpose4(uint32_t (&x)[4]) {
+  const int t = threadIdx.x & 3, tl = t & 1, th = t >> 1;
+  const uint32_t r0 = (uint32_t)__shfl_xor((int)(tl ? x[0] : x[1]), 1);
+  const uint32_t r1 = (uint32_t)__shfl_xor((int)(tl ? x[2] : x[3]), 1);
+  // e_ab = B[2a + tl][2 th + b]
+  const uint32_t e00 = tl ? r0 : x[0], e01 = tl ? x[1] : r0;
+  const uint32_t e10 = tl ? r1 : x[2], e11 = tl ? x[3] : r1;
+  const uint32_t ra = (uint32_t)__shfl_xor((int)(th ? e00 : e10), 2);
+  const uint32_t rb = (uint32_t)__shfl_xor((int)(th ? e01 : e11), 2);
+  const uint32_t ka = th ? e10 : e00, kb = th ? e11 : e01;
+  x[0] = th ? ra : ka;
+  x[1] = th ? rb : kb;
+  x[2] = th ? ka : ra;
+  x[3] = th ? kb : rb;
+}
+
 template <int NJ, int NKB>
 __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], int r, float scale,
                                                 int64_t M, int64_t m_base, int seg, int tile,
@@ -370,24 +388,52 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
         }
       // Columns of frozen factors between leaves belong to no leaf.
       if (k < lc0 || k - lc0 >= lrk) continue;
-      const int64_t row = ((int64_t)seg * lrk + (k - lc0)) * M;
+      (void)lpe;
+      (void)l16;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int64_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
         if (m < M) {
-          const float v = scale * acc[j][kb][i];
-          // The stored copy (summed after clipping) is in the leaf's dtype,
-          // as the reference's per-example gradients are; the norm below
-          // uses the fp32 value.
-          if (l16)
-            ((uint16_t*)lpe)[row + m] = odp_f2bf(v);
-          else
-            lpe[row + m] = v;
           // Non-finite entries count as 0 (nan_to_num); squares are taken
           // in fp32 like the reference's float32 accumulation dtype.
+          const float v = scale * acc[j][kb][i];
           const float vf = isfinite(v) ? v : 0.f;
           cs[i] += (double)__fmul_rn(vf, vf);
         }
+      }
+    }
+    // The stored copy (summed after clipping) is in the leaf's dtype, as the
+    // reference's per-example gradients are (the norm above uses the fp32
+    // values).  After a quad transpose each lane holds 4 consecutive
+    // columns of one row: 8-byte (bf16) or 16-byte (f32) stores.
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      uint32_t x[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = __float_as_uint(scale * acc[j][kb][i]);
+      quad_transpose4(x);
+      const int k = kb * 16 + 4 * (lane >> 4) + (lane & 3);
+      const int64_t mq = m_base + (NJ * wave + j) * 16 + 4 * ((lane & 15) >> 2);
+      if (k >= r || mq >= M) continue;
+      float* lpe = L.pe[0];
+      int lc0 = L.col0[0], lrk = L.rank[0], l16 = L.pe16[0];
+#pragma unroll
+      for (int q = 1; q < 4; ++q)
+        if (q < L.n && k >= L.col0[q]) {
+          lpe = L.pe[q];
+          lc0 = L.col0[q];
+          lrk = L.rank[q];
+          l16 = L.pe16[q];
+        }
+      if (k < lc0 || k - lc0 >= lrk) continue;
+      const int64_t at = ((int64_t)seg * lrk + (k - lc0)) * M + mq;
+      if (l16) {
+        uint2 v;
+        v.x = (uint32_t)odp_f2bf(__uint_as_float(x[0])) | ((uint32_t)odp_f2bf(__uint_as_float(x[1])) << 16);
+        v.y = (uint32_t)odp_f2bf(__uint_as_float(x[2])) | ((uint32_t)odp_f2bf(__uint_as_float(x[3])) << 16);
+        *(uint2*)((uint16_t*)lpe + at) = v;
+      } else {
+        *(u32x4_t*)(lpe + at) = u32x4_t{x[0], x[1], x[2], x[3]};
       }
     }
     // Sum over the 16 lanes that share a column (same lane >> 4), then add
