@@ -15,7 +15,7 @@ namespace {
 constexpr int CL_THREADS = 256;
 constexpr int CL_MAX_GROUPS = 1024;
 constexpr int SS_THREADS = 256;
-constexpr int SS_ELEMS = 4;  // elements per thread
+constexpr int SS_ELEMS = 8;  // elements per thread
 
 __device__ __forceinline__ double block_sum_fixed(double v, double* red) {
   const int t = threadIdx.x;
@@ -81,8 +81,9 @@ __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
   }
 }
 
-// Clipped sum of one leaf per problem: 4 consecutive elements per thread,
-// summed over the leaf's segments in segment order.
+// Clipped sum of one leaf per problem: 8 consecutive elements per thread
+// (one 16-byte load per segment for bf16), summed over the leaf's segments
+// in segment order.
 __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
     const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
     const int32_t* __restrict__ sex, const float* __restrict__ scales, int n_ex, int n_groups,
@@ -106,49 +107,79 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
   const int64_t e0 = ((int64_t)(bid - ws[p]) * SS_THREADS + threadIdx.x) * SS_ELEMS;
   if (e0 >= E) return;
   const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
-  const bool vec = pdt == ODP_DTYPE_F32 && (E & 3) == 0;
-  const bool vec16 = pdt == ODP_DTYPE_BF16 && (E & 3) == 0;
-
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  f32x4_t acc2 = {0.f, 0.f, 0.f, 0.f};
+  // Whole 8-element pieces load as vectors (rows of E elements stay 16-byte
+  // aligned when E is a multiple of 8).
+  const bool whole = (E & 7) == 0;
+  float acc[SS_ELEMS], acc2[SS_ELEMS];
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = 0.f;
   for (int s = 0; s < n_seg; ++s) {
     const float c = sc[sex[seg_first + s]];
-    f32x4_t v;
-    if (vec) {
-      v = *(const f32x4_t*)(pe + (int64_t)s * E + e0);
-    } else if (vec16) {
-      const uint2 w = *(const uint2*)((const uint16_t*)pe + (int64_t)s * E + e0);
-      v[0] = __uint_as_float(w.x << 16);
-      v[1] = __uint_as_float(w.x & 0xffff0000u);
-      v[2] = __uint_as_float(w.y << 16);
-      v[3] = __uint_as_float(w.y & 0xffff0000u);
+    float v[SS_ELEMS];
+    if (whole && pdt == ODP_DTYPE_F32) {
+      const f32x4_t a = *(const f32x4_t*)(pe + (int64_t)s * E + e0);
+      const f32x4_t b = *(const f32x4_t*)(pe + (int64_t)s * E + e0 + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = a[i];
+        v[4 + i] = b[i];
+      }
+    } else if (whole && pdt == ODP_DTYPE_BF16) {
+      const uint4 w = *(const uint4*)((const uint16_t*)pe + (int64_t)s * E + e0);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(ww[i] << 16);
+        v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+      }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < SS_ELEMS; ++i)
         v[i] = e0 + i < E ? odp_load_as_float(pe, (int64_t)s * E + e0 + i, pdt) : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < SS_ELEMS; ++i) {
       if (!isfinite(v[i])) v[i] = 0.f;  // nan_to_num of the per-example value
       const float y = __fmul_rn(c, v[i]);
       acc[i] = __fadd_rn(acc[i], y);
       acc2[i] = __fadd_rn(acc2[i], __fmul_rn(y, y));
     }
   }
+  float x[SS_ELEMS], x2[SS_ELEMS];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < SS_ELEMS; ++i) {
+    x[i] = odp_round_to(acc[i], odt);
+    if (normalize_by != 1.0f) x[i] = odp_round_to(__fdiv_rn(x[i], normalize_by), odt);
+    x2[i] = odp_round_to(acc2[i], odt);
+    if (normalize_by != 1.0f) x2[i] = odp_round_to(__fdiv_rn(x2[i], normalize_by), odt);
+  }
+  if (whole && !transpose && (odt == ODP_DTYPE_BF16 || odt == ODP_DTYPE_F32)) {
+    // 8 consecutive outputs: one 16-byte store (bf16) or two (f32).
+    auto put = [&](void* dst, const float (&y)[SS_ELEMS]) {
+      if (odt == ODP_DTYPE_BF16) {
+        uint4 w;
+        w.x = (uint32_t)odp_f2bf(y[0]) | ((uint32_t)odp_f2bf(y[1]) << 16);
+        w.y = (uint32_t)odp_f2bf(y[2]) | ((uint32_t)odp_f2bf(y[3]) << 16);
+        w.z = (uint32_t)odp_f2bf(y[4]) | ((uint32_t)odp_f2bf(y[5]) << 16);
+        w.w = (uint32_t)odp_f2bf(y[6]) | ((uint32_t)odp_f2bf(y[7]) << 16);
+        *(uint4*)((uint16_t*)dst + e0) = w;
+      } else {
+        *(f32x4_t*)((float*)dst + e0) = f32x4_t{y[0], y[1], y[2], y[3]};
+        *(f32x4_t*)((float*)dst + e0 + 4) = f32x4_t{y[4], y[5], y[6], y[7]};
+      }
+    };
+    put(out, x);
+    if (out2) put(out2, x2);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) {
     const int64_t e = e0 + i;
     if (e >= E) break;
     const int64_t k = e / M, m = e - k * M;
     const int64_t o = transpose ? m * rank + k : e;
-    float x = odp_round_to(acc[i], odt);
-    if (normalize_by != 1.0f) x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
-    odp_store_from_float(out, o, odt, x);
-    if (out2) {
-      float x2 = odp_round_to(acc2[i], odt);
-      if (normalize_by != 1.0f) x2 = odp_round_to(__fdiv_rn(x2, normalize_by), odt);
-      odp_store_from_float(out2, o, odt, x2);
-    }
+    odp_store_from_float(out, o, odt, x[i]);
+    if (out2) odp_store_from_float(out2, o, odt, x2[i]);
   }
 }
 
