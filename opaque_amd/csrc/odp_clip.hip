@@ -157,15 +157,16 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
     // 8 consecutive outputs: one 16-byte store (bf16) or two (f32).
     auto put = [&](void* dst, const float (&y)[SS_ELEMS]) {
       if (odt == ODP_DTYPE_BF16) {
-        uint4 w;
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 w;
         w.x = (uint32_t)odp_f2bf(y[0]) | ((uint32_t)odp_f2bf(y[1]) << 16);
         w.y = (uint32_t)odp_f2bf(y[2]) | ((uint32_t)odp_f2bf(y[3]) << 16);
         w.z = (uint32_t)odp_f2bf(y[4]) | ((uint32_t)odp_f2bf(y[5]) << 16);
         w.w = (uint32_t)odp_f2bf(y[6]) | ((uint32_t)odp_f2bf(y[7]) << 16);
-        *(uint4*)((uint16_t*)dst + e0) = w;
+        odp_gstore((u32x4*)((uint16_t*)dst + e0), w);
       } else {
-        *(f32x4_t*)((float*)dst + e0) = f32x4_t{y[0], y[1], y[2], y[3]};
-        *(f32x4_t*)((float*)dst + e0 + 4) = f32x4_t{y[4], y[5], y[6], y[7]};
+        odp_gstore((f32x4_t*)((float*)dst + e0), f32x4_t{y[0], y[1], y[2], y[3]});
+        odp_gstore((f32x4_t*)((float*)dst + e0 + 4), f32x4_t{y[4], y[5], y[6], y[7]});
       }
     };
     put(out, x);

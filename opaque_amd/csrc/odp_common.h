@@ -45,14 +45,24 @@ __device__ __forceinline__ bool odp_row_in_segments(int64_t row, const int32_t* 
   return row < (int64_t)start[lo] + (int64_t)len[lo];
 }
 
+// Stores to global memory through the global address space.  A store
+// through a generic pointer becomes a flat store, which also counts in the
+// LDS counter: every later wait for an LDS read or lane exchange would then
+// wait for the store to complete as well.
+#define ODP_GMEM __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ void odp_gstore(T* p, T v) {
+  *(ODP_GMEM T*)(ODP_GMEM void*)p = v;
+}
+
 __device__ __forceinline__ float odp_load_as_float(const void* p, int64_t i, int dtype) {
   if (dtype == ODP_DTYPE_BF16) return odp_bf2f(((const uint16_t*)p)[i]);
   return ((const float*)p)[i];
 }
 
 __device__ __forceinline__ void odp_store_from_float(void* p, int64_t i, int dtype, float v) {
-  if (dtype == ODP_DTYPE_BF16) ((uint16_t*)p)[i] = odp_f2bf(v);
-  else ((float*)p)[i] = v;
+  if (dtype == ODP_DTYPE_BF16) odp_gstore((uint16_t*)p + i, odp_f2bf(v));
+  else odp_gstore((float*)p + i, v);
 }
 
 // Rounds a float to the value it takes when stored in `dtype`.

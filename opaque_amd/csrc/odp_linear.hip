@@ -731,7 +731,7 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
     if (t >= n_rows) break;
     u32x4_t v = {0u, 0u, 0u, 0u};
     if (rowin[r]) v = scale_bf16x8(*(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(X + t * ldx + 8 * pc), rowc[r]);
-    *(u32x4_t*)(out + t * d + 8 * pc) = v;
+    odp_gstore((u32x4_t*)(out + t * d + 8 * pc), v);
   }
 }
 

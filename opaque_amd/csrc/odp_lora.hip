@@ -243,8 +243,8 @@ __global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict_
         for (int i = 0; i < 4; ++i) {
           if (rb + i < n_rows) {
             const uint16_t h = odp_f2bf(acc[b][kb][i]);
-            qhi[rb + i] = h;
-            qlo[rb + i] = odp_f2bf(acc[b][kb][i] - odp_bf2f(h));
+            odp_gstore(qhi + rb + i, h);
+            odp_gstore(qlo + rb + i, odp_f2bf(acc[b][kb][i] - odp_bf2f(h)));
           }
         }
       }
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) void k_project_f32(const int64_t* __restrict__
       float* q = Q + (int64_t)col * ldq;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (rb + i < n_rows) q[rb + i] = acc[kb][i];
+        if (rb + i < n_rows) odp_gstore(q + rb + i, acc[kb][i]);
     }
   }
 }
@@ -341,17 +341,25 @@ __device__ __forceinline__ FactorLeaves read_leaves(const int64_t* f) {
   return L;
 }
 
+// Value of the lane t ^ 1 (X1) or t ^ 2 (X2) of the same quad, by DPP.
+__device__ __forceinline__ uint32_t quad_x1(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+}
+__device__ __forceinline__ uint32_t quad_x2(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+}
+
 // 4 x 4 transpose within each quad of lanes: lane t of the quad holds
 // x[i] = B[i][t] on entry and x[c] = B[t][c] on return (two exchanges).
 __device__ __forceinline__ void quad_transpose4(uint32_t (&x)[4]) {
   const int t = threadIdx.x & 3, tl = t & 1, th = t >> 1;
-  const uint32_t r0 = (uint32_t)__shfl_xor((int)(tl ? x[0] : x[1]), 1);
-  const uint32_t r1 = (uint32_t)__shfl_xor((int)(tl ? x[2] : x[3]), 1);
+  const uint32_t r0 = quad_x1(tl ? x[0] : x[1]);
+  const uint32_t r1 = quad_x1(tl ? x[2] : x[3]);
   // e_ab = B[2a + tl][2 th + b]
   const uint32_t e00 = tl ? r0 : x[0], e01 = tl ? x[1] : r0;
   const uint32_t e10 = tl ? r1 : x[2], e11 = tl ? x[3] : r1;
-  const uint32_t ra = (uint32_t)__shfl_xor((int)(th ? e00 : e10), 2);
-  const uint32_t rb = (uint32_t)__shfl_xor((int)(th ? e01 : e11), 2);
+  const uint32_t ra = quad_x2(th ? e00 : e10);
+  const uint32_t rb = quad_x2(th ? e01 : e11);
   const uint32_t ka = th ? e10 : e00, kb = th ? e11 : e01;
   x[0] = th ? ra : ka;
   x[1] = th ? rb : kb;
@@ -428,12 +436,11 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
       if (k < lc0 || k - lc0 >= lrk) continue;
       const int64_t at = ((int64_t)seg * lrk + (k - lc0)) * M + mq;
       if (l16) {
-        uint2 v;
-        v.x = (uint32_t)odp_f2bf(__uint_as_float(x[0])) | ((uint32_t)odp_f2bf(__uint_as_float(x[1])) << 16);
-        v.y = (uint32_t)odp_f2bf(__uint_as_float(x[2])) | ((uint32_t)odp_f2bf(__uint_as_float(x[3])) << 16);
-        *(uint2*)((uint16_t*)lpe + at) = v;
+        const uint32_t lo = (uint32_t)odp_f2bf(__uint_as_float(x[0])) | ((uint32_t)odp_f2bf(__uint_as_float(x[1])) << 16);
+        const uint32_t hi = (uint32_t)odp_f2bf(__uint_as_float(x[2])) | ((uint32_t)odp_f2bf(__uint_as_float(x[3])) << 16);
+        odp_gstore((u32x2_t*)((uint16_t*)lpe + at), u32x2_t{lo, hi});
       } else {
-        *(u32x4_t*)(lpe + at) = u32x4_t{x[0], x[1], x[2], x[3]};
+        odp_gstore((u32x4_t*)(lpe + at), u32x4_t{x[0], x[1], x[2], x[3]});
       }
     }
     // Sum over the 16 lanes that share a column (same lane >> 4), then add
@@ -459,7 +466,7 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
       double v = wsum[q];
       v += __shfl_xor(v, 16);
       v += __shfl_xor(v, 32);
-      if (lane == 0) part[(int64_t)ex * part_stride + L.slot[q] + ODP_FT_WAVE_SLOTS * tile + wave] = v;
+      if (lane == 0) odp_gstore(part + (int64_t)ex * part_stride + L.slot[q] + ODP_FT_WAVE_SLOTS * tile + wave, v);
     }
   }
 }
@@ -787,22 +794,18 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       const uint32_t h0 = pend[2 * j] & 0xffffu, h1 = pend[2 * j] >> 16;
       const uint32_t h2 = pend[2 * j + 1] & 0xffffu, h3 = pend[2 * j + 1] >> 16;
       // Rows of the other parity to the odd/even neighbour.
-      const uint32_t r1 = (uint32_t)__shfl_xor((int)(tl ? (h0 | (h2 << 16)) : (h1 | (h3 << 16))), 1);
+      const uint32_t r1 = quad_x1(tl ? (h0 | (h2 << 16)) : (h1 | (h3 << 16)));
       // Rows 4g + 2a + tl, columns of this lane pair (low half: even column).
       const uint32_t p0 = tl ? ((r1 & 0xffffu) | (h1 << 16)) : (h0 | (r1 << 16));
       const uint32_t p1 = tl ? ((r1 >> 16) | (h3 << 16)) : (h2 | (r1 & 0xffff0000u));
       // Row pairs across the two lane pairs of the quad.
-      const uint32_t r2 = (uint32_t)__shfl_xor((int)(th ? p0 : p1), 2);
+      const uint32_t r2 = quad_x2(th ? p0 : p1);
       const uint32_t keep = th ? p1 : p0;
       const int32_t m = pend_m0 + (NJ * wave + j) * 16 + 4 * ((lane & 15) >> 2);
-      if (k < r && m < M) {
-        uint2 v;
-        v.x = th ? r2 : keep;
-        v.y = th ? keep : r2;
-        *(uint2*)(pe0 + ((int64_t)seg * r + k) * M + m) = v;
-      }
+      if (k < r && m < M)
+        odp_gstore((u32x2_t*)(pe0 + ((int64_t)seg * r + k) * M + m), u32x2_t{th ? r2 : keep, th ? keep : r2});
     }
-    if (lane == 0) part[(int64_t)ex * part_stride + L.slot[0] + ODP_FT_WAVE_SLOTS * pend_tile + wave] = pend_sq;
+    if (lane == 0) odp_gstore(part + (int64_t)ex * part_stride + L.slot[0] + ODP_FT_WAVE_SLOTS * pend_tile + wave, pend_sq);
     pend_m0 = -1;
   };
   // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
@@ -835,13 +838,17 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
         else if (c + 1 < nchunks)
           load(buf ^ 1, tc0, m_base + FP_MT, qv);
         if (st == 0) {
-          flush();
+          // B's loads before the stores: the MFMAs that wait for B then do
+          // not wait for the stores too (memory operations complete in
+          // issue order as far as s_waitcnt counts them).
 #pragma unroll
           for (int ks = 0; ks < FP_MT / 32; ++ks) {
             const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
             const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
             wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
           }
+          __builtin_amdgcn_sched_barrier(0);
+          flush();
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
         const uint16_t* sp = lds + buf * STAGE;
@@ -900,8 +907,8 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
           const int32_t t = tb + i;
           if (t >= rs && t < t_hi) {
             const uint16_t h = odp_f2bf(acc_u[st][i]);
-            uh[t] = h;
-            ul[t] = odp_f2bf(acc_u[st][i] - odp_bf2f(h));
+            odp_gstore(uh + t, h);
+            odp_gstore(ul + t, odp_f2bf(acc_u[st][i] - odp_bf2f(h)));
           }
         }
       }
