@@ -38,7 +38,9 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default 100 for c3, about 1.3 s, so that the GPU reaches its "
+                         "steady clocks; 2 for c4)")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--workload", choices=["c3", "c4"], default="c3",
                     help="c3: LoRA r=16 (the headline metric); c4: full-weight linears")
@@ -282,6 +284,8 @@ def main():
 
     N.load()
     dev = torch.device("cuda", 0)
+    if args.warmup is None:
+        args.warmup = 2 if args.workload == "c4" else 100
     if args.workload == "c4":
         args.batch = 8 if args.batch is None else args.batch
         args.seq = 4096 if args.seq is None else args.seq
