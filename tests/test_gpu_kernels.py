@@ -153,14 +153,18 @@ def test_clip_factor_arithmetic_is_bit_exact():
             assert torch.equal(ct.cpu().bool(), nrm.float() > C)
 
 
-def test_materialized_leaf_path():
+@pytest.mark.parametrize("dt,shape", [(torch.float32, (3, 7)), (torch.bfloat16, (3, 7)),
+                                      (torch.bfloat16, (6, 40)), (torch.float32, (5, 48))])
+def test_materialized_leaf_path(dt, shape):
+    """Odd sizes take the scale-sum's element-wise path, multiples of 8 its vector path."""
+    print(f"materialized leaf: {dt} {shape}", flush=True)
     g = torch.Generator().manual_seed(5)
-    pe = torch.randn(5, 3, 7, generator=g)  # 5 examples of a [3, 7] leaf, odd sizes
+    pe = torch.randn(5, *shape, generator=g).to(dt)  # 5 examples of the leaf
     seg = Segments.padded(5, 1)
-    acc, rnd = leaf_guards([(3, 7)], [torch.float32])
-    rel, ab = guard_constants(torch.float32, rnd)
-    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[2.0], effective=2.0, guards=[(rel, ab, torch.float32)])
-    plan = GhostPlan(segments=seg, leaves=[LeafOut((3, 7), torch.float32)], clip=clip,
+    acc, rnd = leaf_guards([shape], [dt])
+    rel, ab = guard_constants(dt, rnd)
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[2.0], effective=2.0, guards=[(rel, ab, dt)])
+    plan = GhostPlan(segments=seg, leaves=[LeafOut(shape, dt)], clip=clip,
                      materialized=[MaterializedLeaf(pe.to(DEV), 0)], device=DEV)
     res = plan.run()
     torch.cuda.synchronize()
@@ -169,11 +173,14 @@ def test_materialized_leaf_path():
     outs, norms = [], []
     for i in range(5):
         c, nrm, _ = dp_ref.clip_pytree({"w": pe[i]}, 2.0)
-        outs.append(c["w"])
+        outs.append(c["w"].float())
         norms.append(nrm)
-    want = torch.stack(outs).sum(0)
-    assert torch.allclose(res.leaves[0].cpu(), want, rtol=1e-6, atol=1e-6)
-    assert torch.allclose(res.norms.cpu(), torch.stack(norms), rtol=1e-6)
+    want = torch.stack(outs).sum(0).to(dt)
+    tol = 1e-6 if dt == torch.float32 else 2e-2
+    got = res.leaves[0].cpu()
+    assert got.dtype == dt and got.shape == shape
+    assert torch.allclose(got.float(), want.float(), rtol=tol, atol=tol)
+    assert torch.allclose(res.norms.cpu(), torch.stack(norms).float(), rtol=1e-6 if dt == torch.float32 else 1e-5)
 
 
 def test_noise_kernel_matches_oracle_and_is_deterministic():
