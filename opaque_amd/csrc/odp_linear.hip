@@ -349,16 +349,14 @@ __device__ __forceinline__ void zero_acc(f32x4_t (&acc)[I][J]) {
     for (int j = 0; j < J; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 }
 
-// Work decoding.  Workgroups are dispatched round-robin over the 8 XCDs
-// (blockIdx % 8), each with its own L2, and every problem's block count is
-// a multiple of 8 so that blockIdx % 8 == local % 8.  With BY_XCD and 8 or
-// more segments, XCD j works through segments j, j + 8, ... so that an
-// example's rows are cached by one L2 only (this pays for the Gram form,
-// whose workgroups drift apart in the feature loop).  Returns false for
-// padding blocks.
-template <bool BY_XCD>
+// Work decoding of the Gram form.  Workgroups are dispatched round-robin
+// over the 8 XCDs (blockIdx % 8), each with its own L2, and every problem's
+// block count is a multiple of 8 so that blockIdx % 8 == local % 8.  With 8
+// or more segments, XCD j works through segments j, j + 8, ... so that an
+// example's rows are cached by one L2 only (the workgroups drift apart in
+// the feature loop).  Returns false for padding blocks.
 __device__ __forceinline__ bool seg_item(int local, int n_seg, int per_seg, int& seg, int& item) {
-  if (BY_XCD && n_seg >= 8) {
+  if (n_seg >= 8) {
     const int k = local >> 3;
     seg = (local & 7) + 8 * (k / per_seg);
     item = k % per_seg;
@@ -539,7 +537,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
   const int nb = (int)f[ODP_LN_NB];
   const int items = (int)gram_items(nb);
   int seg, item;
-  if (!seg_item<true>(bid - ws[p], P.n_seg, items, seg, item)) return;
+  if (!seg_item(bid - ws[p], P.n_seg, items, seg, item)) return;
   int tb = 0, rem = item;
   while (rem >= (nb - tb + 1) / 2) {
     rem -= (nb - tb + 1) / 2;
