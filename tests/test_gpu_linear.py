@@ -339,3 +339,31 @@ def test_storage_takes_the_outer_form():
         res[b] = (r.leaves[0].double().cpu(), r.norms.double().cpu())
     assert torch.allclose(res[None][1], res[0][1], rtol=1e-4)
     assert (res[None][0] - res[0][0]).norm() <= 1e-2 * res[0][0].norm()
+
+
+def test_stored_path_zeroes_non_finite_entries():
+    """A NaN activation makes one column of one example's weight gradient NaN.
+    The reference zeroes non-finite per-example entries before the norm and
+    the scale (nan_to_num, clipping/_pytree.py:520-527); so does the path
+    that stores the per-example gradients (the clipped-sum GEMM would
+    propagate the NaN instead)."""
+    print("stored path: non-finite entries", flush=True)
+    n_ex, T, d_in, d_out = 4, 48, 136, 72
+    X, G, seg = _case(n_ex, T, d_in, d_out, [48, 30, 48, 20], seed=41)
+    X[T + 5, 17] = float("nan")  # example 1, feature 17
+    pe, _ = _ref_norms(X, G, seg)
+    assert torch.isnan(pe[1][:, 17]).all() and not torch.isnan(pe[0]).any()
+    finite = torch.nan_to_num(pe, nan=0.0)
+    C = float(finite.pow(2).sum((1, 2)).sqrt().median())
+    plan, res, _ = _plan(X, G, seg, C=C, mode=N.CLIP_FIXED, form=None, normalize_by=2.0)
+    assert plan.lin_pe.numel() > 0
+    outs, norms = [], []
+    for i in range(n_ex):
+        c, nrm, _ = dp_ref.clip_pytree({"w": pe[i].to(torch.bfloat16)}, C)
+        outs.append(c["w"])
+        norms.append(nrm)
+    want = (torch.stack(outs).sum(0, dtype=torch.float32).to(torch.bfloat16) / 2.0).double()
+    got = res.leaves[0].double().cpu()
+    assert torch.isfinite(got).all()
+    assert (got - want).norm() <= 2e-2 * want.norm()
+    assert torch.allclose(res.norms.double().cpu(), torch.stack(norms).double(), rtol=2e-3)
