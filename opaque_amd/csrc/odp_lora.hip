@@ -349,6 +349,37 @@ __device__ __forceinline__ uint32_t quad_x2(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
 }
 
+// fp64 sums across lanes on the VALU (DPP and readlane instead of LDS lane
+// permutes, which would compete with the kernels' LDS reads).  row_sum16
+// adds exactly what an xor 1, 2, 4, 8 butterfly adds, in the same order
+// (quad pairs, quads, half rows by half-row mirror, rows by row mirror), so
+// every lane of a row gets the same value; rows_sum4 returns
+// (R0 + R1) + (R2 + R3) of the four rows' values (lanes 0, 16, 32, 48), as
+// an xor 16, 32 butterfly does in lane 0.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double row_sum16(double v) {
+  v += dpp_f64<0xB1>(v);   // quad_perm 1,0,3,2
+  v += dpp_f64<0x4E>(v);   // quad_perm 2,3,0,1
+  v += dpp_f64<0x141>(v);  // row_half_mirror
+  v += dpp_f64<0x140>(v);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ double lane_f64(double v, int l) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double rows_sum4(double v) {
+  return (lane_f64(v, 0) + lane_f64(v, 16)) + (lane_f64(v, 32) + lane_f64(v, 48));
+}
+
 // 4 x 4 transpose within each quad of lanes: lane t of the quad holds
 // x[i] = B[i][t] on entry and x[c] = B[t][c] on return (two exchanges).
 __device__ __forceinline__ void quad_transpose4(uint32_t (&x)[4]) {
@@ -447,11 +478,7 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
     // the column to its leaf's sum.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      double v = cs[i];
-      v += __shfl_xor(v, 1);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
+      const double v = row_sum16(cs[i]);
       const int k = kb * 16 + 4 * (lane >> 4) + i;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -463,9 +490,7 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     if (q < L.n) {
-      double v = wsum[q];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      const double v = rows_sum4(wsum[q]);
       if (lane == 0) odp_gstore(part + (int64_t)ex * part_stride + L.slot[q] + ODP_FT_WAVE_SLOTS * tile + wave, v);
     }
   }
@@ -767,16 +792,10 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      double v = cs[i];
-      v += __shfl_xor(v, 1);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
+      const double v = row_sum16(cs[i]);
       if (4 * (lane >> 4) + i < r) wsum += v;
     }
-    wsum += __shfl_xor(wsum, 16);
-    wsum += __shfl_xor(wsum, 32);
-    pend_sq = wsum;
+    pend_sq = rows_sum4(wsum);
     pend_m0 = m_base;
     pend_tile = tile;
   };
