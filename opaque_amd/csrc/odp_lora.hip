@@ -15,6 +15,8 @@
 //   k_project_*  : Q^T = (P W^T)^T for every row of a segment      (U, V)
 //   k_factor_*   : pe[s] = s * Q_s^T P_s per segment, plus fp64 sums of
 //                  squares per leaf and M-tile                   (dA, dB)
+#include <type_traits>
+
 #include "odp_internal.h"
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -731,8 +733,8 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       (const uint16_t*)f[qplane ? ODP_FT_QLO : ODP_FT_Q] + (int64_t)qrow * ldq;
   uint16_t* const qdst_base = lds + PTILE + (qplane * QROWS + qrow) * QP + 8 * qpc;
 
-  auto load = [&](int b, int32_t t0, int32_t m_base, u32x4_t& qv) {
-    uint16_t* dst = lds + b * STAGE + 16 * wave * PP;
+  auto load = [&](uint16_t* stage, int32_t t0, int32_t m_base, u32x4_t& qv) {
+    uint16_t* dst = stage + 16 * wave * PP;
 #pragma unroll
     for (int i = 0; i < FP_T / 4 / 2; ++i) {
       const int row = 16 * wave + 2 * i + gh;
@@ -802,10 +804,18 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   // Each 16 x 16 block of dB rows leaves as 8-byte pieces: a 4 x 4
   // transpose within each quad of lanes (two exchanges) turns lane
   // (g, 4q + t)'s column of rows 4g .. 4g + 3 into row 4g + t, columns
-  // 4q .. 4q + 3.
+  // 4q .. 4q + 3.  The stores are buffer stores issued unconditionally
+  // (an offset past the end drops a store with nothing to write): the
+  // compiler then knows that exactly NJ + 1 of them follow B's loads, and
+  // the MFMAs that wait for B do not wait for the stores.
+  const __amdgpu_buffer_rsrc_t pe_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((uint16_t*)L.pe[0] + (int64_t)seg * r * M), (short)0, (int)((uint32_t)r * (uint32_t)M * 2u),
+      ODP_BUFFER_DWORD3);
+  const __amdgpu_buffer_rsrc_t part_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(part + (int64_t)ex * part_stride + L.slot[0]), (short)0,
+      (int)(ODP_FT_WAVE_SLOTS * (uint32_t)nchunks * 8u), ODP_BUFFER_DWORD3);
   auto flush = [&]() {
-    if (pend_m0 < 0) return;
-    uint16_t* pe0 = (uint16_t*)L.pe[0];
+    const bool live = pend_m0 >= 0;
     const int t = lane & 3, tl = t & 1, th = t >> 1;
     const int k = 4 * (lane >> 4) + t;
 #pragma unroll
@@ -821,10 +831,11 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       const uint32_t r2 = quad_x2(th ? p0 : p1);
       const uint32_t keep = th ? p1 : p0;
       const int32_t m = pend_m0 + (NJ * wave + j) * 16 + 4 * ((lane & 15) >> 2);
-      if (k < r && m < M)
-        odp_gstore((u32x2_t*)(pe0 + ((int64_t)seg * r + k) * M + m), u32x2_t{th ? r2 : keep, th ? keep : r2});
+      const uint32_t off = live && k < r && m < M ? ((uint32_t)k * (uint32_t)M + (uint32_t)m) * 2u : 0x80000000u;
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{th ? r2 : keep, th ? keep : r2}, pe_rsrc, (int)off, 0, 0);
     }
-    if (lane == 0) odp_gstore(part + (int64_t)ex * part_stride + L.slot[0] + ODP_FT_WAVE_SLOTS * pend_tile + wave, pend_sq);
+    const uint32_t poff = live && lane == 0 ? (uint32_t)(ODP_FT_WAVE_SLOTS * pend_tile + wave) * 8u : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, pend_sq), part_rsrc, (int)poff, 0, 0);
     pend_m0 = -1;
   };
   // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
@@ -834,7 +845,7 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
 
   u32x4_t qv;
   int buf = 0;
-  if (nsteps > 0 && nchunks > 0) load(0, t_lo, 0, qv);
+  if (nsteps > 0 && nchunks > 0) load(lds, t_lo, 0, qv);
   for (int c = 0; c < nchunks; ++c) {
     const int32_t m_base = c * FP_MT;
     // The first token of the steps, re-read per chunk: address arithmetic
@@ -847,65 +858,90 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // One step: the next stage's loads go into `nxt` while the step reads
+    // `sp`.  The two are restrict-qualified, so the compiler's scoped alias
+    // information tells them apart and the transposing reads of `sp` do
+    // not wait for the loads just issued into `nxt` (a barrier at the top
+    // of each step already waits for the stage's own loads).
+    auto step = [&](uint16_t* __restrict__ nxt, const uint16_t* __restrict__ sp,
+                    int st) __attribute__((always_inline)) {
+      if (st + 1 < nsteps)
+        load(nxt, tc0 + (st + 1) * FP_T, m_base, qv);
+      else if (c + 1 < nchunks)
+        load(nxt, tc0, m_base + FP_MT, qv);
+      if (st == 0) {
+        // B's loads before the stores: the MFMAs that wait for B then do
+        // not wait for the stores too (memory operations complete in
+        // issue order as far as s_waitcnt counts them).
 #pragma unroll
-    for (int st = 0; st < FP_STEPS; ++st) {
-      if (st < nsteps) {
-        store_q(buf, tc0 + st * FP_T, qv);
-        __syncthreads();  // also waits for this wave's loads into the stage
-        if (st + 1 < nsteps)
-          load(buf ^ 1, tc0 + (st + 1) * FP_T, m_base, qv);
-        else if (c + 1 < nchunks)
-          load(buf ^ 1, tc0, m_base + FP_MT, qv);
-        if (st == 0) {
-          // B's loads before the stores: the MFMAs that wait for B then do
-          // not wait for the stores too (memory operations complete in
-          // issue order as far as s_waitcnt counts them).
-#pragma unroll
-          for (int ks = 0; ks < FP_MT / 32; ++ks) {
-            const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
-            const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
-            wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
-          }
-          __builtin_amdgcn_sched_barrier(0);
-          flush();
+        for (int ks = 0; ks < FP_MT / 32; ++ks) {
+          const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
+          const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
+          wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
         }
-        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-        const uint16_t* sp = lds + buf * STAGE;
-        // dB rows: B operand = G columns by transposing reads, A = V hi / lo.
-#pragma unroll
-        for (int u = 0; u < FP_T / 32; ++u) {
-          const int tc = 32 * u + 8 * (lane >> 4);
-          const u32x4_t hv = *(const u32x4_t*)&sp[PTILE + (lane & 15) * QP + tc];
-          const u32x4_t lv = *(const u32x4_t*)&sp[PTILE + (QROWS + (lane & 15)) * QP + tc];
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const int m0 = (NJ * wave + j) * 16, cc = lane & 15;
-            const int row = 32 * u + 8 * (lane >> 4) + (cc >> 2);
-            const uint16_t* src = sp + row * PP + 4 * (((m0 >> 2) + (cc & 3)) ^ ft_swz(row));
-            const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
-            const v4i16_t tt[2] = {t0, t1};
-            const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
-            acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hv), bop,
-                                                                acc[j][0], 0, 0, 0);
-            acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lv), bop,
-                                                                acc[j][0], 0, 0, 0);
-          }
-        }
-        // U rows 16 wave .. + 15 of the step: A = G rows (8 consecutive
-        // columns per lane; a swizzled chunk pair stays contiguous).
-        {
-          const int row = 16 * wave + (lane & 15);
-#pragma unroll
-          for (int ks = 0; ks < FP_MT / 32; ++ks) {
-            const int chunk = 8 * ks + 2 * (lane >> 4);
-            const u32x4_t av = *(const u32x4_t*)&sp[row * PP + 4 * (chunk ^ ft_swz(row))];
-            acc_u[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), wf[ks],
-                                                                acc_u[st], 0, 0, 0);
-          }
-        }
-        buf ^= 1;
+        __builtin_amdgcn_sched_barrier(0);
+        flush();
       }
-    }
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+      // dB rows: B operand = G columns by transposing reads, A = V hi / lo.
+#pragma unroll
+      for (int u = 0; u < FP_T / 32; ++u) {
+        const int tc = 32 * u + 8 * (lane >> 4);
+        const u32x4_t hv = *(const u32x4_t*)&sp[PTILE + (lane & 15) * QP + tc];
+        const u32x4_t lv = *(const u32x4_t*)&sp[PTILE + (QROWS + (lane & 15)) * QP + tc];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int m0 = (NJ * wave + j) * 16, cc = lane & 15;
+          const int row = 32 * u + 8 * (lane >> 4) + (cc >> 2);
+          const uint16_t* src = sp + row * PP + 4 * (((m0 >> 2) + (cc & 3)) ^ ft_swz(row));
+          const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
+          const v4i16_t tt[2] = {t0, t1};
+          const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
+          acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hv), bop,
+                                                              acc[j][0], 0, 0, 0);
+          acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lv), bop,
+                                                              acc[j][0], 0, 0, 0);
+        }
+      }
+      // U rows 16 wave .. + 15 of the step: A = G rows (8 consecutive
+      // columns per lane; a swizzled chunk pair stays contiguous).
+      {
+        const int row = 16 * wave + (lane & 15);
+#pragma unroll
+        for (int ks = 0; ks < FP_MT / 32; ++ks) {
+          const int chunk = 8 * ks + 2 * (lane >> 4);
+          const u32x4_t av = *(const u32x4_t*)&sp[row * PP + 4 * (chunk ^ ft_swz(row))];
+          acc_u[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), wf[ks],
+                                                              acc_u[st], 0, 0, 0);
+        }
+      }
+    };
+    // Steps as nested conditionals (step st + 1 inside step st): each step
+    // is then reached only from the one before it, and the compiler counts
+    // the memory operations in flight exactly across them.
+    auto steps = [&](auto self, auto I) __attribute__((always_inline)) {
+      constexpr int st = decltype(I)::value;
+      if constexpr (st < FP_STEPS) {
+        if (st < nsteps) {
+          store_q(buf, tc0 + st * FP_T, qv);
+          // The stage's loads (this wave's) must have landed and its V piece
+          // be written before the barrier.  Vector memory operations complete
+          // in issue order as s_waitcnt counts them, and step 0 issues the
+          // stage's loads before B's loads and the NJ + 1 stores of the
+          // previous chunk: at step 1, vmcnt <= NJ + 1 covers the stage while
+          // the stores drain.  Other steps wait for everything.
+          if (st == 1)
+            __builtin_amdgcn_s_waitcnt(0x0070 | (NJ + 1));  // vmcnt(NJ + 1) lgkmcnt(0)
+          else
+            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+          __asm__ volatile("s_barrier" ::: "memory");
+          step(lds + (buf ^ 1) * STAGE, lds + buf * STAGE, st);
+          buf ^= 1;
+          self(self, std::integral_constant<int, st + 1>{});
+        }
+      }
+    };
+    steps(steps, std::integral_constant<int, 0>{});
     hold(acc, m_base, c);
     if (nsteps == 0) flush();  // no step of the next chunk will
   }
