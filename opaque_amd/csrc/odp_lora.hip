@@ -82,8 +82,15 @@ __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
 // W is staged through LDS once per workgroup per step.  All loads are
 // branch-free (clamped addresses, data zeroed when consumed).
 // ---------------------------------------------------------------------------
+// Workgroups per CU the compiler must fit registers for: each of these
+// fits its LDS tiles that many times in 160 KB without spilling, and the
+// extra loads in flight measured 1-5 % faster (one rank block of the factor
+// kernel: no difference, left to the compiler).
+__host__ __device__ constexpr int pj_min_blocks(int nkb) { return nkb == 1 ? 6 : nkb == 2 ? 3 : 1; }
+__host__ __device__ constexpr int ft_min_blocks(int nkb) { return nkb == 2 ? 3 : nkb == 3 ? 4 : 1; }
+
 template <int NKB>
-__global__ __launch_bounds__(256) void k_project_bf16(const int64_t* __restrict__ probs,
+__global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const int64_t* __restrict__ probs,
                                                       const int32_t* __restrict__ ws, int n_prob,
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen) {
@@ -513,7 +520,7 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
 __device__ __forceinline__ int ft_swz(int row) { return ((row & 3) | ((row >> 1) & 4)) << 2; }
 
 template <int NKB>
-__global__ __launch_bounds__(256) void k_factor_bf16(const int64_t* __restrict__ probs,
+__global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const int64_t* __restrict__ probs,
                                                      const int32_t* __restrict__ ws, int n_prob,
                                                      const int32_t* __restrict__ sstart,
                                                      const int32_t* __restrict__ slen,
