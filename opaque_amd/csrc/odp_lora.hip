@@ -847,8 +847,12 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   };
   // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
   // lane holds B[lane & 15][32 ks + 8 (lane >> 4) .. + 7].  Loaded after the
-  // chunk's first barrier, like the stores above.
-  const uint16_t* wrow = W + (int64_t)((lane & 15) < r ? (lane & 15) : 0) * M;
+  // chunk's first barrier, like the stores above, through a buffer resource
+  // over B's r rows: columns past M and rows past r arrive as zeros, with
+  // no select that would make the wave wait for the loads at once.
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)W, (short)0, (int)((uint32_t)r * (uint32_t)M * 2u), ODP_BUFFER_DWORD3);
+  const uint32_t wrow = (lane & 15) < r ? (uint32_t)(lane & 15) * (uint32_t)M : 0x40000000u;
 
   u32x4_t qv;
   int buf = 0;
@@ -883,8 +887,8 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
 #pragma unroll
         for (int ks = 0; ks < FP_MT / 32; ++ks) {
           const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
-          const u32x4_t v = ld16(wrow + (m < M ? m : M - 8));
-          wf[ks] = __builtin_bit_cast(bf16x8_t, m < M ? v : u32x4_t{0u, 0u, 0u, 0u});
+          const uint32_t off = m < M ? (wrow + (uint32_t)m) * 2u : 0x80000000u;
+          wf[ks] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)off, 0, 0));
         }
         __builtin_amdgcn_sched_barrier(0);
         flush();
