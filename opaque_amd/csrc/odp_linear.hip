@@ -478,7 +478,10 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
       const int r = 8 * k + (lane >> 3), qq = lane & 7;
       const u32x4_t v = *(const u32x4_t*)&stg[r * WN + 8 * (qq ^ ((r >> 2) & 7))];
       const int64_t o = ob + r, n = nb + 8 * qq;
-      if (o < P.d_out && n < P.d_in) *(ODP_GLOBAL u32x4_t*)(ODP_GLOBAL void*)(dst + o * P.d_in + n) = v;
+      // Non-temporal: the stored gradients are read again only by a later
+      // launch, and should not evict this launch's operands from L2.
+      if (o < P.d_out && n < P.d_in)
+        __builtin_nontemporal_store(v, (ODP_GLOBAL u32x4_t*)(ODP_GLOBAL void*)(dst + o * P.d_in + n));
     }
   }
 }
