@@ -102,6 +102,7 @@ __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const 
   constexpr int RB = pj_rpw(NKB), WR = 16 * RB;  // row blocks and rows per wave
   constexpr int NPR = RB * KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
   constexpr int NW = (RP * (KS / 8) + 255) / 256;  // W pieces per thread per step
+  static_assert(KS % 128 == 0, "each P load covers 128 columns of 4 rows (16 lanes x 16 B per row)");
   __shared__ __attribute__((aligned(16))) uint16_t wlds[2 * RP * WPITCH];
   __shared__ __attribute__((aligned(16))) uint16_t plds[4 * WR * PPITCH];
   const int bid = blockIdx.x;
