@@ -239,10 +239,21 @@ int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* w
  * g_t[o] bf16(c_s x_t[i])) and then round_out(out / normalize_by) if
  * normalize_by != 1, with c_s = scales[cls][group][seg_example[s]] (the
  * clip factor folded into X's rows, in registers or, with prescaled != 0,
- * by odp_linear_prescale beforehand; non-finite inputs propagate); one
- * workgroup per 256 x 256 output tile (odp_linear_sum_blocks, padded to a
- * multiple of 8).  Replaces clip_pytree's scale and the batch sum
- * (clipping/_pytree.py:553, clipping/_clipped_fun.py:115-134,821-824).      */
+ * by odp_linear_prescale beforehand); one workgroup per 256 x 256 output
+ * tile (odp_linear_sum_blocks, padded to a multiple of 8).  Replaces
+ * clip_pytree's scale and the batch sum (clipping/_pytree.py:553,
+ * clipping/_clipped_fun.py:115-134,821-824).
+ *
+ * Non-finite inputs.  The reference replaces every non-finite entry of each
+ * per-example gradient by 0 before the norm and the scale
+ * (clipping/_pytree.py:520-527).  An entry M_s[o][i] is non-finite exactly
+ * when column i of X or column o of G holds a NaN/Inf in one of the
+ * segment's rows, so zeroing those columns within the segment turns M_s
+ * into nan_to_num(M_s).  odp_nonfinite_columns finds the columns; the Gram
+ * norm, the prescale and the clipped sum zero them wherever ODP_LN_XMASK /
+ * ODP_LN_GMASK are set (the outer norm zeroes non-finite entries of M_s by
+ * itself).  Finite inputs whose per-example product overflows float32 are
+ * zeroed by the outer form only.                                            */
 enum {
   ODP_LN_X = 0, ODP_LN_LDX = 1, ODP_LN_G = 2, ODP_LN_LDG = 3,
   ODP_LN_DIN = 4, ODP_LN_DOUT = 5, ODP_LN_SEG_FIRST = 6, ODP_LN_NSEG = 7,
@@ -253,8 +264,32 @@ enum {
   ODP_LN_NROWS = 12, /* prescale: rows of X (the output X' is [n_rows][d_in]) */
   ODP_LN_PE = 13,    /* OUTER sqnorm: address of bf16 [n_seg][d_out][d_in]
                         that receives each M_s (RNE), or 0                  */
-  ODP_LN_FIELDS = 16
+  ODP_LN_XMASK = 14, /* GRAM sqnorm, prescale, clipped sum: address of the
+                        uint32 column masks of X ([n_seg][ceil(d_in / 32)],
+                        odp_nonfinite_columns) or 0 for none                */
+  ODP_LN_GMASK = 15, /* GRAM sqnorm, clipped sum: the masks of G
+                        ([n_seg][ceil(d_out / 32)]) or 0                    */
+  ODP_LN_NFFLAG = 16,/* OUTER sqnorm: address of a uint32 that is OR-ed with
+                        1 when an entry of some M_s is non-finite, or 0     */
+  ODP_LN_FIELDS = 20
 };
+
+/* ---- odp_nonfinite_columns: per-segment masks of non-finite columns ------
+ * For a bf16 row tensor P [n_rows][d] (row pitch ODP_NF_LDP, d a multiple of
+ * 8) and each segment s of the problem, writes mask[s][w] (uint32,
+ * w < ceil(d / 32)) whose bit j is set when column 32 w + j holds a NaN or
+ * Inf in one of the segment's rows.  Every word is written, so the masks
+ * need no clearing.  One workgroup per (segment, 256 columns)
+ * (odp_nonfinite_blocks).  Feeds ODP_LN_XMASK / ODP_LN_GMASK.             */
+enum {
+  ODP_NF_P = 0, ODP_NF_LDP = 1, ODP_NF_D = 2, ODP_NF_SEG_FIRST = 3, ODP_NF_NSEG = 4,
+  ODP_NF_MASK = 5,   /* address of the uint32 masks [n_seg][ceil(d / 32)]   */
+  ODP_NF_FIELDS = 8
+};
+int64_t odp_nonfinite_blocks(int64_t d, int64_t n_seg);
+int odp_nonfinite_columns(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                          int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
+                          const int32_t* seg_row_len);
 int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len);
 /* Workgroups of one sqnorm problem (n_seg segments; padded to a multiple of
  * 8 so that work maps onto the 8 XCDs predictably).                        */
@@ -269,12 +304,13 @@ int64_t odp_linear_sum_blocks(int64_t d_in, int64_t d_out);
  * The per-example scaling of clip_pytree (scale * leaf, clipping/_pytree.py:
  * 553) moved onto the activations: for every row t of a segment of example
  * i, X'[t] = bf16(c_i * x_t) with c_i the clip factor of the problem's
- * (class, group) (ODP_LN_FLAGS as for the clipped sum); rows in no segment
- * get 0.  odp_linear_clipped_sum with prescaled != 0 reads such an X' in
+ * (class, group) (ODP_LN_FLAGS as for the clipped sum); rows in no segment,
+ * rows of an example whose factor is 0 and columns set in ODP_LN_XMASK get
+ * 0.  odp_linear_clipped_sum with prescaled != 0 reads such an X' in
  * every problem (ODP_LN_X = X', ODP_LN_LDX = d_in) and skips its own
  * scaling; the result is bit-identical.  Problem rows: ODP_LN_X, LDX, DIN,
- * SEG_FIRST, NSEG, NROWS, FLAGS, OUT = X' (bf16); one workgroup per 16 rows
- * (odp_linear_prescale_blocks).                                            */
+ * SEG_FIRST, NSEG, NROWS, FLAGS, XMASK, OUT = X' (bf16); one workgroup per
+ * 16 rows (odp_linear_prescale_blocks).                                    */
 int64_t odp_linear_prescale_blocks(int64_t n_rows);
 int odp_linear_prescale(odp_stream_t stream, const int64_t* problems,
                         const int32_t* work_start, int32_t n_prob, int32_t total_blocks,

@@ -12,6 +12,9 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libopaque_dp.so"
 
 ODP_OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_UNSUPPORTED = 2
+ERR_HIP = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CLIP_FIXED = 0
@@ -32,8 +35,11 @@ NZ_FIELDS = 8
 NZ_IN, NZ_OUT, NZ_N, NZ_FLAT_OFFSET, NZ_SIGMA, NZ_DTYPES = range(6)
 SQ_FIELDS = 8
 SQ_X, SQ_N, SQ_NSEG, SQ_SEG_FIRST, SQ_SLOT, SQ_DTYPE = range(6)
-LN_FIELDS = 16
+LN_FIELDS = 20
 LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB, LN_NROWS, LN_PE = range(14)
+LN_XMASK, LN_GMASK, LN_NFFLAG = 14, 15, 16
+NF_FIELDS = 8
+NF_P, NF_LDP, NF_D, NF_SEG_FIRST, NF_NSEG, NF_MASK = range(6)
 FORM_OUTER = 0
 FORM_GRAM = 1
 
@@ -82,6 +88,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_linear_norm_blocks": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64]),
     "odp_linear_sqnorm": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
     "odp_linear_sum_blocks": (_c_i64, [_c_i64, _c_i64]),
+    "odp_nonfinite_blocks": (_c_i64, [_c_i64, _c_i64]),
+    "odp_nonfinite_columns": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr]),
     "odp_linear_clipped_sum": (
         _c_int,
         [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32, _c_i32],

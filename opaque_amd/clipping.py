@@ -321,6 +321,10 @@ class _ClipEngine:
         self.compute_dtype = compute_dtype
         self.scale_fn = scale_fn
         self._discovery: tuple[tuple, _Discovery] | None = None
+        # Keyword arguments for every GhostPlan this engine builds (for
+        # example {"linear_pe_bytes": 0} to keep full-weight per-example
+        # gradients out of HBM and take the clipped-sum GEMM instead).
+        self.plan_options: dict[str, Any] = {}
         if microbatch_size is not None and int(microbatch_size) <= 0:
             raise ValueError(f"microbatch_size must be positive, got {microbatch_size}")
 
@@ -482,10 +486,12 @@ class _ClipEngine:
                 for k, (s, dt) in enumerate(zip(shapes, dtypes))]
         plan = GhostPlan(segments=segments, leaves=outs, clip=spec, lora_sites=sites,
                          materialized=mats, linear_sites=list(lins), device=device,
-                         second_moment=self.second_moment)
+                         second_moment=self.second_moment, **self.plan_options)
         res = plan.run()
         if all_finite is not None and plan.pe_views():
             all_finite = all_finite & _pe_finite(plan)
+        if all_finite is not None and lins:
+            all_finite = all_finite & plan.linear_finite()
         # ||scaled gradient||: per group, scale * group norm (class 0 scale).
         cn2 = (res.scales[0] * res.group_norms).square().sum(0).sqrt()
         step = _StepOut(

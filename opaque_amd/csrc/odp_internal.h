@@ -3,7 +3,7 @@
 
 #include "odp_common.h"
 
-#define ODP_ABI_VERSION 1
+#define ODP_ABI_VERSION 2
 
 void odp_set_error(const char* fmt, ...);
 int odp_check_launch(const char* what);

@@ -140,12 +140,25 @@ __device__ __forceinline__ void outer_compute(const uint16_t* ta, const uint16_t
 }
 
 // One pipeline step: rows [t0, t0 + OK) clipped to its segment [tb, te).
-// Plain 32-bit fields (row counts stay below 2^31): a struct of mixed
-// widths and a bool was kept in memory by the compiler when copied
-// conditionally.
+// `fix`: the segment has non-finite columns inside the tile, which the step
+// zeroes in LDS before its MFMAs.  Plain 32-bit fields (row counts stay
+// below 2^31): a struct of mixed widths and a bool was kept in memory by
+// the compiler when copied conditionally.
 struct Step {
-  int32_t t0, tb, te, seg, live;
+  int32_t t0, tb, te, seg, live, fix;
 };
+
+// Element (r, c) of a token-major tile of row pitch `pitch` (the XOR swizzle
+// above).
+__device__ __forceinline__ int tile_at(int r, int c, int pitch) {
+  return r * pitch + 4 * ((c >> 2) ^ swz(r)) + (c & 3);
+}
+
+// Bit `c` of a segment's column mask (uint32 words, bit j of word w =
+// column 32 w + j).
+__device__ __forceinline__ bool mask_bit(const uint32_t* m, int64_t c) {
+  return (m[c >> 5] >> (c & 31)) & 1u;
+}
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 
@@ -241,9 +254,12 @@ __device__ __forceinline__ uint16_t* lin_stage(int k) {
 // loads, one step fewer; the clipped sum, whose workgroups stream 32768 tokens
 // against operands shared with many other tiles, measured faster that way
 // (less cache pressure), the per-example norms slower.
-template <bool SCALE, bool DEEP, typename Next, typename Scale>
+// FIX: a step whose `fix` is set calls fixup(stage, step) once its loads
+// have landed, then waits for every wave before the MFMAs (segments with
+// non-finite columns only).
+template <bool SCALE, bool DEEP, bool FIX, typename Next, typename Scale, typename Fixup>
 __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, int64_t n0, Step first,
-                                             Next next, Scale scale, OuterAcc& acc) {
+                                             Next next, Scale scale, Fixup fixup, OuterAcc& acc) {
   auto stage = [&](int k) -> uint16_t* { return lin_stage(k); };
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -305,6 +321,10 @@ __device__ __forceinline__ void dma_mainloop(const LinProblem& P, int64_t o0, in
       // This step's loads have landed; the later RING - 2 steps' may fly.
       __builtin_amdgcn_s_waitcnt(vmcnt_imm((RING - 2) * DMA_PER_STEP));
       __asm__ volatile("s_barrier" ::: "memory");
+      if (FIX && cur.fix) {
+        fixup(stage(k), cur);
+        __syncthreads();
+      }
       // Loads of step ld go into the stage computed at the previous step.
       const Step x = ld;
       const int kn = (k + RING - 1) % RING;
@@ -382,16 +402,19 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
   return t;
 }
 
-// fp32 squares of the finite entries, summed in fp64.
+// fp32 squares of the finite entries, summed in fp64; `nonfinite` is set
+// when an entry was not finite (and counted as 0).
 template <int I, int J>
-__device__ __forceinline__ double acc_sq(const f32x4_t (&acc)[I][J]) {
+__device__ __forceinline__ double acc_sq(const f32x4_t (&acc)[I][J], bool& nonfinite) {
   double s = 0.0;
   static_for<I * J>([&](auto q) {
     constexpr int i = decltype(q)::value / J, j = decltype(q)::value % J;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float v = acc[i][j][e];
-      const float vf = isfinite(v) ? v : 0.f;
+      const bool fin = isfinite(v);
+      nonfinite |= !fin;
+      const float vf = fin ? v : 0.f;
       s += (double)__fmul_rn(vf, vf);
     }
     // One tile's accumulators at a time in VGPRs.
@@ -441,17 +464,23 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
 
   OuterAcc acc;
   zero_acc(acc);
-  const Step first = {(int32_t)t_begin, (int32_t)t_begin, (int32_t)t_end, seg, t_end > t_begin ? 1 : 0};
+  const Step first = {(int32_t)t_begin, (int32_t)t_begin, (int32_t)t_end, seg, t_end > t_begin ? 1 : 0, 0};
   auto next = [&](const Step& st) {
     Step n = st;
     n.t0 = st.t0 + OK;
     n.live = n.t0 < st.te ? 1 : 0;
     return n;
   };
-  dma_mainloop<false, true>(P, o0, n0, first, next, [](const Step&) { return 1.0f; }, acc);
+  dma_mainloop<false, true, false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; },
+                                   [](uint16_t*, const Step&) {}, acc);
   // Columns/rows past the matrix were zero operands, so they add nothing.
-  const double tot = block_sum(acc_sq(acc), red);
+  // Non-finite entries of M_s count 0 (nan_to_num before the norm).
+  bool nonfinite = false;
+  const double tot = block_sum(acc_sq(acc, nonfinite), red);
   if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
+  uint32_t* nfflag = (uint32_t*)f[ODP_LN_NFFLAG];
+  // Every writer stores the same value, so a plain store suffices.
+  if (nfflag != nullptr && nonfinite) odp_gstore(nfflag, 1u);
   // Optionally keep the tile of M_s itself, rounded to bf16, for a later
   // clipped sum over stored per-example gradients.  Each wave's WM x WN
   // block goes through its own part of the (now idle) LDS ring so that rows
@@ -512,6 +541,8 @@ __host__ __device__ constexpr int64_t gram_items(int64_t nb) {
   return (nb & 1) ? ((nb + 1) / 2) * ((nb + 1) / 2) : (nb / 2) * (nb / 2 + 1);
 }
 
+static_assert(GR_K == 32, "one 32-bit column-mask word per Gram step");
+
 __device__ __forceinline__ int gr_swz(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ gr_swz(row)); }
 
@@ -557,6 +588,21 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // Non-finite columns of this segment (odp_nonfinite_columns): `fix` when
+  // any is set, then each step zeroes its masked features in LDS.
+  const int xw = (int)((P.d_in + 31) / 32), gw = (int)((P.d_out + 31) / 32);
+  const uint32_t* xm = (const uint32_t*)f[ODP_LN_XMASK];
+  const uint32_t* gm = (const uint32_t*)f[ODP_LN_GMASK];
+  if (xm != nullptr) xm += (int64_t)seg * xw;
+  if (gm != nullptr) gm += (int64_t)seg * gw;
+  int fix = 0;
+  if (xm != nullptr || gm != nullptr) {
+    int any = 0;
+    for (int w = threadIdx.x; w < xw + gw; w += 512)
+      any |= (w < xw ? (xm != nullptr ? xm[w] : 0u) : (gm != nullptr ? gm[w - xw] : 0u)) != 0u;
+    fix = __syncthreads_or(any);
+  }
 
   // Rows of the stage: 0..127 block tb, 128..255 block sb0, 256..383 sb0 + 1.
   // Wave w loads stage rows 48 w .. + 47, 16 per load; lane l lands in row
@@ -636,7 +682,14 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
     issue(nxt, x);
     if (live) compute(cur, acc);
   };
-  auto phase = [&](int lo, int hi, int live, f32x4_t (&acc)[4][4]) {
+  // Zeroes the features of a landed stage whose bits are set in `word`
+  // (the step's 32 features), for all 384 rows.
+  auto zero_features = [&](uint16_t* st, uint32_t word) {
+    const int fc = threadIdx.x & 31;
+    if ((word >> fc) & 1u)
+      for (int r = threadIdx.x >> 5; r < GR_ROWS; r += 16) st[gr_at(r, fc >> 3) + (fc & 7)] = 0;
+  };
+  auto phase = [&](int lo, int hi, int live, const uint32_t* mask, f32x4_t (&acc)[4][4]) {
     for (int g0 = lo; g0 < hi; g0 += GR_RING) {
 #pragma unroll
       for (int k = 0; k < GR_RING; ++k) {
@@ -644,14 +697,21 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
         // This step's loads have landed; the later GR_RING - 2 steps' may fly.
         __builtin_amdgcn_s_waitcnt(vmcnt_imm((GR_RING - 2) * GR_LOADS));
         __asm__ volatile("s_barrier" ::: "memory");
+        if (fix && mask != nullptr && g - lo < live) {
+          const uint32_t word = mask[g - lo];  // features [32 (g - lo), + 32)
+          if (word != 0u) {
+            zero_features(stage(k), word);
+            __syncthreads();
+          }
+        }
         step(stage((k + GR_RING - 1) % GR_RING), stage(k), g + GR_RING - 1, g - lo < live, acc);
       }
     }
   };
 #pragma unroll
   for (int x = 0; x < GR_RING - 1; ++x) issue(stage(x), x);
-  phase(0, px, nx, sx);
-  phase(px, total, ng, sg);
+  phase(0, px, nx, xm, sx);
+  phase(px, total, ng, gm, sg);
   __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
 
   // Off-diagonal blocks count twice (the (s, t) block is not computed);
@@ -696,12 +756,15 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
                                                       int n_groups) {
   __shared__ float rowc[PS_ROWS];
   __shared__ int rowin[PS_ROWS];
+  __shared__ int rowseg[PS_ROWS];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
   const uint16_t* X = (const uint16_t*)f[ODP_LN_X];
   const int64_t ldx = f[ODP_LN_LDX], d = f[ODP_LN_DIN], n_rows = f[ODP_LN_NROWS];
   uint16_t* out = (uint16_t*)f[ODP_LN_OUT];
+  const uint32_t* xm = (const uint32_t*)f[ODP_LN_XMASK];
+  const int64_t xw = (d + 31) / 32;
   const int seg_first = (int)f[ODP_LN_SEG_FIRST], n_seg = (int)f[ODP_LN_NSEG];
   const int64_t flags = f[ODP_LN_FLAGS];
   const int grp = (int)((flags >> 8) & 0xffff), cls = (int)((flags >> 24) & 0xffff);
@@ -721,8 +784,11 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
     }
     const int s = lo - 1;
     const bool in = t < n_rows && s >= 0 && t < (int64_t)sstart[seg_first + s] + slen[seg_first + s];
-    rowin[tid] = in ? 1 : 0;
-    rowc[tid] = in ? sc[sex[seg_first + s]] : 0.f;
+    const float c = in ? sc[sex[seg_first + s]] : 0.f;
+    // A zero factor writes zeros (by select: 0 * Inf would be NaN).
+    rowin[tid] = in && c != 0.f ? 1 : 0;
+    rowc[tid] = c;
+    rowseg[tid] = in ? s : 0;
   }
   __syncthreads();
   const int64_t pieces = d / 8;
@@ -731,7 +797,21 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
     const int64_t pc = i - (int64_t)r * pieces, t = row0 + r;
     if (t >= n_rows) break;
     u32x4_t v = {0u, 0u, 0u, 0u};
-    if (rowin[r]) v = scale_bf16x8(*(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(X + t * ldx + 8 * pc), rowc[r]);
+    if (rowin[r]) {
+      v = scale_bf16x8(*(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(X + t * ldx + 8 * pc), rowc[r]);
+      if (xm != nullptr) {
+        // Columns holding a non-finite value in this segment become 0.
+        const uint32_t bits = (xm[rowseg[r] * xw + (8 * pc >> 5)] >> (8 * pc & 31)) & 0xffu;
+        if (bits != 0u) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t m = (((bits >> (2 * k)) & 1u) ? 0x0000ffffu : 0u) |
+                               (((bits >> (2 * k + 1)) & 1u) ? 0xffff0000u : 0u);
+            v[k] &= ~m;
+          }
+        }
+      }
+    }
     odp_gstore((u32x4_t*)(out + t * d + 8 * pc), v);
   }
 }
@@ -775,6 +855,27 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
   // must not wait behind the vector loads in flight.
   const ODP_CONST int32_t* cstart = (const ODP_CONST int32_t*)(sstart + P.seg_first);
   const ODP_CONST int32_t* clen = (const ODP_CONST int32_t*)(slen + P.seg_first);
+  // Column masks of non-finite inputs (odp_nonfinite_columns), if any.
+  const int xw = (int)((P.d_in + 31) / 32), gw = (int)((P.d_out + 31) / 32);
+  const ODP_CONST uint32_t* xm = (const ODP_CONST uint32_t*)f[ODP_LN_XMASK];
+  const ODP_CONST uint32_t* gm = (const ODP_CONST uint32_t*)f[ODP_LN_GMASK];
+  // Whether segment sg masks a column of this tile.
+  auto tile_masked = [&](int sg) -> int32_t {
+    uint32_t any = 0u;
+    if (xm != nullptr) {
+      const int w0 = (int)(n0 >> 5);
+#pragma unroll
+      for (int w = 0; w < ON / 32; ++w)
+        if (w0 + w < xw) any |= xm[(int64_t)sg * xw + w0 + w];
+    }
+    if (gm != nullptr) {
+      const int w0 = (int)(o0 >> 5);
+#pragma unroll
+      for (int w = 0; w < OM / 32; ++w)
+        if (w0 + w < gw) any |= gm[(int64_t)sg * gw + w0 + w];
+    }
+    return any != 0u ? 1 : 0;
+  };
   auto at_segment = [&](int sg) {
     while (sg < P.n_seg && clen[sg] <= 0) ++sg;
     Step st;
@@ -783,7 +884,18 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
     st.tb = st.live ? cstart[sg] : 0;
     st.te = st.live ? st.tb + clen[sg] : 0;
     st.t0 = st.tb;
+    st.fix = st.live && (xm != nullptr || gm != nullptr) ? tile_masked(sg) : 0;
     return st;
+  };
+  // Zeroes the masked G columns (tile rows o) and X columns (tile columns n)
+  // of a landed stage, so that the step adds nothing to those entries.
+  auto fixup = [&](uint16_t* st, const Step& s) {
+    const int c = threadIdx.x & 255;
+    const int64_t o = o0 + c, n = n0 + c;
+    if (gm != nullptr && o < P.d_out && mask_bit((const uint32_t*)(gm + (int64_t)s.seg * gw), o))
+      for (int r = threadIdx.x >> 8; r < OK; r += OUTER_THREADS / 256) st[tile_at(r, c, OM)] = 0;
+    if (xm != nullptr && c < ON && n < P.d_in && mask_bit((const uint32_t*)(xm + (int64_t)s.seg * xw), n))
+      for (int r = threadIdx.x >> 8; r < OK; r += OUTER_THREADS / 256) st[A_TILE + tile_at(r, c, ON)] = 0;
   };
   // Also valid on a finished step (which stays finished).
   auto next = [&](const Step& st) {
@@ -798,7 +910,7 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
   const ODP_CONST float* csc = (const ODP_CONST float*)sc;
   auto scale = [&](const Step& st) { return csc[cex[st.seg]]; };
   // PRESCALED: X already holds c_i x_t (odp_linear_prescale).
-  dma_mainloop<!PRESCALED, false>(P, o0, n0, at_segment(0), next, scale, acc);
+  dma_mainloop<!PRESCALED, false, true>(P, o0, n0, at_segment(0), next, scale, fixup, acc);
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -820,11 +932,99 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
   });
 }
 
+// ---------------------------------------------------------------------------
+// Column masks of non-finite values per segment.  Workgroup = (segment,
+// strip of 256 columns): 32 lanes cover a strip row in 16-byte pieces, 8 row
+// groups walk the segment's rows, and the per-lane 8-bit masks are OR-ed
+// over the row groups and packed into the strip's 8 words.  HBM-bound: one
+// read of the segment's rows.
+// ---------------------------------------------------------------------------
+constexpr int NF_THREADS = 256;
+constexpr int NF_STRIP = 256;  // columns per workgroup
+
+// Bit k set when bf16 element k of the 8 is NaN or Inf (exponent all ones).
+__device__ __forceinline__ uint32_t nonfinite8(u32x4_t v) {
+  uint32_t b = 0u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    b |= ((v[k] & 0x00007f80u) == 0x00007f80u ? 1u : 0u) << (2 * k);
+    b |= ((v[k] & 0x7f800000u) == 0x7f800000u ? 1u : 0u) << (2 * k + 1);
+  }
+  return b;
+}
+
+__global__ __launch_bounds__(NF_THREADS) void k_nonfinite_cols(const int64_t* __restrict__ probs,
+                                                               const int32_t* __restrict__ ws, int n_prob,
+                                                               const int32_t* __restrict__ sstart,
+                                                               const int32_t* __restrict__ slen) {
+  __shared__ uint32_t red[NF_THREADS / 32][32];
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_NF_FIELDS;
+  const uint16_t* P = (const uint16_t*)f[ODP_NF_P];
+  const int64_t ldp = f[ODP_NF_LDP], d = f[ODP_NF_D];
+  const int seg_first = (int)f[ODP_NF_SEG_FIRST];
+  uint32_t* mask = (uint32_t*)f[ODP_NF_MASK];
+  const int strips = (int)((d + NF_STRIP - 1) / NF_STRIP);
+  const int64_t words = (d + 31) / 32;
+  const int local = bid - ws[p];
+  const int seg = local / strips, strip = local - seg * strips;
+  const int64_t t0 = sstart[seg_first + seg];
+  const int len = slen[seg_first + seg];
+  const int lane = threadIdx.x & 31, rg = threadIdx.x >> 5;
+  const int64_t col = (int64_t)strip * NF_STRIP + 8 * lane;
+  uint32_t bits = 0u;
+  if (col < d) {
+    const uint16_t* base = P + t0 * ldp + col;
+    auto row = [&](int r) { return *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(base + (int64_t)r * ldp); };
+    int r = rg;
+    // Four rows in flight per lane.
+    for (; r + 24 < len; r += 32) {
+      const u32x4_t a = row(r), b = row(r + 8), c = row(r + 16), e = row(r + 24);
+      bits |= nonfinite8(a) | nonfinite8(b) | nonfinite8(c) | nonfinite8(e);
+    }
+    for (; r < len; r += 8) bits |= nonfinite8(row(r));
+  }
+  red[rg][lane] = bits;
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    uint32_t b = 0u;
+#pragma unroll
+    for (int k = 0; k < NF_THREADS / 32; ++k) b |= red[k][lane];
+    // Lanes 4w .. 4w + 3 hold the four bytes of the strip's word w.
+    uint32_t w = b << (8 * (lane & 3));
+    w |= __shfl_xor(w, 1, 32);
+    w |= __shfl_xor(w, 2, 32);
+    const int64_t wi = (int64_t)strip * (NF_STRIP / 32) + (lane >> 2);
+    if ((lane & 3) == 0 && wi < words) odp_gstore(mask + (int64_t)seg * words + wi, w);
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+
+extern "C" int64_t odp_nonfinite_blocks(int64_t d, int64_t n_seg) {
+  if (d <= 0 || n_seg <= 0) return 0;
+  return n_seg * ((d + NF_STRIP - 1) / NF_STRIP);
+}
+
+extern "C" int odp_nonfinite_columns(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                                     int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
+                                     const int32_t* seg_row_len) {
+  int rc = odp_check_table("odp_nonfinite_columns", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_row_start == nullptr || seg_row_len == nullptr) {
+    odp_set_error("odp_nonfinite_columns: null segment arrays");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_nonfinite_cols, dim3(total_blocks), dim3(NF_THREADS), 0, odp_hip_stream(stream),
+                     problems, work_start, n_prob, seg_row_start, seg_row_len);
+  return odp_check_launch("odp_nonfinite_columns");
+}
 
 extern "C" int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len) {
   if (d_in <= 0 || d_out <= 0) return 0;

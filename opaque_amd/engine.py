@@ -385,6 +385,10 @@ class GhostPlan:
         dev = self.device
         reg = _SegRegistry(seg)
         self._segreg = reg
+        # Row views of each linear site's x and g, made once (a view that
+        # needs a copy would otherwise be copied again at every use).
+        lin_x: list[torch.Tensor] = []
+        lin_g: list[torch.Tensor] = []
         for ls in lins:
             if ls.x.device != dev or ls.g.device != dev:
                 raise ValueError("linear site tensors must be on the plan device")
@@ -396,8 +400,10 @@ class GhostPlan:
                 raise ValueError("linear site row count does not match the segments")
             if not (supports_rows(ls.x) and supports_rows(ls.g)):
                 raise ValueError("linear site feature sizes must be multiples of 8")
+            lin_x.append(_rows(ls.x))
+            lin_g.append(_rows(ls.g))
             # The kernels address one segment's rows through 32-bit buffer ranges.
-            ld = max(_rows(ls.x).stride(0), _rows(ls.g).stride(0))
+            ld = max(lin_x[-1].stride(0), lin_g[-1].stride(0))
             if reg.view(ls.segments).max_len * ld * 2 >= 2**31:
                 raise ValueError("a linear site's longest segment spans 2 GiB or more of x or g")
             shape = tuple(self.leaves[ls.w_leaf].shape)
@@ -554,7 +560,11 @@ class GhostPlan:
             return (1 << 32) if pe_dt[i] == torch.bfloat16 else 0
 
         self._pe_addr, self._pe_bits = pe_addr, pe_bits
-        self.part = torch.zeros((seg.n_ex, self.n_slots), dtype=torch.float64, device=dev)
+        # fp64 partials [n_ex][n_slots], then one word that kernels set when a
+        # per-example weight gradient held a non-finite entry; zeroed together.
+        self._part_buf = torch.zeros(seg.n_ex * self.n_slots + 1, dtype=torch.float64, device=dev)
+        self.part = self._part_buf[: seg.n_ex * self.n_slots].view(seg.n_ex, self.n_slots)
+        self._nf_flag_addr = self._part_buf.data_ptr() + seg.n_ex * self.n_slots * 8
 
         # Output leaves: one flat buffer per output dtype, views in leaf order.
         self.flat: dict[torch.dtype, torch.Tensor] = {}
@@ -738,6 +748,36 @@ class GhostPlan:
             mat_pe[m.leaf] = pe_m
 
         self.lin_pe = torch.empty(pe_total, dtype=torch.bfloat16, device=dev)
+
+        # Sites whose per-example gradients are not stored read X and G in
+        # the Gram norm and the clipped-sum GEMM, which zero the feature
+        # columns holding a non-finite value within each segment (so that the
+        # result is nan_to_num of every per-example gradient).  One mask per
+        # distinct tensor and segment list, found by odp_nonfinite_columns.
+        masks: dict[tuple, tuple[torch.Tensor, _SegView, int]] = {}
+        mask_words = 0
+
+        def mask_of(t: torch.Tensor, v: _SegView) -> int:
+            nonlocal mask_words
+            key = (t.data_ptr(), tuple(t.shape), tuple(t.stride()), v.first)
+            if key not in masks:
+                masks[key] = (t, v, mask_words)
+                mask_words += v.n_seg * ((t.shape[1] + 31) // 32)
+            return masks[key][2]
+
+        site_mask = {i: (mask_of(lin_x[i], lin_view[i]), mask_of(lin_g[i], lin_view[i]))
+                     for i in range(len(lins)) if i not in lin_pe}
+        self.nf_mask = torch.empty(max(mask_words, 1), dtype=torch.int32, device=dev)
+        self._has_masks = mask_words > 0
+
+        def mask_addr(w: int) -> int:
+            return self.nf_mask.data_ptr() + 4 * w
+
+        nft = _Table(N.NF_FIELDS)
+        for t, v, off in masks.values():
+            nft.add({N.NF_P: t.data_ptr(), N.NF_LDP: t.stride(0), N.NF_D: t.shape[1],
+                     N.NF_SEG_FIRST: v.first, N.NF_NSEG: v.n_seg, N.NF_MASK: mask_addr(off)},
+                    int(lib.odp_nonfinite_blocks(t.shape[1], v.n_seg)), v.valid * t.shape[1] * 2)
         if self.second_moment and len(lin_pe) < len(lins):
             raise ValueError("second moments of full-weight linear sites need their per-example "
                              "gradients stored (outer form, within linear_pe_bytes)")
@@ -754,7 +794,7 @@ class GhostPlan:
             if i in lin_pe:
                 site_chunk.append(None)
                 continue
-            x, lf = _rows(ls.x), self.leaves[ls.w_leaf]
+            x, lf = lin_x[i], self.leaves[ls.w_leaf]
             nbytes = -(-x.shape[0] * x.shape[1] * 2 // 256) * 256
             if nbytes > self.prescale_bytes:
                 site_chunk.append(None)
@@ -775,15 +815,16 @@ class GhostPlan:
         xs_sum = [_Table(N.LN_FIELDS) for _ in xs_chunks]
         for c, members in enumerate(xs_chunks):
             for off, i in members.values():
-                x, v, lf = _rows(lins[i].x), lin_view[i], self.leaves[lins[i].w_leaf]
+                x, v, lf = lin_x[i], lin_view[i], self.leaves[lins[i].w_leaf]
                 xs_pre[c].add({N.LN_X: x.data_ptr(), N.LN_LDX: x.stride(0), N.LN_DIN: x.shape[1],
                                N.LN_SEG_FIRST: v.first, N.LN_NSEG: v.n_seg, N.LN_NROWS: x.shape[0],
-                               N.LN_FLAGS: (lf.group << 8) | (lf.cls << 24), N.LN_OUT: self.xs[off:].data_ptr()},
+                               N.LN_FLAGS: (lf.group << 8) | (lf.cls << 24), N.LN_OUT: self.xs[off:].data_ptr(),
+                               N.LN_XMASK: mask_addr(site_mask[i][0])},
                               int(lib.odp_linear_prescale_blocks(x.shape[0])), 2 * v.valid * x.shape[1] * 2)
         lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS)}
         lsum = _Table(N.LN_FIELDS)
         for i, ls in enumerate(lins):
-            x, g = _rows(ls.x), _rows(ls.g)
+            x, g = lin_x[i], lin_g[i]
             self._keep += [x, g]
             d_in, d_out = x.shape[1], g.shape[1]
             form = lin_form[i]
@@ -793,6 +834,9 @@ class GhostPlan:
                 N.LN_X: x.data_ptr(), N.LN_LDX: x.stride(0), N.LN_G: g.data_ptr(), N.LN_LDG: g.stride(0),
                 N.LN_DIN: d_in, N.LN_DOUT: d_out, N.LN_SEG_FIRST: v.first, N.LN_NSEG: n_seg,
             }
+            if i in site_mask:
+                common[N.LN_XMASK] = mask_addr(site_mask[i][0])
+                common[N.LN_GMASK] = mask_addr(site_mask[i][1])
             if form == N.FORM_GRAM:
                 fl = sum(ln * ln for ln in v.segs.lengths) * (d_in + d_out)
             else:
@@ -801,7 +845,7 @@ class GhostPlan:
             nb_max = (v.max_len + 127) // 128
             pe_at = self.lin_pe[lin_pe[i]:].data_ptr() if i in lin_pe else 0
             lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_off[i], N.LN_NB: nb_max,
-                           N.LN_PE: pe_at}, blocks,
+                           N.LN_PE: pe_at, N.LN_NFFLAG: self._nf_flag_addr}, blocks,
                           valid * (d_in + d_out) * 2 + (n_seg * d_in * d_out * 2 if pe_at else 0), fl)
             if i in lin_pe:
                 continue
@@ -874,6 +918,7 @@ class GhostPlan:
         for key in sorted(ft, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("factor", key, ft[key]))
         tabs.append(("sqnorm", None, sq))
+        tabs.append(("nonfinite", None, nft))
         tabs.append(("lin_norm", N.FORM_OUTER, lnt[N.FORM_OUTER]))
         tabs.append(("lin_norm", N.FORM_GRAM, lnt[N.FORM_GRAM]))
         tabs.append(("scale_sum", None, ss))
@@ -997,6 +1042,15 @@ class GhostPlan:
                 return s.b_transposed
         return False
 
+    def linear_finite(self) -> torch.Tensor:
+        """Device bool: no per-example weight gradient of a linear site held a
+        non-finite entry in the last run (outer-form norms flag them; the
+        other sites' column masks record them)."""
+        ok = self._part_buf[-1:].view(torch.int64)[0] == 0
+        if self._has_masks:
+            ok = ok & (self.nf_mask == 0).all()
+        return ok
+
     def pe_views(self) -> list[torch.Tensor]:
         """The per-example factor gradients each LoRA leaf stored ([n_seg * r * M], parameter dtype)."""
         return [self.pe[dt][o : o + n] for dt, o, n in self._pe_slices]
@@ -1006,7 +1060,7 @@ class GhostPlan:
         """Launch the step on the current stream.
 
         ``events`` may map a stage name ("project", "factor_project",
-        "factor", "sqnorm", "lin_norm", "clip", "scale_sum", "lin_sum") to a
+        "factor", "sqnorm", "nonfinite", "lin_norm", "clip", "scale_sum", "lin_sum") to a
         (start, end) pair of torch.cuda.Event that are recorded around that
         stage's launches ("lin_sum" spans the clipped sums and their
         prescale launches).  ``launch_log``, when a
@@ -1017,7 +1071,7 @@ class GhostPlan:
         stream = _stream()
         seg = self.segments
         ev = events or {}
-        self.part.zero_()
+        self._part_buf.zero_()
         live = [t for t in self.tables if t[5] > 0 and t[0] not in _AFTER_CLIP]
 
         def mark(name, dt):
@@ -1050,6 +1104,9 @@ class GhostPlan:
             elif name == "sqnorm":
                 N.check(lib.odp_sqnorm(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                        self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
+            elif name == "nonfinite":
+                N.check(lib.odp_nonfinite_columns(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                                  self.seg_start.data_ptr(), self.seg_len.data_ptr()), name)
             elif name == "lin_norm":
                 N.check(lib.odp_linear_sqnorm(stream, dt, probs.data_ptr(), ws.data_ptr(), n, total,
                                               self.seg_start.data_ptr(), self.seg_len.data_ptr(),

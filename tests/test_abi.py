@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_buffer(lib):
-    assert lib.odp_abi_version() == 1
+    assert lib.odp_abi_version() == 2
     assert isinstance(N.last_error(), str)
 
 
@@ -66,6 +66,13 @@ def test_field_indices_match_header():
     assert value("ODP_SS_FIELDS") == N.SS_FIELDS
     assert value("ODP_SQ_FIELDS") == N.SQ_FIELDS
     assert value("ODP_NZ_FIELDS") == N.NZ_FIELDS
+    assert value("ODP_LN_FIELDS") == N.LN_FIELDS
+    assert value("ODP_LN_PE") == N.LN_PE
+    assert value("ODP_LN_XMASK") == N.LN_XMASK
+    assert value("ODP_LN_GMASK") == N.LN_GMASK
+    assert value("ODP_LN_NFFLAG") == N.LN_NFFLAG
+    assert value("ODP_NF_FIELDS") == N.NF_FIELDS
+    assert value("ODP_NF_MASK") == N.NF_MASK
     assert value("ODP_CLIP_AUTOS") == N.CLIP_AUTOS
     assert value("ODP_DTYPE_BF16") == N.DTYPE_BF16
 
@@ -81,3 +88,59 @@ def test_block_helpers_are_pure_host_code(lib):
     assert lib.odp_sqnorm_blocks(1) >= 1
     assert lib.odp_scale_sum_blocks(4096) >= 1
     assert lib.odp_seg_factor_tiles(N.DTYPE_BF16, 4096, 16) >= 1
+    assert lib.odp_nonfinite_blocks(256, 3) == 3
+    assert lib.odp_nonfinite_blocks(264, 2) == 4
+    assert lib.odp_nonfinite_blocks(0, 2) == 0
+
+
+# ---------------------------------------------------------------------------
+# The error contract: invalid arguments return a status code and set the
+# thread's error text before any device work (so these run without a GPU).
+# ---------------------------------------------------------------------------
+
+_BAD = ctypes.c_void_p(16)  # a non-null address; never dereferenced on these paths
+
+
+def _err(lib, rc, code, fragment):
+    assert rc == code, (rc, N.last_error())
+    assert fragment in N.last_error(), N.last_error()
+
+
+def test_table_checks(lib):
+    _err(lib, lib.odp_gaussian_noise(None, None, None, -1, 0, 0, 0), N.ERR_INVALID_ARGUMENT, "negative n_prob")
+    _err(lib, lib.odp_sqnorm(None, None, None, 2, 4, None, None, 1), N.ERR_INVALID_ARGUMENT,
+         "null problem table")
+    _err(lib, lib.odp_scale_sum(None, None, None, 0, 3, None, None, 1, 1, 1.0), N.ERR_INVALID_ARGUMENT,
+         "total_blocks must be 0")
+    _err(lib, lib.odp_nonfinite_columns(None, _BAD, _BAD, 1, 1, None, None), N.ERR_INVALID_ARGUMENT,
+         "null segment arrays")
+
+
+def test_kernel_argument_checks(lib):
+    _err(lib, lib.odp_project(None, 7, None, None, 0, 0, None, None, 1), N.ERR_UNSUPPORTED, "unsupported dtype")
+    _err(lib, lib.odp_project(None, N.DTYPE_BF16, None, None, 0, 0, None, None, 5), N.ERR_UNSUPPORTED, "nkb=5")
+    _err(lib, lib.odp_seg_factor(None, N.DTYPE_F32, None, None, 0, 0, None, None, None, None, 1, 0),
+         N.ERR_UNSUPPORTED, "nkb=0")
+    _err(lib, lib.odp_seg_factor_project(None, _BAD, _BAD, 1, 1, None, None, None, None, 1),
+         N.ERR_INVALID_ARGUMENT, "null segment")
+    _err(lib, lib.odp_linear_sqnorm(None, 9, None, None, 0, 0, None, None, None, None, 1),
+         N.ERR_INVALID_ARGUMENT, "unknown form 9")
+    _err(lib, lib.odp_scale_sum(None, None, None, 0, 0, None, None, 1, 1, 0.0), N.ERR_INVALID_ARGUMENT,
+         "normalize_by must be > 0")
+    _err(lib, lib.odp_linear_clipped_sum(None, None, None, 0, 0, None, None, None, None, 1, 1, -1.0, 0),
+         N.ERR_INVALID_ARGUMENT, "normalize_by must be > 0")
+    _err(lib, lib.odp_philox_words(None, 0, 0, 0, 0, -1, None), N.ERR_INVALID_ARGUMENT, "bad n")
+
+
+def test_clip_factor_argument_checks(lib):
+    def call(n_ex=1, n_groups=1, n_cls=1, mode=N.CLIP_FIXED, gamma=0.0):
+        return lib.odp_clip_factors(None, None, 1, n_ex, None, n_groups, None, 1.0, mode, gamma, n_cls,
+                                    None, None, None, None, None, None, None)
+
+    _err(lib, call(n_groups=0), N.ERR_UNSUPPORTED, "n_groups=0")
+    _err(lib, call(n_cls=9), N.ERR_UNSUPPORTED, "n_cls=9")
+    _err(lib, call(mode=3), N.ERR_INVALID_ARGUMENT, "unknown mode 3")
+    _err(lib, call(mode=N.CLIP_AUTOS, gamma=0.0), N.ERR_INVALID_ARGUMENT, "gamma must be positive")
+    _err(lib, call(n_ex=-1), N.ERR_INVALID_ARGUMENT, "negative n_ex")
+    _err(lib, call(), N.ERR_INVALID_ARGUMENT, "null required pointer")
+    assert call(n_ex=0) == N.ODP_OK  # an empty batch launches nothing

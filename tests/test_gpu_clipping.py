@@ -286,8 +286,14 @@ def test_empty_batch():
     assert aux.batch_size == 0 and aux.clipping_rate == 0.0
 
 
-def test_full_weight_linear_seams_match_oracle():
-    """bf16 full-weight linears through the Gram/outer + clipped-sum kernels, per-group clipping."""
+@pytest.mark.parametrize("pe_bytes", [None, 0])
+def test_full_weight_linear_seams_match_oracle(pe_bytes):
+    """bf16 full-weight linears, per-group clipping.  pe_bytes None: the
+    per-example weight gradients fit in HBM, so the outer-form norm kernel
+    stores them and the clipped sum runs over storage; 0: nothing is stored,
+    so the kernels pick the token-Gram norm form (short examples) and the
+    clipped-sum GEMM."""
+    print(f"drop-in full-weight linears: linear_pe_bytes={pe_bytes}", flush=True)
     g = torch.Generator().manual_seed(21)
     d, h = 64, 96
     params = {
@@ -306,12 +312,14 @@ def test_full_weight_linear_seams_match_oracle():
     def plain(x, W, b):
         return torch.nn.functional.linear(x, W, b)
 
-    n, T = 8, 48  # short examples: the kernels pick the token-Gram norm form for both weights
+    n, T = 8, 48
     x = (torch.randn(n, T, d, generator=g) * torch.logspace(-1, 0.5, n).view(n, 1, 1)).to(torch.bfloat16)
     y = torch.randn(n, T, d, generator=g).to(torch.bfloat16)
     pg = per_group(params, up=0.05, down=0.08)
     fn, st = clipped_grad(make(capture.linear), clipping_norm=pg, batch_argnums=(1, 2), return_aux=True,
                           normalize_by=4.0)
+    if pe_bytes is not None:
+        fn.engine.plan_options["linear_pe_bytes"] = pe_bytes
     (res, aux), _ = fn({k: v.to(DEV) for k, v in params.items()}, x.to(DEV), y.to(DEV), state=st)
     disc = fn.engine._discovery[1]
     assert len(disc.eligible) == 2  # both weights captured; the bias is materialised
@@ -320,3 +328,40 @@ def test_full_weight_linear_seams_match_oracle():
         assert rel(res.pytree[k], ref[k]) <= 2e-2, (k, rel(res.pytree[k], ref[k]))
     for name, v in raux["group_norms"].items():
         assert rel(aux.group_norms[name], v) <= 2e-2
+
+
+@pytest.mark.parametrize("pe_bytes", [None, 0])
+def test_full_weight_non_finite_activation(pe_bytes):
+    """A NaN in one example's activations: the reference zeroes the non-finite
+    entries of that example's weight gradient (nan_to_num,
+    clipping/_pytree.py:520-527) and reports all_finite=False
+    (_clipped_fun.py:98-112,695); a clean batch reports True."""
+    print(f"drop-in non-finite activation: linear_pe_bytes={pe_bytes}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    d, h, n, T = 64, 96, 6, 40
+    params = {"w": (torch.randn(h, d, generator=g) / d**0.5).to(torch.bfloat16)}
+
+    def make(lin):
+        def loss(p, xi, yi):
+            return (lin(xi, p["w"], None).float() * yi.float()).sum() / T
+
+        return loss
+
+    def plain(x, W, b):
+        return torch.nn.functional.linear(x, W, b)
+
+    x = torch.randn(n, T, d, generator=g).to(torch.bfloat16)
+    y = torch.randn(n, T, h, generator=g).to(torch.bfloat16)
+    for bad in (False, True):
+        xb = x.clone()
+        if bad:
+            xb[2, 11, 5] = float("nan")
+        fn, st = clipped_grad(make(capture.linear), clipping_norm=0.5, batch_argnums=(1, 2), return_stats=True)
+        if pe_bytes is not None:
+            fn.engine.plan_options["linear_pe_bytes"] = pe_bytes
+        (res, stats), _ = fn({k: v.to(DEV) for k, v in params.items()}, xb.to(DEV), y.to(DEV), state=st)
+        assert len(fn.engine._discovery[1].eligible) == 1
+        assert stats.all_finite is (not bad)
+        assert torch.isfinite(res.pytree["w"].float()).all()
+        ref, _ = dp_ref.clipped_grad(make(plain), params, (xb, y), clipping_norm=0.5)
+        assert rel(res.pytree["w"], ref["w"]) <= 2e-2, rel(res.pytree["w"], ref["w"])

@@ -341,22 +341,55 @@ def test_storage_takes_the_outer_form():
     assert (res[None][0] - res[0][0]).norm() <= 1e-2 * res[0][0].norm()
 
 
-def test_stored_path_zeroes_non_finite_entries():
-    """A NaN activation makes one column of one example's weight gradient NaN.
-    The reference zeroes non-finite per-example entries before the norm and
-    the scale (nan_to_num, clipping/_pytree.py:520-527); so does the path
-    that stores the per-example gradients (the clipped-sum GEMM would
-    propagate the NaN instead)."""
-    print("stored path: non-finite entries", flush=True)
+# Paths a full-weight site can take: (norm form, linear_pe_bytes, prescale_bytes).
+_PATHS = {
+    "stored": (None, None, 8 << 30),        # outer norms store each M_s; clipped sum over storage
+    "gemm_outer": (N.FORM_OUTER, 0, 8 << 30),  # outer norms; prescaled X' and the clipped-sum GEMM
+    "gemm_gram": (N.FORM_GRAM, 0, 8 << 30),    # token-Gram norms; prescaled X' and the GEMM
+    "gemm_inreg": (N.FORM_GRAM, 0, 0),      # token-Gram norms; clip factors applied in registers
+}
+
+
+@pytest.mark.parametrize("kind", ["clean", "nan_x", "inf_g", "both"])
+@pytest.mark.parametrize("path", sorted(_PATHS))
+def test_non_finite_entries_are_zeroed(path, kind):
+    """Non-finite activations / output gradients make whole columns / rows of
+    one example's weight gradient non-finite.  The reference zeroes the
+    non-finite per-example entries before the norm and the scale
+    (nan_to_num, clipping/_pytree.py:520-527) and its test asserts a finite
+    clipped sum (test_clipped_grad.py:64-87); every path does the same and
+    reports it through linear_finite().  Non-finite values in padding rows
+    (in no segment) are ignored."""
+    print(f"non-finite entries: path={path} kind={kind}", flush=True)
+    form, pe_bytes, pre_bytes = _PATHS[path]
     n_ex, T, d_in, d_out = 4, 48, 136, 72
     X, G, seg = _case(n_ex, T, d_in, d_out, [48, 30, 48, 20], seed=41)
-    X[T + 5, 17] = float("nan")  # example 1, feature 17
+    X[T + 40, 3] = float("nan")  # example 1 has 30 rows: a padding row
+    if kind in ("nan_x", "both"):
+        X[T + 5, 17] = float("nan")  # example 1, feature 17
+    if kind in ("inf_g", "both"):
+        G[2 * T + 40, 3] = float("inf")  # example 2, output 3
+        G[3 * T + 2, 70] = float("-inf")  # example 3, output 70
+        X[3 * T + 7, 130] = float("inf")  # example 3, feature 130
     pe, _ = _ref_norms(X, G, seg)
-    assert torch.isnan(pe[1][:, 17]).all() and not torch.isnan(pe[0]).any()
-    finite = torch.nan_to_num(pe, nan=0.0)
+    if kind == "nan_x":
+        assert torch.isnan(pe[1][:, 17]).all() and torch.isfinite(pe[0]).all()
+    finite = torch.nan_to_num(pe, nan=0.0, posinf=0.0, neginf=0.0)
     C = float(finite.pow(2).sum((1, 2)).sqrt().median())
-    plan, res, _ = _plan(X, G, seg, C=C, mode=N.CLIP_FIXED, form=None, normalize_by=2.0)
-    assert plan.lin_pe.numel() > 0
+    d_in, d_out = X.shape[1], G.shape[1]
+    _, rnd = leaf_guards([(d_out, d_in)], [torch.bfloat16])
+    rel_, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[C], effective=C, normalize_by=2.0,
+                    guards=[(rel_, ab, torch.bfloat16)])
+    plan = GhostPlan(segments=seg, leaves=[LeafOut((d_out, d_in), torch.bfloat16)], clip=clip,
+                     linear_sites=[LinearSite(X.to(DEV), G.to(DEV), 0, form)], device=DEV,
+                     linear_pe_bytes=pe_bytes, prescale_bytes=pre_bytes)
+    res = plan.run()
+    finite_flag = bool(plan.linear_finite().item())
+    torch.cuda.synchronize()
+    assert (plan.lin_pe.numel() > 0) == (path == "stored")
+    kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
+    assert kinds == {N.FORM_GRAM if form == N.FORM_GRAM else N.FORM_OUTER}
     outs, norms = [], []
     for i in range(n_ex):
         c, nrm, _ = dp_ref.clip_pytree({"w": pe[i].to(torch.bfloat16)}, C)
@@ -367,3 +400,11 @@ def test_stored_path_zeroes_non_finite_entries():
     assert torch.isfinite(got).all()
     assert (got - want).norm() <= 2e-2 * want.norm()
     assert torch.allclose(res.norms.double().cpu(), torch.stack(norms).double(), rtol=2e-3)
+    assert finite_flag == (kind == "clean")
+    if path != "stored":
+        words = (d_in + 31) // 32
+        xmask = plan.nf_mask[: n_ex * words].view(n_ex, words).cpu()
+        want_cols = {"clean": [], "nan_x": [(1, 17)], "inf_g": [(3, 130)], "both": [(1, 17), (3, 130)]}[kind]
+        got_cols = [(s, 32 * w + b) for s in range(n_ex) for w in range(words) for b in range(32)
+                    if (int(xmask[s, w]) >> b) & 1]
+        assert got_cols == want_cols
