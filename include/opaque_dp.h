@@ -58,7 +58,12 @@ typedef enum odp_status {
   ODP_ERR_HIP = 3
 } odp_status;
 
-typedef enum odp_dtype { ODP_DTYPE_F32 = 0, ODP_DTYPE_BF16 = 1 } odp_dtype;
+typedef enum odp_dtype {
+  ODP_DTYPE_F32 = 0,
+  ODP_DTYPE_BF16 = 1,
+  ODP_DTYPE_F16 = 2, /* noise, sqnorm and scale-sum only */
+  ODP_DTYPE_F64 = 3  /* noise, sqnorm and scale-sum only */
+} odp_dtype;
 
 typedef enum odp_clip_mode {
   ODP_CLIP_FIXED = 0, /* ratio = C / ||g||, clamped to 1 (clip_pytree) */
@@ -324,30 +329,46 @@ int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
                            int32_t n_groups, float normalize_by, int32_t prescaled);
 
 /* ---- odp_gaussian_noise --------------------------------------------------
- * out[i] = round_out(in[i] + f32(sigma * sqrt 2) * erfinv(2u - 1)) with
- * u = clamp((x >> 8) * 2^-24, eps, 1 - eps), x = word (e & 3) of
- * Philox4x32-10(counter = {e >> 2 (64-bit), stream_tag, 0}, key = seed)
- * and e = flat_offset + i the element's index in the flattened pytree.
- * sigma == 0 copies the input.  With the bounded flag the Gaussian is
- * renormalised over [low, high] (u -> Phi(za) + u (Phi(zb) - Phi(za))) and
- * the result clamped, as the reference's bounded mode does.  in and out may
- * alias.                                                                   */
+ * out[i] = round_out(in[i] + sigma * sqrt(2) * erfinv(2u - 1)) for element
+ * e = flat_offset + i of the flattened pytree: the inverse-CDF sampler of
+ * _gaussian.py:252-266, with u = clamp(u, eps, 1 - eps) of the compute
+ * dtype.  Float32 compute (the default) takes the 24-bit uniform u = k 2^-24
+ * of a float32 torch.rand, with k = bits [24 (e mod 16), + 24) of the
+ * 384-bit string made of the Philox4x32-10 outputs (words in order, bit 0
+ * first) for counters 3 (e >> 4) + b, b = 0, 1, 2; erfinv is evaluated as
+ * x P(log2(1 - x^2)) (max relative error 4e-7).  Float64 compute
+ * (compute_dtype ODP_DTYPE_F64) takes u = (w >> 11) 2^-53 with w = words
+ * 2 (e & 1) + 1 : 2 (e & 1) of the block for counter e >> 1, in float64
+ * (library erfinv), and casts the result to the output dtype.  A Philox
+ * counter is {c (64-bit), stream_tag, 0} and the key the 64-bit seed, so the
+ * stream is a pure function of (seed, stream_tag, e).  Inputs are converted
+ * to the compute dtype and results rounded to nearest-even in the output
+ * dtype.  sigma == 0 copies the input.  With bounded != 0 the Gaussian is
+ * renormalised over [low, high] (u -> Phi(za) + u (Phi(zb) - Phi(za)),
+ * za = (low - in) / sigma) and the result clamped, as the reference's
+ * bounded mode does (low <= 0 <= high).  in and out may alias.  One
+ * workgroup covers 4096 consecutive elements (odp_gaussian_noise_blocks).   */
 enum {
   ODP_NZ_IN = 0, ODP_NZ_OUT = 1, ODP_NZ_N = 2, ODP_NZ_FLAT_OFFSET = 3,
   ODP_NZ_SIGMA = 4,     /* double bit pattern                               */
-  ODP_NZ_DTYPES = 5,    /* in dtype | out dtype << 8 | bounded << 16        */
-  ODP_NZ_LOW = 6,       /* double bit pattern (bounded only)                */
-  ODP_NZ_HIGH = 7,      /* double bit pattern (bounded only)                */
+  ODP_NZ_DTYPES = 5,    /* in dtype | out dtype << 8 (odp_dtype)            */
   ODP_NZ_FIELDS = 8
 };
 int64_t odp_gaussian_noise_blocks(int64_t flat_offset, int64_t n);
 int odp_gaussian_noise(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
-                       int32_t n_prob, int32_t total_blocks, uint64_t seed, uint32_t stream_tag);
+                       int32_t n_prob, int32_t total_blocks, uint64_t seed, uint32_t stream_tag,
+                       int32_t compute_dtype, int32_t bounded, double low, double high);
 
 /* Raw Philox4x32-10 words for counters [ctr0, ctr0 + n), key = seed: for
  * known-answer and determinism tests of the device stream.               */
 int odp_philox_words(odp_stream_t stream, uint64_t ctr0, uint32_t ctr2, uint32_t ctr3,
                      uint64_t seed, int64_t n, uint32_t* out /* [n][4] */);
+
+/* The float32 inverse-CDF transform of the noise kernel on its own:
+ * out[i] = sqrt(2) * erfinv(2u - 1) for the 24-bit uniform k = k0 + i
+ * (u = clamp(k 2^-24, eps, 1 - eps)), k0 + n <= 2^24: for exhaustive
+ * accuracy tests against a float64 erfinv.                               */
+int odp_noise_icdf(odp_stream_t stream, uint32_t k0, int64_t n, float* out);
 
 /* ---- library -------------------------------------------------------------- */
 int odp_abi_version(void);

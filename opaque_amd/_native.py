@@ -17,6 +17,8 @@ ERR_UNSUPPORTED = 2
 ERR_HIP = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
+DTYPE_F64 = 3
 CLIP_FIXED = 0
 CLIP_AUTOS = 1
 
@@ -80,8 +82,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i32, _c_i32, _c_f32],
     ),
     "odp_gaussian_noise_blocks": (_c_i64, [_c_i64, _c_i64]),
-    "odp_gaussian_noise": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _c_u64, _c_u32]),
+    "odp_gaussian_noise": (
+        _c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _c_u64, _c_u32, _c_i32, _c_i32, _c_f64, _c_f64]),
     "odp_philox_words": (_c_int, [_ptr, _c_u64, _c_u32, _c_u32, _c_u64, _c_i64, _ptr]),
+    "odp_noise_icdf": (_c_int, [_ptr, _c_u32, _c_i64, _ptr]),
     "odp_linear_tiles": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64]),
     "odp_linear_prescale_blocks": (_c_i64, [_c_i64]),
     "odp_linear_prescale": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32]),

@@ -55,18 +55,43 @@ __device__ __forceinline__ void odp_gstore(T* p, T v) {
   *(ODP_GMEM T*)(ODP_GMEM void*)p = v;
 }
 
+// Element i of a tensor of `dtype` as float (float64 rounds to nearest).
 __device__ __forceinline__ float odp_load_as_float(const void* p, int64_t i, int dtype) {
   if (dtype == ODP_DTYPE_BF16) return odp_bf2f(((const uint16_t*)p)[i]);
+  if (dtype == ODP_DTYPE_F16) return (float)((const _Float16*)p)[i];
+  if (dtype == ODP_DTYPE_F64) return (float)((const double*)p)[i];
   return ((const float*)p)[i];
 }
 
+// Stores v rounded to nearest-even in `dtype`.
 __device__ __forceinline__ void odp_store_from_float(void* p, int64_t i, int dtype, float v) {
   if (dtype == ODP_DTYPE_BF16) odp_gstore((uint16_t*)p + i, odp_f2bf(v));
+  else if (dtype == ODP_DTYPE_F16) odp_gstore((_Float16*)p + i, (_Float16)v);
+  else if (dtype == ODP_DTYPE_F64) odp_gstore((double*)p + i, (double)v);
   else odp_gstore((float*)p + i, v);
+}
+
+// Element i as double (exact for every dtype).
+__device__ __forceinline__ double odp_load_as_double(const void* p, int64_t i, int dtype) {
+  if (dtype == ODP_DTYPE_F64) return ((const double*)p)[i];
+  return (double)odp_load_as_float(p, i, dtype);
+}
+
+// Stores a double rounded to nearest-even in `dtype` (float first for the
+// 16-bit types, as torch casts float64 tensors).
+__device__ __forceinline__ void odp_store_from_double(void* p, int64_t i, int dtype, double v) {
+  if (dtype == ODP_DTYPE_F64) odp_gstore((double*)p + i, v);
+  else odp_store_from_float(p, i, dtype, (float)v);
 }
 
 // Rounds a float to the value it takes when stored in `dtype`.
 __device__ __forceinline__ float odp_round_to(float v, int dtype) {
   if (dtype == ODP_DTYPE_BF16) return odp_bf2f(odp_f2bf(v));
+  if (dtype == ODP_DTYPE_F16) return (float)(_Float16)v;
   return v;
+}
+
+// Bytes per element of `dtype`.
+__host__ __device__ __forceinline__ int odp_dtype_size(int dtype) {
+  return dtype == ODP_DTYPE_F64 ? 8 : dtype == ODP_DTYPE_F32 ? 4 : 2;
 }

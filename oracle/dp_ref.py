@@ -290,19 +290,41 @@ def clipped_count(norms: torch.Tensor, threshold: float) -> int:
 # ---------------------------------------------------------------------------
 
 
-def gaussian_noise_reference(tree, stddev: float, key: int, step: int, compute_dtype=torch.float32):
-    """Inverse-CDF noise from a CPU mt19937 generator seeded by fold_in(key, step)."""
-    if stddev == 0:
-        return tree
-    seed = fold_in_seed(key_seed(key), step) % (2**63 - 1)
-    gen = torch.Generator().manual_seed(seed)
+def gaussian_noise_reference(tree, stddev, key: int, step: int, compute_dtype=torch.float32, bound=None,
+                             stream_fold: int | None = None):
+    """The reference's CPU sampler (DPS/noise/_gaussian.py:235-301,317-405).
+
+    A CPU ``torch.Generator`` seeded by ``fold_in(key, step)`` (or
+    ``fold_in(fold_in(key, stream_fold), step)`` for the paired streams,
+    :329-334) reduced modulo 2^63 - 1 (ENG/random/_engine.py:98-101) draws
+    ``torch.rand`` uniforms leaf by leaf in sorted-key order; a leaf whose
+    stddev is 0 draws nothing and is returned (clamped to the bound, if any).
+    ``stddev`` is a float or a dict path -> float (per-group sigma).
+    """
+    seed = fold_in_seed(key_seed(key), step) if stream_fold is None else \
+        fold_in_seed(key_seed(key), stream_fold, step)
+    gen = torch.Generator().manual_seed(seed % (2**63 - 1))
     eps = torch.finfo(compute_dtype).eps
+    sqrt2 = math.sqrt(2.0)
     out = {}
     for p, c in flatten(tree):
+        sd = float(stddev[p]) if isinstance(stddev, dict) else float(stddev)
+        if sd == 0:
+            out[p] = c if bound is None else torch.clamp(c, min=bound[0], max=bound[1])
+            continue
         u = torch.rand(c.shape, dtype=compute_dtype, generator=gen)
-        u = torch.clamp(u, min=eps, max=1.0 - eps)
-        x = c.to(compute_dtype) + stddev * math.sqrt(2.0) * torch.erfinv(2.0 * u - 1.0)
-        out[p] = x.to(c.dtype)
+        cc = c.to(compute_dtype) if c.dtype != compute_dtype else c
+        if bound is None:
+            u = torch.clamp(u, min=eps, max=1.0 - eps)
+            x = cc + sd * sqrt2 * torch.erfinv(2.0 * u - 1.0)
+        else:
+            low, high = bound
+            z_low, z_high = (low - cc) / sd, (high - cc) / sd
+            alpha = 0.5 * (1.0 + torch.erf(z_low / sqrt2))
+            beta = 0.5 * (1.0 + torch.erf(z_high / sqrt2))
+            u = torch.clamp(alpha + u * (beta - alpha), min=eps, max=1.0 - eps)
+            x = torch.clamp(cc + sd * sqrt2 * torch.erfinv(2.0 * u - 1.0), min=low, max=high)
+        out[p] = x.to(c.dtype) if c.dtype != compute_dtype else x
     return rebuild(tree, out)
 
 

@@ -107,7 +107,13 @@ def _err(lib, rc, code, fragment):
 
 
 def test_table_checks(lib):
-    _err(lib, lib.odp_gaussian_noise(None, None, None, -1, 0, 0, 0), N.ERR_INVALID_ARGUMENT, "negative n_prob")
+    _err(lib, lib.odp_gaussian_noise(None, None, None, -1, 0, 0, 0, 0, 0, 0.0, 0.0), N.ERR_INVALID_ARGUMENT,
+         "negative n_prob")
+    _err(lib, lib.odp_gaussian_noise(None, None, None, 0, 0, 0, 0, N.DTYPE_BF16, 0, 0.0, 0.0), N.ERR_UNSUPPORTED,
+         "compute_dtype 1")
+    _err(lib, lib.odp_gaussian_noise(None, None, None, 0, 0, 0, 0, N.DTYPE_F32, 1, 0.5, 2.0),
+         N.ERR_INVALID_ARGUMENT, "low <= 0 <= high")
+    _err(lib, lib.odp_noise_icdf(None, 0, (1 << 24) + 1, _BAD), N.ERR_INVALID_ARGUMENT, "n <= 2^24")
     _err(lib, lib.odp_sqnorm(None, None, None, 2, 4, None, None, 1), N.ERR_INVALID_ARGUMENT,
          "null problem table")
     _err(lib, lib.odp_scale_sum(None, None, None, 0, 3, None, None, 1, 1, 1.0), N.ERR_INVALID_ARGUMENT,

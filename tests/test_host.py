@@ -15,7 +15,7 @@ from opaque_amd.clipping import auto_clipped_grad, clipped_grad, per_group
 from opaque_amd.noise import gaussian_noise
 from opaque_amd.noise_allocation import paired_noise_stddevs, per_group_noise_stddev
 from opaque_amd.pytree import param_path, tree_flatten_with_paths, tree_unflatten
-from opaque_amd.random import RngKey, fold_in, key, split
+from opaque_amd.random import RngKey, fold_in, key, split, generator_from_key
 from opaque_amd.types import ClippedPytree, NoisedPytree, PerGroup, clipped
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -111,6 +111,22 @@ def test_rng_keys_match_oracle():
     a, b, c = split(k, 3)
     assert len({a.seed, b.seed, c.seed}) == 3
     assert key(-1).seed == 2**64 - 1
+
+
+def test_rng_keys_known_answers():
+    """fold_in of the product against BLAKE2b digests of literal byte strings
+    in the reference's format (ENG/random/_engine.py:27-35: 16-byte
+    little-endian signed ints or UTF-8, each followed by b"|")."""
+    import hashlib
+
+    def digest(hexbytes):
+        return int.from_bytes(hashlib.blake2b(bytes.fromhex(hexbytes), digest_size=8).digest(), "little")
+
+    assert fold_in(key(42), 7).seed == digest("2a" + "00" * 15 + "7c" + "07" + "00" * 15 + "7c")
+    assert fold_in(key(-1), -3).seed == digest("ff" * 8 + "00" * 8 + "7c" + "fd" + "ff" * 15 + "7c")
+    assert fold_in(key(5), "rank").seed == digest("05" + "00" * 15 + "7c" + "72616e6b" + "7c")
+    k = fold_in(key(42), 7)
+    assert generator_from_key(k).initial_seed() == k.seed % (2**63 - 1)
 
 
 def test_pytree_order_sorted_keys_and_roundtrip():

@@ -245,3 +245,212 @@ def test_fold_in_variadic_equals_sequential():
     k = dp_ref.key_seed(42)
     assert dp_ref.fold_in_seed(dp_ref.fold_in_seed(k, 7), 3) == dp_ref.fold_in_seed(k, 7, 3)
     assert dp_ref.fold_in_seed(k, "noise") != dp_ref.fold_in_seed(k, "sampling")
+
+
+# ---------------------------------------------------------------------------
+# fold_in: known answers from the byte format of ENG/random/_engine.py:27-35
+# (each part as a 16-byte little-endian signed int, or UTF-8 text, followed
+# by b"|"; BLAKE2b with an 8-byte digest read little-endian).  The expected
+# values hash literal byte strings, so a width, sign, byte-order or
+# separator slip in the restatement fails.
+# ---------------------------------------------------------------------------
+
+FOLD_IN_KAT = [
+    # (seed, datum, literal digest input in hex)
+    (42, 7, "2a" + "00" * 15 + "7c" + "07" + "00" * 15 + "7c"),
+    (2**64 - 1, -3, "ff" * 8 + "00" * 8 + "7c" + "fd" + "ff" * 15 + "7c"),
+    (5, "rank", "05" + "00" * 15 + "7c" + "72616e6b" + "7c"),
+    (0, 0, "00" * 16 + "7c" + "00" * 16 + "7c"),
+    (2**40 + 3, 2**33, "03000000" + "0001" + "00" * 10 + "7c" + "00000000" + "02" + "00" * 11 + "7c"),
+]
+
+
+def _blake_le(hexbytes: str) -> int:
+    import hashlib
+
+    return int.from_bytes(hashlib.blake2b(bytes.fromhex(hexbytes), digest_size=8).digest(), "little")
+
+
+@pytest.mark.parametrize("seed,datum,hexbytes", FOLD_IN_KAT)
+def test_fold_in_known_answers(seed, datum, hexbytes):
+    assert dp_ref.fold_in_seed(seed, datum) == _blake_le(hexbytes)
+
+
+def test_key_reduces_to_uint64():
+    assert dp_ref.key_seed(-1) == 2**64 - 1
+    assert dp_ref.key_seed(2**64 + 5) == 5
+
+
+# ---------------------------------------------------------------------------
+# The reference's CPU sampler (dp_ref.gaussian_noise_reference)
+# ---------------------------------------------------------------------------
+
+
+def _ref_uniforms(key: int, step: int, shapes, dtype=torch.float32, stream_fold=None):
+    """The generator the reference seeds for (key, step): its seed from the
+    fold_in known answers above (fold_in(key, step) mod 2^63 - 1), draws in
+    sorted-key order."""
+    seed = dp_ref.fold_in_seed(dp_ref.key_seed(key), *(() if stream_fold is None else (stream_fold,)), step)
+    gen = torch.Generator().manual_seed(seed % (2**63 - 1))
+    return [torch.rand(s, dtype=dtype, generator=gen) for s in shapes]
+
+
+def test_reference_sampler_statistics():
+    """KS, mean and std as the reference's noise tests check them
+    (DPS-T/noise/test_noise.py:98-114, test_gaussian_compute_dtype.py:26-39)."""
+    from scipy import stats
+
+    out = dp_ref.gaussian_noise_reference({"a": torch.zeros(10_000)}, 1.0, key=42, step=0)["a"].double().numpy()
+    assert abs(out.mean()) < 0.05
+    assert abs(out.std() - 1.0) < 0.1
+    assert stats.kstest(out, "norm").pvalue > 0.01
+    bf = dp_ref.gaussian_noise_reference({"a": torch.zeros(16384, dtype=torch.bfloat16)}, 2.0, key=7, step=0)["a"]
+    assert bf.dtype == torch.bfloat16 and abs(bf.float().std().item() - 2.0) < 0.05
+
+
+def test_reference_sampler_determinism_and_passthrough():
+    """Same key and step give the same values, another key or step other
+    values (test_noise.py:214-259); sigma = 0 returns the input unchanged and
+    a bound clamps it (_gaussian.py:245-250)."""
+    tree = {"w": torch.randn(50, generator=torch.Generator().manual_seed(0))}
+    a = dp_ref.gaussian_noise_reference(tree, 0.5, key=3, step=1)["w"]
+    assert torch.equal(a, dp_ref.gaussian_noise_reference(tree, 0.5, key=3, step=1)["w"])
+    assert not torch.equal(a, dp_ref.gaussian_noise_reference(tree, 0.5, key=4, step=1)["w"])
+    assert not torch.equal(a, dp_ref.gaussian_noise_reference(tree, 0.5, key=3, step=2)["w"])
+    assert dp_ref.gaussian_noise_reference(tree, 0.0, key=3, step=1)["w"] is tree["w"]
+    clamped = dp_ref.gaussian_noise_reference(tree, 0.0, key=3, step=1, bound=(-0.5, 0.25))["w"]
+    assert torch.equal(clamped, tree["w"].clamp(-0.5, 0.25))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_reference_sampler_is_the_inverse_cdf_of_its_stream(dtype):
+    """Phi((x - c) / sigma) equals the clamped uniform the generator drew for
+    that element, leaf by leaf in sorted-key order, with a sigma = 0 leaf
+    drawing nothing; a wrong seed, draw order, sqrt(2) or 2u - 1 fails."""
+    from scipy.stats import norm
+
+    g = torch.Generator().manual_seed(1)
+    tree = {"z": torch.randn(300, generator=g).to(dtype), "a": torch.randn(4, 5, generator=g).to(dtype),
+            "m": torch.randn(7, generator=g).to(dtype)}
+    sd = {("a",): 0.7, ("m",): 0.0, ("z",): 1.3}
+    out = dp_ref.gaussian_noise_reference(tree, sd, key=11, step=4, compute_dtype=dtype)
+    ua, uz = _ref_uniforms(11, 4, [(4, 5), (300,)], dtype)  # "m" draws nothing
+    eps = torch.finfo(dtype).eps
+    tol = 2e-6 if dtype == torch.float32 else 1e-12
+    for name, u, s in (("a", ua, 0.7), ("z", uz, 1.3)):
+        got = norm.cdf(((out[name] - tree[name]).double() / s).numpy())
+        want = u.clamp(eps, 1 - eps).double().numpy()
+        np.testing.assert_allclose(got, want, rtol=0, atol=tol * 8)
+    assert out["m"] is tree["m"]
+
+
+def test_reference_sampler_paired_streams_fold_their_tags():
+    """The paired second-moment streams use fold_in(fold_in(key, 1|2), step)
+    (_gaussian.py:329-334)."""
+    from scipy.stats import norm
+
+    tree = {"g": torch.zeros(64)}
+    for fold in (1, 2):
+        out = dp_ref.gaussian_noise_reference(tree, 1.0, key=9, step=3, stream_fold=fold)["g"]
+        (u,) = _ref_uniforms(9, 3, [(64,)], stream_fold=fold)
+        np.testing.assert_allclose(norm.cdf(out.double().numpy()), u.double().numpy(), atol=2e-5)
+
+
+def test_reference_bounded_sampler_distribution():
+    """With bound B and max_norm 1 the output is a truncated normal on
+    [-B, B] (DPS-T/noise/test_bounded_gaussian.py:220-235) inside the bound
+    (:72-88), with variance below sigma^2 (:237-242)."""
+    from scipy import stats
+
+    out = dp_ref.gaussian_noise_reference({"a": torch.zeros(50_000)}, 1.0, key=42, step=0, bound=(-2.0, 2.0))["a"]
+    x = out.double().numpy()
+    assert x.min() >= -2.0 and x.max() <= 2.0 and x.var() < 1.0
+    assert stats.kstest(x, stats.truncnorm.cdf, args=(-2.0, 2.0, 0.0, 1.0)).pvalue > 0.01
+    asym = dp_ref.gaussian_noise_reference({"a": torch.zeros(10_000)}, 1.0, key=0, step=0, bound=(-1.0, 4.0))["a"]
+    assert asym.min() >= -1.0 and asym.max() <= 4.0
+
+
+def test_reference_bounded_sampler_reduces_to_the_plain_one():
+    """A bound far outside the noise leaves alpha = 0 and beta = 1, so the
+    bounded sampler equals the unbounded one on the same stream."""
+    tree = {"w": torch.randn(500, generator=torch.Generator().manual_seed(2)).double()}
+    a = dp_ref.gaussian_noise_reference(tree, 0.3, key=5, step=1, compute_dtype=torch.float64)["w"]
+    b = dp_ref.gaussian_noise_reference(tree, 0.3, key=5, step=1, compute_dtype=torch.float64,
+                                        bound=(-1e6, 1e6))["w"]
+    torch.testing.assert_close(a, b, rtol=0, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# The device stream restated (philox_ref): bit layout and transforms
+# ---------------------------------------------------------------------------
+
+
+def test_uniform24_bit_layout_brute_force():
+    """Element e's 24-bit uniform is bits [24 (e mod 16), + 24) of the 384-bit
+    string of blocks 3 (e >> 4) .. + 2, sliced here from a Python integer."""
+    seed, tag, off, n = 0x0123456789ABCDEF, 5, 13, 70
+    got = philox_ref.uniform24_for_elements(seed, off, n, tag)
+    for i in range(n):
+        e = off + i
+        big = 0
+        for b in range(3):
+            ctr = 3 * (e >> 4) + b
+            w = philox_ref.philox4x32_10(ctr & 0xFFFFFFFF, ctr >> 32, tag, 0, seed & 0xFFFFFFFF, seed >> 32)
+            for q in range(4):
+                big |= int(w[q]) << (32 * (4 * b + q))
+        assert int(got[i]) == (big >> (24 * (e % 16))) & 0xFFFFFF, i
+
+
+def test_uniform53_bit_layout_brute_force():
+    seed, tag, off, n = 0xFEDCBA9876543210, 2, 7, 9
+    got = philox_ref.uniform53_for_elements(seed, off, n, tag)
+    for i in range(n):
+        e = off + i
+        w = philox_ref.philox4x32_10((e >> 1) & 0xFFFFFFFF, e >> 33, tag, 0, seed & 0xFFFFFFFF, seed >> 32)
+        pair = int(w[2 * (e & 1)]) | (int(w[2 * (e & 1) + 1]) << 32)
+        assert int(got[i]) == pair >> 11
+
+
+def test_uniform24_is_uniform():
+    """Chi-square of the top 8 bits over 2^18 elements, and every value in range."""
+    from scipy import stats
+
+    k = philox_ref.uniform24_for_elements(99, 0, 1 << 18)
+    assert k.min() >= 0 and k.max() < (1 << 24)
+    hist = np.bincount(k >> 16, minlength=256)
+    assert stats.chisquare(hist).pvalue > 1e-3
+
+
+def test_device_stream_transform_is_the_inverse_cdf():
+    """Phi of the noise equals the clamped uniform (float32 and float64 grids)."""
+    from scipy.stats import norm
+
+    for wide, bits in ((False, 24), (True, 53)):
+        x = philox_ref.gaussian_noise(np.zeros(4000), 1.7, seed=77, flat_offset=123, tag=1, wide=wide)
+        k = (philox_ref.uniform53_for_elements if wide else philox_ref.uniform24_for_elements)(77, 123, 4000, 1)
+        np.testing.assert_allclose(norm.cdf(x / 1.7), philox_ref.uniforms(k, bits), rtol=0, atol=1e-12)
+
+
+def test_device_stream_bounded_sampler():
+    """Truncated normal on the bound; a far bound reduces to the plain sampler;
+    sigma = 0 clamps."""
+    from scipy import stats
+
+    x = philox_ref.gaussian_noise_bounded(np.zeros(50_000), 1.0, -2.0, 2.0, seed=42)
+    assert x.min() >= -2.0 and x.max() <= 2.0
+    assert stats.kstest(x, stats.truncnorm.cdf, args=(-2.0, 2.0, 0.0, 1.0)).pvalue > 0.01
+    c = np.linspace(-3, 3, 300)
+    far = philox_ref.gaussian_noise_bounded(c, 0.4, -1e6, 1e6, seed=8, flat_offset=5)
+    np.testing.assert_allclose(far, philox_ref.gaussian_noise(c, 0.4, seed=8, flat_offset=5), atol=1e-9)
+    np.testing.assert_array_equal(philox_ref.gaussian_noise_bounded(c, 0.0, -1.0, 2.0, seed=1), np.clip(c, -1, 2))
+
+
+@pytest.mark.parametrize("wide", [False, True])
+def test_device_stream_ks_p_values_are_uniform_over_seeds(wide):
+    """A fixed-seed KS test can fail by chance; over many seeds the p-values
+    of a sound stream are uniform on [0, 1]."""
+    from scipy import stats
+
+    ps = [stats.kstest(philox_ref.gaussian_noise(np.zeros(20_000), 1.0, seed=s, wide=wide), "norm").pvalue
+          for s in range(60)]
+    assert stats.kstest(ps, "uniform").pvalue > 0.01
