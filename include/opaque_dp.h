@@ -61,8 +61,8 @@ typedef enum odp_status {
 typedef enum odp_dtype {
   ODP_DTYPE_F32 = 0,
   ODP_DTYPE_BF16 = 1,
-  ODP_DTYPE_F16 = 2, /* noise, sqnorm and scale-sum only */
-  ODP_DTYPE_F64 = 3  /* noise, sqnorm and scale-sum only */
+  ODP_DTYPE_F16 = 2, /* noise, sqnorm, clip factors and scale-sum only */
+  ODP_DTYPE_F64 = 3  /* noise, sqnorm, clip factors and scale-sum only */
 } odp_dtype;
 
 typedef enum odp_clip_mode {
@@ -171,13 +171,14 @@ int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
 
 /* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
  * For leaves that are not behind a captured linear op, the per-example
- * gradients X[n_seg][n] are materialised; each workgroup sums
- * f32(x)^2 (non-finite x counted as 0) over a chunk of one segment in fp64
- * and writes part[seg_example[s] * part_stride + slot + chunk]; a problem
- * uses odp_sqnorm_blocks(n) slots.                                        */
+ * gradients X[n_seg][n] are materialised; each workgroup sums x^2
+ * (non-finite x counted as 0; squared in float32, or in float64 with bit 8
+ * of ODP_SQ_DTYPE, as clip_pytree's accumulation dtype does) over a chunk
+ * of one segment in fp64 and writes part[seg_example[s] * part_stride +
+ * slot + chunk]; a problem uses odp_sqnorm_blocks(n) slots.               */
 enum {
   ODP_SQ_X = 0, ODP_SQ_N = 1, ODP_SQ_NSEG = 2, ODP_SQ_SEG_FIRST = 3,
-  ODP_SQ_SLOT = 4, ODP_SQ_DTYPE = 5,
+  ODP_SQ_SLOT = 4, ODP_SQ_DTYPE = 5, /* x dtype | square in float64 << 8  */
   ODP_SQ_FIELDS = 8
 };
 int64_t odp_sqnorm_blocks(int64_t n);
@@ -192,8 +193,9 @@ int odp_sqnorm(odp_stream_t stream, const int64_t* problems, const int32_t* work
  * R_g, device), guard[2 * n_cls] and cls_dtype[n_cls] (device).  Per example:
  * group squared norms in fp64, ratio per group (mode), then per dtype class
  * c: scale = ratio * guard[2c] - guard[2c+1]; min(1, .) for FIXED;
- * non-finite -> 0; max(0, .); rounded to cls_dtype[c].
- * Outputs: scale_out[c][g][ex] (f32 holding the rounded value),
+ * non-finite -> 0; max(0, .); rounded to cls_dtype[c] (any odp_dtype).
+ * Outputs: scale_out[c][g][ex] (float64 holding the value as the class
+ * dtype stores it),
  * norm_out[ex] = f32(sqrt(total)), group_norm_out[g][ex] (may be null),
  * clipped_out[g][ex] = f32(group norm) > f32(threshold) (uint8, may be
  * null), clipped_total_out[ex] = norm_out > f32(effective threshold).       */
@@ -201,28 +203,31 @@ int odp_clip_factors(odp_stream_t stream, const double* part, int64_t n_slots, i
                      const int64_t* group_slot_start, int32_t n_groups, const double* thresholds,
                      double effective_threshold, int32_t mode, double gamma,
                      int32_t n_cls, const double* guard, const int32_t* cls_dtype,
-                     float* scale_out, float* norm_out, float* group_norm_out,
+                     double* scale_out, float* norm_out, float* group_norm_out,
                      uint8_t* clipped_out, uint8_t* clipped_total_out);
 
 /* ---- odp_scale_sum: clipped batch sum of stored per-segment gradients ----
- * out = round_out(sum_s scale[cls][grp][seg_example[s]] * pe[s]) and then,
- * if normalize_by != 1, round_out(out / normalize_by).  Optional second
- * output out2 = same for (scale * pe)^2.                                   */
+ * out = round_out(sum_s t_s) with t_s = round_pe(scale[cls][grp]
+ * [seg_example[s]] * pe[s]) (clip_pytree's `scale.to(dtype) * leaf`), the
+ * sum in float32, or in float64 for float64 pe or the wide flag; then, if
+ * normalize_by != 1, round_out(out / normalize_by).  Optional second
+ * output out2 = the same for round_pe(t_s^2).                              */
 enum {
-  ODP_SS_PE = 0,        /* address of f32 [n_seg][rank][M]                  */
+  ODP_SS_PE = 0,        /* address of [n_seg][rank][M] in the pe dtype      */
   ODP_SS_M = 1, ODP_SS_RANK = 2,
   ODP_SS_SEG_FIRST = 3, ODP_SS_NSEG = 4,
   ODP_SS_OUT = 5,       /* address of the output leaf                       */
   ODP_SS_FLAGS = 6,     /* out dtype | transpose << 8 | group << 16 | cls << 40
-                           | pe dtype << 56; transpose 0 writes [rank][M],
-                           1 writes [M][rank]; non-finite pe values count 0 */
+                           | wide << 48 | pe dtype << 56; transpose 0 writes
+                           [rank][M], 1 writes [M][rank]; non-finite pe
+                           values count 0                                   */
   ODP_SS_OUT2 = 7,      /* address of the second-moment output or 0         */
   ODP_SS_FIELDS = 8
 };
 int64_t odp_scale_sum_blocks(int64_t n_elems);
 int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                   int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
-                  const float* scales, int32_t n_ex, int32_t n_groups, float normalize_by);
+                  const double* scales, int32_t n_ex, int32_t n_groups, float normalize_by);
 
 /* ---- full-weight linears: per-example norms and the clipped sum ---------
  * A linear y = x W^T over rows of X [n_rows][d_in] and output gradients
@@ -320,12 +325,12 @@ int64_t odp_linear_prescale_blocks(int64_t n_rows);
 int odp_linear_prescale(odp_stream_t stream, const int64_t* problems,
                         const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                         const int32_t* seg_row_start, const int32_t* seg_row_len,
-                        const int32_t* seg_example, const float* scales, int32_t n_ex,
+                        const int32_t* seg_example, const double* scales, int32_t n_ex,
                         int32_t n_groups);
 int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
                            const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                            const int32_t* seg_row_start, const int32_t* seg_row_len,
-                           const int32_t* seg_example, const float* scales, int32_t n_ex,
+                           const int32_t* seg_example, const double* scales, int32_t n_ex,
                            int32_t n_groups, float normalize_by, int32_t prescaled);
 
 /* ---- odp_gaussian_noise --------------------------------------------------

@@ -60,7 +60,8 @@ from opaque_amd.types import (
     clipped,
 )
 
-_KERNEL_DTYPES = (torch.float32, torch.bfloat16)
+_KERNEL_DTYPES = (torch.float32, torch.bfloat16)  # the seam-capture kernels
+_LEAF_DTYPES = (torch.float32, torch.bfloat16, torch.float16, torch.float64)  # materialised leaves
 _DEFAULT_GAMMA = 0.01
 
 
@@ -386,16 +387,18 @@ class _ClipEngine:
         return leaf_group, names, [float(cn.values[g]) for g in names]
 
     def _clip_spec(self, shapes: list[tuple], dtypes: list[torch.dtype], thresholds: list[float],
-                   normalize_by: float) -> tuple[ClipSpec, list[int]]:
-        """Clip constants and, per leaf, its guard class (one per storage dtype)."""
+                   normalize_by: float, capture: bool) -> tuple[ClipSpec, list[int], bool]:
+        """Clip constants, per leaf its guard class (one per storage dtype), and
+        whether materialised leaves square in float64."""
         acc_request = self.compute_dtype
-        if acc_request is not None and acc_request.is_floating_point and (
+        if capture and acc_request is not None and acc_request.is_floating_point and (
             torch.finfo(acc_request).eps < torch.finfo(torch.float32).eps
         ):
-            # The kernels square in float32 and sum in float64, so a wider request
-            # is guarded as float32 (the guard must cover the arithmetic done).
+            # The seam kernels square in float32 and sum in float64, so a wider
+            # request is guarded as float32 (the guard must cover the arithmetic
+            # done).  Materialised leaves square in the requested dtype.
             acc_request = torch.float32
-        _, rnd = leaf_guards(shapes, dtypes, acc_request)
+        acc, rnd = leaf_guards(shapes, dtypes, acc_request)
         cls_of: dict[torch.dtype, int] = {}
         guards = []
         leaf_cls = []
@@ -415,7 +418,7 @@ class _ClipEngine:
             normalize_by=float(normalize_by),
             guards=guards,
         )
-        return spec, leaf_cls
+        return spec, leaf_cls, acc == torch.float64
 
     # -- discovery -------------------------------------------------------------
     def _discover(self, args: tuple, kwargs: dict, leaves: list[torch.Tensor], treedef) -> _Discovery:
@@ -481,19 +484,23 @@ class _ClipEngine:
                 normalize_by: float, out_dtype_of, values, loss_aux, all_finite,
                 lins: list[LinearSite] = ()) -> tuple:
         leaf_group, names, thresholds = self._groups(paths)
-        spec, leaf_cls = self._clip_spec(shapes, dtypes, thresholds, normalize_by)
+        capture = bool(sites) or bool(lins)
+        spec, leaf_cls, square_f64 = self._clip_spec(shapes, dtypes, thresholds, normalize_by, capture)
         outs = [LeafOut(tuple(s), out_dtype_of(dt), leaf_group[k], leaf_cls[k])
                 for k, (s, dt) in enumerate(zip(shapes, dtypes))]
+        # The batch sum accumulates in compute_dtype when one is given
+        # (_clipped_fun.py:115-134): float64 on request, float32 otherwise.
         plan = GhostPlan(segments=segments, leaves=outs, clip=spec, lora_sites=sites,
                          materialized=mats, linear_sites=list(lins), device=device,
-                         second_moment=self.second_moment, **self.plan_options)
+                         second_moment=self.second_moment, square_f64=square_f64,
+                         sum_f64=self.compute_dtype == torch.float64, **self.plan_options)
         res = plan.run()
         if all_finite is not None and plan.pe_views():
             all_finite = all_finite & _pe_finite(plan)
         if all_finite is not None and lins:
             all_finite = all_finite & plan.linear_finite()
         # ||scaled gradient||: per group, scale * group norm (class 0 scale).
-        cn2 = (res.scales[0] * res.group_norms).square().sum(0).sqrt()
+        cn2 = (res.scales[0].float() * res.group_norms).square().sum(0).sqrt()
         step = _StepOut(
             leaves=list(res.leaves), squared=None if res.second_moment is None else list(res.second_moment),
             norms=res.norms, group_norms=res.group_norms, clipped=res.clipped,
@@ -519,9 +526,10 @@ class _ClipEngine:
         for p, t in zip(paths, pe):
             if not isinstance(t, torch.Tensor):
                 raise TypeError(f"per-example gradient leaf at {p!r} is not a tensor")
-            if t.dtype not in _KERNEL_DTYPES:
+            if t.dtype not in _LEAF_DTYPES:
                 raise TypeError(
-                    f"opaque_amd kernels support float32 and bfloat16 gradient leaves, got {t.dtype} at {p!r}"
+                    "opaque_amd kernels support float32, bfloat16, float16 and float64 gradient leaves, "
+                    f"got {t.dtype} at {p!r}"
                 )
         all_finite = None
         if want_finite:

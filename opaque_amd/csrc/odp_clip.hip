@@ -12,51 +12,65 @@
 
 namespace {
 
-constexpr int CL_THREADS = 256;
+constexpr int CL_THREADS = 1024;  // one workgroup per example
 constexpr int CL_MAX_GROUPS = 1024;
 constexpr int SS_THREADS = 256;
 constexpr int SS_ELEMS = 8;  // elements per thread
 
+// Workgroup sum in a fixed order (a butterfly within each wave, then the
+// wave sums in wave order), so that runs are bitwise reproducible.  The
+// result is valid in every thread.
 __device__ __forceinline__ double block_sum_fixed(double v, double* red) {
-  const int t = threadIdx.x;
-  red[t] = v;
-  __syncthreads();
 #pragma unroll
-  for (int w = CL_THREADS / 2; w > 0; w >>= 1) {
-    if (t < w) red[t] = red[t] + red[t + w];
-    __syncthreads();
-  }
-  const double out = red[0];
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
   __syncthreads();
-  return out;
+  double t = 0.0;
+#pragma unroll
+  for (int w = 0; w < CL_THREADS / 64; ++w) t += red[w];
+  __syncthreads();
+  return t;
 }
 
-__device__ __forceinline__ float finalize_scale(double ratio, double rel, double abs_, int clamp_one,
-                                                int dtype) {
+// The scale as the leaf dtype holds it (float64 leaves keep every bit).
+__device__ __forceinline__ double finalize_scale(double ratio, double rel, double abs_, int clamp_one,
+                                                 int dtype) {
   double s = __dsub_rn(__dmul_rn(ratio, rel), abs_);
   if (clamp_one && !(s < 1.0) && !isnan(s)) s = 1.0;
   if (!isfinite(s)) s = 0.0;
   if (s < 0.0) s = 0.0;
-  return odp_round_to((float)s, dtype);
+  if (dtype == ODP_DTYPE_F64) return s;
+  return (double)odp_round_to((float)s, dtype);
 }
 
 // One workgroup per example.  Group g owns slots [gstart[g], gstart[g+1]).
+// Each thread keeps four loads in flight (the sum of an example's partials
+// is bound by load latency, not bandwidth).
 __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
     const double* __restrict__ part, int64_t n_slots, int n_ex, const int64_t* __restrict__ gstart, int n_groups,
     const double* __restrict__ thr, double eff_thr, int mode, double gamma, int n_cls,
     const double* __restrict__ guard, const int32_t* __restrict__ cls_dtype,
-    float* __restrict__ scale_out, float* __restrict__ norm_out, float* __restrict__ gnorm_out,
+    double* __restrict__ scale_out, float* __restrict__ norm_out, float* __restrict__ gnorm_out,
     uint8_t* __restrict__ clip_out, uint8_t* __restrict__ clip_total_out) {
   const int ex = blockIdx.x;
   const int t = threadIdx.x;
-  __shared__ double red[CL_THREADS];
+  __shared__ double red[CL_THREADS / 64];
   __shared__ double gsq[CL_MAX_GROUPS];
+  const double* row = part + (int64_t)ex * n_slots;
 
   for (int g = 0; g < n_groups; ++g) {
-    double acc = 0.0;
-    for (int64_t s = gstart[g] + t; s < gstart[g + 1]; s += CL_THREADS)
-      acc += part[(int64_t)ex * n_slots + s];
-    const double tot = block_sum_fixed(acc, red);
+    const int64_t hi = gstart[g + 1];
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    int64_t s = gstart[g] + t;
+    for (; s + 3 * CL_THREADS < hi; s += 4 * CL_THREADS) {
+      a0 += row[s];
+      a1 += row[s + CL_THREADS];
+      a2 += row[s + 2 * CL_THREADS];
+      a3 += row[s + 3 * CL_THREADS];
+    }
+    for (; s < hi; s += CL_THREADS) a0 += row[s];
+    const double tot = block_sum_fixed((a0 + a1) + (a2 + a3), red);
     if (t == 0) gsq[g] = tot;
   }
   __syncthreads();
@@ -83,10 +97,65 @@ __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
 
 // Clipped sum of one leaf per problem: 8 consecutive elements per thread
 // (one 16-byte load per segment for bf16), summed over the leaf's segments
-// in segment order.
+// in segment order.  Each term is scale * value rounded to the value's dtype
+// (clip_pytree's `scale.to(dtype) * leaf`), accumulated in float32, or in
+// float64 (Acc = double) for float64 values or a float64 compute dtype.
+// This element-wise form serves float16/float64 and the float64 sums; the
+// kernel below vectorises float32/bfloat16.
+template <typename Acc>
+__device__ __forceinline__ void scale_sum_generic(const void* pe, int pdt, int64_t E, int64_t e0, int n_seg,
+                                                  int seg_first, const int32_t* __restrict__ sex,
+                                                  const double* __restrict__ sc, float normalize_by, void* out,
+                                                  void* out2, int odt, int transpose, int64_t M, int rank) {
+  Acc acc[SS_ELEMS], acc2[SS_ELEMS];
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = (Acc)0;
+  for (int s = 0; s < n_seg; ++s) {
+    const double c = sc[sex[seg_first + s]];
+#pragma unroll
+    for (int i = 0; i < SS_ELEMS; ++i) {
+      if (e0 + i >= E) break;
+      const double v = odp_load_as_double(pe, (int64_t)s * E + e0 + i, pdt);
+      double y = 0.0, yy = 0.0;
+      if (isfinite(v)) {  // nan_to_num of the per-example value
+        if (pdt == ODP_DTYPE_F64) {
+          y = c * v;
+          yy = y * y;
+        } else {
+          y = (double)odp_round_to(__fmul_rn((float)c, (float)v), pdt);
+          yy = (double)odp_round_to(__fmul_rn((float)y, (float)y), pdt);
+        }
+      }
+      acc[i] += (Acc)y;
+      acc2[i] += (Acc)yy;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) {
+    const int64_t e = e0 + i;
+    if (e >= E) break;
+    const int64_t k = e / M, m = e - k * M;
+    const int64_t o = transpose ? m * rank + k : e;
+    // Cast to the output dtype, then divide in it (the reference's order).
+    if (odt == ODP_DTYPE_F64) {
+      const double x = (double)acc[i], x2 = (double)acc2[i];
+      odp_store_from_double(out, o, odt, normalize_by != 1.0f ? x / (double)normalize_by : x);
+      if (out2) odp_store_from_double(out2, o, odt, normalize_by != 1.0f ? x2 / (double)normalize_by : x2);
+    } else {
+      float x = odp_round_to((float)acc[i], odt), x2 = odp_round_to((float)acc2[i], odt);
+      if (normalize_by != 1.0f) {
+        x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
+        x2 = odp_round_to(__fdiv_rn(x2, normalize_by), odt);
+      }
+      odp_store_from_float(out, o, odt, x);
+      if (out2) odp_store_from_float(out2, o, odt, x2);
+    }
+  }
+}
+
 __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
     const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
-    const int32_t* __restrict__ sex, const float* __restrict__ scales, int n_ex, int n_groups,
+    const int32_t* __restrict__ sex, const double* __restrict__ scales, int n_ex, int n_groups,
     float normalize_by) {
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -101,12 +170,23 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
   const int odt = (int)(flags & 0xff);
   const int transpose = (int)((flags >> 8) & 0xff);
   const int grp = (int)((flags >> 16) & 0xffffff);
-  const int cls = (int)((flags >> 40) & 0xffff);
+  const int cls = (int)((flags >> 40) & 0xff);
+  const int wide = (int)((flags >> 48) & 1);
   const int pdt = (int)((flags >> 56) & 0xff);
   const int64_t E = M * rank;
   const int64_t e0 = ((int64_t)(bid - ws[p]) * SS_THREADS + threadIdx.x) * SS_ELEMS;
   if (e0 >= E) return;
-  const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
+  const double* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
+  if (wide || pdt == ODP_DTYPE_F64) {
+    scale_sum_generic<double>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
+                              M, rank);
+    return;
+  }
+  if (pdt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F64) {
+    scale_sum_generic<float>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
+                             M, rank);
+    return;
+  }
   // Whole 8-element pieces load as vectors (rows of E elements stay 16-byte
   // aligned when E is a multiple of 8).
   const bool whole = (E & 7) == 0;
@@ -137,12 +217,18 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
       for (int i = 0; i < SS_ELEMS; ++i)
         v[i] = e0 + i < E ? odp_load_as_float(pe, (int64_t)s * E + e0 + i, pdt) : 0.f;
     }
+    const bool bf = pdt == ODP_DTYPE_BF16;
 #pragma unroll
     for (int i = 0; i < SS_ELEMS; ++i) {
       if (!isfinite(v[i])) v[i] = 0.f;  // nan_to_num of the per-example value
-      const float y = __fmul_rn(c, v[i]);
+      // The term as the leaf dtype stores it (scale.to(dtype) * leaf).
+      float y = __fmul_rn(c, v[i]), yy = __fmul_rn(y, y);
+      if (bf) {
+        y = odp_round_bf16(y);
+        yy = odp_round_bf16(__fmul_rn(y, y));
+      }
       acc[i] = __fadd_rn(acc[i], y);
-      acc2[i] = __fadd_rn(acc2[i], __fmul_rn(y, y));
+      acc2[i] = __fadd_rn(acc2[i], yy);
     }
   }
   float x[SS_ELEMS], x2[SS_ELEMS];
@@ -184,10 +270,10 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
   }
 }
 
-// Per-segment sums of squares of materialised per-example tensors
-// (x^2 in fp32 as clip_pytree squares in its float32 accumulation dtype,
-// summed in fp64).  Each workgroup reduces SQ_CHUNK elements of one
-// segment and writes one slot.
+// Per-segment sums of squares of materialised per-example tensors: x^2 in
+// clip_pytree's accumulation dtype (float32, or float64 with the flag bit 8
+// of ODP_SQ_DTYPE, as for float64 leaves), summed in fp64.  Each workgroup
+// reduces SQ_CHUNK elements of one segment and writes one slot.
 constexpr int SQ_THREADS = 256;
 constexpr int64_t SQ_CHUNK = 8192;
 
@@ -203,16 +289,25 @@ __global__ __launch_bounds__(SQ_THREADS) void k_sqnorm(const int64_t* __restrict
   const int64_t n = f[ODP_SQ_N];
   const int seg_first = (int)f[ODP_SQ_SEG_FIRST];
   const int64_t slot = f[ODP_SQ_SLOT];
-  const int dt = (int)f[ODP_SQ_DTYPE];
+  const int dt = (int)(f[ODP_SQ_DTYPE] & 0xff);
+  const bool sq64 = ((f[ODP_SQ_DTYPE] >> 8) & 1) != 0;
   const int64_t nchunk = (n + SQ_CHUNK - 1) / SQ_CHUNK;
   const int64_t local = bid - ws[p];
   const int64_t seg = local / nchunk, chunk = local % nchunk;
   const int64_t lo = chunk * SQ_CHUNK, hi = lo + SQ_CHUNK < n ? lo + SQ_CHUNK : n;
   double acc = 0.0;
-  for (int64_t i = lo + threadIdx.x; i < hi; i += SQ_THREADS) {
-    float x = odp_load_as_float(X, seg * n + i, dt);
-    if (!isfinite(x)) x = 0.f;  // nan_to_num before the norm
-    acc += (double)__fmul_rn(x, x);
+  if (sq64) {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += SQ_THREADS) {
+      double x = odp_load_as_double(X, seg * n + i, dt);
+      if (!isfinite(x)) x = 0.0;  // nan_to_num before the norm
+      acc += x * x;
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += SQ_THREADS) {
+      float x = odp_load_as_float(X, seg * n + i, dt);
+      if (!isfinite(x)) x = 0.f;
+      acc += (double)__fmul_rn(x, x);
+    }
   }
   __shared__ double red[SQ_THREADS];
   red[threadIdx.x] = acc;
@@ -249,7 +344,7 @@ extern "C" int odp_clip_factors(odp_stream_t stream, const double* part, int64_t
                                 int32_t n_ex, const int64_t* group_slot_start, int32_t n_groups,
                                 const double* thresholds, double effective_threshold, int32_t mode,
                                 double gamma, int32_t n_cls, const double* guard,
-                                const int32_t* cls_dtype, float* scale_out, float* norm_out,
+                                const int32_t* cls_dtype, double* scale_out, float* norm_out,
                                 float* group_norm_out, uint8_t* clipped_out,
                                 uint8_t* clipped_total_out) {
   if (n_ex < 0 || n_slots < 0) {
@@ -292,7 +387,7 @@ extern "C" int64_t odp_scale_sum_blocks(int64_t n_elems) {
 
 extern "C" int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                              int32_t n_prob, int32_t total_blocks, const int32_t* seg_example,
-                             const float* scales, int32_t n_ex, int32_t n_groups,
+                             const double* scales, int32_t n_ex, int32_t n_groups,
                              float normalize_by) {
   int rc = odp_check_table("odp_scale_sum", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;

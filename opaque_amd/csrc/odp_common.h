@@ -21,6 +21,12 @@ __device__ __forceinline__ float odp_bf2f(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
 
+// A finite float rounded to nearest-even bfloat16, by the hardware
+// conversion (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ float odp_round_bf16(float f) {
+  return odp_bf2f(__builtin_bit_cast(uint16_t, (__bf16)f));
+}
+
 // Largest p in [0, n) with start[p] <= x. `start` is non-decreasing with
 // start[0] == 0 and x < start[n].
 __device__ __forceinline__ int odp_find_problem(const int32_t* __restrict__ start, int n, int x) {

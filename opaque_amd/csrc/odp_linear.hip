@@ -752,7 +752,7 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen,
                                                       const int32_t* __restrict__ sex,
-                                                      const float* __restrict__ scales, int n_ex,
+                                                      const double* __restrict__ scales, int n_ex,
                                                       int n_groups) {
   __shared__ float rowc[PS_ROWS];
   __shared__ int rowin[PS_ROWS];
@@ -768,7 +768,7 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
   const int seg_first = (int)f[ODP_LN_SEG_FIRST], n_seg = (int)f[ODP_LN_NSEG];
   const int64_t flags = f[ODP_LN_FLAGS];
   const int grp = (int)((flags >> 8) & 0xffff), cls = (int)((flags >> 24) & 0xffff);
-  const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
+  const double* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
   const int64_t row0 = (int64_t)(bid - ws[p]) * PS_ROWS;
   const int tid = threadIdx.x;
   if (tid < PS_ROWS) {
@@ -784,7 +784,7 @@ __global__ __launch_bounds__(256) void k_lin_prescale(const int64_t* __restrict_
     }
     const int s = lo - 1;
     const bool in = t < n_rows && s >= 0 && t < (int64_t)sstart[seg_first + s] + slen[seg_first + s];
-    const float c = in ? sc[sex[seg_first + s]] : 0.f;
+    const float c = in ? (float)sc[sex[seg_first + s]] : 0.f;  // exact: a bf16 class scale
     // A zero factor writes zeros (by select: 0 * Inf would be NaN).
     rowin[tid] = in && c != 0.f ? 1 : 0;
     rowc[tid] = c;
@@ -829,7 +829,7 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen,
                                                       const int32_t* __restrict__ sex,
-                                                      const float* __restrict__ scales, int n_ex,
+                                                      const double* __restrict__ scales, int n_ex,
                                                       int n_groups, float normalize_by) {
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -840,7 +840,7 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
   const int odt = (int)(flags & 0xff);
   const int grp = (int)((flags >> 8) & 0xffff);
   const int cls = (int)((flags >> 24) & 0xffff);
-  const float* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
+  const double* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
   const int tn_count = (int)((P.d_in + ON - 1) / ON);
   const int tm_count = (int)((P.d_out + OM - 1) / OM);
   const int tile = bid - ws[p];
@@ -907,8 +907,8 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
     return at_segment(st.seg + 1 < P.n_seg ? st.seg + 1 : P.n_seg);
   };
   const ODP_CONST int32_t* cex = (const ODP_CONST int32_t*)(sex + P.seg_first);
-  const ODP_CONST float* csc = (const ODP_CONST float*)sc;
-  auto scale = [&](const Step& st) { return csc[cex[st.seg]]; };
+  const ODP_CONST double* csc = (const ODP_CONST double*)sc;
+  auto scale = [&](const Step& st) { return (float)csc[cex[st.seg]]; };
   // PRESCALED: X already holds c_i x_t (odp_linear_prescale).
   dma_mainloop<!PRESCALED, false, true>(P, o0, n0, at_segment(0), next, scale, fixup, acc);
 
@@ -1083,7 +1083,7 @@ extern "C" int64_t odp_linear_prescale_blocks(int64_t n_rows) {
 extern "C" int odp_linear_prescale(odp_stream_t stream, const int64_t* problems,
                                    const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                                    const int32_t* seg_row_start, const int32_t* seg_row_len,
-                                   const int32_t* seg_example, const float* scales, int32_t n_ex,
+                                   const int32_t* seg_example, const double* scales, int32_t n_ex,
                                    int32_t n_groups) {
   int rc = odp_check_table("odp_linear_prescale", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
@@ -1102,7 +1102,7 @@ extern "C" int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* proble
                                       const int32_t* work_start, int32_t n_prob,
                                       int32_t total_blocks, const int32_t* seg_row_start,
                                       const int32_t* seg_row_len, const int32_t* seg_example,
-                                      const float* scales, int32_t n_ex, int32_t n_groups,
+                                      const double* scales, int32_t n_ex, int32_t n_groups,
                                       float normalize_by, int32_t prescaled) {
   int rc = odp_check_table("odp_linear_clipped_sum", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;

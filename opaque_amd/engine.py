@@ -27,8 +27,9 @@ import torch
 
 from opaque_amd import _native as N
 
-_DTYPE_CODE = {torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
-_ALIGN = {torch.float32: 4, torch.bfloat16: 8}  # element multiple for 16-byte rows
+_DTYPE_CODE = {torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16, torch.float16: N.DTYPE_F16,
+               torch.float64: N.DTYPE_F64}
+_ALIGN = {torch.float32: 4, torch.bfloat16: 8}  # the LoRA and linear kernels' dtypes; 16-byte rows
 MAX_RANK_PER_PASS = 64
 MAX_LEAVES_PER_PASS = 4
 
@@ -37,7 +38,7 @@ def dtype_code(dt: torch.dtype) -> int:
     try:
         return _DTYPE_CODE[dt]
     except KeyError:
-        raise TypeError(f"opaque_amd kernels support float32 and bfloat16, got {dt}") from None
+        raise TypeError(f"opaque_amd kernels support float32, bfloat16, float16 and float64, got {dt}") from None
 
 
 def _f64_bits(x: float) -> int:
@@ -248,7 +249,7 @@ class GhostResult:
     group_norms: torch.Tensor  # [G, n_ex] f32
     clipped: torch.Tensor  # [G, n_ex] uint8
     clipped_total: torch.Tensor  # [n_ex] uint8
-    scales: torch.Tensor  # [n_cls, G, n_ex] f32
+    scales: torch.Tensor  # [n_cls, G, n_ex] f64 (each value as its class dtype holds it)
     second_moment: list[torch.Tensor] | None
     flat: dict[torch.dtype, torch.Tensor]
 
@@ -340,6 +341,10 @@ class GhostPlan:
     the stored per-example gradients of full-weight sites (bf16); None uses
     half of the free device memory, 0 stores none.  ``prescale_bytes``: at
     most this much of prescaled activations per clipped-sum chunk.
+    ``square_f64``: materialised leaves are squared in float64 (the
+    reference's accumulation dtype when a leaf is float64 or
+    compute_dtype=float64); ``sum_f64``: the clipped sums of stored
+    gradients accumulate in float64 (compute_dtype=float64).
     """
 
     def __init__(
@@ -356,6 +361,8 @@ class GhostPlan:
         fuse_g_side: bool = True,
         prescale_bytes: int = 8 << 30,
         linear_pe_bytes: int | None = None,
+        square_f64: bool = False,
+        sum_f64: bool = False,
     ) -> None:
         N.load()
         dev = torch.device(device)
@@ -369,10 +376,14 @@ class GhostPlan:
         self.fuse_g_side = fuse_g_side
         self.prescale_bytes = int(prescale_bytes)
         self.linear_pe_bytes = linear_pe_bytes
+        self.square_f64 = bool(square_f64)
+        self.sum_f64 = bool(sum_f64)
         self.n_groups = len(clip.thresholds)
         self.n_cls = max(1, len(clip.guards))
         if self.n_groups < 1:
             raise ValueError("at least one clip group is required")
+        if self.n_cls > 8:
+            raise ValueError("at most 8 storage dtype classes")
         for lf in leaves:
             if not 0 <= lf.group < self.n_groups or not 0 <= lf.cls < self.n_cls:
                 raise ValueError("leaf group/class out of range")
@@ -585,7 +596,7 @@ class GhostPlan:
             self.out2 = [torch.empty(lf.shape, dtype=lf.out_dtype, device=dev) for lf in self.leaves]
 
         G, C, E = self.n_groups, self.n_cls, seg.n_ex
-        self.scales = torch.empty((C, G, E), dtype=torch.float32, device=dev)
+        self.scales = torch.empty((C, G, E), dtype=torch.float64, device=dev)
         self.norms = torch.empty(E, dtype=torch.float32, device=dev)
         self.group_norms = torch.empty((G, E), dtype=torch.float32, device=dev)
         self.clipped = torch.empty((G, E), dtype=torch.uint8, device=dev)
@@ -740,7 +751,8 @@ class GhostPlan:
             sq.add(
                 {
                     N.SQ_X: pe_m.data_ptr(), N.SQ_N: n, N.SQ_NSEG: n_seg, N.SQ_SEG_FIRST: v.first,
-                    N.SQ_SLOT: slot_base[m.leaf], N.SQ_DTYPE: dtype_code(pe_m.dtype),
+                    N.SQ_SLOT: slot_base[m.leaf],
+                    N.SQ_DTYPE: dtype_code(pe_m.dtype) | ((1 if self.square_f64 else 0) << 8),
                 },
                 n_seg * lib.odp_sqnorm_blocks(n),
                 n_seg * n * pe_m.element_size(),
@@ -873,7 +885,8 @@ class GhostPlan:
                 o2 = self.out2[ls.w_leaf]
                 out2 = (o2 if ls.index is None else o2[ls.index]).data_ptr()
             M = ls.x.shape[-1] * ls.g.shape[-1]
-            flags = dtype_code(lf.out_dtype) | (lf.group << 16) | (lf.cls << 40) | (N.DTYPE_BF16 << 56)
+            flags = (dtype_code(lf.out_dtype) | (lf.group << 16) | (lf.cls << 40) | (int(self.sum_f64) << 48)
+                     | (N.DTYPE_BF16 << 56))
             ss.add({N.SS_PE: self.lin_pe[off:].data_ptr(), N.SS_M: M, N.SS_RANK: 1, N.SS_SEG_FIRST: v.first,
                     N.SS_NSEG: v.n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2},
                    lib.odp_scale_sum_blocks(M),
@@ -892,7 +905,8 @@ class GhostPlan:
                 rank, M = leaf_rank_m[i]
                 transpose = 1 if self._leaf_transposed(i, sites) else 0
                 pdt, pe_a = dtype_code(pe_dt[i]), pe_addr(i)
-            flags = dtype_code(lf.out_dtype) | (transpose << 8) | (lf.group << 16) | (lf.cls << 40) | (pdt << 56)
+            flags = (dtype_code(lf.out_dtype) | (transpose << 8) | (lf.group << 16) | (lf.cls << 40)
+                     | (int(self.sum_f64) << 48) | (pdt << 56))
             ss.add(
                 {
                     N.SS_PE: pe_a, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: v.first,

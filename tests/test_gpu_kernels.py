@@ -128,14 +128,16 @@ def test_clip_factor_arithmetic_is_bit_exact():
     n = sq.numel()
     part = sq.reshape(n, 1).to(DEV)
     for C, mode in [(1.0, N.CLIP_FIXED), (0.7, N.CLIP_FIXED), (float("inf"), N.CLIP_FIXED), (1.0, N.CLIP_AUTOS)]:
-        for store in (torch.float32, torch.bfloat16):
-            rnd = dp_ref.roundoff(torch.float32, 7, 3000)
+        for store in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
+            rnd = dp_ref.roundoff(torch.float64 if store == torch.float64 else torch.float32, 7, 3000)
             rel, ab = guard_constants(store, rnd)
             gs = torch.tensor([0, 1], dtype=torch.int64, device=DEV)
             thr = torch.tensor([C], dtype=torch.float64, device=DEV)
             guard = torch.tensor([rel, ab], dtype=torch.float64, device=DEV)
-            cls = torch.tensor([N.DTYPE_BF16 if store == torch.bfloat16 else N.DTYPE_F32], dtype=torch.int32, device=DEV)
-            scale = torch.empty((1, 1, n), dtype=torch.float32, device=DEV)
+            code = {torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16, torch.float16: N.DTYPE_F16,
+                    torch.float64: N.DTYPE_F64}[store]
+            cls = torch.tensor([code], dtype=torch.int32, device=DEV)
+            scale = torch.empty((1, 1, n), dtype=torch.float64, device=DEV)
             norms = torch.empty(n, dtype=torch.float32, device=DEV)
             gn = torch.empty((1, n), dtype=torch.float32, device=DEV)
             cl = torch.empty((1, n), dtype=torch.uint8, device=DEV)
@@ -147,7 +149,7 @@ def test_clip_factor_arithmetic_is_bit_exact():
             nrm = torch.sqrt(sq)
             c_t = torch.clamp(torch.tensor(C, dtype=torch.float64), min=0.0)
             ratio = c_t / (nrm + 0.01) if mode == N.CLIP_AUTOS else c_t / nrm
-            want = dp_ref.finalize(ratio, store, rnd, mode == N.CLIP_FIXED).to(store).float()
+            want = dp_ref.finalize(ratio, store, rnd, mode == N.CLIP_FIXED).to(store).double()
             assert torch.equal(scale.view(-1).cpu(), want), (C, mode, store, scale.view(-1).cpu(), want)
             assert torch.equal(norms.cpu(), nrm.float())
             assert torch.equal(ct.cpu().bool(), nrm.float() > C)

@@ -317,9 +317,12 @@ def test_stored_linear_gradients_second_moment():
     for k, ls in enumerate(lins):
         X, G = ls.x.cpu(), ls.g.cpu()
         pe = lora_ref.linear_per_example(X.float(), G.float(), seg.starts, seg.lengths).to(torch.bfloat16)
-        c = scales[0, leaves[k].group].double().view(-1, 1, 1)
-        y = c * pe.double()
-        want, want2 = y.sum(0) / 2.0, (y * y).sum(0) / 2.0
+        # clip_pytree's `scale.to(bf16) * leaf` and the square of the clipped
+        # bf16 leaf, each rounded to bf16, summed in fp32, then / 2.
+        c = scales[0, leaves[k].group].to(torch.bfloat16).view(-1, 1, 1)
+        y = c * pe
+        want = (y.sum(0, dtype=torch.float32) / 2.0).double()
+        want2 = (y.square().sum(0, dtype=torch.float32) / 2.0).double()
         assert (r.leaves[k].double().cpu() - want).norm() <= 2e-4 * want.norm(), k
         assert (r.second_moment[k].double().cpu() - want2).norm() <= 2e-4 * want2.norm(), k
 
