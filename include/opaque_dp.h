@@ -206,6 +206,28 @@ int odp_clip_factors(odp_stream_t stream, const double* part, int64_t n_slots, i
                      double* scale_out, float* norm_out, float* group_norm_out,
                      uint8_t* clipped_out, uint8_t* clipped_total_out);
 
+/* ---- odp_clip_materialized_noalloc: the above without caller scratch ------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Computes what odp_sqnorm (on the table sq_problems /
+ * sq_work_start, partial stride n_slots) followed by odp_clip_factors
+ * (same remaining arguments and outputs) compute, with the fp64 partials in
+ * a static device array of odp_noalloc_max_partials() doubles (8 MiB) that
+ * each GPU holds until the process ends, cleared at every call: it returns
+ * ODP_ERR_UNSUPPORTED when n_ex * n_slots exceeds that.  Allocates nothing.
+ * Calls that overlap on one GPU share the array and race; the stream must
+ * belong to the current device.                                          */
+int64_t odp_noalloc_max_partials(void);
+int odp_clip_materialized_noalloc(odp_stream_t stream, const int64_t* sq_problems,
+                                  const int32_t* sq_work_start, int32_t sq_n_prob,
+                                  int32_t sq_total_blocks, const int32_t* seg_example,
+                                  int64_t n_slots, int32_t n_ex, const int64_t* group_slot_start,
+                                  int32_t n_groups, const double* thresholds,
+                                  double effective_threshold, int32_t mode, double gamma,
+                                  int32_t n_cls, const double* guard, const int32_t* cls_dtype,
+                                  double* scale_out, float* norm_out, float* group_norm_out,
+                                  uint8_t* clipped_out, uint8_t* clipped_total_out);
+
 /* ---- odp_scale_sum: clipped batch sum of stored per-segment gradients ----
  * out = round_out(sum_s t_s) with t_s = round_pe(scale[cls][grp]
  * [seg_example[s]] * pe[s]) (clip_pytree's `scale.to(dtype) * leaf`), the

@@ -76,6 +76,14 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _c_i32, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
         ],
     ),
+    "odp_noalloc_max_partials": (_c_i64, []),
+    "odp_clip_materialized_noalloc": (
+        _c_int,
+        [
+            _ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _c_i64, _c_i32, _ptr, _c_i32, _ptr, _c_f64, _c_i32, _c_f64,
+            _c_i32, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,
+        ],
+    ),
     "odp_scale_sum_blocks": (_c_i64, [_c_i64]),
     "odp_scale_sum": (
         _c_int,

@@ -8,6 +8,8 @@
 // min(1, .) for fixed clipping with NaN propagating as in torch.minimum,
 // non-finite -> 0, clamp at 0, then rounded to the leaf dtype the way
 // torch casts a float64 tensor (to float32, then to bfloat16).
+#include <mutex>
+
 #include "odp_internal.h"
 
 namespace {
@@ -340,6 +342,40 @@ extern "C" int odp_sqnorm(odp_stream_t stream, const int64_t* problems, const in
   return odp_check_launch("odp_sqnorm");
 }
 
+// Argument checks shared by odp_clip_factors and its allocation-free
+// variant (everything but the partials pointer).
+static int check_clip_args(const char* what, int64_t n_slots, int32_t n_ex, const int64_t* group_slot_start,
+                           int32_t n_groups, const double* thresholds, int32_t mode, double gamma, int32_t n_cls,
+                           const double* guard, const int32_t* cls_dtype, const double* scale_out,
+                           const float* norm_out) {
+  if (n_ex < 0 || n_slots < 0) {
+    odp_set_error("%s: negative n_ex or n_slots", what);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (n_groups < 1 || n_groups > CL_MAX_GROUPS) {
+    odp_set_error("%s: n_groups=%d outside [1, %d]", what, n_groups, CL_MAX_GROUPS);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  if (n_cls < 1 || n_cls > 8) {
+    odp_set_error("%s: n_cls=%d outside [1, 8]", what, n_cls);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  if (mode != ODP_CLIP_FIXED && mode != ODP_CLIP_AUTOS) {
+    odp_set_error("%s: unknown mode %d", what, mode);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (mode == ODP_CLIP_AUTOS && !(gamma > 0.0)) {
+    odp_set_error("%s: gamma must be positive, got %g", what, gamma);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  if (n_ex > 0 && (group_slot_start == nullptr || thresholds == nullptr || guard == nullptr ||
+                   cls_dtype == nullptr || scale_out == nullptr || norm_out == nullptr)) {
+    odp_set_error("%s: null required pointer", what);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  return ODP_OK;
+}
+
 extern "C" int odp_clip_factors(odp_stream_t stream, const double* part, int64_t n_slots,
                                 int32_t n_ex, const int64_t* group_slot_start, int32_t n_groups,
                                 const double* thresholds, double effective_threshold, int32_t mode,
@@ -347,29 +383,11 @@ extern "C" int odp_clip_factors(odp_stream_t stream, const double* part, int64_t
                                 const int32_t* cls_dtype, double* scale_out, float* norm_out,
                                 float* group_norm_out, uint8_t* clipped_out,
                                 uint8_t* clipped_total_out) {
-  if (n_ex < 0 || n_slots < 0) {
-    odp_set_error("odp_clip_factors: negative n_ex or n_slots");
-    return ODP_ERR_INVALID_ARGUMENT;
-  }
-  if (n_groups < 1 || n_groups > CL_MAX_GROUPS) {
-    odp_set_error("odp_clip_factors: n_groups=%d outside [1, %d]", n_groups, CL_MAX_GROUPS);
-    return ODP_ERR_UNSUPPORTED;
-  }
-  if (n_cls < 1 || n_cls > 8) {
-    odp_set_error("odp_clip_factors: n_cls=%d outside [1, 8]", n_cls);
-    return ODP_ERR_UNSUPPORTED;
-  }
-  if (mode != ODP_CLIP_FIXED && mode != ODP_CLIP_AUTOS) {
-    odp_set_error("odp_clip_factors: unknown mode %d", mode);
-    return ODP_ERR_INVALID_ARGUMENT;
-  }
-  if (mode == ODP_CLIP_AUTOS && !(gamma > 0.0)) {
-    odp_set_error("odp_clip_factors: gamma must be positive, got %g", gamma);
-    return ODP_ERR_INVALID_ARGUMENT;
-  }
+  int rc = check_clip_args("odp_clip_factors", n_slots, n_ex, group_slot_start, n_groups, thresholds, mode,
+                           gamma, n_cls, guard, cls_dtype, scale_out, norm_out);
+  if (rc != ODP_OK) return rc;
   if (n_ex == 0) return ODP_OK;
-  if ((n_slots > 0 && part == nullptr) || group_slot_start == nullptr || thresholds == nullptr ||
-      guard == nullptr || cls_dtype == nullptr || scale_out == nullptr || norm_out == nullptr) {
+  if (n_slots > 0 && part == nullptr) {
     odp_set_error("odp_clip_factors: null required pointer");
     return ODP_ERR_INVALID_ARGUMENT;
   }
@@ -404,4 +422,107 @@ extern "C" int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const
                      problems, work_start, n_prob, seg_example, scales, n_ex, n_groups,
                      normalize_by);
   return odp_check_launch("odp_scale_sum");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free clipping of materialised per-example gradients.
+//
+// odp_sqnorm fills caller-provided fp64 partials that odp_clip_factors then
+// reads.  Callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc) call
+// odp_clip_materialized_noalloc instead: the partials live in `scratch`, a
+// file-scope device array each GPU holds until the process ends.  The array
+// is found by its address per device (hipGetSymbolAddress on the first call
+// made with that device current); host code never passes the array's name
+// itself to a kernel.  Every call on a GPU shares that GPU's array, so calls
+// that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) double scratch[ODP_NOALLOC_MAX_PARTIALS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+double* g_scratch_ptr[kMaxDevices] = {};
+
+// The address of this device's `scratch`, looked up once per device.
+int scratch_on_current_device(double** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    odp_set_error("odp_clip_materialized_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return ODP_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    odp_set_error("odp_clip_materialized_noalloc: device %d outside [0, %d)", dev, kMaxDevices);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      odp_set_error("odp_clip_materialized_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                    hipGetErrorString(e));
+      return ODP_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = (double*)ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ODP_OK;
+}
+
+// Clears n partials (a kernel, not a memset: the call may be captured into
+// a graph).
+__global__ __launch_bounds__(256) void k_zero_partials(double* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.0;
+}
+
+}  // namespace
+
+extern "C" int64_t odp_noalloc_max_partials(void) { return ODP_NOALLOC_MAX_PARTIALS; }
+
+extern "C" int odp_clip_materialized_noalloc(
+    odp_stream_t stream, const int64_t* sq_problems, const int32_t* sq_work_start, int32_t sq_n_prob,
+    int32_t sq_total_blocks, const int32_t* seg_example, int64_t n_slots, int32_t n_ex,
+    const int64_t* group_slot_start, int32_t n_groups, const double* thresholds, double effective_threshold,
+    int32_t mode, double gamma, int32_t n_cls, const double* guard, const int32_t* cls_dtype, double* scale_out,
+    float* norm_out, float* group_norm_out, uint8_t* clipped_out, uint8_t* clipped_total_out) {
+  const char* what = "odp_clip_materialized_noalloc";
+  int rc = odp_check_table(what, sq_problems, sq_work_start, sq_n_prob, sq_total_blocks);
+  if (rc != ODP_OK) return rc;
+  rc = check_clip_args(what, n_slots, n_ex, group_slot_start, n_groups, thresholds, mode, gamma, n_cls, guard,
+                       cls_dtype, scale_out, norm_out);
+  if (rc != ODP_OK) return rc;
+  if (n_ex == 0) return ODP_OK;
+  if (n_slots > ODP_NOALLOC_MAX_PARTIALS / n_ex) {
+    odp_set_error("%s: %d examples x %lld slots exceed the %lld partials of the static scratch", what, n_ex,
+                  (long long)n_slots, (long long)ODP_NOALLOC_MAX_PARTIALS);
+    return ODP_ERR_UNSUPPORTED;
+  }
+  if (sq_total_blocks > 0 && seg_example == nullptr) {
+    odp_set_error("%s: null seg_example", what);
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  double* part = nullptr;
+  rc = scratch_on_current_device(&part);
+  if (rc != ODP_OK) return rc;
+  hipStream_t s = odp_hip_stream(stream);
+  const int64_t n = (int64_t)n_ex * n_slots;
+  if (n > 0) {
+    hipLaunchKernelGGL(k_zero_partials, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, n);
+    rc = odp_check_launch(what);
+    if (rc != ODP_OK) return rc;
+  }
+  if (sq_total_blocks > 0) {
+    hipLaunchKernelGGL(k_sqnorm, dim3(sq_total_blocks), dim3(SQ_THREADS), 0, s, sq_problems, sq_work_start,
+                       sq_n_prob, seg_example, part, n_slots);
+    rc = odp_check_launch(what);
+    if (rc != ODP_OK) return rc;
+  }
+  hipLaunchKernelGGL(k_clip_factors, dim3(n_ex), dim3(CL_THREADS), 0, s, part, n_slots, n_ex, group_slot_start,
+                     n_groups, thresholds, effective_threshold, mode, gamma, n_cls, guard, cls_dtype, scale_out,
+                     norm_out, group_norm_out, clipped_out, clipped_total_out);
+  return odp_check_launch(what);
 }
