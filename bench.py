@@ -122,65 +122,103 @@ def build_workload(layers, B, T, r, seed, device):
     return lengths, sites
 
 
-def cpu_baseline(r, seed):
-    """The reference algorithm on the host: vmap(grad) per-example LoRA
-    gradients of one Llama layer for a few examples, reference AUTO-S scaling,
-    fp32-accumulated sum and mt19937 inverse-CDF noise (oracle.dp_ref)."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+CPU_LAYERS = 2  # of the 32: the sample of the CPU baseline
+
+
+def cpu_baseline(r, seed, lengths):
+    """The reference algorithm on the host (oracle.dp_ref): vmap(grad)
+    per-example LoRA gradients, reference AUTO-S scaling, fp32-accumulated sum
+    and mt19937 inverse-CDF noise, for every example of the GPU step at its
+    own valid length (no padding) over CPU_LAYERS of the 32 layers; 2
+    warm-ups, median of 5."""
     from oracle import dp_ref
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    T, n_ex = 1024, 2
     g = torch.Generator().manual_seed(seed)
-    params, xs, gs = {}, {}, {}
-    for name, (d_in, d_out) in LAYER_SHAPES.items():
-        params[name + ".A"] = (torch.randn(d_in, r, generator=g) / math.sqrt(d_in)).to(torch.bfloat16)
-        params[name + ".B"] = (torch.randn(r, d_out, generator=g) * 0.02).to(torch.bfloat16)
-    for key, d in (("qkv", 4096), ("o", 4096), ("gu", 4096), ("down", 14336)):
-        xs[key] = torch.randn(n_ex, T, d, generator=g).to(torch.bfloat16)
-    for name, (d_in, d_out) in LAYER_SHAPES.items():
-        gs[name] = torch.randn(n_ex, T, d_out, generator=g).to(torch.bfloat16)
+    names = list(LAYER_SHAPES)
+    keys = ("qkv", "o", "gu", "down")
+    din = {"qkv": 4096, "o": 4096, "gu": 4096, "down": 14336}
+    params = {}
+    for layer in range(CPU_LAYERS):
+        for name, (d_in, d_out) in LAYER_SHAPES.items():
+            params[f"{layer}.{name}.A"] = (torch.randn(d_in, r, generator=g) / math.sqrt(d_in)).to(torch.bfloat16)
+            params[f"{layer}.{name}.B"] = (torch.randn(r, d_out, generator=g) * 0.02).to(torch.bfloat16)
+    # Activations and output gradients are windows of one random pool at
+    # random offsets: the values only need to be bf16 normals, and drawing
+    # the full 1.4 G of them would take longer than the timed work.
+    pool = torch.randn(1 << 26, generator=g).to(torch.bfloat16)
 
-    def loss(p, xq, xo, xg, xd, gq, gk, gv, go, gg, gu, gd):
-        xin = {"q": xq, "k": xq, "v": xq, "o": xo, "gate": xg, "up": xg, "down": xd}
-        gin = {"q": gq, "k": gk, "v": gv, "o": go, "gate": gg, "up": gu, "down": gd}
+    def draw(L, d):
+        off = int(torch.randint(0, pool.numel() - L * d + 1, (1,), generator=g))
+        return pool[off : off + L * d].view(1, L, d)
+
+    examples = []
+    for L in lengths:
+        batch = []
+        for layer in range(CPU_LAYERS):
+            batch += [draw(L, din[k]) for k in keys]
+            batch += [draw(L, LAYER_SHAPES[n][1]) for n in names]
+        examples.append(tuple(batch))
+
+    def loss(p, *b):
         tot = 0.0
-        for name in LAYER_SHAPES:
-            y = 2.0 * (xin[name] @ p[name + ".A"]) @ p[name + ".B"]
-            tot = tot + (y.float() * gin[name].float()).sum()
+        per = len(keys) + len(names)
+        for layer in range(CPU_LAYERS):
+            xs = dict(zip(keys, b[layer * per : layer * per + len(keys)]))
+            gs = dict(zip(names, b[layer * per + len(keys) : (layer + 1) * per]))
+            for name in names:
+                x = xs[SHARED_INPUT[name]]
+                y = 2.0 * (x @ p[f"{layer}.{name}.A"]) @ p[f"{layer}.{name}.B"]
+                tot = tot + (y.float() * gs[name].float()).sum()
         return tot
 
-    batch = (xs["qkv"], xs["o"], xs["gu"], xs["down"], *(gs[n] for n in LAYER_SHAPES))
+    B = len(lengths)
 
     def once():
-        res, _ = dp_ref.clipped_grad(loss, params, batch, clipping_norm=1.0, normalize_by=float(n_ex), autos=True)
-        sigma = 1.0 * 1.0 / n_ex
-        dp_ref.gaussian_noise_reference(res, sigma, key=42, step=0)
+        total = None
+        for batch in examples:  # one example at a time: its own length
+            res, _ = dp_ref.clipped_grad(loss, params, batch, clipping_norm=1.0, normalize_by=float(B), autos=True)
+            f = {k: v.float() for k, v in res.items()}
+            total = f if total is None else {k: total[k] + f[k] for k in f}
+        dp_ref.gaussian_noise_reference({k: v.to(torch.bfloat16) for k, v in total.items()}, 1.0 / B, key=42, step=0)
 
-    once()
+    for _ in range(2):
+        once()
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         once()
         times.append(time.perf_counter() - t0)
     t = sorted(times)[len(times) // 2]
-    # n_ex examples through 1 of the 32 layers -> examples/sec of the whole model.
-    value = n_ex / (t * 32)
+    value = B / (t * 32 / CPU_LAYERS)  # the 32-layer model's examples/sec
     return {
         "value": value,
         "unit": "examples/sec",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 of 32 Llama-3-8B LoRA r={r} layers, {n_ex} examples x {T} tokens, bf16 on CPU "
-                  f"(oracle vmap(grad) + AUTO-S + mt19937 noise), median of 3 after 1 warm-up, "
-                  f"scaled by 1/32; cpu={platform.processor() or platform.machine()}",
+        "sample": f"{CPU_LAYERS} of 32 Llama-3-8B LoRA r={r} layers, all {B} examples of the GPU step at their "
+                  f"valid lengths (sum {sum(lengths)} tokens, no padding), bf16 on the host (oracle vmap(grad) "
+                  f"per example + AUTO-S + fp32 sum + mt19937 noise), median of 5 after 2 warm-ups "
+                  f"({t:.2f} s), scaled by 32/{CPU_LAYERS}; cpu={cpu_model()}",
     }
 
 
 def setup_c3(args, dev):
     """C3: captured LoRA seams, AUTO-S, one clip group."""
     from opaque_amd import _native as N
-    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments
+    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments, leaves_key, plan_key
     from opaque_amd.guard import guard_constants, leaf_guards
 
     B, T, r = args.batch, args.seq, args.rank
@@ -203,10 +241,79 @@ def setup_c3(args, dev):
         "workload": "C3: Llama-3-8B-shaped LoRA r=16, 32 layers x 7 linears, batch 16 x seq 1024, "
                     "ragged lengths U[256,1024], AUTO-S R=1 gamma=0.01, noise multiplier 1.0",
         "global_batch": B, "seq_len": T, "layers": args.layers, "rank": r,
-        "valid_tokens": valid, "parallelism": "single GPU",
+        "valid_tokens": valid, "lengths": lengths, "parallelism": "single GPU",
     }
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16"
+
+    lkey = leaves_key(leaves)
+
+    def rebind_once():
+        """What a call with new inputs of this structure costs the host
+        before the plan runs: its key, and pointing its tables at them."""
+        key = plan_key(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev, leaves_key_=lkey)
+        if not plan.rebind(lsites, [], [], clip, key=key):
+            raise RuntimeError("the C3 plan refused its own inputs")
+
+    plan.bench_rebind = rebind_once
     return plan, 1.0 / B, config, metric, flops, ("project", "factor_project", "factor", "clip", "scale_sum", "noise"), "hbm"
+
+
+def dropin_overhead(args, dev, step_ms):
+    """Host time the drop-in auto_clipped_grad adds per call at C3's
+    structure (32 layers x 7 LoRA seams, q/k/v and gate/up sharing their
+    input, batch 16, AUTO-S).  The host work depends on the seams and
+    segments, not on the tokens, so the model runs 64-token sequences to keep
+    its forward/backward short.  The first call builds the plan; the next
+    ones rebind it."""
+    from opaque_amd import capture
+    from opaque_amd.clipping import auto_clipped_grad
+
+    B, T, r = args.batch, 64, args.rank
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    W = {n: torch.zeros(d_out, d_in, device=dev, dtype=bf) for n, (d_in, d_out) in LAYER_SHAPES.items()}
+    params = {}
+    for layer in range(args.layers):
+        for n, (d_in, d_out) in LAYER_SHAPES.items():
+            params[f"{layer}.{n}.A"] = (torch.randn(d_in, r, device=dev, generator=g) / math.sqrt(d_in)).to(bf)
+            params[f"{layer}.{n}.B"] = (torch.randn(r, d_out, device=dev, generator=g) * 0.02).to(bf)
+    din = {"qkv": 4096, "o": 4096, "gu": 4096, "down": 14336}
+
+    def batch():
+        xs = {f"{layer}.{k}": torch.randn(B, T, d, device=dev, generator=g).to(bf)
+              for layer in range(args.layers) for k, d in din.items()}
+        gs = {f"{layer}.{n}": (torch.randn(B, T, d_out, device=dev, generator=g) * 0.1).to(bf)
+              for layer in range(args.layers) for n, (_, d_out) in LAYER_SHAPES.items()}
+        return xs, gs
+
+    def loss(p, xs, gs):
+        tot = 0.0
+        for layer in range(args.layers):
+            for n in LAYER_SHAPES:
+                y = capture.lora_linear(xs[f"{layer}.{SHARED_INPUT[n]}"], W[n], p[f"{layer}.{n}.A"],
+                                        p[f"{layer}.{n}.B"], 2.0)
+                tot = tot + (y.float() * gs[f"{layer}.{n}"].float()).sum()
+        return tot
+
+    fn, st = auto_clipped_grad(loss, R=1.0, gamma=0.01, normalize_by=float(B), batch_argnums=(1, 2))
+    batches = [batch() for _ in range(2)]
+    prep, total, rebound = [], [], []
+    for i in range(8):
+        fn(params, *batches[i % 2], state=st)
+        torch.cuda.synchronize()
+        prep.append(fn.engine.last_prep_ms)
+        total.append(fn.engine.last_plan_ms)
+        rebound.append(fn.engine.last_rebound)
+    if rebound[0] or not all(rebound[1:]):
+        raise RuntimeError(f"drop-in plan reuse: expected build then rebinds, got {rebound}")
+    med = lambda v: sorted(v)[len(v) // 2]
+    p_ms = med(prep[1:])
+    return {
+        "prep_ms": p_ms, "prep_plus_enqueue_ms": med(total[1:]), "first_call_prep_ms": prep[0],
+        "frac_of_step": p_ms / step_ms,
+        "sample": f"auto_clipped_grad, {args.layers} layers x 7 LoRA r={r} seams, batch {B} x {T} tokens; "
+                  "prep = spec + plan key + rebind on calls 2-8 (median), alternating two input batches",
+    }
 
 
 C4_THRESHOLDS = {"q": 1.0, "k": 0.5, "v": 0.5, "o": 1.0, "gate": 2.0, "up": 2.0, "down": 2.0}
@@ -372,9 +479,18 @@ def main():
         "executed_mfma_tflops": (sum(f for *_, f in plan.launch_info) / (ms * 1e-3) / 1e12
                                  if args.workload == "c4" else None),
         "clipped_fraction": float(res.clipped_total.float().mean().item()),
+        "plan_build_ms": plan.build_ms,
     }
+    if args.workload == "c3":
+        t_rb = []
+        for _ in range(5):
+            t1 = time.perf_counter()
+            plan.bench_rebind()
+            t_rb.append((time.perf_counter() - t1) * 1e3)
+        out["plan_rebind_ms"] = sorted(t_rb)[2]
+        out["dropin_overhead"] = dropin_overhead(args, dev, ms)
     if args.cpu_baseline == "on" and args.workload == "c3":
-        out["cpu_baseline"] = cpu_baseline(args.rank, args.seed)
+        out["cpu_baseline"] = cpu_baseline(args.rank, args.seed, config["lengths"])
     print(json.dumps(out), flush=True)
 
 

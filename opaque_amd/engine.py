@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import math
 import struct
+import time
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -270,13 +271,26 @@ class _Pack:
         self._size = off + arr.nbytes
         return len(self._chunks) - 1
 
-    def upload(self, device: torch.device) -> list[torch.Tensor]:
+    def array(self, i: int) -> np.ndarray:
+        return self._chunks[i]
+
+    def _pinned(self) -> torch.Tensor:
         host = torch.empty(max(self._size, 1), dtype=torch.uint8, pin_memory=True)
         hn = host.numpy()
         for arr, off in zip(self._chunks, self._offsets):
             hn[off : off + arr.nbytes] = arr.view(np.uint8).reshape(-1)
-        dev = host.to(device, non_blocking=True)
-        self._host = host  # keep the pinned source alive until the copy is done
+        return host
+
+    def refresh(self) -> None:
+        """Copies the (patched) host arrays into the same device buffer.  The
+        copy is ordered on the current stream after earlier launches that read
+        the buffer; torch's pinned-memory allocator keeps the source alive
+        until the copy is done."""
+        self._dev.copy_(self._pinned(), non_blocking=True)
+
+    def upload(self, device: torch.device) -> list[torch.Tensor]:
+        dev = self._pinned().to(device, non_blocking=True)
+        self._dev = dev
         views = []
         for arr, off in zip(self._chunks, self._offsets):
             tdt = {
@@ -319,6 +333,77 @@ class _Table:
 
 def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
+
+
+def _layout(ext: dict[tuple, torch.Tensor]) -> list[tuple]:
+    """Shapes, strides, dtypes and storage sharing of a plan's input tensors:
+    a new call's inputs may replace them only if this matches."""
+    storages: dict[int, int] = {}
+    out = []
+    for k, t in ext.items():
+        base = t.untyped_storage().data_ptr()
+        out.append((k, tuple(t.shape), tuple(t.stride()), t.dtype, storages.setdefault(base, len(storages)),
+                    t.data_ptr() - base))
+    return out
+
+
+def _seg_key(segs: Segments | None) -> tuple | None:
+    if segs is None:
+        return None
+    return (tuple(segs.starts), tuple(segs.lengths), tuple(segs.examples), segs.n_ex, segs.n_rows)
+
+
+def _tensor_key(t: torch.Tensor) -> tuple:
+    return (t.shape, t.stride(), t.dtype, t.get_device(), t.data_ptr() & 15)
+
+
+def leaves_key(leaves: list[LeafOut]) -> tuple:
+    """The part of plan_key that the output leaves fix (callers that reuse
+    one leaf list may compute it once and pass it to plan_key)."""
+    return tuple((tuple(lf.shape), lf.out_dtype, lf.group, lf.cls) for lf in leaves)
+
+
+# GhostPlan's keyword options and their defaults (part of a plan's key).
+_PLAN_OPTIONS = {"second_moment": False, "fuse_g_side": True, "prescale_bytes": 8 << 30,
+                 "linear_pe_bytes": None, "square_f64": False, "sum_f64": False}
+
+
+def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_sites=(), materialized=(),
+             linear_sites=(), device=None, leaves_key_: tuple | None = None, **options) -> tuple:
+    """What fixes a GhostPlan's tables: a plan built from inputs with this key
+    can be rebound (GhostPlan.rebind) to other inputs with the same key.
+    Threshold values, gamma and normalize_by are not part of it."""
+    firsts: dict[int, int] = {}
+    xkeys: list[tuple] = []
+
+    def shared(t: torch.Tensor):  # index of the first site input at this address
+        p = t.data_ptr()
+        i = firsts.get(p)
+        if i is None:
+            i = firsts[p] = len(xkeys)
+            xkeys.append(_tensor_key(t))
+            return i
+        k = _tensor_key(t)
+        return i if k == xkeys[i] else (i, k)  # another view at the same address
+
+    # The factors are copied (A transposed) into buffers of the activation's
+    # dtype, so only their shapes and devices shape the tables.
+    lora = tuple((shared(s.x), _tensor_key(s.g), s.A.shape, s.A.get_device(), s.B.shape, s.B.get_device(),
+                  float(s.scaling), s.a_leaf, s.b_leaf, s.a_transposed, s.b_transposed,
+                  None if s.segments is None else _seg_key(s.segments)) for s in lora_sites)
+    mats = tuple((_tensor_key(m.per_example), m.leaf, _seg_key(m.segments)) for m in materialized)
+    lins = tuple((shared(ls.x), _tensor_key(ls.g), ls.w_leaf, ls.form, ls.index,
+                  _seg_key(ls.segments)) for ls in linear_sites)
+    outs = leaves_key(leaves) if leaves_key_ is None else leaves_key_
+    clip_s = (clip.mode, len(clip.thresholds), tuple(g[2] for g in clip.guards))
+    unknown = set(options) - set(_PLAN_OPTIONS)
+    if unknown:
+        raise TypeError(f"unknown GhostPlan options {sorted(unknown)}")
+    opts = tuple((k, options.get(k, v)) for k, v in _PLAN_OPTIONS.items())
+    dev = torch.device(device) if device is not None else None
+    if dev is not None and dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return (str(dev), _seg_key(segments), outs, clip_s, tuple(xkeys), lora, mats, lins, opts)
 
 
 # ---------------------------------------------------------------------------
@@ -364,6 +449,7 @@ class GhostPlan:
         square_f64: bool = False,
         sum_f64: bool = False,
     ) -> None:
+        t_build = time.perf_counter()
         N.load()
         dev = torch.device(device)
         if dev.type == "cuda" and dev.index is None:
@@ -388,7 +474,14 @@ class GhostPlan:
             if not 0 <= lf.group < self.n_groups or not 0 <= lf.cls < self.n_cls:
                 raise ValueError("leaf group/class out of range")
         self._keep: list[torch.Tensor] = []
+        # The structure this plan was built for: rebind(key=...) with an equal
+        # key skips re-deriving the input layout.
+        self.key = plan_key(segments=segments, leaves=leaves, clip=clip, lora_sites=lora_sites,
+                            materialized=materialized, linear_sites=linear_sites, device=dev,
+                            second_moment=second_moment, fuse_g_side=fuse_g_side, prescale_bytes=prescale_bytes,
+                            linear_pe_bytes=linear_pe_bytes, square_f64=square_f64, sum_f64=sum_f64)
         self._build(list(lora_sites), list(materialized), list(linear_sites))
+        self.build_ms = (time.perf_counter() - t_build) * 1e3  # host time of the construction
 
     # -- construction --------------------------------------------------------
     def _build(self, sites: list[LoraSite], mats: list[MaterializedLeaf], lins: list[LinearSite]) -> None:
@@ -396,10 +489,6 @@ class GhostPlan:
         dev = self.device
         reg = _SegRegistry(seg)
         self._segreg = reg
-        # Row views of each linear site's x and g, made once (a view that
-        # needs a copy would otherwise be copied again at every use).
-        lin_x: list[torch.Tensor] = []
-        lin_g: list[torch.Tensor] = []
         for ls in lins:
             if ls.x.device != dev or ls.g.device != dev:
                 raise ValueError("linear site tensors must be on the plan device")
@@ -411,10 +500,8 @@ class GhostPlan:
                 raise ValueError("linear site row count does not match the segments")
             if not (supports_rows(ls.x) and supports_rows(ls.g)):
                 raise ValueError("linear site feature sizes must be multiples of 8")
-            lin_x.append(_rows(ls.x))
-            lin_g.append(_rows(ls.g))
             # The kernels address one segment's rows through 32-bit buffer ranges.
-            ld = max(lin_x[-1].stride(0), lin_g[-1].stride(0))
+            ld = max(_rows(ls.x).stride(0), _rows(ls.g).stride(0))
             if reg.view(ls.segments).max_len * ld * 2 >= 2**31:
                 raise ValueError("a linear site's longest segment spans 2 GiB or more of x or g")
             shape = tuple(self.leaves[ls.w_leaf].shape)
@@ -425,7 +512,7 @@ class GhostPlan:
                 raise ValueError("a stacked linear site's leaf must be shaped [E, d_out, d_in] with index < E")
         # Group sites by activation tensor, then chunk by rank/leaf budget.
         for s in sites:
-            if s.x.device != dev or s.g.device != dev:
+            if s.x.device != dev or s.g.device != dev or s.A.device != dev or s.B.device != dev:
                 raise ValueError("LoRA site tensors must be on the plan device")
             if s.x.dtype != s.g.dtype:
                 raise TypeError("x and g of a LoRA site must share a dtype")
@@ -455,6 +542,24 @@ class GhostPlan:
                 rtot += r
             if cur:
                 chunks.append(cur)
+        # The tables point into tensors that come from the caller's inputs
+        # (row views of x and g, weight copies, materialised leaves), each
+        # made once under a key that rebind() reproduces from the next
+        # call's inputs.
+        site_index = {id(s): k for k, s in enumerate(sites)}
+        self._chunk_sites = [[site_index[id(s)] for s in ch] for ch in chunks]
+        self._lwx_groups = self._factor_groups(chunks)
+        self._ext_keys = self._external_keys(chunks, len(mats), len(lins))
+        ext = dict(zip(self._ext_keys, self._external_list(chunks, mats, lins)))
+        self._ext = ext
+        self._layout_in = _layout(ext)
+        # Tensors that are their input itself or a view at the same address
+        # (no copy was made): with an equal plan key the next call's input
+        # stands in for the view (rebind's fast path).
+        src = self._ext_sources(chunks, mats, lins)
+        self._direct = [k in src and ext[k].data_ptr() == src[k].data_ptr() for k in self._ext_keys]
+        lin_x = [ext[("linx", i)] for i in range(len(lins))]
+        lin_g = [ext[("ling", i)] for i in range(len(lins))]
 
         # Slot allocation: leaf -> number of partial slots, assigned in group order.
         leaf_slots: dict[int, int] = {}
@@ -577,30 +682,7 @@ class GhostPlan:
         self.part = self._part_buf[: seg.n_ex * self.n_slots].view(seg.n_ex, self.n_slots)
         self._nf_flag_addr = self._part_buf.data_ptr() + seg.n_ex * self.n_slots * 8
 
-        # Output leaves: one flat buffer per output dtype, views in leaf order.
-        self.flat: dict[torch.dtype, torch.Tensor] = {}
-        sizes: dict[torch.dtype, int] = {}
-        for lf in self.leaves:
-            sizes[lf.out_dtype] = sizes.get(lf.out_dtype, 0) + (math.prod(lf.shape) + 63) // 64 * 64
-        for dt, n in sizes.items():
-            self.flat[dt] = torch.empty(max(n, 1), dtype=dt, device=dev)
-        self.out: list[torch.Tensor] = []
-        cursor = dict.fromkeys(sizes, 0)
-        for lf in self.leaves:
-            n = math.prod(lf.shape)
-            c = cursor[lf.out_dtype]
-            self.out.append(self.flat[lf.out_dtype][c : c + n].view(lf.shape))
-            cursor[lf.out_dtype] = c + (n + 63) // 64 * 64
-        self.out2: list[torch.Tensor] | None = None
-        if self.second_moment:
-            self.out2 = [torch.empty(lf.shape, dtype=lf.out_dtype, device=dev) for lf in self.leaves]
-
-        G, C, E = self.n_groups, self.n_cls, seg.n_ex
-        self.scales = torch.empty((C, G, E), dtype=torch.float64, device=dev)
-        self.norms = torch.empty(E, dtype=torch.float32, device=dev)
-        self.group_norms = torch.empty((G, E), dtype=torch.float32, device=dev)
-        self.clipped = torch.empty((G, E), dtype=torch.uint8, device=dev)
-        self.clipped_total = torch.empty(E, dtype=torch.uint8, device=dev)
+        ext.update(self._alloc_outputs())
 
         # Q planes (U and V) for every chunk, carved from one allocation per dtype.
         q_need: dict[torch.dtype, int] = {}
@@ -627,7 +709,7 @@ class GhostPlan:
             return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
 
         elem = {torch.bfloat16: 2, torch.float32: 4}
-        for ch, (dt, rtot, rows_alloc, planes, vbase, ubase, ldq) in zip(chunks, chunk_layout):
+        for ci, (ch, (dt, rtot, rows_alloc, planes, vbase, ubase, ldq)) in enumerate(zip(chunks, chunk_layout)):
             qb = self.qbuf[dt]
             es = elem[dt]
             plane = rows_alloc * ldq
@@ -637,15 +719,13 @@ class GhostPlan:
             def qaddr(base: int, row: int, lo: bool, qb=qb, plane=plane, ldq=ldq, es=es) -> int:
                 return qb.data_ptr() + (base + (plane if lo else 0) + row * ldq) * es
 
-            x = _rows(ch[0].x)
-            self._keep.append(x)
+            x = ext[("lx", ci)]
             d_in = x.shape[1]
             # V = X [A_1 .. A_k]
-            wx = torch.cat([s.A.detach().to(dt).t() for s in ch], dim=0).contiguous()
-            self._keep.append(wx)
+            wx = ext[("lwx", ci)]
             if self._mirrored(ch, dt, v):
-                self._mirror_rows(ch[0], x, wx, dt, v, qaddr, vbase, ubase, ldq, planes, es, pj, ft, tab,
-                                  fused_rows, slot_base)
+                self._mirror_rows(ch[0], x, wx, ext[("lg", ci, 0)], ext[("lwb", ci, 0)], dt, v, qaddr, vbase,
+                                  ubase, ldq, planes, es, pj, ft, tab, fused_rows, slot_base)
                 continue
             tab(pj, dt, rtot, N.PJ_FIELDS).add(
                 {
@@ -659,12 +739,10 @@ class GhostPlan:
             )
             c0 = 0
             a_leaves = []
-            for s in ch:
+            for j, s in enumerate(ch):
                 r = s.A.shape[1]
-                g = _rows(s.g)
-                self._keep.append(g)
-                wb = s.B.detach().to(dt).contiguous()
-                self._keep.append(wb)
+                g = ext[("lg", ci, j)]
+                wb = ext[("lwb", ci, j)]
                 d_out = g.shape[1]
                 if s.a_leaf is not None:
                     a_leaves.append((s.a_leaf, c0, r))
@@ -693,8 +771,11 @@ class GhostPlan:
                         row = dict(frow)
                         row[N.FT_SEG_FIRST] = sf + j
                         row[N.FT_LEAF0] = pe0 + j * r * d_out * pe_es
+                        # G rows, the U/V planes and the dB rows of the segment;
+                        # B itself is counted once per site.
                         fused_rows.append((-ln * d_out, len(fused_rows), row, 1,
-                                           (ln * d_out + r * d_out + 2 * planes * r * ln) * es + r * d_out * es))
+                                           (ln * d_out + 2 * planes * r * ln) * es + r * d_out * es
+                                           + (r * d_out * es if j == 0 else 0)))
                     c0 += r
                     continue
                 # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
@@ -739,14 +820,10 @@ class GhostPlan:
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
-        for m in mats:
-            pe_m = m.per_example.detach()
-            if pe_m.dtype not in _DTYPE_CODE:
-                pe_m = pe_m.float()
+        for mi, m in enumerate(mats):
+            pe_m = ext[("mat", mi)]
             v = leaf_view[m.leaf]
             n_seg = v.n_seg
-            pe_m = pe_m.reshape(n_seg, -1).contiguous()
-            self._keep.append(pe_m)
             n = pe_m.shape[1]
             sq.add(
                 {
@@ -837,7 +914,6 @@ class GhostPlan:
         lsum = _Table(N.LN_FIELDS)
         for i, ls in enumerate(lins):
             x, g = lin_x[i], lin_g[i]
-            self._keep += [x, g]
             d_in, d_out = x.shape[1], g.shape[1]
             form = lin_form[i]
             v = lin_view[i]
@@ -951,7 +1027,14 @@ class GhostPlan:
         idx["cls_dt"] = pack.add(np.asarray([dtype_code(g[2]) for g in guards], dtype=np.int32))
         views = pack.upload(dev)
         self._views = views
-        self._host = pack._host
+        self._pack = pack
+        self._thr_idx, self._guard_idx = idx["thr"], idx["guard"]
+        # ext now also holds the output buffers, after the inputs' tensors.
+        patch_keys, patches = self._pointer_fields([pack.array(pi) for _, _, pi, _, _, _, _ in tab_idx], ext)
+        pos = {k: i for i, k in enumerate(ext)}
+        src_pos = np.asarray([pos[k] for k in patch_keys], dtype=np.int64)
+        self._patches = [(vals, sel, src_pos[kidx], off) for vals, sel, kidx, off in patches]
+        self._stream_id = _stream()
         self.seg_start, self.seg_len, self.seg_ex = (views[idx[k]] for k in ("seg_start", "seg_len", "seg_ex"))
         self.gstart, self.thr = views[idx["gstart"]], views[idx["thr"]]
         self.guard, self.cls_dt = views[idx["guard"]], views[idx["cls_dt"]]
@@ -960,6 +1043,222 @@ class GhostPlan:
         info = [(name, dt, total, nb[0], nb[1]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
         after_clip = _AFTER_CLIP
         self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
+
+    @staticmethod
+    def _pointer_fields(arrays: list[np.ndarray], ext: dict[tuple, torch.Tensor]) -> tuple[list, list[tuple]]:
+        """Every table field that holds an address inside one of the tensors of
+        `ext`: the keys of those tensors, and per array that has such fields
+        (flat view, field indices, key indices, byte offsets into the tensor)."""
+        keys, lo, hi = [], [], []
+        for k, t in ext.items():
+            if t.numel() == 0:
+                continue
+            extent = 1 + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
+            keys.append(k)
+            lo.append(t.data_ptr())
+            hi.append(t.data_ptr() + extent * t.element_size())
+        order = np.argsort(np.asarray(lo, dtype=np.int64), kind="stable")
+        lo_s = np.asarray(lo, dtype=np.int64)[order]
+        hi_s = np.asarray(hi, dtype=np.int64)[order]
+        out = []
+        for arr in arrays:
+            vals = arr.reshape(-1)
+            pos = np.searchsorted(lo_s, vals, side="right") - 1
+            ok = (pos >= 0) & (vals < hi_s[np.maximum(pos, 0)])
+            sel = np.nonzero(ok)[0]
+            if sel.size:
+                out.append((vals, sel, order[pos[sel]], vals[sel] - lo_s[pos[sel]]))
+        return keys, out
+
+    def rebind(self, lora_sites: list[LoraSite] = (), materialized: list[MaterializedLeaf] = (),
+               linear_sites: list[LinearSite] = (), clip: ClipSpec | None = None, key: tuple | None = None) -> bool:
+        """Points the plan at a new call's inputs with the same structure and
+        gives it fresh outputs; scratch buffers and tables are reused.
+
+        The caller guarantees the structure (the same sites, leaf layout and
+        segments in the same order).  With ``key``, the new inputs' plan_key,
+        equal to the plan's own, shapes, strides, dtypes, devices, alignment
+        and activation sharing are known to match; without it the tensors
+        derived from the new inputs are checked to lay out like the ones the
+        plan was built from.  Returns False (and leaves the plan unusable)
+        when they do not, or when the current stream is not the one the plan
+        ran on (its scratch is ordered on that stream).
+        """
+        if _stream() != self._stream_id:
+            return False
+        sites, mats, lins = list(lora_sites), list(materialized), list(linear_sites)
+        try:
+            chunks = [[sites[k] for k in idx] for idx in self._chunk_sites]
+        except IndexError:
+            return False
+        if clip is not None and (len(clip.thresholds) != self.n_groups or clip.mode != self.clip.mode
+                                 or len(clip.guards) != len(self.clip.guards)):
+            return False
+        trusted = key is not None and key == self.key
+        if not trusted:
+            # The sites of a chunk read one activation (the plan projects it once).
+            for ch in chunks:
+                x0 = ch[0].x
+                for s in ch[1:]:
+                    if s.x.data_ptr() != x0.data_ptr() or s.x.shape != x0.shape or s.x.stride() != x0.stride():
+                        return False
+        tensors = self._external_list(chunks, mats, lins, self._direct if trusted else None)
+        if not trusted and _layout(dict(zip(self._ext_keys, tensors))) != self._layout_in:
+            return False
+        tensors += self._alloc_outputs().values()
+        ptr = np.fromiter((t.data_ptr() for t in tensors), dtype=np.int64, count=len(tensors))
+        for vals, sel, pos, off in self._patches:
+            vals[sel] = ptr[pos] + off
+        if clip is not None:
+            self.clip = clip
+            self._pack.array(self._thr_idx)[:] = np.asarray(clip.thresholds, dtype=np.float64)
+            guards = clip.guards or [(1.0, 0.0, torch.float32)]
+            self._pack.array(self._guard_idx)[:] = np.asarray([[g[0], g[1]] for g in guards],
+                                                              dtype=np.float64).reshape(-1)
+        self._ext = tensors  # kept alive while the plan points at them
+        self._pack.refresh()
+        return True
+
+    @staticmethod
+    def _ext_sources(chunks: list[list[LoraSite]], mats: list[MaterializedLeaf],
+                     lins: list[LinearSite]) -> dict[tuple, torch.Tensor]:
+        """The input tensor each external tensor other than "lwx" derives from."""
+        src: dict[tuple, torch.Tensor] = {}
+        for ci, ch in enumerate(chunks):
+            src[("lx", ci)] = ch[0].x
+            for j, s in enumerate(ch):
+                src[("lg", ci, j)] = s.g
+                src[("lwb", ci, j)] = s.B
+        for mi, m in enumerate(mats):
+            src[("mat", mi)] = m.per_example
+        for i, ls in enumerate(lins):
+            src[("linx", i)] = ls.x
+            src[("ling", i)] = ls.g
+        return src
+
+    @staticmethod
+    def _factor_groups(chunks: list[list[LoraSite]]) -> list[list[int]]:
+        """Chunks whose stacked A^T come out of one copy: same dtype and d_in."""
+        by_width: dict[tuple, list[int]] = {}
+        for ci, ch in enumerate(chunks):
+            by_width.setdefault((ch[0].x.dtype, ch[0].A.shape[0]), []).append(ci)
+        return list(by_width.values())
+
+    def _external_keys(self, chunks: list[list[LoraSite]], n_mats: int, n_lins: int) -> list[tuple]:
+        """Keys of the tensors _external_list returns, in its order: per LoRA
+        chunk the concatenated A^T of its sites ("lwx", c), its activation
+        rows ("lx", c) and per site of the chunk its output gradient rows
+        ("lg", c, j) and B ("lwb", c, j); materialised leaves ("mat", m) as
+        [n_seg, n]; linear sites' rows ("linx", i), ("ling", i)."""
+        keys = [("lwx", ci) for cis in self._lwx_groups for ci in cis]
+        for ci, ch in enumerate(chunks):
+            keys.append(("lx", ci))
+            for j in range(len(ch)):
+                keys += [("lg", ci, j), ("lwb", ci, j)]
+        keys += [("mat", mi) for mi in range(n_mats)]
+        for i in range(n_lins):
+            keys += [("linx", i), ("ling", i)]
+        return keys
+
+    def _external_list(self, chunks: list[list[LoraSite]], mats: list[MaterializedLeaf],
+                       lins: list[LinearSite], direct: list[bool] | None = None) -> list[torch.Tensor]:
+        """The tensors the tables point to that come from the caller's inputs
+        (keys from _external_keys).  Where ``direct`` is set the input tensor
+        itself stands in for its row view."""
+        out: list[torch.Tensor] = []
+        with torch.no_grad():
+            # Per group, the A of all its chunks side by side, transposed in
+            # one copy; each chunk's A^T rows are a view of it.
+            for cis in self._lwx_groups:
+                dt = chunks[cis[0]][0].x.dtype
+                parts = [s.A if s.A.dtype == dt else s.A.to(dt) for ci in cis for s in chunks[ci]]
+                side = torch.cat(parts, dim=1) if len(parts) > 1 else parts[0]
+                out += side.t().contiguous().split([sum(s.A.shape[1] for s in chunks[ci]) for ci in cis])
+            p = len(out)
+            for ch in chunks:
+                dt = ch[0].x.dtype
+                x = ch[0].x
+                out.append(x if direct and direct[p] else _rows(x))
+                p += 1
+                for s in ch:
+                    out.append(s.g if direct and direct[p] else _rows(s.g))
+                    b = s.B
+                    out.append(b if b.dtype == dt and b.is_contiguous() else b.to(dt).contiguous())
+                    p += 2
+        for m in mats:
+            if direct and direct[p]:
+                out.append(m.per_example)
+            else:
+                pe_m = m.per_example.detach()
+                if pe_m.dtype not in _DTYPE_CODE:
+                    pe_m = pe_m.float()
+                out.append(pe_m.reshape(pe_m.shape[0], -1).contiguous())
+            p += 1
+        for ls in lins:
+            out.append(ls.x if direct and direct[p] else _rows(ls.x))
+            out.append(ls.g if direct and direct[p + 1] else _rows(ls.g))
+            p += 2
+        return out
+
+    def _alloc_outputs(self) -> dict[tuple, torch.Tensor]:
+        """Fresh output buffers: one flat buffer per output dtype (and one more
+        for the second moments), the per-example results, and the leaves as
+        views of the flat buffers.  Returns the buffers the tables point into."""
+        dev = self.device
+        if not hasattr(self, "_out_groups"):
+            self._plan_out_layout()
+        self.flat = {dt: torch.empty(max(n, 1), dtype=dt, device=dev) for dt, n in self._out_sizes.items()}
+        self.out: list[torch.Tensor] = self._leaf_views(self.flat)
+        self.out2: list[torch.Tensor] | None = None
+        outs = {("flat", str(dt)): t for dt, t in self.flat.items()}
+        if self.second_moment:
+            flat2 = {dt: torch.empty(max(n, 1), dtype=dt, device=dev) for dt, n in self._out_sizes.items()}
+            self.out2 = self._leaf_views(flat2)
+            outs.update({("flat2", str(dt)): t for dt, t in flat2.items()})
+        # The per-example results, carved from one allocation (each part
+        # 256-byte aligned).
+        G, C, E = self.n_groups, self.n_cls, self.segments.n_ex
+        parts = [((C, G, E), torch.float64), ((E,), torch.float32), ((G, E), torch.float32),
+                 ((G, E), torch.uint8), ((E,), torch.uint8)]
+        offs, total = [], 0
+        for shape, dt in parts:
+            offs.append(total)
+            total += (math.prod(shape) * dt.itemsize + 255) // 256 * 256
+        buf = torch.empty(total, dtype=torch.uint8, device=dev)
+        self.scales, self.norms, self.group_norms, self.clipped, self.clipped_total = (
+            buf[o : o + math.prod(shape) * dt.itemsize].view(dt).view(shape) for o, (shape, dt) in zip(offs, parts))
+        return outs
+
+    def _plan_out_layout(self) -> None:
+        """Where each leaf lives in its dtype's flat buffer: leaves of one shape
+        back to back, each padded to a multiple of 64 elements (so that every
+        leaf starts 128-byte aligned), groups in order of first appearance."""
+        groups: dict[tuple, list[int]] = {}
+        for i, lf in enumerate(self.leaves):
+            groups.setdefault((lf.out_dtype, tuple(lf.shape)), []).append(i)
+        sizes: dict[torch.dtype, int] = {}
+        self._out_groups = []  # (dtype, offset, count, padded size, size, shape)
+        order = []
+        for (dt, shape), idx in groups.items():
+            n = math.prod(shape)
+            padded = (n + 63) // 64 * 64
+            off = sizes.get(dt, 0)
+            self._out_groups.append((dt, off, len(idx), padded, n, shape))
+            sizes[dt] = off + len(idx) * padded
+            order += idx
+        self._out_sizes = sizes
+        self._out_perm = [0] * len(order)
+        for pos, i in enumerate(order):
+            self._out_perm[i] = pos
+
+    def _leaf_views(self, flat: dict[torch.dtype, torch.Tensor]) -> list[torch.Tensor]:
+        views: list[torch.Tensor] = []
+        for dt, off, k, padded, n, shape in self._out_groups:
+            block = flat[dt][off : off + k * padded].view(k, padded)
+            if n != padded:
+                block = block[:, :n]
+            views.extend(block.view(k, *shape).unbind(0))
+        return [views[p] for p in self._out_perm]
 
     def _mirrored(self, ch: list[LoraSite], dt: torch.dtype, v: _SegView) -> bool:
         """Whether a one-site chunk reads its activation once and its output
@@ -971,14 +1270,11 @@ class GhostPlan:
         x = _rows(s.x)
         return x.shape[1] > s.g.shape[-1] and self._fusable(dt, s.A.shape[1], v, x)
 
-    def _mirror_rows(self, s, x, wx, dt, v, qaddr, vbase, ubase, ldq, planes, es, pj, ft, tab, fused_rows,
+    def _mirror_rows(self, s, x, wx, g, wb, dt, v, qaddr, vbase, ubase, ldq, planes, es, pj, ft, tab, fused_rows,
                      slot_base) -> None:
         lib = N.load()
         r = s.A.shape[1]
         d_in = x.shape[1]
-        g = _rows(s.g)
-        wb = s.B.detach().to(dt).contiguous()
-        self._keep += [g, wb]
         d_out = g.shape[1]
         n_rows, n_seg, valid, sf = v.n_rows, v.n_seg, v.valid, v.first
         # U = G B^T (the projection kernel on G).
@@ -1011,7 +1307,8 @@ class GhostPlan:
             rj[N.FT_SEG_FIRST] = sf + j
             rj[N.FT_LEAF0] = pe0 + j * r * d_in * pe_es
             fused_rows.append((-ln * d_in, len(fused_rows), rj, 1,
-                               (ln * d_in + r * d_in + 2 * planes * r * ln) * es + r * d_in * es))
+                               (ln * d_in + 2 * planes * r * ln) * es + r * d_in * es
+                               + (r * d_in * es if j == 0 else 0)))
         # dB^T rows from G and V.
         if s.b_leaf is not None:
             tab(ft, dt, r, N.FT_FIELDS).add(
@@ -1182,6 +1479,7 @@ class GhostPlan:
 
 
 __all__ = [
+    "plan_key",
     "ClipSpec",
     "GhostPlan",
     "GhostResult",
