@@ -500,10 +500,13 @@ class _ClipEngine:
         t0 = time.perf_counter()
         capture = bool(sites) or bool(lins)
         # Clip constants and output leaves depend only on the tree's shapes,
-        # dtypes and paths: kept from the last call when those match.
+        # dtypes and paths and on the thresholds (which adaptive clipping
+        # moves every step): kept from the last call when those match.
+        cn = self.clipping_norm
         memo_key = (tuple(shapes), tuple(dtypes),
-                    tuple(paths) if isinstance(self.clipping_norm, PerGroup) else len(paths),
-                    float(normalize_by), capture)
+                    (tuple(paths), tuple(cn.groups.items()), tuple(cn.values.items()))
+                    if isinstance(cn, PerGroup) else float(cn),
+                    len(paths), float(normalize_by), capture)
         if self._spec_memo is None or self._spec_memo[0] != memo_key:
             leaf_group, names, thresholds = self._groups(paths)
             spec, leaf_cls, square_f64 = self._clip_spec(shapes, dtypes, thresholds, normalize_by, capture)

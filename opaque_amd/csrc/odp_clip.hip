@@ -155,6 +155,128 @@ __device__ __forceinline__ void scale_sum_generic(const void* pe, int pdt, int64
   }
 }
 
+// One clipped-sum term per element: the per-example value with non-finite
+// entries zeroed (nan_to_num), times the scale, rounded to bf16 when the
+// values are bf16 (scale.to(dtype) * leaf); accumulated in float32.
+template <bool SECOND, bool BF>
+__device__ __forceinline__ void ss_term(float v, float c, float& acc, float& acc2) {
+  if (!isfinite(v)) v = 0.f;
+  float y = __fmul_rn(c, v);
+  if (BF) y = odp_round_bf16(y);
+  acc = __fadd_rn(acc, y);
+  if (SECOND) {
+    float yy = __fmul_rn(y, y);
+    if (BF) yy = odp_round_bf16(yy);
+    acc2 = __fadd_rn(acc2, yy);
+  }
+}
+
+// The sum cast to the output dtype, then divided in it (the reference's order).
+__device__ __forceinline__ float ss_finish(float acc, float normalize_by, int odt) {
+  float x = odp_round_to(acc, odt);
+  if (normalize_by != 1.0f) x = odp_round_to(__fdiv_rn(x, normalize_by), odt);
+  return x;
+}
+
+// 8 consecutive outputs: one 16-byte store (bf16) or two (f32).
+__device__ __forceinline__ void ss_put8(void* dst, int64_t o, int odt, const float (&y)[SS_ELEMS]) {
+  if (odt == ODP_DTYPE_BF16) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 w;
+    w.x = (uint32_t)odp_f2bf(y[0]) | ((uint32_t)odp_f2bf(y[1]) << 16);
+    w.y = (uint32_t)odp_f2bf(y[2]) | ((uint32_t)odp_f2bf(y[3]) << 16);
+    w.z = (uint32_t)odp_f2bf(y[4]) | ((uint32_t)odp_f2bf(y[5]) << 16);
+    w.w = (uint32_t)odp_f2bf(y[6]) | ((uint32_t)odp_f2bf(y[7]) << 16);
+    odp_gstore((u32x4*)((uint16_t*)dst + o), w);
+  } else {
+    odp_gstore((f32x4_t*)((float*)dst + o), f32x4_t{y[0], y[1], y[2], y[3]});
+    odp_gstore((f32x4_t*)((float*)dst + o + 4), f32x4_t{y[4], y[5], y[6], y[7]});
+  }
+}
+
+// bf16/f32 values and outputs, E a multiple of 8: a thread sums the 8
+// consecutive elements e0.. over the segments (16-byte loads for bf16).
+template <bool SECOND, bool BF>
+__device__ __forceinline__ void scale_sum_rows(const void* pe, int64_t E, int64_t M, int rank, int64_t e0, int n_seg,
+                                               int seg_first, const int32_t* __restrict__ sex,
+                                               const double* __restrict__ sc, float normalize_by, void* out,
+                                               void* out2, int odt, int transpose) {
+  float acc[SS_ELEMS], acc2[SS_ELEMS];
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = 0.f;
+  for (int s = 0; s < n_seg; ++s) {
+    const float c = (float)sc[sex[seg_first + s]];
+    float v[SS_ELEMS];
+    if (BF) {
+      const uint4 w = *(const uint4*)((const uint16_t*)pe + (int64_t)s * E + e0);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(ww[i] << 16);
+        v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+      }
+    } else {
+      const f32x4_t a = *(const f32x4_t*)((const float*)pe + (int64_t)s * E + e0);
+      const f32x4_t b = *(const f32x4_t*)((const float*)pe + (int64_t)s * E + e0 + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = a[i];
+        v[4 + i] = b[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < SS_ELEMS; ++i) ss_term<SECOND, BF>(v[i], c, acc[i], acc2[i]);
+  }
+  float x[SS_ELEMS], x2[SS_ELEMS];
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) {
+    x[i] = ss_finish(acc[i], normalize_by, odt);
+    if (SECOND) x2[i] = ss_finish(acc2[i], normalize_by, odt);
+  }
+  if (!transpose) {
+    ss_put8(out, e0, odt, x);
+    if (SECOND) ss_put8(out2, e0, odt, x2);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) {
+    const int64_t e = e0 + i;
+    const int64_t k = e / M, m = e - k * M;
+    odp_store_from_float(out, m * rank + k, odt, x[i]);
+    if (SECOND) odp_store_from_float(out2, m * rank + k, odt, x2[i]);
+  }
+}
+
+// Transposed outputs: a thread sums ranks k0..k0+7 of column m (e_first is
+// element (k0, m), rows M apart) and stores them at o = m * rank + k0.
+template <bool SECOND, bool BF>
+__device__ __forceinline__ void scale_sum_cols(const void* pe, int64_t E, int64_t M, int64_t e_first, int n_seg,
+                                               int seg_first, const int32_t* __restrict__ sex,
+                                               const double* __restrict__ sc, float normalize_by, void* out,
+                                               void* out2, int odt, int64_t o) {
+  float acc[SS_ELEMS], acc2[SS_ELEMS];
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = 0.f;
+  for (int s = 0; s < n_seg; ++s) {
+    const float c = (float)sc[sex[seg_first + s]];
+    const int64_t base = (int64_t)s * E + e_first;
+    float v[SS_ELEMS];
+#pragma unroll
+    for (int i = 0; i < SS_ELEMS; ++i)
+      v[i] = BF ? odp_bf2f(((const uint16_t*)pe)[base + i * M]) : ((const float*)pe)[base + i * M];
+#pragma unroll
+    for (int i = 0; i < SS_ELEMS; ++i) ss_term<SECOND, BF>(v[i], c, acc[i], acc2[i]);
+  }
+  float x[SS_ELEMS], x2[SS_ELEMS];
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i) {
+    x[i] = ss_finish(acc[i], normalize_by, odt);
+    if (SECOND) x2[i] = ss_finish(acc2[i], normalize_by, odt);
+  }
+  ss_put8(out, o, odt, x);
+  if (SECOND) ss_put8(out2, o, odt, x2);
+}
+
 __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
     const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
     const int32_t* __restrict__ sex, const double* __restrict__ scales, int n_ex, int n_groups,
@@ -176,99 +298,57 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
   const int wide = (int)((flags >> 48) & 1);
   const int pdt = (int)((flags >> 56) & 0xff);
   const int64_t E = M * rank;
-  const int64_t e0 = ((int64_t)(bid - ws[p]) * SS_THREADS + threadIdx.x) * SS_ELEMS;
-  if (e0 >= E) return;
   const double* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
-  if (wide || pdt == ODP_DTYPE_F64) {
-    scale_sum_generic<double>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
-                              M, rank);
+  const bool generic = wide || pdt == ODP_DTYPE_F64 || pdt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F16 ||
+                       odt == ODP_DTYPE_F64 || (E & 7) != 0;
+  if (generic) {
+    const int64_t e0 = ((int64_t)(bid - ws[p]) * SS_THREADS + threadIdx.x) * SS_ELEMS;
+    if (e0 >= E) return;
+    if (wide || pdt == ODP_DTYPE_F64)
+      scale_sum_generic<double>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
+                                M, rank);
+    else
+      scale_sum_generic<float>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
+                               M, rank);
     return;
   }
-  if (pdt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F64) {
-    scale_sum_generic<float>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
-                             M, rank);
-    return;
-  }
-  // Whole 8-element pieces load as vectors (rows of E elements stay 16-byte
-  // aligned when E is a multiple of 8).
-  const bool whole = (E & 7) == 0;
-  float acc[SS_ELEMS], acc2[SS_ELEMS];
-#pragma unroll
-  for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = 0.f;
-  for (int s = 0; s < n_seg; ++s) {
-    const float c = sc[sex[seg_first + s]];
-    float v[SS_ELEMS];
-    if (whole && pdt == ODP_DTYPE_F32) {
-      const f32x4_t a = *(const f32x4_t*)(pe + (int64_t)s * E + e0);
-      const f32x4_t b = *(const f32x4_t*)(pe + (int64_t)s * E + e0 + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = a[i];
-        v[4 + i] = b[i];
-      }
-    } else if (whole && pdt == ODP_DTYPE_BF16) {
-      const uint4 w = *(const uint4*)((const uint16_t*)pe + (int64_t)s * E + e0);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(ww[i] << 16);
-        v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
-      }
+  const bool bf_in = pdt == ODP_DTYPE_BF16;
+  const int b = bid - ws[p];
+  // Transposed leaves ([M][rank] out of [rank][M] sums) with rank in
+  // {8, 16, 32, 64}: each thread sums 8 consecutive ranks of one column, so
+  // that its outputs are one 16-byte store; lanes take consecutive columns,
+  // so every load instruction reads consecutive elements of a row.
+  const int k8 = rank >> 3;
+  if (transpose && (rank & 7) == 0 && rank <= 64 && SS_THREADS % k8 == 0) {
+    const int cols = SS_THREADS / k8;  // columns per workgroup
+    const int64_t m = (int64_t)b * cols + threadIdx.x % cols;
+    if (m >= M) return;
+    const int64_t e_first = (int64_t)(threadIdx.x / cols) * 8 * M + m;  // element (k0, m)
+    if (out2) {
+      if (bf_in) scale_sum_cols<true, true>(pe, E, M, e_first, n_seg, seg_first, sex, sc, normalize_by, out, out2,
+                                            odt, m * rank + (threadIdx.x / cols) * 8);
+      else scale_sum_cols<true, false>(pe, E, M, e_first, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt,
+                                       m * rank + (threadIdx.x / cols) * 8);
     } else {
-#pragma unroll
-      for (int i = 0; i < SS_ELEMS; ++i)
-        v[i] = e0 + i < E ? odp_load_as_float(pe, (int64_t)s * E + e0 + i, pdt) : 0.f;
+      if (bf_in) scale_sum_cols<false, true>(pe, E, M, e_first, n_seg, seg_first, sex, sc, normalize_by, out,
+                                             nullptr, odt, m * rank + (threadIdx.x / cols) * 8);
+      else scale_sum_cols<false, false>(pe, E, M, e_first, n_seg, seg_first, sex, sc, normalize_by, out, nullptr,
+                                        odt, m * rank + (threadIdx.x / cols) * 8);
     }
-    const bool bf = pdt == ODP_DTYPE_BF16;
-#pragma unroll
-    for (int i = 0; i < SS_ELEMS; ++i) {
-      if (!isfinite(v[i])) v[i] = 0.f;  // nan_to_num of the per-example value
-      // The term as the leaf dtype stores it (scale.to(dtype) * leaf).
-      float y = __fmul_rn(c, v[i]), yy = __fmul_rn(y, y);
-      if (bf) {
-        y = odp_round_bf16(y);
-        yy = odp_round_bf16(__fmul_rn(y, y));
-      }
-      acc[i] = __fadd_rn(acc[i], y);
-      acc2[i] = __fadd_rn(acc2[i], yy);
-    }
-  }
-  float x[SS_ELEMS], x2[SS_ELEMS];
-#pragma unroll
-  for (int i = 0; i < SS_ELEMS; ++i) {
-    x[i] = odp_round_to(acc[i], odt);
-    if (normalize_by != 1.0f) x[i] = odp_round_to(__fdiv_rn(x[i], normalize_by), odt);
-    x2[i] = odp_round_to(acc2[i], odt);
-    if (normalize_by != 1.0f) x2[i] = odp_round_to(__fdiv_rn(x2[i], normalize_by), odt);
-  }
-  if (whole && !transpose && (odt == ODP_DTYPE_BF16 || odt == ODP_DTYPE_F32)) {
-    // 8 consecutive outputs: one 16-byte store (bf16) or two (f32).
-    auto put = [&](void* dst, const float (&y)[SS_ELEMS]) {
-      if (odt == ODP_DTYPE_BF16) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        u32x4 w;
-        w.x = (uint32_t)odp_f2bf(y[0]) | ((uint32_t)odp_f2bf(y[1]) << 16);
-        w.y = (uint32_t)odp_f2bf(y[2]) | ((uint32_t)odp_f2bf(y[3]) << 16);
-        w.z = (uint32_t)odp_f2bf(y[4]) | ((uint32_t)odp_f2bf(y[5]) << 16);
-        w.w = (uint32_t)odp_f2bf(y[6]) | ((uint32_t)odp_f2bf(y[7]) << 16);
-        odp_gstore((u32x4*)((uint16_t*)dst + e0), w);
-      } else {
-        odp_gstore((f32x4_t*)((float*)dst + e0), f32x4_t{y[0], y[1], y[2], y[3]});
-        odp_gstore((f32x4_t*)((float*)dst + e0 + 4), f32x4_t{y[4], y[5], y[6], y[7]});
-      }
-    };
-    put(out, x);
-    if (out2) put(out2, x2);
     return;
   }
-#pragma unroll
-  for (int i = 0; i < SS_ELEMS; ++i) {
-    const int64_t e = e0 + i;
-    if (e >= E) break;
-    const int64_t k = e / M, m = e - k * M;
-    const int64_t o = transpose ? m * rank + k : e;
-    odp_store_from_float(out, o, odt, x[i]);
-    if (out2) odp_store_from_float(out2, o, odt, x2[i]);
+  const int64_t e0 = ((int64_t)b * SS_THREADS + threadIdx.x) * SS_ELEMS;
+  if (e0 >= E) return;
+  if (out2) {
+    if (bf_in) scale_sum_rows<true, true>(pe, E, M, rank, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2,
+                                          odt, transpose);
+    else scale_sum_rows<true, false>(pe, E, M, rank, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt,
+                                     transpose);
+  } else {
+    if (bf_in) scale_sum_rows<false, true>(pe, E, M, rank, e0, n_seg, seg_first, sex, sc, normalize_by, out,
+                                           nullptr, odt, transpose);
+    else scale_sum_rows<false, false>(pe, E, M, rank, e0, n_seg, seg_first, sex, sc, normalize_by, out, nullptr,
+                                      odt, transpose);
   }
 }
 

@@ -249,15 +249,18 @@ def test_per_group_matches_oracle():
     assert aux.clipping_rate is None
 
 
-def test_second_moment_microbatch_stats():
-    out, st, _, summed, aux, C = run_both(torch.float32, second_moment=True, normalize_by=2.0)
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_second_moment_microbatch_stats(dtype, tol):
+    out, st, _, summed, aux, C = run_both(dtype, second_moment=True, normalize_by=2.0)
     res, _ = out
     assert isinstance(res, SecondMomentClippingOutput)
     assert res.squared_grads.max_norm == pytest.approx(C * C / 2.0)
     for k, ref in aux["squared"].items():
-        assert rel(res.squared_grads.pytree[k], ref) <= 1e-5, k
+        assert rel(res.squared_grads.pytree[k], ref) <= tol, k
     for k, ref in summed.items():
-        assert rel(res.grads.pytree[k], ref) <= 1e-5, k
+        assert rel(res.grads.pytree[k], ref) <= tol, k
+    if dtype != torch.float32:
+        return
     # Microbatching gives the same sum.
     out_mb, _, _, summed_mb, _, _ = run_both(torch.float32, microbatch=4, return_aux=False, normalize_by=2.0)
     for k, ref in summed_mb.items():

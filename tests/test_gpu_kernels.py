@@ -75,6 +75,9 @@ def _run_single_site(X, G, A, B, seg, scaling, C=1.0, mode=N.CLIP_FIXED, normali
         (torch.bfloat16, 4, 64, 256, 128, 16, None),
         (torch.bfloat16, 5, 96, 136, 264, 8, [96, 33, 1, 70, 64]),
         (torch.bfloat16, 2, 128, 512, 384, 48, [128, 100]),
+        (torch.bfloat16, 3, 64, 200, 72, 64, [64, 20, 5]),
+        (torch.float32, 2, 48, 104, 96, 32, None),
+        (torch.bfloat16, 2, 32, 72, 40, 4, None),
     ],
 )
 def test_lora_norms_and_factor_grads(dtype, n_ex, T, d_in, d_out, r, lengths):
