@@ -69,7 +69,8 @@ def kernel_label(stage, key):
     if stage == "lin_sum":  # keyed by prescale chunk, None for in-register scaling
         return f"k_lin_clip_sum<{'false' if key is None else 'true'}>"
     if key is None:
-        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum",
+        return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "nonfinite": "k_nonfinite_cols",
+                "pack": "k_pack_factors",
                 "factor_project": "k_factor_project_bf16"}[stage]
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]
@@ -248,12 +249,14 @@ def setup_c3(args, dev):
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16"
 
     lkey = leaves_key(leaves)
+    ptrs = torch.empty(4 * len(lsites), dtype=torch.int64)
 
     def rebind_once():
         """What a call with new inputs of this structure costs the host
         before the plan runs: its key, and pointing its tables at them."""
-        key = plan_key(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev, leaves_key_=lkey)
-        if not plan.rebind(lsites, [], [], clip, key=key):
+        key = plan_key(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev, leaves_key_=lkey,
+                       lora_ptrs=ptrs)
+        if not plan.rebind(lsites, [], [], clip, key=key, lora_ptrs=ptrs):
             raise RuntimeError("the C3 plan refused its own inputs")
 
     plan.bench_rebind = rebind_once

@@ -83,6 +83,27 @@ typedef enum odp_norm_form {
  * whose norm and clip factor the segment contributes to.  A problem refers
  * to the slice [seg_first, seg_first + n_seg) of these device arrays.      */
 
+/* ---- odp_pack_factors: W[j][k] = A[k][j] ---------------------------------
+ * Copies LoRA factors A [d_in][r] (any strides and dtype) into the row-major
+ * A^T operand [r][d_in] that odp_project reads (ODP_PJ_W), converting to the
+ * activation dtype; one problem per seam.  Replaces the transpose of A that
+ * the reference's per-sample gradient forms in torch
+ * (opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176), done here
+ * on the device so that a call's host work does not touch every factor.    */
+enum {
+  ODP_PF_SRC = 0,     /* address of A: element (k, j) at SRC + k LD0 + j LD1 elements */
+  ODP_PF_LD0 = 1,
+  ODP_PF_LD1 = 2,
+  ODP_PF_DTYPES = 3,  /* odp_dtype of A | odp_dtype of W << 8 (W: bf16 or f32)        */
+  ODP_PF_DIN = 4,
+  ODP_PF_R = 5,       /* r <= 64                                                    */
+  ODP_PF_DST = 6,     /* address of W rows: element (j, k) at DST + j DIN + k         */
+  ODP_PF_FIELDS = 8
+};
+int64_t odp_pack_factors_blocks(int64_t d_in);
+int odp_pack_factors(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                     int32_t n_prob, int32_t total_blocks);
+
 /* ---- odp_project: Q^T[k][row] = sum_j P[row][j] * W[k][j] --------------
  * The LoRA rank-space projections U = G B^T and V = X A for rows
  * [0, n_rows); rows outside the problem's segments get 0.  Only columns

@@ -23,6 +23,8 @@ CLIP_FIXED = 0
 CLIP_AUTOS = 1
 
 # Problem-table field layouts (must match include/opaque_dp.h).
+PF_SRC, PF_LD0, PF_LD1, PF_DTYPES, PF_DIN, PF_R, PF_DST = range(7)
+PF_FIELDS = 8
 PJ_FIELDS = 12
 PJ_P, PJ_LDP, PJ_D, PJ_W, PJ_R, PJ_Q, PJ_LDQ, PJ_NROWS, PJ_SEG_FIRST, PJ_NSEG, PJ_QLO = range(11)
 FT_FIELDS = 24
@@ -58,6 +60,8 @@ _ptr = ctypes.c_void_p
 _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_abi_version": (_c_int, []),
     "odp_last_error": (ctypes.c_char_p, []),
+    "odp_pack_factors_blocks": (_c_i64, [_c_i64]),
+    "odp_pack_factors": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32]),
     "odp_project_blocks": (_c_i64, [_c_int, _c_i64, _c_i32]),
     "odp_project": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i32]),
     "odp_seg_factor_tiles": (_c_i64, [_c_int, _c_i64, _c_i32]),

@@ -66,5 +66,25 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+HOST_SRC = CSRC / "odp_host.cpp"
+HOST_DIR = PKG_DIR / "_host_build"
+HOST_NAME = "_odp_host"
+
+
+def build_host(verbose: bool = False) -> Path:
+    """Compile the host-side helper (a torch C++ extension, no device code)
+    into opaque_amd/_host_build/_odp_host.so.  Always recompiles."""
+    import torch.utils.cpp_extension as ext
+
+    HOST_DIR.mkdir(exist_ok=True)
+    for stale in HOST_DIR.glob("*"):
+        if stale.is_file():
+            stale.unlink()
+    ext.load(name=HOST_NAME, sources=[str(HOST_SRC)], build_directory=str(HOST_DIR),
+             extra_cflags=["-O2"], verbose=verbose)
+    return HOST_DIR / f"{HOST_NAME}.so"
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_host(verbose=True))

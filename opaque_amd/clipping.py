@@ -333,6 +333,7 @@ class _ClipEngine:
         # to its own inputs instead of building tables and buffers again.
         self._plan: GhostPlan | None = None
         self._spec_memo: tuple | None = None
+        self._lora_ptrs = torch.empty(0, dtype=torch.int64)  # LoRA site addresses from plan_key
         # Host milliseconds the last call spent from its captured inputs to the
         # plan being ready (spec, plan key, rebind or build: last_prep_ms) and
         # to its last kernel enqueued (last_plan_ms), and whether it rebound
@@ -518,12 +519,14 @@ class _ClipEngine:
         # (_clipped_fun.py:115-134): float64 on request, float32 otherwise.
         kw = dict(second_moment=self.second_moment, square_f64=square_f64,
                   sum_f64=self.compute_dtype == torch.float64, **self.plan_options)
+        if self._lora_ptrs.numel() < 4 * len(sites):
+            self._lora_ptrs = torch.empty(4 * len(sites), dtype=torch.int64)
         key = plan_key(segments=segments, leaves=outs, clip=spec, lora_sites=sites, materialized=mats,
-                       linear_sites=lins, device=device, leaves_key_=outs_key, **kw)
+                       linear_sites=lins, device=device, leaves_key_=outs_key, lora_ptrs=self._lora_ptrs, **kw)
         plan = None
         if self._plan is not None and self._plan.key == key:
             plan = self._plan
-            if not plan.rebind(sites, mats, list(lins), spec, key=key):
+            if not plan.rebind(sites, mats, list(lins), spec, key=key, lora_ptrs=self._lora_ptrs):
                 plan = None
         self.last_rebound = plan is not None
         if plan is None:

@@ -1069,6 +1069,42 @@ __global__ __launch_bounds__(256) void k_factor_f32(const int64_t* __restrict__ 
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// A^T operands of the projection: one thread per row k of A, writing
+// column k of W row by row (coalesced across the workgroup's threads).
+// ---------------------------------------------------------------------------
+constexpr int PF_THREADS = 256;
+
+__global__ __launch_bounds__(PF_THREADS) void k_pack_factors(const int64_t* __restrict__ probs,
+                                                             const int32_t* __restrict__ ws, int n_prob) {
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_PF_FIELDS;
+  const void* src = (const void*)f[ODP_PF_SRC];
+  const int64_t ld0 = f[ODP_PF_LD0], ld1 = f[ODP_PF_LD1], din = f[ODP_PF_DIN];
+  const int sdt = (int)(f[ODP_PF_DTYPES] & 0xff), ddt = (int)((f[ODP_PF_DTYPES] >> 8) & 0xff);
+  const int r = (int)f[ODP_PF_R];
+  void* dst = (void*)f[ODP_PF_DST];
+  const int64_t k = (int64_t)(bid - ws[p]) * PF_THREADS + threadIdx.x;
+  if (k >= din) return;
+  for (int j = 0; j < r; ++j)
+    odp_store_from_float(dst, (int64_t)j * din + k, ddt, odp_load_as_float(src, k * ld0 + (int64_t)j * ld1, sdt));
+}
+
+extern "C" int64_t odp_pack_factors_blocks(int64_t d_in) {
+  return d_in <= 0 ? 0 : (d_in + PF_THREADS - 1) / PF_THREADS;
+}
+
+extern "C" int odp_pack_factors(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                                int32_t n_prob, int32_t total_blocks) {
+  int rc = odp_check_table("odp_pack_factors", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  hipLaunchKernelGGL(k_pack_factors, dim3(total_blocks), dim3(PF_THREADS), 0, odp_hip_stream(stream), problems,
+                     work_start, n_prob);
+  return odp_check_launch("odp_pack_factors");
+}
+
 extern "C" int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r) {
   const int64_t rows = dtype == ODP_DTYPE_BF16 ? 64 * pj_rpw((r + 15) / 16) : PJ_ROWS;
   return n_rows <= 0 ? 0 : (n_rows + rows - 1) / rows;

@@ -26,6 +26,8 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from opaque_amd import _host
+
 from opaque_amd import _native as N
 
 _DTYPE_CODE = {torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16, torch.float16: N.DTYPE_F16,
@@ -369,10 +371,21 @@ _PLAN_OPTIONS = {"second_moment": False, "fuse_g_side": True, "prescale_bytes": 
 
 
 def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_sites=(), materialized=(),
-             linear_sites=(), device=None, leaves_key_: tuple | None = None, **options) -> tuple:
+             linear_sites=(), device=None, leaves_key_: tuple | None = None, lora_ptrs: torch.Tensor | None = None,
+             **options) -> tuple:
     """What fixes a GhostPlan's tables: a plan built from inputs with this key
     can be rebound (GhostPlan.rebind) to other inputs with the same key.
-    Threshold values, gamma and normalize_by are not part of it."""
+    Threshold values, gamma and normalize_by are not part of it.
+
+    With the host helper built, the LoRA sites' part is its byte signature
+    (the same fields), and ``lora_ptrs`` (an int64 CPU tensor of at least 4
+    entries per LoRA site) receives the addresses of each site's x, g, A
+    and B for rebind()."""
+    host = _host.load()
+    lora_sig = None
+    if host is not None:
+        buf = lora_ptrs if lora_ptrs is not None else torch.empty(4 * len(lora_sites), dtype=torch.int64)
+        lora_sig = host.lora_signature(list(lora_sites), buf)
     firsts: dict[int, int] = {}
     xkeys: list[tuple] = []
 
@@ -386,11 +399,14 @@ def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_
         k = _tensor_key(t)
         return i if k == xkeys[i] else (i, k)  # another view at the same address
 
-    # The factors are copied (A transposed) into buffers of the activation's
-    # dtype, so only their shapes and devices shape the tables.
-    lora = tuple((shared(s.x), _tensor_key(s.g), s.A.shape, s.A.get_device(), s.B.shape, s.B.get_device(),
-                  float(s.scaling), s.a_leaf, s.b_leaf, s.a_transposed, s.b_transposed,
-                  None if s.segments is None else _seg_key(s.segments)) for s in lora_sites)
+    # odp_pack_factors reads A with the strides and dtype in its table; B is
+    # copied into the activation's dtype unless it can be read in place.
+    if lora_sig is not None:
+        lora = ("host", lora_sig)
+    else:
+        lora = tuple((shared(s.x), _tensor_key(s.g), _tensor_key(s.A), s.B.shape, s.B.get_device(),
+                      s.B.dtype, s.B.is_contiguous(), float(s.scaling), s.a_leaf, s.b_leaf, s.a_transposed,
+                      s.b_transposed, None if s.segments is None else _seg_key(s.segments)) for s in lora_sites)
     mats = tuple((_tensor_key(m.per_example), m.leaf, _seg_key(m.segments)) for m in materialized)
     lins = tuple((shared(ls.x), _tensor_key(ls.g), ls.w_leaf, ls.form, ls.index,
                   _seg_key(ls.segments)) for ls in linear_sites)
@@ -558,6 +574,34 @@ class GhostPlan:
         # stands in for the view (rebind's fast path).
         src = self._ext_sources(chunks, mats, lins)
         self._direct = [k in src and ext[k].data_ptr() == src[k].data_ptr() for k in self._ext_keys]
+        self._fast = self._fast_map(chunks, ext, len(sites))
+        # A^T of every chunk's sites, [sum of ranks][d_in] in the activation
+        # dtype: plan scratch that odp_pack_factors fills from the caller's A
+        # at the start of every run (one buffer per (dtype, d_in) group).
+        lib = N.load()
+        self._lwx_bufs = []
+        wx_of: dict[int, torch.Tensor] = {}
+        pft = _Table(N.PF_FIELDS)
+        for cis in self._lwx_groups:
+            dt = chunks[cis[0]][0].x.dtype
+            d_in = chunks[cis[0]][0].A.shape[0]
+            rows = sum(s.A.shape[1] for ci in cis for s in chunks[ci])
+            buf = torch.empty((rows, d_in), dtype=dt, device=dev)
+            self._lwx_bufs.append(buf)
+            r0 = 0
+            for ci in cis:
+                rtot = sum(s.A.shape[1] for s in chunks[ci])
+                wx_of[ci] = buf[r0 : r0 + rtot]
+                c0 = 0
+                for j, s in enumerate(chunks[ci]):
+                    A = ext[("la", ci, j)]
+                    r = A.shape[1]
+                    pft.add({N.PF_SRC: A.data_ptr(), N.PF_LD0: A.stride(0), N.PF_LD1: A.stride(1),
+                             N.PF_DTYPES: dtype_code(A.dtype) | (dtype_code(dt) << 8), N.PF_DIN: d_in, N.PF_R: r,
+                             N.PF_DST: buf[r0 + c0 : r0 + c0 + r].data_ptr()},
+                            lib.odp_pack_factors_blocks(d_in), d_in * r * (A.element_size() + buf.element_size()))
+                    c0 += r
+                r0 += rtot
         lin_x = [ext[("linx", i)] for i in range(len(lins))]
         lin_g = [ext[("ling", i)] for i in range(len(lins))]
 
@@ -722,7 +766,7 @@ class GhostPlan:
             x = ext[("lx", ci)]
             d_in = x.shape[1]
             # V = X [A_1 .. A_k]
-            wx = ext[("lwx", ci)]
+            wx = wx_of[ci]
             if self._mirrored(ch, dt, v):
                 self._mirror_rows(ch[0], x, wx, ext[("lg", ci, 0)], ext[("lwb", ci, 0)], dt, v, qaddr, vbase,
                                   ubase, ldq, planes, es, pj, ft, tab, fused_rows, slot_base)
@@ -1001,7 +1045,7 @@ class GhostPlan:
         idx["seg_len"] = pack.add(seg_ln)
         idx["seg_ex"] = pack.add(seg_ex)
         self._launch: list[tuple] = []
-        tabs = []
+        tabs = [("pack", None, pft)]
         for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("project", key, pj[key]))
         tabs.append(("factor_project", None, fp))
@@ -1071,7 +1115,8 @@ class GhostPlan:
         return keys, out
 
     def rebind(self, lora_sites: list[LoraSite] = (), materialized: list[MaterializedLeaf] = (),
-               linear_sites: list[LinearSite] = (), clip: ClipSpec | None = None, key: tuple | None = None) -> bool:
+               linear_sites: list[LinearSite] = (), clip: ClipSpec | None = None, key: tuple | None = None,
+               lora_ptrs: torch.Tensor | None = None) -> bool:
         """Points the plan at a new call's inputs with the same structure and
         gives it fresh outputs; scratch buffers and tables are reused.
 
@@ -1082,19 +1127,25 @@ class GhostPlan:
         derived from the new inputs are checked to lay out like the ones the
         plan was built from.  Returns False (and leaves the plan unusable)
         when they do not, or when the current stream is not the one the plan
-        ran on (its scratch is ordered on that stream).
+        ran on (its scratch is ordered on that stream).  ``lora_ptrs``: the
+        LoRA sites' addresses that plan_key wrote while computing ``key``;
+        with them the LoRA side is re-pointed without reading the site
+        tensors again.
         """
         if _stream() != self._stream_id:
             return False
-        sites, mats, lins = list(lora_sites), list(materialized), list(linear_sites)
-        try:
-            chunks = [[sites[k] for k in idx] for idx in self._chunk_sites]
-        except IndexError:
-            return False
+        sites, mats, lins = lora_sites, list(materialized), list(linear_sites)
         if clip is not None and (len(clip.thresholds) != self.n_groups or clip.mode != self.clip.mode
                                  or len(clip.guards) != len(self.clip.guards)):
             return False
         trusted = key is not None and key == self.key
+        fast = self._fast if trusted and lora_ptrs is not None else None
+        chunks = []
+        if fast is None:
+            try:
+                chunks = [[sites[k] for k in idx] for idx in self._chunk_sites]
+            except IndexError:
+                return False
         if not trusted:
             # The sites of a chunk read one activation (the plan projects it once).
             for ch in chunks:
@@ -1102,11 +1153,20 @@ class GhostPlan:
                 for s in ch[1:]:
                     if s.x.data_ptr() != x0.data_ptr() or s.x.shape != x0.shape or s.x.stride() != x0.stride():
                         return False
-        tensors = self._external_list(chunks, mats, lins, self._direct if trusted else None)
-        if not trusted and _layout(dict(zip(self._ext_keys, tensors))) != self._layout_in:
-            return False
-        tensors += self._alloc_outputs().values()
-        ptr = np.fromiter((t.data_ptr() for t in tensors), dtype=np.int64, count=len(tensors))
+        if fast is not None:
+            src, n_lora = fast
+            outs = list(self._alloc_outputs().values())
+            tail = self._other_external(mats, lins, self._direct, n_lora) + outs
+            ptr = np.empty(len(self._ext_keys) + len(outs), dtype=np.int64)
+            ptr[:n_lora] = lora_ptrs.numpy()[src[:n_lora]]
+            ptr[n_lora:] = np.fromiter((t.data_ptr() for t in tail), dtype=np.int64, count=len(tail))
+            tensors = tail
+        else:
+            tensors = self._external_list(chunks, mats, lins, self._direct if trusted else None)
+            if not trusted and _layout(dict(zip(self._ext_keys, tensors))) != self._layout_in:
+                return False
+            tensors += self._alloc_outputs().values()
+            ptr = np.fromiter((t.data_ptr() for t in tensors), dtype=np.int64, count=len(tensors))
         for vals, sel, pos, off in self._patches:
             vals[sel] = ptr[pos] + off
         if clip is not None:
@@ -1122,19 +1182,46 @@ class GhostPlan:
     @staticmethod
     def _ext_sources(chunks: list[list[LoraSite]], mats: list[MaterializedLeaf],
                      lins: list[LinearSite]) -> dict[tuple, torch.Tensor]:
-        """The input tensor each external tensor other than "lwx" derives from."""
+        """The input tensor each external tensor derives from."""
         src: dict[tuple, torch.Tensor] = {}
         for ci, ch in enumerate(chunks):
             src[("lx", ci)] = ch[0].x
             for j, s in enumerate(ch):
                 src[("lg", ci, j)] = s.g
                 src[("lwb", ci, j)] = s.B
+                src[("la", ci, j)] = s.A
         for mi, m in enumerate(mats):
             src[("mat", mi)] = m.per_example
         for i, ls in enumerate(lins):
             src[("linx", i)] = ls.x
             src[("ling", i)] = ls.g
         return src
+
+    def _fast_map(self, chunks: list[list[LoraSite]], ext: dict[tuple, torch.Tensor], n_sites: int):
+        """Where rebind's fast path finds each LoRA input address: when every
+        LoRA input is read in place, the address of ("lx", c), ("lg", c, j),
+        ("lwb", c, j) and ("la", c, j) is the caller's x, g, B or A (entry
+        4 site + 0, 1, 3 or 2 of the host helper's address list).  None when
+        some input was copied at build time, or without the helper."""
+        if _host.load() is None or not chunks:
+            return None
+        slot = {"lx": 0, "lg": 1, "la": 2, "lwb": 3}
+        keys = self._ext_keys
+        src = np.full(len(keys), -1, dtype=np.int64)
+        n_lora = 0
+        for p, k in enumerate(keys):
+            kind = k[0]
+            if kind not in slot:
+                continue
+            n_lora += 1
+            ci = k[1]
+            j = 0 if kind == "lx" else k[2]
+            s = chunks[ci][j]
+            t = (s.x, s.g, s.A, s.B)[slot[kind]]
+            if ext[k].data_ptr() != t.data_ptr():
+                return None
+            src[p] = 4 * self._chunk_sites[ci][j] + slot[kind]
+        return src, n_lora
 
     @staticmethod
     def _factor_groups(chunks: list[list[LoraSite]]) -> list[list[int]]:
@@ -1146,15 +1233,15 @@ class GhostPlan:
 
     def _external_keys(self, chunks: list[list[LoraSite]], n_mats: int, n_lins: int) -> list[tuple]:
         """Keys of the tensors _external_list returns, in its order: per LoRA
-        chunk the concatenated A^T of its sites ("lwx", c), its activation
-        rows ("lx", c) and per site of the chunk its output gradient rows
-        ("lg", c, j) and B ("lwb", c, j); materialised leaves ("mat", m) as
-        [n_seg, n]; linear sites' rows ("linx", i), ("ling", i)."""
-        keys = [("lwx", ci) for cis in self._lwx_groups for ci in cis]
+        chunk its activation rows ("lx", c) and per site of the chunk its
+        output gradient rows ("lg", c, j), B ("lwb", c, j) and A ("la", c, j);
+        materialised leaves ("mat", m) as [n_seg, n]; linear sites' rows
+        ("linx", i), ("ling", i)."""
+        keys = []
         for ci, ch in enumerate(chunks):
             keys.append(("lx", ci))
             for j in range(len(ch)):
-                keys += [("lg", ci, j), ("lwb", ci, j)]
+                keys += [("lg", ci, j), ("lwb", ci, j), ("la", ci, j)]
         keys += [("mat", mi) for mi in range(n_mats)]
         for i in range(n_lins):
             keys += [("linx", i), ("ling", i)]
@@ -1166,15 +1253,8 @@ class GhostPlan:
         (keys from _external_keys).  Where ``direct`` is set the input tensor
         itself stands in for its row view."""
         out: list[torch.Tensor] = []
+        p = 0
         with torch.no_grad():
-            # Per group, the A of all its chunks side by side, transposed in
-            # one copy; each chunk's A^T rows are a view of it.
-            for cis in self._lwx_groups:
-                dt = chunks[cis[0]][0].x.dtype
-                parts = [s.A if s.A.dtype == dt else s.A.to(dt) for ci in cis for s in chunks[ci]]
-                side = torch.cat(parts, dim=1) if len(parts) > 1 else parts[0]
-                out += side.t().contiguous().split([sum(s.A.shape[1] for s in chunks[ci]) for ci in cis])
-            p = len(out)
             for ch in chunks:
                 dt = ch[0].x.dtype
                 x = ch[0].x
@@ -1184,7 +1264,14 @@ class GhostPlan:
                     out.append(s.g if direct and direct[p] else _rows(s.g))
                     b = s.B
                     out.append(b if b.dtype == dt and b.is_contiguous() else b.to(dt).contiguous())
-                    p += 2
+                    out.append(s.A)  # read in place by odp_pack_factors
+                    p += 3
+        return out + self._other_external(mats, lins, direct, p)
+
+    def _other_external(self, mats: list[MaterializedLeaf], lins: list[LinearSite], direct: list[bool] | None,
+                        p: int) -> list[torch.Tensor]:
+        """_external_list's materialised and linear-site tensors (from position p)."""
+        out: list[torch.Tensor] = []
         for m in mats:
             if direct and direct[p]:
                 out.append(m.per_example)
@@ -1217,16 +1304,29 @@ class GhostPlan:
             outs.update({("flat2", str(dt)): t for dt, t in flat2.items()})
         # The per-example results, carved from one allocation (each part
         # 256-byte aligned).
-        G, C, E = self.n_groups, self.n_cls, self.segments.n_ex
-        parts = [((C, G, E), torch.float64), ((E,), torch.float32), ((G, E), torch.float32),
-                 ((G, E), torch.uint8), ((E,), torch.uint8)]
-        offs, total = [], 0
-        for shape, dt in parts:
-            offs.append(total)
-            total += (math.prod(shape) * dt.itemsize + 255) // 256 * 256
+        if not hasattr(self, "_res_parts"):
+            G, C, E = self.n_groups, self.n_cls, self.segments.n_ex
+            parts = [((C, G, E), torch.float64), ((E,), torch.float32), ((G, E), torch.float32),
+                     ((G, E), torch.uint8), ((E,), torch.uint8)]
+            offs, total = [], 0
+            for shape, dt in parts:
+                offs.append(total)
+                total += (math.prod(shape) * dt.itemsize + 255) // 256 * 256
+            self._res_parts = (parts, offs, total)
+            host = _host.load()
+            self._res_maker = None if host is None else host.ViewMaker(
+                [0] * len(parts), [list(sh) for sh, _ in parts],
+                [[math.prod(sh[i + 1 :]) for i in range(len(sh))] for sh, _ in parts],
+                [o // dt.itemsize for o, (_, dt) in zip(offs, parts)],
+                [torch.empty(0, dtype=dt) for _, dt in parts])
+        parts, offs, total = self._res_parts
         buf = torch.empty(total, dtype=torch.uint8, device=dev)
-        self.scales, self.norms, self.group_norms, self.clipped, self.clipped_total = (
-            buf[o : o + math.prod(shape) * dt.itemsize].view(dt).view(shape) for o, (shape, dt) in zip(offs, parts))
+        if self._res_maker is not None:
+            self.scales, self.norms, self.group_norms, self.clipped, self.clipped_total = self._res_maker.make([buf])
+        else:
+            self.scales, self.norms, self.group_norms, self.clipped, self.clipped_total = (
+                buf[o : o + math.prod(shape) * dt.itemsize].view(dt).view(shape)
+                for o, (shape, dt) in zip(offs, parts))
         return outs
 
     def _plan_out_layout(self) -> None:
@@ -1250,8 +1350,31 @@ class GhostPlan:
         self._out_perm = [0] * len(order)
         for pos, i in enumerate(order):
             self._out_perm[i] = pos
+        # The same views made by the host helper in one call, when it is built.
+        self._views_maker = None
+        host = _host.load()
+        if host is not None:
+            buf_of = {dt: i for i, dt in enumerate(sizes)}
+            where = {}
+            for dt, off, k, padded, n, shape in self._out_groups:
+                for j in range(k):
+                    where[len(where)] = (buf_of[dt], off + j * padded, shape)
+            bufs, shapes, strides, offs = [], [], [], []
+            for i in range(len(self.leaves)):
+                b, o, shape = where[self._out_perm[i]]
+                st, acc = [], 1
+                for d in reversed(shape):
+                    st.append(acc)
+                    acc *= d
+                bufs.append(b)
+                shapes.append(list(shape))
+                strides.append(list(reversed(st)))
+                offs.append(o)
+            self._views_maker = host.ViewMaker(bufs, shapes, strides, offs)
 
     def _leaf_views(self, flat: dict[torch.dtype, torch.Tensor]) -> list[torch.Tensor]:
+        if self._views_maker is not None:
+            return self._views_maker.make([flat[dt] for dt in self._out_sizes])
         views: list[torch.Tensor] = []
         for dt, off, k, padded, n, shape in self._out_groups:
             block = flat[dt][off : off + k * padded].view(k, padded)
@@ -1399,7 +1522,9 @@ class GhostPlan:
             if name in ev and first:
                 ev[name][0].record()
             end_ev = mark(name, dt)
-            if name == "project":
+            if name == "pack":
+                N.check(lib.odp_pack_factors(stream, probs.data_ptr(), ws.data_ptr(), n, total), name)
+            elif name == "project":
                 N.check(lib.odp_project(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                         self.seg_start.data_ptr(), self.seg_len.data_ptr(), dt[1]), name)
             elif name == "factor_project":

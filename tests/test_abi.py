@@ -57,6 +57,8 @@ def test_field_indices_match_header():
         assert m, name
         return int(m.group(1))
 
+    assert value("ODP_PF_FIELDS") == N.PF_FIELDS
+    assert value("ODP_PF_DST") == N.PF_DST
     assert value("ODP_PJ_FIELDS") == N.PJ_FIELDS
     assert value("ODP_PJ_QLO") == N.PJ_QLO
     assert value("ODP_FT_FIELDS") == N.FT_FIELDS
@@ -91,6 +93,8 @@ def test_block_helpers_are_pure_host_code(lib):
     assert lib.odp_nonfinite_blocks(256, 3) == 3
     assert lib.odp_nonfinite_blocks(264, 2) == 4
     assert lib.odp_nonfinite_blocks(0, 2) == 0
+    assert lib.odp_pack_factors_blocks(0) == 0
+    assert lib.odp_pack_factors_blocks(256) == 1 and lib.odp_pack_factors_blocks(257) == 2
 
 
 # ---------------------------------------------------------------------------

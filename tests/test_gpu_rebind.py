@@ -84,9 +84,11 @@ def test_rebind_equals_fresh_plan(pe_bytes, second_moment, keyed):
     r1 = plan.run()
     first = _snapshot(r1)
     held = [t for t in r1.leaves]  # the tensors the first call handed out
-    k2 = plan_key(clip=clip2, lora_sites=l2, linear_sites=n2, materialized=m2, **kw)
+    ptrs = torch.empty(4 * len(l2), dtype=torch.int64)
+    k2 = plan_key(clip=clip2, lora_sites=l2, linear_sites=n2, materialized=m2, lora_ptrs=ptrs, **kw)
     assert plan.key == plan_key(clip=clip1, lora_sites=l1, linear_sites=n1, materialized=m1, **kw) == k2
-    assert plan.rebind(l2, m2, n2, clip2, key=k2 if keyed else None)
+    # keyed: the fast path when the host helper is built (addresses from plan_key)
+    assert plan.rebind(l2, m2, n2, clip2, key=k2 if keyed else None, lora_ptrs=ptrs if keyed else None)
     r2 = plan.run()
     fresh = GhostPlan(clip=clip2, lora_sites=l2, linear_sites=n2, materialized=m2, **kw).run()
     torch.cuda.synchronize()

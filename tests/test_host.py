@@ -283,3 +283,77 @@ def test_adaptive_validation(kwargs, match):
 
     with pytest.raises(ValueError, match=match):
         adaptive_clipped_grad(_loss, key=key(0), **kwargs)
+
+
+def _helper():
+    from opaque_amd import _host
+
+    mod = _host.load()
+    if mod is None:
+        pytest.skip("host helper not built (opaque_amd.build.build_host)")
+    return mod
+
+
+def _lora_sites(seed=0, share=True, **over):
+    from opaque_amd.engine import LoraSite
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(64, 32, generator=g).to(torch.bfloat16)
+    sites = []
+    for k, d_out in enumerate((48, 16)):
+        xs = x if share or k == 0 else x.clone()
+        gt = torch.randn(64, d_out, generator=g).to(torch.bfloat16)
+        A = torch.randn(32, 8, generator=g).to(torch.bfloat16)
+        B = torch.randn(8, d_out, generator=g).to(torch.bfloat16)
+        sites.append(LoraSite(xs, gt, A, B, 2.0, a_leaf=2 * k, b_leaf=2 * k + 1))
+    for k, v in over.items():
+        setattr(sites[1], k, v)
+    return sites
+
+
+def test_host_signature_tracks_structure_and_addresses():
+    """The helper's LoRA-site signature (the plan key's LoRA part when the
+    helper is built) changes with every field that shapes a plan's tables and
+    with nothing else; the addresses it writes are the sites' tensors'."""
+    mod = _helper()
+    ptrs = torch.empty(8, dtype=torch.int64)
+    base = _lora_sites(0)
+    sig = mod.lora_signature(base, ptrs)
+    assert ptrs.tolist() == [t.data_ptr() for s in base for t in (s.x, s.g, s.A, s.B)]
+    assert mod.lora_signature(_lora_sites(1), torch.empty(8, dtype=torch.int64)) == sig  # new values, same structure
+    g_t = base[1].g.t().contiguous().t()  # same shape, other strides
+    changed = {
+        "unshared x": _lora_sites(0, share=False),
+        "g strides": _lora_sites(0, g=g_t),
+        "g dtype": _lora_sites(0, g=base[1].g.float()),
+        "g shape": _lora_sites(0, g=base[1].g[:32]),
+        "g alignment": _lora_sites(0, g=torch.empty(64 * 16 + 1, dtype=torch.bfloat16)[1:].view(64, 16)),
+        "A shape": _lora_sites(0, A=base[1].A[:, :4]),
+        "B non-contiguous": _lora_sites(0, B=base[1].B.t().contiguous().t()),
+        "B dtype": _lora_sites(0, B=base[1].B.float()),
+        "scaling": _lora_sites(0, scaling=4.0),
+        "a_leaf": _lora_sites(0, a_leaf=None),
+        "b_transposed": _lora_sites(0, b_transposed=True),
+    }
+    for what, sites in changed.items():
+        assert mod.lora_signature(sites, torch.empty(8, dtype=torch.int64)) != sig, what
+    from opaque_amd.engine import Segments
+
+    assert mod.lora_signature(_lora_sites(0, segments=Segments.padded(2, 32)), ptrs) is None
+
+
+def test_host_view_maker_matches_torch_views():
+    mod = _helper()
+    a = torch.arange(200, dtype=torch.float32)
+    b = torch.arange(100, dtype=torch.bfloat16)
+    vm = mod.ViewMaker([0, 1, 0], [[3, 4], [10], []], [[4, 1], [1], []], [64, 0, 7])
+    v = vm.make([a, b])
+    assert torch.equal(v[0], a[64:76].view(3, 4)) and v[0].data_ptr() == a.data_ptr() + 64 * 4
+    assert torch.equal(v[1], b[:10]) and v[2].shape == () and v[2].item() == 7.0
+    # views of other dtypes over a byte buffer (offsets count the view's elements)
+    raw = torch.arange(1024, dtype=torch.int32).view(torch.uint8)
+    vm2 = mod.ViewMaker([0, 0], [[2, 3], [4]], [[3, 1], [1]], [32, 512],
+                        [torch.empty(0, dtype=torch.float64), torch.empty(0, dtype=torch.uint8)])
+    d, u = vm2.make([raw])
+    assert d.dtype == torch.float64 and torch.equal(d, raw[256 : 256 + 48].view(torch.float64).view(2, 3))
+    assert u.dtype == torch.uint8 and torch.equal(u, raw[512:516])
