@@ -243,24 +243,29 @@ __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const 
   }
 #endif
 
-  // lane holds D[4*(lane>>4) + i][lane & 15] of each 16x16 block
+  // lane holds D[4*(lane>>4) + i][lane & 15] of each 16x16 block: 4
+  // consecutive rows of one rank column, which are 4 consecutive entries of
+  // that column's plane row, stored as one 8-byte piece per plane (2-byte
+  // stores cost these kernels 11-17 % of their time).  rb is a multiple of
+  // 4 and ldq (a multiple of 8) exceeds n_rows by at least 32, so a group
+  // that runs past n_rows stays inside the plane row; its rows past n_rows
+  // hold zero P rows (rowok), and no kernel reads plane entries of rows
+  // outside segments.
 #pragma unroll
   for (int b = 0; b < RB; ++b) {
     const int64_t rb = row0 + 16 * b + 4 * (lane >> 4);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       const int col = kb * 16 + (lane & 15);
-      if (col < r) {
-        uint16_t* qhi = Q + (int64_t)col * ldq;
-        uint16_t* qlo = Qlo + (int64_t)col * ldq;
+      if (col < r && rb < n_rows) {
+        uint32_t h[4], l[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (rb + i < n_rows) {
-            const uint16_t h = odp_f2bf(acc[b][kb][i]);
-            odp_gstore(qhi + rb + i, h);
-            odp_gstore(qlo + rb + i, odp_f2bf(acc[b][kb][i] - odp_bf2f(h)));
-          }
+          h[i] = odp_f2bf(acc[b][kb][i]);
+          l[i] = odp_f2bf(acc[b][kb][i] - odp_bf2f((uint16_t)h[i]));
         }
+        odp_gstore((u32x2_t*)(Q + (int64_t)col * ldq + rb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+        odp_gstore((u32x2_t*)(Qlo + (int64_t)col * ldq + rb), u32x2_t{l[0] | (l[1] << 16), l[2] | (l[3] << 16)});
       }
     }
   }
@@ -314,16 +319,14 @@ __global__ __launch_bounds__(256) void k_project_f32(const int64_t* __restrict__
       }
     }
   }
+  // 4 consecutive rows of one rank column: one 16-byte piece of the plane
+  // row (rb is a multiple of 4; ldq, a multiple of 8, exceeds n_rows by at
+  // least 32, and plane entries of rows outside segments are never read).
   const int64_t rb = row0 + 4 * (lane >> 4);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     const int col = kb * 16 + (lane & 15);
-    if (kb < nkb && col < r) {
-      float* q = Q + (int64_t)col * ldq;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (rb + i < n_rows) odp_gstore(q + rb + i, acc[kb][i]);
-    }
+    if (kb < nkb && col < r && rb < n_rows) odp_gstore((f32x4_t*)(Q + (int64_t)col * ldq + rb), acc[kb]);
   }
 }
 
@@ -968,7 +971,11 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   flush();
 
   // U: lane holds rows 4 (lane >> 4) + i, column lane & 15 of each step's
-  // 16 x 16 block; tokens outside the segment belong to other workgroups.
+  // 16 x 16 block: 4 consecutive entries of the column's plane row (tb is a
+  // multiple of 4), stored as one 8-byte piece per plane when all four
+  // tokens are the segment's; tokens outside the segment belong to other
+  // workgroups, so a group that straddles a segment end is stored entry by
+  // entry.
   const int col = lane & 15;
   if (col < r) {
     uint16_t* uh = (uint16_t*)f[ODP_FP_U] + (int64_t)col * ldq;
@@ -977,13 +984,23 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
     for (int st = 0; st < FP_STEPS; ++st) {
       if (st < nsteps) {
         const int32_t tb = t_lo + st * FP_T + 16 * wave + 4 * (lane >> 4);
+        uint32_t h[4], l[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int32_t t = tb + i;
-          if (t >= rs && t < t_hi) {
-            const uint16_t h = odp_f2bf(acc_u[st][i]);
-            odp_gstore(uh + t, h);
-            odp_gstore(ul + t, odp_f2bf(acc_u[st][i] - odp_bf2f(h)));
+          h[i] = odp_f2bf(acc_u[st][i]);
+          l[i] = odp_f2bf(acc_u[st][i] - odp_bf2f((uint16_t)h[i]));
+        }
+        if (tb >= rs && tb + 3 < t_hi) {
+          odp_gstore((u32x2_t*)(uh + tb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+          odp_gstore((u32x2_t*)(ul + tb), u32x2_t{l[0] | (l[1] << 16), l[2] | (l[3] << 16)});
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int32_t t = tb + i;
+            if (t >= rs && t < t_hi) {
+              odp_gstore(uh + t, (uint16_t)h[i]);
+              odp_gstore(ul + t, (uint16_t)l[i]);
+            }
           }
         }
       }
