@@ -15,16 +15,17 @@
 namespace {
 
 constexpr int CL_THREADS = 1024;  // one workgroup per example
+constexpr int CL_DEPTH = 8;      // loads in flight per thread (a power of two)
 constexpr int CL_MAX_GROUPS = 1024;
+static_assert(CL_MAX_GROUPS <= CL_THREADS, "thread g finishes group g");
 constexpr int SS_THREADS = 256;
 constexpr int SS_ELEMS = 8;  // elements per thread
 
-// Workgroup sum in a fixed order (a butterfly within each wave, then the
-// wave sums in wave order), so that runs are bitwise reproducible.  The
-// result is valid in every thread.
+// Workgroup sum in a fixed order (a fixed tree within each wave by DPP and
+// lane reads, then the wave sums in wave order), so that runs are bitwise
+// reproducible.  The result is valid in every thread.
 __device__ __forceinline__ double block_sum_fixed(double v, double* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  v = rows_sum4(row_sum16(v));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) red[wave] = v;
   __syncthreads();
@@ -47,8 +48,10 @@ __device__ __forceinline__ double finalize_scale(double ratio, double rel, doubl
 }
 
 // One workgroup per example.  Group g owns slots [gstart[g], gstart[g+1]).
-// Each thread keeps four loads in flight (the sum of an example's partials
-// is bound by load latency, not bandwidth).
+// The sum of an example's partials (a few hundred KB on Llama-shaped
+// models) is bound by what one CU can have in flight, so each thread issues
+// CL_DEPTH 16-byte loads at once; the order of additions is fixed (it does
+// not depend on which loads are masked), so runs are bitwise reproducible.
 __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
     const double* __restrict__ part, int64_t n_slots, int n_ex, const int64_t* __restrict__ gstart, int n_groups,
     const double* __restrict__ thr, double eff_thr, int mode, double gamma, int n_cls,
@@ -59,20 +62,49 @@ __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
   const int t = threadIdx.x;
   __shared__ double red[CL_THREADS / 64];
   __shared__ double gsq[CL_MAX_GROUPS];
+  __shared__ double sguard[16];
+  __shared__ int scls[8];
   const double* row = part + (int64_t)ex * n_slots;
+  // The inputs of the scale arithmetic are read now, so that their load
+  // latency overlaps the partials' instead of following the reduction
+  // (n_groups <= CL_THREADS: thread g finishes group g; the barriers of the
+  // reduction publish sguard and scls).
+  const double thr_t = t < n_groups ? thr[t] : 0.0;
+  if (t < 2 * n_cls) sguard[t] = guard[t];
+  if (t < n_cls) scls[t] = cls_dtype[t];
 
   for (int g = 0; g < n_groups; ++g) {
     const int64_t hi = gstart[g + 1];
-    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-    int64_t s = gstart[g] + t;
-    for (; s + 3 * CL_THREADS < hi; s += 4 * CL_THREADS) {
-      a0 += row[s];
-      a1 += row[s + CL_THREADS];
-      a2 += row[s + 2 * CL_THREADS];
-      a3 += row[s + 3 * CL_THREADS];
+    double a[CL_DEPTH];
+#pragma unroll
+    for (int q = 0; q < CL_DEPTH; ++q) a[q] = 0.0;
+    // Slots are read in 16-byte pairs from the first 16-byte aligned one
+    // (a leading and a trailing odd slot go to thread 0), and every load of
+    // a round is issued before the first add (masked past the group's end).
+    const int64_t lo = gstart[g];
+    int64_t la = lo + (((int64_t)ex * n_slots + lo) & 1);
+    la = la < hi ? la : hi;
+    const int64_t npair = (hi - la) >> 1;
+    if (t == 0) {
+      if (lo < la) a[0] += row[lo];
+      if (la + 2 * npair < hi) a[1] += row[hi - 1];
     }
-    for (; s < hi; s += CL_THREADS) a0 += row[s];
-    const double tot = block_sum_fixed((a0 + a1) + (a2 + a3), red);
+    const double2* pr = (const double2*)(row + la);
+    for (int64_t q0 = t; q0 < npair; q0 += CL_DEPTH * CL_THREADS) {
+      double2 v[CL_DEPTH];
+#pragma unroll
+      for (int q = 0; q < CL_DEPTH; ++q)
+        v[q] = q0 + q * CL_THREADS < npair ? pr[q0 + q * CL_THREADS] : double2{0.0, 0.0};
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < CL_DEPTH; ++q) a[q] = (a[q] + v[q].x) + v[q].y;
+    }
+    // Pairwise over the accumulators, in a fixed order.
+#pragma unroll
+    for (int w = CL_DEPTH / 2; w > 0; w >>= 1)
+#pragma unroll
+      for (int q = 0; q < w; ++q) a[q] = a[2 * q] + a[2 * q + 1];
+    const double tot = block_sum_fixed(a[0], red);
     if (t == 0) gsq[g] = tot;
   }
   __syncthreads();
@@ -85,15 +117,16 @@ __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
     norm_out[ex] = normf;
     if (clip_total_out) clip_total_out[ex] = normf > (float)eff_thr ? 1 : 0;
   }
-  for (int g = t; g < n_groups; g += CL_THREADS) {
+  if (t < n_groups) {
+    const int g = t;
     const double gn = sqrt(gsq[g]);
     if (gnorm_out) gnorm_out[(int64_t)g * n_ex + ex] = (float)gn;
-    if (clip_out) clip_out[(int64_t)g * n_ex + ex] = (float)gn > (float)thr[g] ? 1 : 0;
-    const double c = thr[g] > 0.0 ? thr[g] : 0.0;
+    if (clip_out) clip_out[(int64_t)g * n_ex + ex] = (float)gn > (float)thr_t ? 1 : 0;
+    const double c = thr_t > 0.0 ? thr_t : 0.0;
     const double ratio = mode == ODP_CLIP_AUTOS ? c / (gn + gamma) : c / gn;
     for (int k = 0; k < n_cls; ++k)
       scale_out[((int64_t)k * n_groups + g) * n_ex + ex] =
-          finalize_scale(ratio, guard[2 * k], guard[2 * k + 1], mode == ODP_CLIP_FIXED, cls_dtype[k]);
+          finalize_scale(ratio, sguard[2 * k], sguard[2 * k + 1], mode == ODP_CLIP_FIXED, scls[k]);
   }
 }
 

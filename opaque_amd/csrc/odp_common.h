@@ -101,3 +101,34 @@ __device__ __forceinline__ float odp_round_to(float v, int dtype) {
 __host__ __device__ __forceinline__ int odp_dtype_size(int dtype) {
   return dtype == ODP_DTYPE_F64 ? 8 : dtype == ODP_DTYPE_F32 ? 4 : 2;
 }
+
+// fp64 sums across lanes on the VALU (DPP and readlane instead of LDS lane
+// permutes, which would compete with the kernels' LDS reads).  row_sum16
+// adds exactly what an xor 1, 2, 4, 8 butterfly adds, in the same order
+// (quad pairs, quads, half rows by half-row mirror, rows by row mirror), so
+// every lane of a row gets the same value; rows_sum4 returns
+// (R0 + R1) + (R2 + R3) of the four rows' values (lanes 0, 16, 32, 48), as
+// an xor 16, 32 butterfly does in lane 0.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double row_sum16(double v) {
+  v += dpp_f64<0xB1>(v);   // quad_perm 1,0,3,2
+  v += dpp_f64<0x4E>(v);   // quad_perm 2,3,0,1
+  v += dpp_f64<0x141>(v);  // row_half_mirror
+  v += dpp_f64<0x140>(v);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ double lane_f64(double v, int l) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double rows_sum4(double v) {
+  return (lane_f64(v, 0) + lane_f64(v, 16)) + (lane_f64(v, 32) + lane_f64(v, 48));
+}

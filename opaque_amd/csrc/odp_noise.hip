@@ -64,13 +64,28 @@ __device__ __forceinline__ u32x4s philox4x32_10(uint32_t c0, uint32_t c1, uint32
   return u32x4s{c0, c1, c2, c3};
 }
 
+// Constants the inverse CDF needs in vector registers.  A gfx9 VALU
+// instruction takes at most one literal, so left to itself the compiler
+// re-materialises these with a move for every element; made opaque here,
+// they are moved once per thread (the noise kernel is bound by its VALU
+// instruction count).
+struct IcdfRegs {
+  float c8;       // leading coefficient of the centre polynomial
+  uint32_t kmax;  // largest 24-bit uniform after the clamp
+};
+__device__ __forceinline__ IcdfRegs icdf_regs() {
+  IcdfRegs R{ICDF_CENTRE[8], 0xFFFFFEu};
+  __asm__ volatile("" : "+v"(R.c8), "+v"(R.kmax));
+  return R;
+}
+
 // sqrt(2) erfinv(x) from xf = x 2^23 and L = log2(1 - x^2).
-__device__ __forceinline__ float icdf_poly(float xf, float L) {
+__device__ __forceinline__ float icdf_poly(float xf, float L, const IcdfRegs& R) {
   float p;
   if (L >= ICDF_L_SPLIT) {
-    p = ICDF_CENTRE[8];
+    p = __builtin_fmaf(R.c8, L, ICDF_CENTRE[7]);
 #pragma unroll
-    for (int i = 7; i >= 0; --i) p = __builtin_fmaf(p, L, ICDF_CENTRE[i]);
+    for (int i = 6; i >= 0; --i) p = __builtin_fmaf(p, L, ICDF_CENTRE[i]);
   } else {
     const float t = __builtin_amdgcn_sqrtf(-L) - ICDF_TAIL_MID;
     p = ICDF_TAIL[7];
@@ -84,18 +99,20 @@ __device__ __forceinline__ float icdf_poly(float xf, float L) {
 // 2^-23, float32's machine epsilon), i.e. k clamped to [2, 2^24 - 2].  x =
 // (k - 2^23) 2^-23 and 1 - x^2 (one rounding, by FMA) are exact inputs to
 // the log.
-__device__ __forceinline__ float icdf24(uint32_t k) {
-  k = min(max(k, 2u), 0xFFFFFEu);
+__device__ __forceinline__ float icdf24(uint32_t k, const IcdfRegs& R) {
+  // k = min(max(k, 2), kmax) in one instruction (the compiler splits the
+  // clamp in two once kmax is a register).
+  __asm__("v_med3_u32 %0, %1, 2, %2" : "=v"(k) : "v"(k), "v"(R.kmax));
   const float xf = (float)((int32_t)k - (1 << 23));
   const float r = __builtin_fmaf(-xf, xf * 0x1p-46f, 1.0f);
-  return icdf_poly(xf, __builtin_amdgcn_logf(r));
+  return icdf_poly(xf, __builtin_amdgcn_logf(r), R);
 }
 
 // Same for a float32 u already clamped to [eps, 1 - eps] (bounded mode).
-__device__ __forceinline__ float icdf_u(float u) {
+__device__ __forceinline__ float icdf_u(float u, const IcdfRegs& R) {
   const float x = __builtin_fmaf(2.0f, u, -1.0f);
   const float r = __builtin_fmaf(-x, x, 1.0f);
-  return icdf_poly(x * 0x1p23f, __builtin_amdgcn_logf(r));
+  return icdf_poly(x * 0x1p23f, __builtin_amdgcn_logf(r), R);
 }
 
 // The 16 24-bit uniforms of thread G from its 12 Philox words: element j
@@ -309,9 +326,10 @@ __global__ __launch_bounds__(NZ_THREADS) void k_gaussian_noise(const int64_t* __
   uint32_t k[NZ_GROUP];
   uniforms24(G, tag, k0, k1, k);
   const float sd = (float)P.sigma;
+  const IcdfRegs R = icdf_regs();
   if (!BOUNDED) {
 #pragma unroll
-    for (int j = 0; j < NZ_GROUP; ++j) v[j] = __builtin_fmaf(sd, icdf24(k[j]), v[j]);
+    for (int j = 0; j < NZ_GROUP; ++j) v[j] = __builtin_fmaf(sd, icdf24(k[j], R), v[j]);
   } else {
     // Gaussian renormalised over [lo, hi] by the inverse CDF, then clamped
     // (bounded Gaussian mechanism, _gaussian.py:268-276).
@@ -325,7 +343,7 @@ __global__ __launch_bounds__(NZ_THREADS) void k_gaussian_noise(const int64_t* __
       const float b = 0.5f * (1.0f + erff(__fdiv_rn(zb, sqrt2)));
       float u = __fadd_rn(a, __fmul_rn((float)k[j] * 0x1p-24f, __fsub_rn(b, a)));
       u = fminf(fmaxf(u, eps), 1.0f - eps);
-      v[j] = fminf(fmaxf(__builtin_fmaf(sd, icdf_u(u), c), lo), hi);
+      v[j] = fminf(fmaxf(__builtin_fmaf(sd, icdf_u(u, R), c), lo), hi);
     }
   }
   store16(P.out, i0, P.n, P.odt, vout, v);
@@ -346,7 +364,7 @@ __global__ void k_philox_words(uint64_t ctr0, uint32_t c2, uint32_t c3, uint32_t
 __global__ void k_noise_icdf(uint32_t k0, int64_t n, float* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  out[i] = icdf24((k0 + (uint32_t)i) & 0xFFFFFFu);
+  out[i] = icdf24((k0 + (uint32_t)i) & 0xFFFFFFu, icdf_regs());
 }
 
 }  // namespace
