@@ -107,9 +107,9 @@ int odp_pack_factors(odp_stream_t stream, const int64_t* problems, const int32_t
 /* ---- odp_project: Q^T[k][row] = sum_j P[row][j] * W[k][j] --------------
  * The LoRA rank-space projections U = G B^T and V = X A for rows
  * [0, n_rows); rows outside the problem's segments get 0.  Only columns
- * k < r are written.  bf16 P writes two bf16 planes, hi at ODP_PJ_Q and
- * lo at ODP_PJ_QLO (hi + lo carries ~16 mantissa bits of the fp32 sum),
- * each [k][ldq]; f32 P writes one f32 plane at ODP_PJ_Q.                  */
+ * k < r are written, as one plane [k][ldq] at ODP_PJ_Q in P's dtype (bf16
+ * P: the fp32 sums rounded to bf16, as the reference's bf16 X A and
+ * G B^T are).                                                           */
 enum {
   ODP_PJ_P = 0,      /* address of P, row-major, ld = ODP_PJ_LDP elements     */
   ODP_PJ_LDP = 1,
@@ -121,7 +121,6 @@ enum {
   ODP_PJ_NROWS = 7,
   ODP_PJ_SEG_FIRST = 8,
   ODP_PJ_NSEG = 9,
-  ODP_PJ_QLO = 10,   /* address of the lo plane (bf16 only)                   */
   ODP_PJ_FIELDS = 12
 };
 int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r);
@@ -152,7 +151,6 @@ enum {
                          use the fp32 values), [11+3l] col0 | rank << 16 |
                          pe_bf16 << 32, [12+3l] slot_base;
                          leaves sorted by col0                               */
-  ODP_FT_QLO = 22,    /* lo plane of Q (bf16 only)                           */
   ODP_FT_FIELDS = 24,
   ODP_FT_WAVE_SLOTS = 4 /* partial slots per leaf and tile                   */
 };
@@ -171,8 +169,8 @@ int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
  * (opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176):
  * grad_out_Bt = grad_out @ B^T and dB[i] = s * (X[i] A)^T grad_out[i].
  * One bf16 pass over P = G computes, per segment, what odp_project (U =
- * G B^T into ODP_FP_U / ODP_FP_ULO) and odp_seg_factor (pe rows and norm
- * partials of the dB leaf, Q = the V planes) would, reading G once.
+ * G B^T into the plane at ODP_FP_U) and odp_seg_factor (pe rows and norm
+ * partials of the dB leaf, Q = the V plane) would, reading G once.
  * A problem is an odp_seg_factor row with NLEAF == 1 and r <= 16 plus the
  * fields below; one workgroup per segment (total blocks = sum of n_seg).
  * U is written for the rows of the segments only, as odp_project's planes
@@ -181,8 +179,7 @@ int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
  * odp_seg_factor).  Partial slots and pe layout are odp_seg_factor's.    */
 enum {
   ODP_FP_W = 13,    /* address of B [r][M] bf16 row-major                      */
-  ODP_FP_U = 14,    /* hi plane of U [k][ldq]                                  */
-  ODP_FP_ULO = 15   /* lo plane of U                                           */
+  ODP_FP_U = 14     /* plane of U [k][ldq], bf16                              */
 };
 int64_t odp_factor_project_max_len(void);
 int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,

@@ -26,13 +26,12 @@ CLIP_AUTOS = 1
 PF_SRC, PF_LD0, PF_LD1, PF_DTYPES, PF_DIN, PF_R, PF_DST = range(7)
 PF_FIELDS = 8
 PJ_FIELDS = 12
-PJ_P, PJ_LDP, PJ_D, PJ_W, PJ_R, PJ_Q, PJ_LDQ, PJ_NROWS, PJ_SEG_FIRST, PJ_NSEG, PJ_QLO = range(11)
+PJ_P, PJ_LDP, PJ_D, PJ_W, PJ_R, PJ_Q, PJ_LDQ, PJ_NROWS, PJ_SEG_FIRST, PJ_NSEG = range(10)
 FT_FIELDS = 24
 FT_P, FT_LDP, FT_M, FT_Q, FT_LDQ, FT_R, FT_SEG_FIRST, FT_NSEG, FT_SCALING, FT_NLEAF = range(10)
 FT_LEAF0 = 10
-FT_QLO = 22
 FT_WAVE_SLOTS = 4  # partial slots per LoRA leaf and M-tile
-FP_W, FP_U, FP_ULO = 13, 14, 15
+FP_W, FP_U = 13, 14
 SS_FIELDS = 8
 SS_PE, SS_M, SS_RANK, SS_SEG_FIRST, SS_NSEG, SS_OUT, SS_FLAGS, SS_OUT2 = range(8)
 NZ_FIELDS = 8

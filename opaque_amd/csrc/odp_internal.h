@@ -3,7 +3,7 @@
 
 #include "odp_common.h"
 
-#define ODP_ABI_VERSION 2
+#define ODP_ABI_VERSION 3
 
 // fp64 partials of the static scratch behind odp_clip_materialized_noalloc
 // (8 MiB per GPU).

@@ -113,7 +113,6 @@ __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const 
   const uint16_t* W = (const uint16_t*)f[ODP_PJ_W];
   const int r = (int)f[ODP_PJ_R];
   uint16_t* Q = (uint16_t*)f[ODP_PJ_Q];
-  uint16_t* Qlo = (uint16_t*)f[ODP_PJ_QLO];
   const int64_t ldq = f[ODP_PJ_LDQ], n_rows = f[ODP_PJ_NROWS];
   const int seg_first = (int)f[ODP_PJ_SEG_FIRST], n_seg = (int)f[ODP_PJ_NSEG];
 
@@ -245,8 +244,10 @@ __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const 
 
   // lane holds D[4*(lane>>4) + i][lane & 15] of each 16x16 block: 4
   // consecutive rows of one rank column, which are 4 consecutive entries of
-  // that column's plane row, stored as one 8-byte piece per plane (2-byte
-  // stores cost these kernels 11-17 % of their time).  rb is a multiple of
+  // that column's plane row, rounded to bf16 (the rank-space products of the
+  // reference's per-sample rule, X A and G B^T, are bf16 tensors) and stored
+  // as one 8-byte piece (2-byte stores cost these kernels several % of
+  // their time).  rb is a multiple of
   // 4 and ldq (a multiple of 8) exceeds n_rows by at least 32, so a group
   // that runs past n_rows stays inside the plane row; its rows past n_rows
   // hold zero P rows (rowok), and no kernel reads plane entries of rows
@@ -258,14 +259,10 @@ __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const 
     for (int kb = 0; kb < NKB; ++kb) {
       const int col = kb * 16 + (lane & 15);
       if (col < r && rb < n_rows) {
-        uint32_t h[4], l[4];
+        uint32_t h[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          h[i] = odp_f2bf(acc[b][kb][i]);
-          l[i] = odp_f2bf(acc[b][kb][i] - odp_bf2f((uint16_t)h[i]));
-        }
+        for (int i = 0; i < 4; ++i) h[i] = odp_f2bf(acc[b][kb][i]);
         odp_gstore((u32x2_t*)(Q + (int64_t)col * ldq + rb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
-        odp_gstore((u32x2_t*)(Qlo + (int64_t)col * ldq + rb), u32x2_t{l[0] | (l[1] << 16), l[2] | (l[3] << 16)});
       }
     }
   }
@@ -485,7 +482,7 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
 // ---------------------------------------------------------------------------
 // Factor gradients, bf16 P: MFMA 16x16x32 with K = 32 tokens per step.  Per
 // step the workgroup stages the P tile [32 tokens x 128 m] and the Q^T tile
-// (hi and lo planes, [16*NKB x 32 tokens]) through LDS; each lane gathers its
+// ([16*NKB x 32 tokens]) through LDS; each lane gathers its
 // 8 consecutive tokens of one column for the B operand.  Loads run two steps
 // ahead of the compute; the token mask is applied when a stage is written to
 // LDS (never right after its load, which would stall the prefetch).
@@ -505,10 +502,10 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
                                                      double* __restrict__ part, int64_t part_stride) {
   constexpr int NJ = ft_nj(NKB), MT = 64 * NJ, PP = MT;  // unpadded, XOR-swizzled rows
   constexpr int QP = FT_T + 8, QROWS = 16 * NKB;
-  constexpr int PTILE = FT_T * PP, STAGE = PTILE + 2 * QROWS * QP;
-  constexpr int NPP = NJ * FT_T / 32;                 // P pieces per thread per step
-  constexpr int QPC = FT_T / 8;                       // Q pieces per row per step
-  constexpr int NQP = (2 * QPC * QROWS + 255) / 256;  // Q pieces per thread per step
+  constexpr int PTILE = FT_T * PP, STAGE = PTILE + QROWS * QP;
+  constexpr int NPP = NJ * FT_T / 32;             // P pieces per thread per step
+  constexpr int QPC = FT_T / 8;                   // Q pieces per row per step
+  constexpr int NQP = (QPC * QROWS + 255) / 256;  // Q pieces per thread per step
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -516,7 +513,6 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
   const uint16_t* P = (const uint16_t*)f[ODP_FT_P];
   const int64_t ldp = f[ODP_FT_LDP], M = f[ODP_FT_M];
   const uint16_t* Q = (const uint16_t*)f[ODP_FT_Q];
-  const uint16_t* Qlo = (const uint16_t*)f[ODP_FT_QLO];
   const int64_t ldq = f[ODP_FT_LDQ];
   const int r = (int)f[ODP_FT_R];
   const int seg_first = (int)f[ODP_FT_SEG_FIRST];
@@ -551,10 +547,9 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
     }
 #pragma unroll
     for (int ps = 0; ps < NQP; ++ps) {
-      const int id = (tid + 256 * ps) % (2 * QPC * QROWS);
-      const int plane = id / (QPC * QROWS), rem = id % (QPC * QROWS);
-      const int row = rem / QPC, pc = rem % QPC;
-      S.q[ps] = ld16((plane ? Qlo : Q) + (int64_t)row * ldq + t0 + 8 * pc);
+      const int id = (tid + 256 * ps) % (QPC * QROWS);
+      const int row = id / QPC, pc = id % QPC;
+      S.q[ps] = ld16(Q + (int64_t)row * ldq + t0 + 8 * pc);
     }
   };
   auto store = [&](int b, int64_t c, const Stage& S) {
@@ -572,9 +567,8 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
 #pragma unroll
     for (int ps = 0; ps < NQP; ++ps) {
       const int id = tid + 256 * ps;
-      if (id < 2 * QPC * QROWS) {
-        const int plane = id / (QPC * QROWS), rem = id % (QPC * QROWS);
-        const int row = rem / QPC, pc = rem % QPC;
+      if (id < QPC * QROWS) {
+        const int row = id / QPC, pc = id % QPC;
         const int64_t tq = t0 + 8 * pc;
         u32x4_t v = S.q[ps];
         // Tokens outside [rs, t_hi) contribute nothing.
@@ -584,7 +578,7 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
           v[w] &= ((ta >= rs && ta < t_hi) ? 0x0000ffffu : 0u) |
                   ((ta + 1 >= rs && ta + 1 < t_hi) ? 0xffff0000u : 0u);
         }
-        *(u32x4_t*)&st[PTILE + (plane * QROWS + row) * QP + 8 * pc] = v;
+        *(u32x4_t*)&st[PTILE + row * QP + 8 * pc] = v;
       }
     }
   };
@@ -614,11 +608,8 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
       for (int kb = 0; kb < NKB; ++kb) {
         const int row = kb * 16 + (lane & 15);
         const int tc = 32 * u + 8 * (lane >> 4);
-        const u32x4_t hv = *(const u32x4_t*)&st[PTILE + row * QP + tc];
-        const u32x4_t lv = *(const u32x4_t*)&st[PTILE + (QROWS + row) * QP + tc];
-        acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hv), bop,
-                                                             acc[j][kb], 0, 0, 0);
-        acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lv), bop,
+        const u32x4_t qv = *(const u32x4_t*)&st[PTILE + row * QP + tc];
+        acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qv), bop,
                                                              acc[j][kb], 0, 0, 0);
       }
     }
@@ -668,7 +659,7 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
 constexpr int FP_T = 64, FP_MT = 256, FP_STEPS = 17;
 constexpr uint32_t ODP_BUFFER_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA buffer resource)
 // G's loads are marked non-temporal (cache policy bit NT): G streams
-// through once, and the hint keeps it from evicting the segment's V planes,
+// through once, and the hint keeps it from evicting the segment's V plane,
 // which every chunk reads again (4.5 % faster on C3 shapes).
 constexpr int FP_G_NT = 2;
 
@@ -681,9 +672,9 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
                                                                 int64_t part_stride) {
   constexpr int NJ = FP_MT / 64, PP = FP_MT;  // unpadded, XOR-swizzled G rows
   constexpr int QP = FP_T + 8, QROWS = 16;
-  constexpr int PTILE = FP_T * PP, STAGE = PTILE + 2 * QROWS * QP;
+  constexpr int PTILE = FP_T * PP, STAGE = PTILE + QROWS * QP;
   constexpr int QPC = FP_T / 8;                // V pieces per row per step
-  static_assert(2 * QPC * QROWS == 256, "one V piece per thread");
+  static_assert(QPC * QROWS == 128, "one V piece per thread of waves 0 and 1");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -715,11 +706,13 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   // 16 wave + 2 i + (l >> 5), so it fetches the logical slot that the XOR
   // swizzle maps there.
   const int gh = lane >> 5, gslot = lane & 31;
-  // Thread's V piece: plane, rank row and 8 tokens of a step.
-  const int qplane = tid / (QPC * QROWS), qrow = (tid % (QPC * QROWS)) / QPC, qpc = tid % QPC;
-  const uint16_t* qsrc =
-      (const uint16_t*)f[qplane ? ODP_FT_QLO : ODP_FT_Q] + (int64_t)qrow * ldq;
-  uint16_t* const qdst_base = lds + PTILE + (qplane * QROWS + qrow) * QP + 8 * qpc;
+  // Waves 0 and 1 load V, one piece per thread: rank row and 8 tokens of a
+  // step (`vown` is wave-uniform, so the V loads and stores are scalar
+  // branches and waves 2 and 3 issue none).
+  const bool vown = __builtin_amdgcn_readfirstlane(wave) < 2;
+  const int qrow = (tid % (QPC * QROWS)) / QPC, qpc = tid % QPC;
+  const uint16_t* qsrc = (const uint16_t*)f[ODP_FT_Q] + (int64_t)qrow * ldq;
+  uint16_t* const qdst_base = lds + PTILE + qrow * QP + 8 * qpc;
 
   auto load = [&](uint16_t* stage, int32_t t0, int32_t m_base, u32x4_t& qv) {
     uint16_t* dst = stage + 16 * wave * PP;
@@ -732,10 +725,11 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       __builtin_amdgcn_raw_ptr_buffer_load_lds(grsrc, (ODP_LDS void*)(dst + 2 * i * PP), 16, off, 0, 0, FP_G_NT);
     }
     const int32_t tq = t0 + 8 * qpc;
-    qv = ld16(qsrc + (tq < t_hi ? tq : t_lo));
+    if (vown) qv = ld16(qsrc + (tq < t_hi ? tq : t_lo));
   };
   // V's tokens outside [rs, t_hi) are zeroed when its piece is written.
   auto store_q = [&](int b, int32_t t0, u32x4_t v) {
+    if (!vown) return;
     const int32_t tq = t0 + 8 * qpc;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -875,12 +869,11 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
         flush();
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-      // dB rows: B operand = G columns by transposing reads, A = V hi / lo.
+      // dB rows: B operand = G columns by transposing reads, A = V.
 #pragma unroll
       for (int u = 0; u < FP_T / 32; ++u) {
         const int tc = 32 * u + 8 * (lane >> 4);
-        const u32x4_t hv = *(const u32x4_t*)&sp[PTILE + (lane & 15) * QP + tc];
-        const u32x4_t lv = *(const u32x4_t*)&sp[PTILE + (QROWS + (lane & 15)) * QP + tc];
+        const u32x4_t vv = *(const u32x4_t*)&sp[PTILE + (lane & 15) * QP + tc];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const int m0 = (NJ * wave + j) * 16, cc = lane & 15;
@@ -889,9 +882,7 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
           const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
           const v4i16_t tt[2] = {t0, t1};
           const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
-          acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hv), bop,
-                                                              acc[j][0], 0, 0, 0);
-          acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lv), bop,
+          acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vv), bop,
                                                               acc[j][0], 0, 0, 0);
         }
       }
@@ -941,35 +932,26 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
 
   // U: lane holds rows 4 (lane >> 4) + i, column lane & 15 of each step's
   // 16 x 16 block: 4 consecutive entries of the column's plane row (tb is a
-  // multiple of 4), stored as one 8-byte piece per plane when all four
-  // tokens are the segment's; tokens outside the segment belong to other
-  // workgroups, so a group that straddles a segment end is stored entry by
-  // entry.
+  // multiple of 4), stored as one 8-byte piece when all four tokens are the
+  // segment's; tokens outside the segment belong to other workgroups, so a
+  // group that straddles a segment end is stored entry by entry.
   const int col = lane & 15;
   if (col < r) {
-    uint16_t* uh = (uint16_t*)f[ODP_FP_U] + (int64_t)col * ldq;
-    uint16_t* ul = (uint16_t*)f[ODP_FP_ULO] + (int64_t)col * ldq;
+    uint16_t* uq = (uint16_t*)f[ODP_FP_U] + (int64_t)col * ldq;
 #pragma unroll
     for (int st = 0; st < FP_STEPS; ++st) {
       if (st < nsteps) {
         const int32_t tb = t_lo + st * FP_T + 16 * wave + 4 * (lane >> 4);
-        uint32_t h[4], l[4];
+        uint32_t h[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          h[i] = odp_f2bf(acc_u[st][i]);
-          l[i] = odp_f2bf(acc_u[st][i] - odp_bf2f((uint16_t)h[i]));
-        }
+        for (int i = 0; i < 4; ++i) h[i] = odp_f2bf(acc_u[st][i]);
         if (tb >= rs && tb + 3 < t_hi) {
-          odp_gstore((u32x2_t*)(uh + tb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
-          odp_gstore((u32x2_t*)(ul + tb), u32x2_t{l[0] | (l[1] << 16), l[2] | (l[3] << 16)});
+          odp_gstore((u32x2_t*)(uq + tb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int32_t t = tb + i;
-            if (t >= rs && t < t_hi) {
-              odp_gstore(uh + t, (uint16_t)h[i]);
-              odp_gstore(ul + t, (uint16_t)l[i]);
-            }
+            if (t >= rs && t < t_hi) odp_gstore(uq + t, (uint16_t)h[i]);
           }
         }
       }

@@ -735,7 +735,7 @@ class GhostPlan:
             dt = ch[0].x.dtype
             rtot = sum(s.A.shape[1] for s in ch)
             rows_alloc = (rtot + 15) // 16 * 16 + 16
-            planes = 2 if dt == torch.bfloat16 else 1
+            planes = 1  # one plane in the activation dtype (bf16: the reference's rounding of X A, G B^T)
             ldq = (reg.view(ch[0].segments).n_rows + 32 + 7) // 8 * 8
             per = planes * rows_alloc * ldq
             base = q_need.get(dt, 0)
@@ -756,12 +756,11 @@ class GhostPlan:
         for ci, (ch, (dt, rtot, rows_alloc, planes, vbase, ubase, ldq)) in enumerate(zip(chunks, chunk_layout)):
             qb = self.qbuf[dt]
             es = elem[dt]
-            plane = rows_alloc * ldq
             v = reg.view(ch[0].segments)
             n_rows, n_seg, valid, sf = v.n_rows, v.n_seg, v.valid, v.first
 
-            def qaddr(base: int, row: int, lo: bool, qb=qb, plane=plane, ldq=ldq, es=es) -> int:
-                return qb.data_ptr() + (base + (plane if lo else 0) + row * ldq) * es
+            def qaddr(base: int, row: int, qb=qb, ldq=ldq, es=es) -> int:
+                return qb.data_ptr() + (base + row * ldq) * es
 
             x = ext[("lx", ci)]
             d_in = x.shape[1]
@@ -775,7 +774,7 @@ class GhostPlan:
                 {
                     N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
                     N.PJ_W: wx.data_ptr(), N.PJ_R: rtot,
-                    N.PJ_Q: qaddr(vbase, 0, False), N.PJ_QLO: qaddr(vbase, 0, True),
+                    N.PJ_Q: qaddr(vbase, 0),
                     N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                 },
                 lib.odp_project_blocks(dtype_code(dt), n_rows, rtot),
@@ -795,7 +794,7 @@ class GhostPlan:
                 if s.b_leaf is not None:
                     frow = {
                         N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
-                        N.FT_Q: qaddr(vbase, c0, False), N.FT_QLO: qaddr(vbase, c0, True),
+                        N.FT_Q: qaddr(vbase, c0),
                         N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
                         N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
                         N.FT_LEAF0: pe_addr(s.b_leaf),
@@ -807,8 +806,7 @@ class GhostPlan:
                     # segment: a row per segment, so that the launch can run
                     # the longest first (the segment's pe rows start at its
                     # own offset).
-                    frow.update({N.FP_W: wb.data_ptr(), N.FP_U: qaddr(ubase, c0, False),
-                                 N.FP_ULO: qaddr(ubase, c0, True), N.FT_NSEG: 1})
+                    frow.update({N.FP_W: wb.data_ptr(), N.FP_U: qaddr(ubase, c0), N.FT_NSEG: 1})
                     pe0 = pe_addr(s.b_leaf)
                     pe_es = self.pe[pe_dt[s.b_leaf]].element_size()
                     for j, ln in enumerate(v.segs.lengths):
@@ -827,7 +825,7 @@ class GhostPlan:
                     {
                         N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
                         N.PJ_W: wb.data_ptr(), N.PJ_R: r,
-                        N.PJ_Q: qaddr(ubase, c0, False), N.PJ_QLO: qaddr(ubase, c0, True),
+                        N.PJ_Q: qaddr(ubase, c0),
                         N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                     },
                     lib.odp_project_blocks(dtype_code(dt), n_rows, r),
@@ -1405,7 +1403,7 @@ class GhostPlan:
             {
                 N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
                 N.PJ_W: wb.data_ptr(), N.PJ_R: r,
-                N.PJ_Q: qaddr(ubase, 0, False), N.PJ_QLO: qaddr(ubase, 0, True),
+                N.PJ_Q: qaddr(ubase, 0),
                 N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
             },
             lib.odp_project_blocks(dtype_code(dt), n_rows, r),
@@ -1418,12 +1416,12 @@ class GhostPlan:
         pe_es = self.pe[dt].element_size()
         row = {
             N.FT_P: x.data_ptr(), N.FT_LDP: x.stride(0), N.FT_M: d_in,
-            N.FT_Q: qaddr(ubase, 0, False), N.FT_QLO: qaddr(ubase, 0, True),
+            N.FT_Q: qaddr(ubase, 0),
             N.FT_LDQ: ldq, N.FT_R: r, N.FT_NSEG: 1,
             N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
             N.FT_LEAF0 + 1: 0 | (r << 16) | self._pe_bits(s.a_leaf),
             N.FT_LEAF0 + 2: slot_base[s.a_leaf],
-            N.FP_W: wx.data_ptr(), N.FP_U: qaddr(vbase, 0, False), N.FP_ULO: qaddr(vbase, 0, True),
+            N.FP_W: wx.data_ptr(), N.FP_U: qaddr(vbase, 0),
         }
         for j, ln in enumerate(v.segs.lengths):
             rj = dict(row)
@@ -1437,7 +1435,7 @@ class GhostPlan:
             tab(ft, dt, r, N.FT_FIELDS).add(
                 {
                     N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
-                    N.FT_Q: qaddr(vbase, 0, False), N.FT_QLO: qaddr(vbase, 0, True),
+                    N.FT_Q: qaddr(vbase, 0),
                     N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
                     N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
                     N.FT_LEAF0: self._pe_addr(s.b_leaf),
@@ -1457,7 +1455,7 @@ class GhostPlan:
     def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, seg_first, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
             N.FT_P: x.data_ptr(), N.FT_LDP: x.stride(0), N.FT_M: d_in,
-            N.FT_Q: qaddr(ubase, col0, False), N.FT_QLO: qaddr(ubase, col0, True),
+            N.FT_Q: qaddr(ubase, col0),
             N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: seg_first, N.FT_NSEG: n_seg,
             N.FT_SCALING: _f64_bits(scaling), N.FT_NLEAF: len(leaves),
         }

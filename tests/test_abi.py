@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_buffer(lib):
-    assert lib.odp_abi_version() == 2
+    assert lib.odp_abi_version() == 3
     assert isinstance(N.last_error(), str)
 
 
@@ -60,10 +60,8 @@ def test_field_indices_match_header():
     assert value("ODP_PF_FIELDS") == N.PF_FIELDS
     assert value("ODP_PF_DST") == N.PF_DST
     assert value("ODP_PJ_FIELDS") == N.PJ_FIELDS
-    assert value("ODP_PJ_QLO") == N.PJ_QLO
     assert value("ODP_FT_FIELDS") == N.FT_FIELDS
     assert value("ODP_FT_LEAF0") == N.FT_LEAF0
-    assert value("ODP_FT_QLO") == N.FT_QLO
     assert value("ODP_FT_WAVE_SLOTS") == N.FT_WAVE_SLOTS
     assert value("ODP_SS_FIELDS") == N.SS_FIELDS
     assert value("ODP_SQ_FIELDS") == N.SQ_FIELDS
