@@ -154,51 +154,19 @@ def test_clip_factor_argument_checks(lib):
     assert call(n_ex=0) == N.ODP_OK  # an empty batch launches nothing
 
 
-def _status(lib, name, *args):
-    rc = getattr(lib, name)(*args)
-    return rc, N.last_error()
 
-
-def test_error_contract(lib):
-    """Bad arguments return ODP_ERR_* and leave a message naming the entry point
-    and the argument; these checks run before anything reaches the device."""
-    null = None
-    # odp_project: dtype, nkb and table checks
-    rc, msg = _status(lib, "odp_project", null, 99, null, null, 0, 0, null, null, 1)
-    assert rc == N.ERR_UNSUPPORTED and "odp_project" in msg and "dtype 99" in msg, msg
-    rc, msg = _status(lib, "odp_project", null, N.DTYPE_BF16, null, null, 0, 0, null, null, 5)
-    assert rc == N.ERR_UNSUPPORTED and "nkb=5" in msg, msg
-    rc, msg = _status(lib, "odp_project", null, N.DTYPE_BF16, null, null, 1, 4, null, null, 1)
-    assert rc == N.ERR_INVALID_ARGUMENT and "null problem table" in msg, msg
-    rc, msg = _status(lib, "odp_project", null, N.DTYPE_BF16, null, null, 0, 3, null, null, 1)
-    assert rc == N.ERR_INVALID_ARGUMENT and "total_blocks must be 0" in msg, msg
-    rc, msg = _status(lib, "odp_seg_factor_project", null, null, null, -1, 0, null, null, null, null, 0)
-    assert rc == N.ERR_INVALID_ARGUMENT and "negative" in msg, msg
-    # odp_clip_factors: groups, classes, mode, gamma
-    args = [null, null, 4, 2, null, 0, null, 1.0, N.CLIP_FIXED, 0.0, 1, null, null, null, null, null, null, null]
-    rc, msg = _status(lib, "odp_clip_factors", *args)
-    assert rc == N.ERR_UNSUPPORTED and "n_groups=0" in msg, msg
+def test_clip_argument_checks(lib):
+    """odp_clip_factors: groups, classes, mode, gamma and required pointers;
+    N.check turns a status into an exception carrying the message."""
+    args = [None, None, 4, 2, None, 0, None, 1.0, N.CLIP_FIXED, 0.0, 1, None, None, None, None, None, None, None]
+    _err(lib, lib.odp_clip_factors(*args), N.ERR_UNSUPPORTED, "n_groups=0")
     args[5], args[10] = 1, 9
-    rc, msg = _status(lib, "odp_clip_factors", *args)
-    assert rc == N.ERR_UNSUPPORTED and "n_cls=9" in msg, msg
+    _err(lib, lib.odp_clip_factors(*args), N.ERR_UNSUPPORTED, "n_cls=9")
     args[10], args[8] = 1, 7
-    rc, msg = _status(lib, "odp_clip_factors", *args)
-    assert rc == N.ERR_INVALID_ARGUMENT and "unknown mode 7" in msg, msg
+    _err(lib, lib.odp_clip_factors(*args), N.ERR_INVALID_ARGUMENT, "unknown mode 7")
     args[8] = N.CLIP_AUTOS
-    rc, msg = _status(lib, "odp_clip_factors", *args)
-    assert rc == N.ERR_INVALID_ARGUMENT and "gamma must be positive" in msg, msg
+    _err(lib, lib.odp_clip_factors(*args), N.ERR_INVALID_ARGUMENT, "gamma must be positive")
     args[9] = 0.01
-    rc, msg = _status(lib, "odp_clip_factors", *args)
-    assert rc == N.ERR_INVALID_ARGUMENT and "null" in msg, msg
-    # odp_gaussian_noise: compute dtype and bound
-    rc, msg = _status(lib, "odp_gaussian_noise", null, null, null, 0, 0, 1, 0, N.DTYPE_F16, 0, 0.0, 0.0)
-    assert rc == N.ERR_UNSUPPORTED and "compute_dtype" in msg, msg
-    rc, msg = _status(lib, "odp_gaussian_noise", null, null, null, 0, 0, 1, 0, N.DTYPE_F32, 1, 0.5, 1.0)
-    assert rc == N.ERR_INVALID_ARGUMENT and "bound" in msg, msg
-    rc, msg = _status(lib, "odp_philox_words", null, 0, 0, 0, 1, -1, null)
-    assert rc == N.ERR_INVALID_ARGUMENT and "odp_philox_words" in msg, msg
-    rc, msg = _status(lib, "odp_noise_icdf", null, 0, (1 << 24) + 1, null)
-    assert rc == N.ERR_INVALID_ARGUMENT and "2^24" in msg, msg
-    # N.check turns a status into an exception carrying the message
+    _err(lib, lib.odp_clip_factors(*args), N.ERR_INVALID_ARGUMENT, "null")
     with pytest.raises(RuntimeError, match="odp_noise_icdf failed with status 1"):
         N.check(lib.odp_noise_icdf(None, 0, (1 << 24) + 1, None), "odp_noise_icdf")
