@@ -425,6 +425,12 @@ class _ClipEngine:
             leaf_cls.append(cls_of[dt])
         cn = self.clipping_norm
         effective = cn.effective if isinstance(cn, PerGroup) else float(cn)
+        if self.scale_fn is not None:
+            # The values arrive already scaled by the caller's _scale_fn: the
+            # kernels sum them with every scale 1 (an infinite threshold
+            # passes a gradient through unchanged, _pytree.py:513-518).
+            thresholds = [float("inf")] * len(thresholds)
+            effective = float("inf")
         spec = ClipSpec(
             mode=N.CLIP_AUTOS if self.autos else N.CLIP_FIXED,
             thresholds=thresholds,
@@ -557,13 +563,26 @@ class _ClipEngine:
         transform = self.transform
         gv = torch.func.grad_and_value(loss, argnums=self.argnums_raw, has_aux=True)
 
+        scale_fn = self.scale_fn
+
         def per_example(*a):
             g, (v, aux) = gv(*a, **kwargs)
             g = transform(g)
-            return g, v, aux
+            if scale_fn is None:
+                return g, v, aux
+            # _clipped_fun.py:673-700: the caller's scale function returns the
+            # scaled gradient and its norm record; finiteness is of the
+            # unscaled gradient.
+            fin = torch.ones((), dtype=torch.bool, device=v.device)
+            for t in tree_flatten_with_paths(g)[1]:
+                fin = fin & torch.isfinite(t).all()
+            scaled, info = scale_fn(g)
+            gn = getattr(info, "group_norms", None)
+            return scaled, v, aux, (info.norm, gn if gn is not None else {}, fin)
 
         in_dims = self._in_dims(args)
-        grads, values, loss_aux = torch.func.vmap(per_example, in_dims=in_dims, randomness="same")(*args)
+        out = torch.func.vmap(per_example, in_dims=in_dims, randomness="same")(*args)
+        grads, values, loss_aux = out[:3]
         paths, pe, treedef = tree_flatten_with_paths(grads)
         for p, t in zip(paths, pe):
             if not isinstance(t, torch.Tensor):
@@ -574,7 +593,7 @@ class _ClipEngine:
                     f"got {t.dtype} at {p!r}"
                 )
         all_finite = None
-        if want_finite:
+        if want_finite and scale_fn is None:
             all_finite = torch.ones((), dtype=torch.bool, device=pe[0].device)
             for t in pe:
                 all_finite = all_finite & torch.isfinite(t).all()
@@ -582,8 +601,34 @@ class _ClipEngine:
         shapes = [tuple(t.shape[1:]) for t in pe]
         dtypes = [t.dtype for t in pe]
         seg = Segments.padded(n, 1)
-        return self._finish(n, paths, treedef, shapes, dtypes, pe[0].device, [], mats, seg,
-                            normalize_by, out_dtype_of, values.detach(), loss_aux, all_finite)
+        step, names, treedef = self._finish(n, paths, treedef, shapes, dtypes, pe[0].device, [], mats, seg,
+                                            normalize_by, out_dtype_of, values.detach(), loss_aux, all_finite)
+        if scale_fn is not None:
+            step = self._scaled_step(step, names, *out[3])
+        return step, names, treedef
+
+    def _scaled_step(self, step: _StepOut, names: list[str], norms: torch.Tensor, gnorms: dict,
+                     finite: torch.Tensor) -> _StepOut:
+        """Diagnostics of a call with a custom _scale_fn: the norms are the ones
+        the scale function reported, the clipped norms those of the scaled
+        gradients the kernels summed, and the clip counts compare the reported
+        norms with the thresholds (_clipped_fun.py:472-523, 675-700)."""
+        cn = self.clipping_norm
+        norms = norms.detach()
+        if isinstance(cn, PerGroup) and gnorms:
+            gn = torch.stack([gnorms[name].detach().to(step.group_norms.dtype) for name in names])
+            thr = torch.tensor([float(cn.values[name]) for name in names], dtype=gn.dtype,
+                               device=gn.device).unsqueeze(1)
+            clipped_mask = (gn > thr).to(torch.uint8)
+        else:
+            gn = norms.to(step.group_norms.dtype).unsqueeze(0).expand(step.group_norms.shape[0], -1)
+            clipped_mask = (gn > float(cn.effective if isinstance(cn, PerGroup) else cn)).to(torch.uint8)
+        eff = cn.effective if isinstance(cn, PerGroup) else float(cn)
+        return _StepOut(
+            leaves=step.leaves, squared=step.squared, norms=norms, group_norms=gn, clipped=clipped_mask,
+            clipped_total=(norms > eff).to(torch.uint8), clipped_norms=step.norms, values=step.values,
+            loss_aux=step.loss_aux, all_finite=finite.all() if self.want_stats else None,
+        )
 
     def _run_capture(self, args, kwargs, n, paths, leaves, treedef, disc, normalize_by, out_dtype_of):
         device = leaves[0].device
@@ -947,16 +992,11 @@ def clipped_grad(
     _validate_clipping_norm(clipping_norm)
     if compute_dtype is not None and not compute_dtype.is_floating_point:
         raise TypeError(f"compute_dtype must be a real floating-point dtype, got {compute_dtype!r}.")
-    if _scale_fn is not None:
-        raise NotImplementedError(
-            "opaque_amd clipped_grad implements fixed clipping and AUTO-S (auto_clipped_grad) natively; "
-            "a custom _scale_fn is not supported"
-        )
     fn = _make(loss_fn, argnums, has_aux, clipping_norm=clipping_norm, autos=False, gamma=0.0,
                normalize_by=normalize_by, batch_argnums=batch_argnums, return_aux=return_aux,
                return_stats=return_stats, second_moment=second_moment,
                pre_clipping_transform=pre_clipping_transform, microbatch_size=microbatch_size,
-               dtype=dtype, compute_dtype=compute_dtype, scale_fn=None, aux_cls=ClippedGradAux,
+               dtype=dtype, compute_dtype=compute_dtype, scale_fn=_scale_fn, aux_cls=ClippedGradAux,
                label="opaque::clipped_grad")
     return fn, FixedClipState()
 

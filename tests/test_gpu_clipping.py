@@ -228,6 +228,55 @@ def test_materialised_route_matches_oracle_fixed_clip():
     assert res.max_norm == 3.0 / 4.0
 
 
+def test_custom_scale_fn():
+    """clipped_grad(_scale_fn=...) (_clipped_fun.py:660-700): the caller's
+    per-example scaling replaces the built-in clip; the kernels sum the
+    scaled gradients, the aux norms are the ones the function reports."""
+    import types
+
+    g = torch.Generator().manual_seed(5)
+    params = {"w": torch.randn(12, 5, generator=g), "b": torch.randn(5, generator=g)}
+    x = torch.randn(9, 12, generator=g) * torch.logspace(-1, 1, 9).view(9, 1)
+    y = torch.randn(9, 5, generator=g)
+    C = 30.0  # four of the nine examples exceed it
+
+    def f(p, xi, yi):
+        return ((xi @ p["w"] + p["b"] - yi) ** 2).sum()
+
+    def halve_above(grad):  # a bounding scheme of the caller's: examples above C are halved
+        nrm = torch.sqrt(sum((t.double() ** 2).sum() for t in grad.values()))
+        s = torch.where(nrm > C, torch.full_like(nrm, 0.5), torch.ones_like(nrm))
+        return {k: v * s.to(v.dtype) for k, v in grad.items()}, types.SimpleNamespace(norm=nrm, group_norms=None)
+
+    # Expected on the CPU: per-example gradients, the same scaling, a float32 sum.
+    pe = torch.func.vmap(torch.func.grad(f), in_dims=(None, 0, 0))(params, x, y)
+    def tensors_only(grad):
+        sc, rec = halve_above(grad)
+        return sc, rec.norm
+
+    scaled, norm = torch.func.vmap(tensors_only)(pe)
+    want = {k: v.sum(0) / 4.0 for k, v in scaled.items()}
+    want_cn = torch.sqrt(sum((v.double() ** 2).flatten(1).sum(1) for v in scaled.values()))
+
+    pd = {k: v.to(DEV) for k, v in params.items()}
+    fn, st = clipped_grad(f, clipping_norm=C, batch_argnums=(1, 2), return_aux=True, normalize_by=4.0,
+                          _scale_fn=halve_above)
+    (res, aux), _ = fn(pd, x.to(DEV), y.to(DEV), state=st)
+    for k in params:
+        assert rel(res.pytree[k], want[k]) <= 1e-5, k
+    assert res.max_norm == C / 4.0
+    assert rel(aux.grad_norms, norm) <= 1e-6  # the function's own norms (fp32 gradients on either side)
+    assert rel(aux.clipped_grad_norms, want_cn) <= 1e-5
+    above = int((norm > C).sum())
+    assert 0 < above < 9
+    assert aux.clipping_rate == pytest.approx(above / 9)
+    fs, sst = clipped_grad(f, clipping_norm=C, batch_argnums=(1, 2), return_stats=True, _scale_fn=halve_above)
+    (res2, stats), _ = fs(pd, x.to(DEV), y.to(DEV), state=sst)
+    assert stats.num_clipped == float(above) and stats.batch_size == 9 and stats.all_finite
+    for k in params:
+        assert rel(res2.pytree[k], want[k] * 4.0) <= 1e-5, k
+
+
 def test_per_group_matches_oracle():
     frozen, train = make_model(torch.float32)
     pg = per_group(train, up=0.3, down=0.2, norm=0.5)
