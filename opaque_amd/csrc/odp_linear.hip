@@ -30,6 +30,10 @@
 #include "odp_internal.h"
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// The same 16 bytes read from memory last written as other types (a tile
+// staged element by element in LDS): may_alias keeps the compiler from
+// moving the read above those writes.
+typedef u32x4_t u32x4_alias_t __attribute__((may_alias));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
@@ -505,7 +509,7 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
 #pragma unroll
     for (int k = 0; k < WM / 8; ++k) {
       const int r = 8 * k + (lane >> 3), qq = lane & 7;
-      const u32x4_t v = *(const u32x4_t*)&stg[r * WN + 8 * (qq ^ ((r >> 2) & 7))];
+      const u32x4_t v = *(const u32x4_alias_t*)&stg[r * WN + 8 * (qq ^ ((r >> 2) & 7))];
       const int64_t o = ob + r, n = nb + 8 * qq;
       // Non-temporal: the stored gradients are read again only by a later
       // launch, and should not evict this launch's operands from L2.
