@@ -51,6 +51,10 @@ def parse_args():
     ap.add_argument("--linear-pe-gb", type=float, default=None,
                     help="c4: HBM for stored per-example weight gradients (default: free memory after "
                          "the inputs less 32 GiB; 0: clipped-sum GEMM for every site)")
+    ap.add_argument("--norm-form", choices=["auto", "rule"], default="auto",
+                    help="c4: auto = the engine's choice (fewer flops at the measured kernel speeds, outer form "
+                         "with stored gradients while the budget lasts); rule = Gram where T^2 < d_in*d_out, else "
+                         "outer (ties outer), forced per linear type")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--dropin-overhead", choices=["on", "off"], default="on",
                     help="c3: also time the drop-in auto_clipped_grad's per-call host work")
@@ -334,6 +338,13 @@ def setup_c4(args, dev):
     N_rows = B * T
     gd = torch.Generator(device=dev).manual_seed(args.seed + 1)
     names = list(LAYER_SHAPES)
+    # --norm-form rule: the per-layer rule by T^2 vs d_in * d_out (Gram when
+    # the T x T Gram matrices are the smaller), which forces the Gram form on
+    # gate/up/down at T = 4096 and leaves those sites to the clipped-sum GEMM.
+    forms = {}
+    if args.norm_form == "rule":
+        forms = {n: (N.FORM_GRAM if T * T < d_in * d_out else N.FORM_OUTER)
+                 for n, (d_in, d_out) in LAYER_SHAPES.items()}
     leaves, lins, shapes = [], [], []
     for _ in range(args.layers):
         xs = {}
@@ -342,7 +353,7 @@ def setup_c4(args, dev):
             if key_ not in xs:
                 xs[key_] = torch.randn(N_rows, d_in, dtype=torch.bfloat16, device=dev, generator=gd)
             g = torch.randn(N_rows, d_out, dtype=torch.bfloat16, device=dev, generator=gd)
-            lins.append(LinearSite(xs[key_], g, len(leaves)))
+            lins.append(LinearSite(xs[key_], g, len(leaves), forms.get(name)))
             leaves.append(LeafOut((d_out, d_in), torch.bfloat16, group=names.index(name)))
             shapes.append((d_out, d_in))
     seg = Segments.padded(B, T)
@@ -370,6 +381,8 @@ def setup_c4(args, dev):
                     "PerGroup fixed clipping (one threshold per linear type), noise multiplier 1.0",
         "global_batch": B, "seq_len": T, "layers": args.layers,
         "thresholds": C4_THRESHOLDS, "parallelism": "single GPU",
+        "norm_form": args.norm_form,
+        "norm_forms": {n: ("gram" if f == N.FORM_GRAM else "outer") for n, f in forms.items()} or "engine",
         "stored_per_example_gb": round(plan.lin_pe.numel() * 2 / 2**30, 1),
     }
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B full-weight per-example clipping"
