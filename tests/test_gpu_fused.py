@@ -111,3 +111,27 @@ def test_fused_g_side_unaligned_segments_match_oracle(d_in, d_out):
     assert (gb - dB.sum(0)).norm() <= 2e-2 * dB.sum(0).norm()
     ga = r1.leaves[0].double().cpu()
     assert (ga - dA.sum(0)).norm() <= 2e-2 * dA.sum(0).norm()
+
+
+@pytest.mark.parametrize("d_in,d_out", [(96, 200), (328, 72)])
+def test_segment_past_the_fused_limit_takes_the_two_pass_path(d_in, d_out):
+    """A segment longer than odp_factor_project_max_len() rows: the plan
+    leaves the fused kernel out for that site even with fusion on, and the
+    two-kernel path it takes instead matches the oracle."""
+    limit = int(N.load().odp_factor_project_max_len())
+    lengths = [limit + 37, 11, 0]
+    T = limit + 37
+    print(f"past the fused limit: limit={limit} lengths={lengths} d_in={d_in} d_out={d_out}", flush=True)
+    seg = Segments.padded(3, T, lengths)
+    X, sites, leaves, shapes = _sites(3 * T, d_in, [d_out], [16], seed=11)
+    p1, r1 = _plan(X, sites, leaves, shapes, seg, fuse=True, C=1e30)
+    assert not any(t[0] == "factor_project" and t[5] > 0 for t in p1.tables)
+    G, A, B, _, _ = sites[0]
+    starts = [i * T for i in range(3)]
+    dA, dB = lora_ref.lora_per_example(X, G, A, B, 2.0, starts, lengths)
+    want = (dA.pow(2).sum((1, 2)) + dB.pow(2).sum((1, 2))).sqrt()
+    got = r1.norms.double().cpu()
+    assert torch.allclose(got, want, rtol=2e-2, atol=1e-30), (got, want)
+    ga, gb = r1.leaves[0].double().cpu(), r1.leaves[1].double().cpu()
+    assert (ga - dA.sum(0)).norm() <= 2e-2 * dA.sum(0).norm()
+    assert (gb - dB.sum(0)).norm() <= 2e-2 * dB.sum(0).norm()
