@@ -45,14 +45,13 @@ constexpr int FT_T = ODP_FT_T;
 constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 
 // bf16 factor: 16-wide m blocks per wave (M-tile = 64 NJ).  256-wide tiles
-// (512-byte contiguous runs of each P row) measured fastest.
+// (512-byte contiguous runs of each P row) measured fastest for every rank
+// (three rank blocks: 11 % faster than 128-wide tiles at two workgroups per
+// CU; 512-wide tiles slower).
 #ifndef ODP_FT_NJ
 #define ODP_FT_NJ 4
 #endif
-#ifndef ODP_FT_NJ_WIDE
-#define ODP_FT_NJ_WIDE 2  // rank blocks 3 and 4
-#endif
-__host__ __device__ constexpr int ft_nj(int nkb) { return nkb <= 2 ? ODP_FT_NJ : ODP_FT_NJ_WIDE; }
+__host__ __device__ constexpr int ft_nj(int) { return ODP_FT_NJ; }
 
 // Table pointers arrive as integers (generic address space); loads through
 // them are issued as global (not flat) loads so that they only count in
@@ -89,9 +88,10 @@ __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
 // Workgroups per CU the compiler must fit registers for: each of these
 // fits its LDS tiles that many times in 160 KB without spilling, and the
 // extra loads in flight measured 1-5 % faster (one rank block of the factor
-// kernel: no difference, left to the compiler).
+// kernel: no difference, left to the compiler; three rank blocks: two
+// workgroups, the registers of a 256-wide tile without spills).
 __host__ __device__ constexpr int pj_min_blocks(int nkb) { return nkb == 1 ? 6 : nkb == 2 ? 3 : 1; }
-__host__ __device__ constexpr int ft_min_blocks(int nkb) { return nkb == 2 ? 3 : nkb == 3 ? 4 : 1; }
+__host__ __device__ constexpr int ft_min_blocks(int nkb) { return nkb == 2 ? 3 : nkb == 3 ? 2 : 1; }
 
 template <int NKB>
 __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const int64_t* __restrict__ probs,
