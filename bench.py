@@ -55,6 +55,9 @@ def parse_args():
                     help="c4: auto = the engine's choice (fewer flops at the measured kernel speeds, outer form "
                          "with stored gradients while the budget lasts); rule = Gram where T^2 < d_in*d_out, else "
                          "outer (ties outer), forced per linear type")
+    ap.add_argument("--serial", action="store_true",
+                    help="launch every table on one stream (no side streams for the projection and factor "
+                         "stages)")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--dropin-overhead", choices=["on", "off"], default="on",
                     help="c3: also time the drop-in auto_clipped_grad's per-call host work")
@@ -420,6 +423,7 @@ def main():
         args.seq = 1024 if args.seq is None else args.seq
         plan, sigma, config, metric, flops, stages, bound = setup_c3(args, dev)
     B = args.batch
+    plan.serial = args.serial
     # Stages with no launch in this plan record no events.
     present = {("lin_sum" if i[0] == "lin_prescale" else i[0]) for i in plan.launch_info} | {"clip", "noise"}
     stages = tuple(s for s in stages if s in present)

@@ -337,6 +337,24 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+# Launches of these stages read and write disjoint buffers (the projection
+# planes of different activations; the per-example gradients and partial
+# slots of different leaves), so the tables of one stage run side by side on
+# forked streams: each launch's last, partly filled round of workgroups then
+# overlaps the others instead of idling the CUs between launches.
+_CONCURRENT = ("project", "factor")
+_SIDE: dict[int, list[torch.cuda.Stream]] = {}
+
+
+def _side_streams(device: torch.device, n: int) -> list[torch.cuda.Stream]:
+    """n streams of the device at the default priority, created once per process."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    have = _SIDE.setdefault(idx, [])
+    while len(have) < n:
+        have.append(torch.cuda.Stream(device=idx))
+    return have[:n]
+
+
 def _layout(ext: dict[tuple, torch.Tensor]) -> list[tuple]:
     """Shapes, strides, dtypes and storage sharing of a plan's input tensors:
     a new call's inputs may replace them only if this matches."""
@@ -471,6 +489,9 @@ class GhostPlan:
         if dev.type == "cuda" and dev.index is None:
             dev = torch.device("cuda", torch.cuda.current_device())
         self.device = dev
+        # True launches every table on the caller's stream in table order
+        # (the concurrent stages then run one launch at a time).
+        self.serial = False
         self.segments = segments
         self.leaves = leaves
         self.clip = clip
@@ -1500,55 +1521,82 @@ class GhostPlan:
         with freshly recorded timing events, in ``launch_info`` order.
         """
         lib = N.load()
-        stream = _stream()
+        main = torch.cuda.current_stream()
+        stream = main.cuda_stream
         seg = self.segments
         ev = events or {}
         self._part_buf.zero_()
         live = [t for t in self.tables if t[5] > 0 and t[0] not in _AFTER_CLIP]
 
-        def mark(name, dt):
+        def mark(name, dt, on):
             if launch_log is None:
                 return None
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
+            e0.record(on)
             launch_log.append((name, dt, e0, e1))
             return e1
 
-        for idx, (name, dt, probs, ws, n, total) in enumerate(live):
-            first = idx == 0 or live[idx - 1][0] != name
-            last = idx == len(live) - 1 or live[idx + 1][0] != name
-            if name in ev and first:
-                ev[name][0].record()
-            end_ev = mark(name, dt)
+        def launch(name, dt, probs, ws, n, total, s):
             if name == "pack":
-                N.check(lib.odp_pack_factors(stream, probs.data_ptr(), ws.data_ptr(), n, total), name)
+                N.check(lib.odp_pack_factors(s, probs.data_ptr(), ws.data_ptr(), n, total), name)
             elif name == "project":
-                N.check(lib.odp_project(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_project(s, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                         self.seg_start.data_ptr(), self.seg_len.data_ptr(), dt[1]), name)
             elif name == "factor_project":
-                N.check(lib.odp_seg_factor_project(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_seg_factor_project(s, probs.data_ptr(), ws.data_ptr(), n, total,
                                                    self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                                    self.seg_ex.data_ptr(), self.part.data_ptr(),
                                                    self.n_slots), name)
             elif name == "factor":
-                N.check(lib.odp_seg_factor(stream, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_seg_factor(s, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                            self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                            self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots,
                                            dt[1]), name)
             elif name == "sqnorm":
-                N.check(lib.odp_sqnorm(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_sqnorm(s, probs.data_ptr(), ws.data_ptr(), n, total,
                                        self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
             elif name == "nonfinite":
-                N.check(lib.odp_nonfinite_columns(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_nonfinite_columns(s, probs.data_ptr(), ws.data_ptr(), n, total,
                                                   self.seg_start.data_ptr(), self.seg_len.data_ptr()), name)
             elif name == "lin_norm":
-                N.check(lib.odp_linear_sqnorm(stream, dt, probs.data_ptr(), ws.data_ptr(), n, total,
+                N.check(lib.odp_linear_sqnorm(s, dt, probs.data_ptr(), ws.data_ptr(), n, total,
                                               self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                               self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
-            if end_ev is not None:
-                end_ev.record()
-            if name in ev and last:
-                ev[name][1].record()
+
+        # Runs of consecutive tables of one stage; a run of a _CONCURRENT stage
+        # forks: table j > 0 goes to side stream j - 1 after an event of the
+        # caller's stream, and the caller's stream waits for every side stream
+        # before the next stage (so buffers the caller frees afterwards are
+        # only reused behind all of them).
+        runs: list[list[tuple]] = []
+        for t in live:
+            if runs and runs[-1][0][0] == t[0]:
+                runs[-1].append(t)
+            else:
+                runs.append([t])
+        for run_ in runs:
+            name = run_[0][0]
+            if name in ev:
+                ev[name][0].record(main)
+            side = (_side_streams(self.device, len(run_) - 1)
+                    if name in _CONCURRENT and len(run_) > 1 and not self.serial else [])
+            if side:
+                fork = torch.cuda.Event()
+                fork.record(main)
+            for j, (_, dt, probs, ws, n, total) in enumerate(run_):
+                on = side[j - 1] if side and j > 0 else main
+                if on is not main:
+                    on.wait_event(fork)
+                end_ev = mark(name, dt, on)
+                launch(name, dt, probs, ws, n, total, on.cuda_stream)
+                if end_ev is not None:
+                    end_ev.record(on)
+            for s in side:
+                done = torch.cuda.Event()
+                done.record(s)
+                main.wait_event(done)
+            if name in ev:
+                ev[name][1].record(main)
         if "clip" in ev:
             ev["clip"][0].record()
         N.check(
@@ -1569,7 +1617,7 @@ class GhostPlan:
             st = stage[idx]
             if st in ev and st not in stage[:idx]:
                 ev[st][0].record()
-            end_ev = mark(name, dt)
+            end_ev = mark(name, dt, main)
             if name == "scale_sum":
                 N.check(lib.odp_scale_sum(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                           self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
