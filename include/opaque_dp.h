@@ -72,7 +72,8 @@ typedef enum odp_clip_mode {
 
 typedef enum odp_norm_form {
   ODP_FORM_OUTER = 0, /* ||sum_t g_t a_t^T||_F^2 */
-  ODP_FORM_GRAM = 1   /* sum_{t,s} (g_t . g_s)(a_t . a_s) */
+  ODP_FORM_GRAM = 1,  /* sum_{t,s} (g_t . g_s)(a_t . a_s), 128-row blocks */
+  ODP_FORM_GRAM256 = 2 /* the same sum over 256-row blocks, with scratch  */
 } odp_norm_form;
 
 /* ---- segments -----------------------------------------------------------
@@ -280,7 +281,11 @@ int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* w
  * OUTER; the token-Gram identity sum_{t,u}(x_t.x_u)(g_t.g_u) for GRAM);
  * odp_linear_tiles(form, ...) is the number of slots (and workgroups per
  * segment) a problem uses; GRAM needs ODP_LN_NB = ceil(max_len / 128) of
- * the problem's longest segment.  Replaces the per-example weight
+ * the problem's longest segment.  GRAM256 computes the GRAM sum over pairs
+ * of 256-row blocks (nb (nb + 1) / 2 slots per segment, ODP_LN_NB =
+ * ceil(max_len / 256)), fewer loads per flop than GRAM; it writes each
+ * pair's X block to ODP_LN_SCRATCH, which must hold 65536 floats per
+ * (segment, slot) of the problem: n_seg * nb (nb + 1) / 2 * 256 KB.  Replaces the per-example weight
  * gradients that the reference materialises under vmap(grad)
  * (opaque-engine/src/opaque/api/engine/clipping/_clipped_fun.py:756-762)
  * and their squared norms (clipping/_pytree.py:224-265).
@@ -310,7 +315,8 @@ enum {
   ODP_LN_SLOT = 8,   /* sqnorm: first partial slot of the weight            */
   ODP_LN_OUT = 9,    /* clipped sum: address of out [d_out][d_in]           */
   ODP_LN_FLAGS = 10, /* clipped sum: out dtype | group << 8 | cls << 24     */
-  ODP_LN_NB = 11,    /* GRAM: 128-row blocks of the longest segment         */
+  ODP_LN_NB = 11,    /* GRAM (GRAM256): 128- (256-) row blocks of the longest
+                        segment                                             */
   ODP_LN_NROWS = 12, /* prescale: rows of X (the output X' is [n_rows][d_in]) */
   ODP_LN_PE = 13,    /* OUTER sqnorm: address of bf16 [n_seg][d_out][d_in]
                         that receives each M_s (RNE), or 0                  */
@@ -321,6 +327,8 @@ enum {
                         ([n_seg][ceil(d_out / 32)]) or 0                    */
   ODP_LN_NFFLAG = 16,/* OUTER sqnorm: address of a uint32 that is OR-ed with
                         1 when an entry of some M_s is non-finite, or 0     */
+  ODP_LN_SCRATCH = 17,/* GRAM256 sqnorm: address of the fp32 scratch of the
+                        problem ([n_seg][slots][65536], 16-byte aligned)    */
   ODP_LN_FIELDS = 20
 };
 

@@ -40,11 +40,12 @@ SQ_FIELDS = 8
 SQ_X, SQ_N, SQ_NSEG, SQ_SEG_FIRST, SQ_SLOT, SQ_DTYPE = range(6)
 LN_FIELDS = 20
 LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB, LN_NROWS, LN_PE = range(14)
-LN_XMASK, LN_GMASK, LN_NFFLAG = 14, 15, 16
+LN_XMASK, LN_GMASK, LN_NFFLAG, LN_SCRATCH = 14, 15, 16, 17
 NF_FIELDS = 8
 NF_P, NF_LDP, NF_D, NF_SEG_FIRST, NF_NSEG, NF_MASK = range(6)
 FORM_OUTER = 0
 FORM_GRAM = 1
+FORM_GRAM256 = 2
 
 _c_int = ctypes.c_int
 _c_i32 = ctypes.c_int32

@@ -742,6 +742,221 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
 }
 
 // ---------------------------------------------------------------------------
+// Gram form over 256-row blocks (ODP_FORM_GRAM256).  Item (tb, sb), tb <= sb,
+// of a segment pairs the t block (rows 256 tb ..) with the s block (rows
+// 256 sb ..); eight waves in 2 x 4 each own 128 x 64 of the 256 x 256 block
+// pair, as in the outer-form kernels, and a step moves 512 rows x 64 bytes
+// into LDS: 128 flop per byte loaded against 87 for the 128 x 256 pairs of
+// k_lin_gram_norm, whose loads into LDS bound it.  The two Gram blocks of a
+// 256 x 256 pair do not fit in registers together, so the X block
+// P = X_t X_s^T is accumulated first and written to the item's fp32 scratch
+// in register order (each lane its own 16-byte pieces, 1 KB per wave and
+// block), then G's block Q is accumulated and the item's partial
+// sum_{t,s} P Q is formed against the scratch read back by the same lanes.
+// A diagonal item (tb == sb) loads its rows once and reads both operands
+// from them.  Same row swizzle, non-finite column handling and work order
+// as k_lin_gram_norm.
+// ---------------------------------------------------------------------------
+constexpr int G2_B = 256;                                 // rows per block
+constexpr int G2_ROWS = 2 * G2_B;                         // t block + s block
+constexpr int G2_STAGE = G2_ROWS * GR_K;                  // elements (32 KB)
+constexpr int G2_RING = 4;
+constexpr int G2_LOADS = G2_ROWS * GR_K * 2 / 1024 / 8;  // 1 KB loads per wave per step
+constexpr int64_t G2_SCRATCH = (int64_t)G2_B * G2_B;      // floats per (segment, item)
+static_assert(G2_LOADS == 4, "four loads per wave per step");
+
+__host__ __device__ constexpr int64_t gram2_items(int64_t nb) { return nb * (nb + 1) / 2; }
+
+__global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __restrict__ probs,
+                                                              const int32_t* __restrict__ ws, int n_prob,
+                                                              const int32_t* __restrict__ sstart,
+                                                              const int32_t* __restrict__ slen,
+                                                              const int32_t* __restrict__ sex,
+                                                              double* __restrict__ part, int64_t part_stride) {
+  __shared__ __attribute__((aligned(16))) uint16_t q0[G2_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t q1[G2_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t q2[G2_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t q3[G2_STAGE];
+  __shared__ double red[8];
+  static_assert(G2_RING == 4, "four ring stages");
+  auto stage = [&](int k) -> uint16_t* { return k == 0 ? q0 : k == 1 ? q1 : k == 2 ? q2 : q3; };
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
+  const LinProblem P = read_problem(f);
+  const int64_t slot = f[ODP_LN_SLOT];
+  const int nb = (int)f[ODP_LN_NB];
+  const int items = (int)gram2_items(nb);
+  int seg, item;
+  if (!seg_item(bid - ws[p], P.n_seg, items, seg, item)) return;
+  int tb = 0, rem = item;
+  while (rem >= nb - tb) {
+    rem -= nb - tb;
+    ++tb;
+  }
+  const int sb = tb + rem;
+  const bool diag = sb == tb;
+  const int gs = P.seg_first + seg;
+  const int32_t t_begin = sstart[gs], len = slen[gs];
+  const int ex = sex[gs];
+  double* dst = part + (int64_t)ex * part_stride + slot + item;
+  if ((int64_t)sb * G2_B >= len) {  // item past this segment's length
+    if (threadIdx.x == 0) *dst = 0.0;
+    return;
+  }
+  float* scr = (float*)f[ODP_LN_SCRATCH] + ((int64_t)seg * items + item) * G2_SCRATCH;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  const int xw = (int)((P.d_in + 31) / 32), gw = (int)((P.d_out + 31) / 32);
+  const uint32_t* xm = (const uint32_t*)f[ODP_LN_XMASK];
+  const uint32_t* gm = (const uint32_t*)f[ODP_LN_GMASK];
+  if (xm != nullptr) xm += (int64_t)seg * xw;
+  if (gm != nullptr) gm += (int64_t)seg * gw;
+  int fix = 0;
+  if (xm != nullptr || gm != nullptr) {
+    int any = 0;
+    for (int w = threadIdx.x; w < xw + gw; w += 512)
+      any |= (w < xw ? (xm != nullptr ? xm[w] : 0u) : (gm != nullptr ? gm[w - xw] : 0u)) != 0u;
+    fix = __syncthreads_or(any);
+  }
+
+  // Stage rows 0..255: block tb; 256..511: block sb (not loaded for a
+  // diagonal item).  Wave w loads rows 64 w .. + 63, 16 per load.
+  uint32_t lbase[G2_LOADS];
+  int lslot[G2_LOADS];
+  bool lload[G2_LOADS];
+#pragma unroll
+  for (int i = 0; i < G2_LOADS; ++i) {
+    const int row = 64 * wave + 16 * i + (lane >> 2);
+    lbase[i] = (uint32_t)((row < G2_B ? tb : sb) * G2_B + (row & (G2_B - 1)));
+    lslot[i] = (lane & 3) ^ gr_swz(row);
+    lload[i] = row < G2_B || !diag;
+  }
+  const uint32_t nrow = (uint32_t)len;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(P.X + (int64_t)t_begin * P.ldx), (short)0, (int)(nrow * (uint32_t)P.ldx * 2u), LIN_BUF_DWORD3);
+  const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(P.G + (int64_t)t_begin * P.ldg), (short)0, (int)(nrow * (uint32_t)P.ldg * 2u), LIN_BUF_DWORD3);
+  const int nx = (int)((P.d_in + GR_K - 1) / GR_K), ng = (int)((P.d_out + GR_K - 1) / GR_K);
+  const int px = (nx + G2_RING - 1) / G2_RING * G2_RING;
+  const int total = px + (ng + G2_RING - 1) / G2_RING * G2_RING;
+  const uint32_t ldx = (uint32_t)P.ldx, ldg = (uint32_t)P.ldg;
+  const int32_t din = (int32_t)P.d_in, dout = (int32_t)P.d_out;
+
+  auto issue = [&](uint16_t* st, int x) __attribute__((always_inline)) {
+    const bool isx = x < px;
+    const int32_t kx = isx ? x : x - px;
+    const int32_t k0 = kx * GR_K;
+    const int32_t d = x < total && kx < (isx ? nx : ng) ? (isx ? din : dout) : 0;
+    const uint32_t ld = isx ? ldx : ldg;
+    const __amdgpu_buffer_rsrc_t rs = isx ? xr : gr;
+#pragma unroll
+    for (int i = 0; i < G2_LOADS; ++i) {
+      const int32_t col = k0 + 8 * lslot[i];
+      const uint32_t o = (lbase[i] * ld + (uint32_t)col) * 2u;
+      const uint32_t off = col < d && lload[i] ? o : LIN_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (ODP_LDS void*)(st + (64 * wave + 16 * i) * GR_K), 16, off, 0,
+                                               0, 0);
+    }
+  };
+
+  // Wave w: t rows 128 (w & 1) .., s rows 64 (w >> 1) .. of the s half (the
+  // t half itself for a diagonal item).
+  const int wt = 128 * (wave & 1), wsr = (diag ? 0 : G2_B) + 64 * (wave >> 1);
+  f32x4_t acc[8][4];
+  zero_acc(acc);
+  auto compute = [&](const uint16_t* st, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+    const int r = lane & 15, kq = lane >> 4;
+    bf16x8_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wsr + 16 * j + r, kq)]);
+    // A fragments stream one ahead of the MFMAs that consume them.
+    bf16x8_t a[2];
+    a[0] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wt + r, kq)]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + 1 < 8)
+        a[(i + 1) & 1] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wt + 16 * (i + 1) + r, kq)]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i & 1], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  auto step = [&](uint16_t* __restrict__ nxt, const uint16_t* __restrict__ cur, int x, bool live,
+                  f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+    issue(nxt, x);
+    if (live) compute(cur, acc);
+  };
+  auto zero_features = [&](uint16_t* st, uint32_t word) __attribute__((always_inline)) {
+    const int fc = threadIdx.x & 31;
+    if ((word >> fc) & 1u)
+      for (int r = threadIdx.x >> 5; r < G2_ROWS; r += 16) st[gr_at(r, fc >> 3) + (fc & 7)] = 0;
+  };
+  auto phase = [&](int lo, int hi, int live, const uint32_t* mask, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+    for (int g0 = lo; g0 < hi; g0 += G2_RING) {
+#pragma unroll
+      for (int k = 0; k < G2_RING; ++k) {
+        const int g = g0 + k;
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((G2_RING - 2) * G2_LOADS));
+        __asm__ volatile("s_barrier" ::: "memory");
+        if (fix && mask != nullptr && g - lo < live) {
+          const uint32_t word = mask[g - lo];
+          if (word != 0u) {
+            zero_features(stage(k), word);
+            __syncthreads();
+          }
+        }
+        step(stage((k + G2_RING - 1) % G2_RING), stage(k), g + G2_RING - 1, g - lo < live, acc);
+      }
+    }
+  };
+#pragma unroll
+  for (int x = 0; x < G2_RING - 1; ++x) issue(stage(x), x);
+  phase(0, px, nx, xm, acc);
+  // P leaves in register order; lane l of wave w holds block (i, j) at
+  // ((w * 8 + i) * 4 + j) * 64 + l (16 bytes each).
+  f32x4_t ODP_GLOBAL* sp = (f32x4_t ODP_GLOBAL*)(ODP_GLOBAL void*)scr + wave * 8 * 4 * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sp[(i * 4 + j) * 64] = acc[i][j];
+      acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  __asm__ volatile("" ::: "memory");  // P is read back from memory, not kept live
+  phase(px, total, ng, gm, acc);
+  __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
+
+  // P comes back four pieces at a time (the fence keeps the compiler from
+  // issuing all 32 loads while the 128 accumulator registers are live).
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f32x4_t pv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pv[j] = sp[(i * 4 + j) * 64];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += (double)pv[j][e] * (double)acc[i][j][e];
+    __asm__ volatile("" ::: "memory");
+  }
+  if (!diag) s *= 2.0;  // the (s, t) pair is not computed
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) t += red[w];
+    *dst = t;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Prescale for the clipped sum: X'[t] = c_i x_t (fp32 product rounded to
 // bf16, as the clipped sum would form it in registers) for the rows t of
 // example i's segments, 0 for rows in no segment.  With X' the clipped sum
@@ -1036,6 +1251,10 @@ extern "C" int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64
     const int64_t nb = max_seg_len > 0 ? (max_seg_len + LT - 1) / LT : 0;
     return gram_items(nb);
   }
+  if (form == ODP_FORM_GRAM256) {
+    const int64_t nb = max_seg_len > 0 ? (max_seg_len + G2_B - 1) / G2_B : 0;
+    return gram2_items(nb);
+  }
   return ((d_out + OM - 1) / OM) * ((d_in + ON - 1) / ON);
 }
 
@@ -1043,7 +1262,7 @@ extern "C" int64_t odp_linear_norm_blocks(int form, int64_t d_in, int64_t d_out,
                                           int64_t n_seg) {
   const int64_t per = odp_linear_tiles(form, d_in, d_out, max_seg_len);
   if (per <= 0 || n_seg <= 0) return 0;
-  if (form == ODP_FORM_GRAM && n_seg >= 8) return 8 * ((n_seg + 7) / 8) * per;
+  if ((form == ODP_FORM_GRAM || form == ODP_FORM_GRAM256) && n_seg >= 8) return 8 * ((n_seg + 7) / 8) * per;
   return (n_seg * per + 7) / 8 * 8;
 }
 
@@ -1059,7 +1278,7 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
                                  const int32_t* seg_example, double* part, int64_t part_stride) {
   int rc = odp_check_table("odp_linear_sqnorm", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
-  if (form != ODP_FORM_OUTER && form != ODP_FORM_GRAM) {
+  if (form != ODP_FORM_OUTER && form != ODP_FORM_GRAM && form != ODP_FORM_GRAM256) {
     odp_set_error("odp_linear_sqnorm: unknown form %d", form);
     return ODP_ERR_INVALID_ARGUMENT;
   }
@@ -1073,6 +1292,9 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
   const dim3 grid(total_blocks), block(OUTER_THREADS);
   if (form == ODP_FORM_GRAM)
     hipLaunchKernelGGL(k_lin_gram_norm, grid, dim3(512), 0, s, problems, work_start, n_prob,
+                       seg_row_start, seg_row_len, seg_example, part, part_stride);
+  else if (form == ODP_FORM_GRAM256)
+    hipLaunchKernelGGL(k_lin_gram2_norm, grid, dim3(512), 0, s, problems, work_start, n_prob,
                        seg_row_start, seg_row_len, seg_example, part, part_stride);
   else
     hipLaunchKernelGGL(k_lin_outer_norm, grid, block, 0, s, problems, work_start, n_prob,

@@ -194,8 +194,9 @@ class LinearSite:
     ``w_leaf`` indexes the plan's leaf list; the leaf is W's gradient,
     shaped [d_out, d_in], or with ``index`` one slice of a stacked
     [E, d_out, d_in] leaf (each slice produced by one site).  ``form`` picks the per-example norm algorithm
-    (``N.FORM_OUTER`` / ``N.FORM_GRAM``); None chooses the one with fewer
-    MFMA flops for the longest segment.
+    (``N.FORM_OUTER`` / ``N.FORM_GRAM``; ``N.FORM_GRAM256`` forces the
+    256-row-block Gram kernel); None chooses the one with fewer MFMA flops
+    for the longest segment.
     """
 
     x: torch.Tensor
@@ -210,12 +211,25 @@ class LinearSite:
 # measured on MI355X (C4 shapes: 1264 vs 746 TFLOP/s).
 GRAM_FLOP_COST = 1.6
 
+# A site in the Gram form whose longest segment spans at least
+# GRAM256_MIN_LEN rows takes the 256-row-block kernel (N.FORM_GRAM256: fewer
+# loads per flop) while its scratch, GRAM256_ITEM_BYTES per segment and block
+# pair, fits within GRAM256_SCRATCH_BYTES and a quarter of the free device
+# memory at plan build; the others take the 128-row-block kernel.
+GRAM256_MIN_LEN = 512
+GRAM256_SCRATCH_BYTES = 32 << 30
+GRAM256_ITEM_BYTES = 256 * 256 * 4
+# Its time per flop relative to the outer form, measured on MI355X (C4
+# gate/up/down at 4096 tokens: 1010 vs 1209 TFLOP/s).
+GRAM256_FLOP_COST = 1.2
+
 
 def choose_form(max_len: int, d_in: int, d_out: int) -> int:
     """The faster form: GRAM costs L^2 (d_in + d_out) flops per example (upper
-    triangle) at GRAM_FLOP_COST times the outer kernel's time per flop, OUTER
-    2 L d_in d_out."""
-    return N.FORM_GRAM if GRAM_FLOP_COST * max_len * (d_in + d_out) < 2 * d_in * d_out else N.FORM_OUTER
+    triangle) at GRAM_FLOP_COST (GRAM256_FLOP_COST from GRAM256_MIN_LEN rows)
+    times the outer kernel's time per flop, OUTER 2 L d_in d_out."""
+    cost = GRAM256_FLOP_COST if max_len >= GRAM256_MIN_LEN else GRAM_FLOP_COST
+    return N.FORM_GRAM if cost * max_len * (d_in + d_out) < 2 * d_in * d_out else N.FORM_OUTER
 
 
 @dataclass
@@ -681,6 +695,9 @@ class GhostPlan:
                 budget = (torch.cuda.mem_get_info(dev)[0] + cached) // 2
         lin_pe: dict[int, int] = {}  # site -> element offset in self.lin_pe
         pe_total = 0
+        lin_scr: dict[int, int] = {}  # site -> byte offset in self.gram_scr (GRAM256 sites)
+        scr_total = 0
+        scr_budget = None
         lin_form: list[int] = []
         lin_view: list[_SegView] = []
         lin_off: list[int] = []
@@ -696,6 +713,18 @@ class GhostPlan:
                 form = N.FORM_OUTER
             else:
                 form = ls.form if ls.form is not None else choose_form(v.max_len, d_in, d_out)
+            if (form == N.FORM_GRAM and v.max_len >= GRAM256_MIN_LEN) or form == N.FORM_GRAM256:
+                need = v.n_seg * int(lib.odp_linear_tiles(N.FORM_GRAM256, d_in, d_out, v.max_len)) \
+                    * GRAM256_ITEM_BYTES
+                if scr_budget is None:
+                    scr_budget = GRAM256_SCRATCH_BYTES
+                    if dev.type == "cuda":
+                        cached = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
+                        scr_budget = min(scr_budget, (torch.cuda.mem_get_info(dev)[0] + cached) // 4)
+                if form == N.FORM_GRAM256 or scr_total + need <= scr_budget:
+                    form = N.FORM_GRAM256
+                    lin_scr[i] = scr_total
+                    scr_total += need
             tiles = int(lib.odp_linear_tiles(form, d_in, d_out, v.max_len))
             lin_form.append(form)
             lin_view.append(v)
@@ -973,7 +1002,11 @@ class GhostPlan:
                                N.LN_FLAGS: (lf.group << 8) | (lf.cls << 24), N.LN_OUT: self.xs[off:].data_ptr(),
                                N.LN_XMASK: mask_addr(site_mask[i][0])},
                               int(lib.odp_linear_prescale_blocks(x.shape[0])), 2 * v.valid * x.shape[1] * 2)
-        lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS)}
+        lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS),
+               N.FORM_GRAM256: _Table(N.LN_FIELDS)}
+        # fp32 scratch of the 256-row-block Gram kernel (its X blocks).
+        self.gram_scr = (torch.empty(scr_total // 4, dtype=torch.float32, device=dev) if scr_total
+                         else None)
         lsum = _Table(N.LN_FIELDS)
         for i, ls in enumerate(lins):
             x, g = lin_x[i], lin_g[i]
@@ -988,15 +1021,16 @@ class GhostPlan:
             if i in site_mask:
                 common[N.LN_XMASK] = mask_addr(site_mask[i][0])
                 common[N.LN_GMASK] = mask_addr(site_mask[i][1])
-            if form == N.FORM_GRAM:
+            if form in (N.FORM_GRAM, N.FORM_GRAM256):
                 fl = sum(ln * ln for ln in v.segs.lengths) * (d_in + d_out)
             else:
                 fl = 2 * valid * d_in * d_out
             blocks = int(lib.odp_linear_norm_blocks(form, d_in, d_out, v.max_len, n_seg))
-            nb_max = (v.max_len + 127) // 128
+            nb_max = (v.max_len + 255) // 256 if form == N.FORM_GRAM256 else (v.max_len + 127) // 128
             pe_at = self.lin_pe[lin_pe[i]:].data_ptr() if i in lin_pe else 0
+            scr_at = self.gram_scr.data_ptr() + lin_scr[i] if i in lin_scr else 0
             lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_off[i], N.LN_NB: nb_max,
-                           N.LN_PE: pe_at, N.LN_NFFLAG: self._nf_flag_addr}, blocks,
+                           N.LN_PE: pe_at, N.LN_NFFLAG: self._nf_flag_addr, N.LN_SCRATCH: scr_at}, blocks,
                           valid * (d_in + d_out) * 2 + (n_seg * d_in * d_out * 2 if pe_at else 0), fl)
             if i in lin_pe:
                 continue
@@ -1074,6 +1108,7 @@ class GhostPlan:
         tabs.append(("nonfinite", None, nft))
         tabs.append(("lin_norm", N.FORM_OUTER, lnt[N.FORM_OUTER]))
         tabs.append(("lin_norm", N.FORM_GRAM, lnt[N.FORM_GRAM]))
+        tabs.append(("lin_norm", N.FORM_GRAM256, lnt[N.FORM_GRAM256]))
         tabs.append(("scale_sum", None, ss))
         for c in range(len(xs_chunks)):
             tabs.append(("lin_prescale", c, xs_pre[c]))

@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from opaque_amd import _native as N
+from opaque_amd import engine
 from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LinearSite, MaterializedLeaf, Segments, choose_form
 from opaque_amd.guard import guard_constants, leaf_guards
 from oracle import dp_ref, lora_ref
@@ -62,13 +63,42 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("n_ex,T,d_in,d_out,lengths", SHAPES)
-@pytest.mark.parametrize("form", [N.FORM_OUTER, N.FORM_GRAM])
+@pytest.mark.parametrize("form", [N.FORM_OUTER, N.FORM_GRAM, N.FORM_GRAM256])
 def test_linear_norms_match_oracle(n_ex, T, d_in, d_out, lengths, form):
     X, G, seg = _case(n_ex, T, d_in, d_out, lengths, seed=d_in + d_out)
     _, want = _ref_norms(X, G, seg)
     _, res, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=form)
     got = res.norms.double().cpu()
     assert torch.allclose(got, want.float().double(), rtol=2e-3, atol=1e-6), (got, want)
+
+
+# The 256-row-block Gram kernel: ragged segments across block edges, a
+# one-row and an empty segment, n_seg >= 8 (work decoded in XCD order), up
+# to five blocks (diagonal and off-diagonal pairs).
+GRAM256_CASES = [
+    # n_ex, T, d_in, d_out, lengths
+    (3, 600, 136, 264, [600, 1, 300]),
+    (9, 520, 128, 96, [520, 256, 255, 257, 0, 512, 100, 511, 3]),
+    (2, 1100, 392, 200, [1100, 700]),
+]
+
+
+@pytest.mark.parametrize("n_ex,T,d_in,d_out,lengths", GRAM256_CASES)
+def test_gram256_matches_oracle_and_gram128(n_ex, T, d_in, d_out, lengths, monkeypatch):
+    """Norms of the 256-row-block kernel against the fp64 oracle (rel 2e-3)
+    and against the 128-row-block kernel (rel 1e-5: the same products, fp32
+    Gram blocks summed in fp64 in another order)."""
+    print(f"gram256: n_ex={n_ex} T={T} d_in={d_in} d_out={d_out}", flush=True)
+    X, G, seg = _case(n_ex, T, d_in, d_out, lengths, seed=T + d_in)
+    _, want = _ref_norms(X, G, seg)
+    plan, res, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=N.FORM_GRAM)
+    assert {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0} == {N.FORM_GRAM256}
+    got = res.norms.double().cpu().clone()
+    assert torch.allclose(got, want.float().double(), rtol=2e-3, atol=1e-6), (got, want)
+    monkeypatch.setattr(engine, "GRAM256_MIN_LEN", 1 << 30)
+    plan2, r2, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=N.FORM_GRAM)
+    assert {t[1] for t in plan2.tables if t[0] == "lin_norm" and t[5] > 0} == {N.FORM_GRAM}
+    assert torch.allclose(got, r2.norms.double().cpu(), rtol=1e-5, atol=1e-9)
 
 
 def test_outer_and_gram_forms_agree():
@@ -350,6 +380,7 @@ _PATHS = {
     "gemm_outer": (N.FORM_OUTER, 0, 8 << 30),  # outer norms; prescaled X' and the clipped-sum GEMM
     "gemm_gram": (N.FORM_GRAM, 0, 8 << 30),    # token-Gram norms; prescaled X' and the GEMM
     "gemm_inreg": (N.FORM_GRAM, 0, 0),      # token-Gram norms; clip factors applied in registers
+    "gemm_gram256": (N.FORM_GRAM256, 0, 8 << 30),  # 256-row-block Gram norms; prescaled X' and the GEMM
 }
 
 
@@ -392,7 +423,7 @@ def test_non_finite_entries_are_zeroed(path, kind):
     torch.cuda.synchronize()
     assert (plan.lin_pe.numel() > 0) == (path == "stored")
     kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
-    assert kinds == {N.FORM_GRAM if form == N.FORM_GRAM else N.FORM_OUTER}
+    assert kinds == {form if form in (N.FORM_GRAM, N.FORM_GRAM256) else N.FORM_OUTER}
     outs, norms = [], []
     for i in range(n_ex):
         c, nrm, _ = dp_ref.clip_pytree({"w": pe[i].to(torch.bfloat16)}, C)

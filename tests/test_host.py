@@ -357,3 +357,19 @@ def test_host_view_maker_matches_torch_views():
     d, u = vm2.make([raw])
     assert d.dtype == torch.float64 and torch.equal(d, raw[256 : 256 + 48].view(torch.float64).view(2, 3))
     assert u.dtype == torch.uint8 and torch.equal(u, raw[512:516])
+
+
+def test_form_choice_at_c4_shapes():
+    """At 4096 tokens the 256-row-block Gram kernel makes the token-Gram norm
+    the cheaper form for gate/up/down (L (d_in + d_out) below d_in d_out at
+    its measured cost per flop); q/o and k/v stay with the outer form, and
+    short segments use the 128-row-block cost."""
+    from opaque_amd import _native as N
+    from opaque_amd.engine import choose_form
+
+    assert choose_form(4096, 4096, 14336) == N.FORM_GRAM
+    assert choose_form(4096, 14336, 4096) == N.FORM_GRAM
+    assert choose_form(4096, 4096, 4096) == N.FORM_OUTER
+    assert choose_form(4096, 4096, 1024) == N.FORM_OUTER
+    assert choose_form(64, 512, 512) == N.FORM_GRAM
+    assert choose_form(500, 700, 700) == N.FORM_OUTER  # 1.6 * 500 * 1400 > 2 * 700 * 700
