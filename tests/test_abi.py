@@ -71,6 +71,9 @@ def test_field_indices_match_header():
     assert value("ODP_LN_XMASK") == N.LN_XMASK
     assert value("ODP_LN_GMASK") == N.LN_GMASK
     assert value("ODP_LN_NFFLAG") == N.LN_NFFLAG
+    assert value("ODP_LN_SCRATCH") == N.LN_SCRATCH
+    assert value("ODP_FORM_GRAM") == N.FORM_GRAM
+    assert value("ODP_FORM_GRAM256") == N.FORM_GRAM256
     assert value("ODP_NF_FIELDS") == N.NF_FIELDS
     assert value("ODP_NF_MASK") == N.NF_MASK
     assert value("ODP_CLIP_AUTOS") == N.CLIP_AUTOS
@@ -93,6 +96,20 @@ def test_block_helpers_are_pure_host_code(lib):
     assert lib.odp_nonfinite_blocks(0, 2) == 0
     assert lib.odp_pack_factors_blocks(0) == 0
     assert lib.odp_pack_factors_blocks(256) == 1 and lib.odp_pack_factors_blocks(257) == 2
+
+
+def test_linear_norm_slots_per_form(lib):
+    """Partial slots per segment: 256 x 256 output tiles (outer), pairs
+    t <= s of 128-row blocks taken two s blocks at a time (Gram), pairs of
+    256-row blocks (Gram256: nb (nb + 1) / 2); the norm launches pad the
+    segment count to a multiple of 8 (work decoded in XCD order)."""
+    assert lib.odp_linear_tiles(N.FORM_OUTER, 4096, 14336, 4096) == 16 * 56
+    for L, nb in ((1, 1), (256, 1), (257, 2), (4096, 16), (4100, 17)):
+        assert lib.odp_linear_tiles(N.FORM_GRAM256, 4096, 14336, L) == nb * (nb + 1) // 2
+    assert lib.odp_linear_tiles(N.FORM_GRAM, 4096, 14336, 4096) == 16 * 17  # 32 blocks
+    assert lib.odp_linear_tiles(N.FORM_GRAM256, 4096, 14336, 0) == 0
+    assert lib.odp_linear_norm_blocks(N.FORM_GRAM256, 4096, 14336, 4096, 9) == 16 * 136
+    assert lib.odp_linear_norm_blocks(N.FORM_GRAM256, 4096, 14336, 4096, 3) == (3 * 136 + 7) // 8 * 8
 
 
 # ---------------------------------------------------------------------------
