@@ -343,8 +343,10 @@ def test_full_weight_linear_seams_match_oracle(pe_bytes):
     """bf16 full-weight linears, per-group clipping.  pe_bytes None: the
     per-example weight gradients fit in HBM, so the outer-form norm kernel
     stores them and the clipped sum runs over storage; 0: nothing is stored,
-    so the kernels pick the token-Gram norm form (short examples) and the
-    clipped-sum GEMM."""
+    so the norms take the form with fewer flops at the measured kernel
+    speeds (at these shapes the outer form: 1.6 * 48 * (64 + 96) is not
+    below 2 * 64 * 96) and the clipped sum is the GEMM over prescaled
+    activations.  The token-Gram kernels are covered in test_gpu_linear."""
     print(f"drop-in full-weight linears: linear_pe_bytes={pe_bytes}", flush=True)
     g = torch.Generator().manual_seed(21)
     d, h = 64, 96
