@@ -227,6 +227,44 @@ __device__ __forceinline__ void ss_put8(void* dst, int64_t o, int odt, const flo
   }
 }
 
+// The sums take segments SS_SG at a time: the scales and values of a group
+// are all loaded before the first of them is accumulated, so several loads
+// are in flight per thread, and the accumulation order (and so every sum)
+// is that of one segment at a time.  Stored per-example values are read
+// once, non-temporally.
+constexpr int SS_SG = 4;
+typedef uint32_t ss_u32x4 __attribute__((ext_vector_type(4)));
+
+// Eight consecutive values at element `at` (bf16: one 16-byte load).
+template <bool BF>
+__device__ __forceinline__ void ss_load8_row(const void* pe, int64_t at, float (&v)[SS_ELEMS]) {
+  if (BF) {
+    const ss_u32x4 w = __builtin_nontemporal_load((const ss_u32x4*)((const uint16_t*)pe + at));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const f32x4_t a = __builtin_nontemporal_load((const f32x4_t*)((const float*)pe + at));
+    const f32x4_t b = __builtin_nontemporal_load((const f32x4_t*)((const float*)pe + at + 4));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+}
+
+// Eight values M elements apart from element `base` (ranks k0.. of a column).
+template <bool BF>
+__device__ __forceinline__ void ss_load8_col(const void* pe, int64_t base, int64_t M, float (&v)[SS_ELEMS]) {
+#pragma unroll
+  for (int i = 0; i < SS_ELEMS; ++i)
+    v[i] = BF ? odp_bf2f(__builtin_nontemporal_load((const uint16_t*)pe + base + i * M))
+              : __builtin_nontemporal_load((const float*)pe + base + i * M);
+}
+
 // bf16/f32 values and outputs, E a multiple of 8: a thread sums the 8
 // consecutive elements e0.. over the segments (16-byte loads for bf16).
 template <bool SECOND, bool BF>
@@ -237,26 +275,23 @@ __device__ __forceinline__ void scale_sum_rows(const void* pe, int64_t E, int64_
   float acc[SS_ELEMS], acc2[SS_ELEMS];
 #pragma unroll
   for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = 0.f;
-  for (int s = 0; s < n_seg; ++s) {
+  int s = 0;
+  for (; s + SS_SG <= n_seg; s += SS_SG) {
+    float c[SS_SG], v[SS_SG][SS_ELEMS];
+#pragma unroll
+    for (int q = 0; q < SS_SG; ++q) {
+      c[q] = (float)sc[sex[seg_first + s + q]];
+      ss_load8_row<BF>(pe, (int64_t)(s + q) * E + e0, v[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < SS_SG; ++q)
+#pragma unroll
+      for (int i = 0; i < SS_ELEMS; ++i) ss_term<SECOND, BF>(v[q][i], c[q], acc[i], acc2[i]);
+  }
+  for (; s < n_seg; ++s) {
     const float c = (float)sc[sex[seg_first + s]];
     float v[SS_ELEMS];
-    if (BF) {
-      const uint4 w = *(const uint4*)((const uint16_t*)pe + (int64_t)s * E + e0);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(ww[i] << 16);
-        v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
-      }
-    } else {
-      const f32x4_t a = *(const f32x4_t*)((const float*)pe + (int64_t)s * E + e0);
-      const f32x4_t b = *(const f32x4_t*)((const float*)pe + (int64_t)s * E + e0 + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = a[i];
-        v[4 + i] = b[i];
-      }
-    }
+    ss_load8_row<BF>(pe, (int64_t)s * E + e0, v);
 #pragma unroll
     for (int i = 0; i < SS_ELEMS; ++i) ss_term<SECOND, BF>(v[i], c, acc[i], acc2[i]);
   }
@@ -290,13 +325,23 @@ __device__ __forceinline__ void scale_sum_cols(const void* pe, int64_t E, int64_
   float acc[SS_ELEMS], acc2[SS_ELEMS];
 #pragma unroll
   for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = 0.f;
-  for (int s = 0; s < n_seg; ++s) {
-    const float c = (float)sc[sex[seg_first + s]];
-    const int64_t base = (int64_t)s * E + e_first;
-    float v[SS_ELEMS];
+  int s = 0;
+  for (; s + SS_SG <= n_seg; s += SS_SG) {
+    float c[SS_SG], v[SS_SG][SS_ELEMS];
 #pragma unroll
-    for (int i = 0; i < SS_ELEMS; ++i)
-      v[i] = BF ? odp_bf2f(((const uint16_t*)pe)[base + i * M]) : ((const float*)pe)[base + i * M];
+    for (int q = 0; q < SS_SG; ++q) {
+      c[q] = (float)sc[sex[seg_first + s + q]];
+      ss_load8_col<BF>(pe, (int64_t)(s + q) * E + e_first, M, v[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < SS_SG; ++q)
+#pragma unroll
+      for (int i = 0; i < SS_ELEMS; ++i) ss_term<SECOND, BF>(v[q][i], c[q], acc[i], acc2[i]);
+  }
+  for (; s < n_seg; ++s) {
+    const float c = (float)sc[sex[seg_first + s]];
+    float v[SS_ELEMS];
+    ss_load8_col<BF>(pe, (int64_t)s * E + e_first, M, v);
 #pragma unroll
     for (int i = 0; i < SS_ELEMS; ++i) ss_term<SECOND, BF>(v[i], c, acc[i], acc2[i]);
   }
