@@ -67,13 +67,23 @@ def _same(a, b):
         assert torch.equal(u, v), i
 
 
+def test_full_weight_second_moment_without_storage_raises():
+    """Second moments of full weights need every example's gradient; with no
+    room to store them (linear_pe_bytes=0) the plan refuses at build time
+    with a clear error rather than return a partial result."""
+    print("rebind: second moment without stored full-weight gradients", flush=True)
+    leaves, clip = _spec([0.5, 0.8])
+    seg = Segments.padded(4, 64, [64, 10, 33, 64])
+    l1, n1, m1 = _inputs(1, gram=False)
+    with pytest.raises(ValueError, match="need their per-example gradients stored"):
+        GhostPlan(clip=clip, lora_sites=l1, linear_sites=n1, materialized=m1, segments=seg, leaves=leaves,
+                  device=DEV, second_moment=True, linear_pe_bytes=0)
+
+
 @pytest.mark.parametrize("keyed", [False, True])
-@pytest.mark.parametrize("pe_bytes", [None, 0])
-@pytest.mark.parametrize("second_moment", [False, True])
+@pytest.mark.parametrize("pe_bytes,second_moment", [(None, False), (0, False), (None, True)])
 def test_rebind_equals_fresh_plan(pe_bytes, second_moment, keyed):
     print(f"rebind: pe_bytes={pe_bytes} second_moment={second_moment} keyed={keyed}", flush=True)
-    if second_moment and pe_bytes == 0:
-        pytest.skip("second moments of full weights need their per-example gradients stored")
     leaves, clip1 = _spec([0.5, 0.8])
     _, clip2 = _spec([0.3, 1.1])  # thresholds change between calls (adaptive clipping)
     seg = Segments.padded(4, 64, [64, 10, 33, 64])
