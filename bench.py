@@ -55,6 +55,9 @@ def parse_args():
                     help="c4: auto = the engine's choice (fewer flops at the measured kernel speeds, outer form "
                          "with stored gradients while the budget lasts); rule = Gram where T^2 < d_in*d_out, else "
                          "outer (ties outer), forced per linear type")
+    ap.add_argument("--second-moment", action="store_true",
+                    help="c4: also sum the squared clipped per-example gradients (second_moment=True); "
+                         "sites without stored gradients then take the moments kernel")
     ap.add_argument("--serial", action="store_true",
                     help="launch every table on one stream (no side streams for the projection and factor "
                          "stages)")
@@ -73,6 +76,8 @@ def kernel_label(stage, key):
         return {1: "k_lin_gram_norm", 2: "k_lin_gram2_norm"}.get(key, "k_lin_outer_norm")
     if stage == "lin_prescale":
         return "k_lin_prescale"
+    if stage == "lin_moments":
+        return "k_lin_moments"
     if stage == "lin_sum":  # keyed by prescale chunk, None for in-register scaling
         return f"k_lin_clip_sum<{'false' if key is None else 'true'}>"
     if key is None:
@@ -370,7 +375,7 @@ def setup_c4(args, dev):
     clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=thr, effective=math.sqrt(sum(v * v for v in thr)),
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=dev,
-                     linear_pe_bytes=pe_bytes)
+                     linear_pe_bytes=pe_bytes, second_moment=args.second_moment)
     # Algorithmic flops of the C4 step: per example and weight the cheaper
     # norm form, min(2 L d_in d_out, 2 L^2 (d_in + d_out)), plus the clipped
     # sum's 2 L d_in d_out, whichever kernels run.
@@ -385,6 +390,7 @@ def setup_c4(args, dev):
         "global_batch": B, "seq_len": T, "layers": args.layers,
         "thresholds": C4_THRESHOLDS, "parallelism": "single GPU",
         "norm_form": args.norm_form,
+        "second_moment": args.second_moment,
         "norm_forms": {n: ("gram" if f == N.FORM_GRAM else "outer") for n, f in forms.items()} or "engine",
         "stored_per_example_gb": round(plan.lin_pe.numel() * 2 / 2**30, 1),
     }
@@ -425,7 +431,8 @@ def main():
     B = args.batch
     plan.serial = args.serial
     # Stages with no launch in this plan record no events.
-    present = {("lin_sum" if i[0] == "lin_prescale" else i[0]) for i in plan.launch_info} | {"clip", "noise"}
+    present = ({("lin_sum" if i[0] in ("lin_prescale", "lin_moments") else i[0]) for i in plan.launch_info}
+               | {"clip", "noise"})
     stages = tuple(s for s in stages if s in present)
     n_params = sum(math.prod(lf.shape) for lf in plan.leaves)
     k0 = key(42)

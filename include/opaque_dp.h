@@ -329,6 +329,8 @@ enum {
                         1 when an entry of some M_s is non-finite, or 0     */
   ODP_LN_SCRATCH = 17,/* GRAM256 sqnorm: address of the fp32 scratch of the
                         problem ([n_seg][slots][65536], 16-byte aligned)    */
+  ODP_LN_OUT2 = 18,  /* moments: address of the second moment [d_out][d_in]
+                        (output dtype of ODP_LN_FLAGS) or 0                 */
   ODP_LN_FIELDS = 20
 };
 
@@ -380,6 +382,24 @@ int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
                            const int32_t* seg_row_start, const int32_t* seg_row_len,
                            const int32_t* seg_example, const double* scales, int32_t n_ex,
                            int32_t n_groups, float normalize_by, int32_t prescaled);
+/* ---- odp_linear_moments: clipped first and second moments ---------------
+ * For each problem (rows as for the clipped sum, plus ODP_LN_OUT2) and each
+ * element of the weight: with m = bf16(M_s[o][i]) (0 where non-finite),
+ * y_s = bf16(c_s m) and
+ *   out[o][i]  = round_out(sum_s y_s),  out2[o][i] = round_out(sum_s bf16(y_s^2)),
+ * each sum in fp32 over the segments in order and then divided by
+ * normalize_by in the output dtype when it is not 1.  These are the
+ * reference's clipped gradient and clipped squared gradient with
+ * second_moment=True (clipping/_clipped_fun.py:675-683,777-782,821-824),
+ * bit-identical to odp_linear_sqnorm's bf16 store of each M_s followed by
+ * odp_scale_sum, without storing M_s.  ODP_LN_OUT2 = 0 writes the first
+ * moment only.  One workgroup per 256 x 128 output tile
+ * (odp_linear_moments_blocks, padded to a multiple of 8).                  */
+int64_t odp_linear_moments_blocks(int64_t d_in, int64_t d_out);
+int odp_linear_moments(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                       int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
+                       const int32_t* seg_row_len, const int32_t* seg_example, const double* scales,
+                       int32_t n_ex, int32_t n_groups, float normalize_by);
 
 /* ---- odp_gaussian_noise --------------------------------------------------
  * out[i] = round_out(in[i] + sigma * sqrt(2) * erfinv(2u - 1)) for element

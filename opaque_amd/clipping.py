@@ -692,7 +692,7 @@ class _ClipEngine:
         for r in recs:
             if r.w_obj is not None and r.segments is not None:
                 kw = obj_leaf[id(r.w_obj)]
-                if (not self.second_moment and r.x.dtype == r.g.dtype == leaves[kw].dtype == torch.bfloat16
+                if (r.x.dtype == r.g.dtype == leaves[kw].dtype == torch.bfloat16
                         and supports_rows(r.x) and supports_rows(r.g)):
                     lins.append(LinearSite(x=r.x, g=r.g, w_leaf=kw, segments=r.segments, index=r.w_index))
                 else:
@@ -702,7 +702,7 @@ class _ClipEngine:
             if r.w_obj is not None:
                 kw = obj_leaf[id(r.w_obj)]
                 t_rows = r.x[0].numel() // r.x.shape[-1]
-                if (t_rows == seq and r.x.shape[0] == n and not self.second_moment
+                if (t_rows == seq and r.x.shape[0] == n
                         and r.x.dtype == r.g.dtype == leaves[kw].dtype == torch.bfloat16
                         and supports_rows(r.x) and supports_rows(r.g)):
                     lins.append(LinearSite(x=r.x, g=r.g, w_leaf=kw))

@@ -460,7 +460,7 @@ def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_
 
 
 # Stages launched after the clip factors, in table order.
-_AFTER_CLIP = ("scale_sum", "lin_prescale", "lin_sum")
+_AFTER_CLIP = ("scale_sum", "lin_prescale", "lin_sum", "lin_moments")
 
 
 class GhostPlan:
@@ -478,6 +478,9 @@ class GhostPlan:
     reference's accumulation dtype when a leaf is float64 or
     compute_dtype=float64); ``sum_f64``: the clipped sums of stored
     gradients accumulate in float64 (compute_dtype=float64).
+    ``second_moment``: the plan also sums the squared clipped per-example
+    gradients; full-weight sites whose gradients are not stored then take
+    the moments kernel instead of the clipped-sum GEMM (both sums in float32).
     """
 
     def __init__(
@@ -946,8 +949,14 @@ class GhostPlan:
                 mask_words += v.n_seg * ((t.shape[1] + 31) // 32)
             return masks[key][2]
 
+        # With second moments, sites without stored gradients take the
+        # moments kernel (odp_linear_moments), which forms each M_s tile and
+        # zeroes its non-finite entries itself: only their Gram-form norms
+        # read the masks.
+        lin_mom = {i for i in range(len(lins)) if i not in lin_pe and self.second_moment}
         site_mask = {i: (mask_of(lin_x[i], lin_view[i]), mask_of(lin_g[i], lin_view[i]))
-                     for i in range(len(lins)) if i not in lin_pe}
+                     for i in range(len(lins))
+                     if i not in lin_pe and (i not in lin_mom or lin_form[i] != N.FORM_OUTER)}
         self.nf_mask = torch.empty(max(mask_words, 1), dtype=torch.int32, device=dev)
         self._has_masks = mask_words > 0
 
@@ -959,9 +968,6 @@ class GhostPlan:
             nft.add({N.NF_P: t.data_ptr(), N.NF_LDP: t.stride(0), N.NF_D: t.shape[1],
                      N.NF_SEG_FIRST: v.first, N.NF_NSEG: v.n_seg, N.NF_MASK: mask_addr(off)},
                     int(lib.odp_nonfinite_blocks(t.shape[1], v.n_seg)), v.valid * t.shape[1] * 2)
-        if self.second_moment and len(lin_pe) < len(lins):
-            raise ValueError("second moments of full-weight linear sites need their per-example "
-                             "gradients stored (outer form, within linear_pe_bytes)")
 
         # Clipped sums read X' = c_i x_t (odp_linear_prescale) from a scratch
         # buffer, one X' per (activation, group, class), filled chunk by chunk
@@ -972,7 +978,7 @@ class GhostPlan:
         cur: dict[tuple, tuple[int, int]] = {}
         cur_bytes = xs_bytes = 0
         for i, ls in enumerate(lins):
-            if i in lin_pe:
+            if i in lin_pe or i in lin_mom:
                 site_chunk.append(None)
                 continue
             x, lf = lin_x[i], self.leaves[ls.w_leaf]
@@ -1008,6 +1014,7 @@ class GhostPlan:
         self.gram_scr = (torch.empty(scr_total // 4, dtype=torch.float32, device=dev) if scr_total
                          else None)
         lsum = _Table(N.LN_FIELDS)
+        lmom = _Table(N.LN_FIELDS)
         for i, ls in enumerate(lins):
             x, g = lin_x[i], lin_g[i]
             d_in, d_out = x.shape[1], g.shape[1]
@@ -1037,6 +1044,13 @@ class GhostPlan:
             lf = self.leaves[ls.w_leaf]
             out = self.out[ls.w_leaf] if ls.index is None else self.out[ls.w_leaf][ls.index]
             flags = dtype_code(lf.out_dtype) | (lf.group << 8) | (lf.cls << 24)
+            if i in lin_mom:
+                o2 = self.out2[ls.w_leaf] if ls.index is None else self.out2[ls.w_leaf][ls.index]
+                lmom.add({**common, N.LN_OUT: out.data_ptr(), N.LN_OUT2: o2.data_ptr(), N.LN_FLAGS: flags},
+                         int(lib.odp_linear_moments_blocks(d_in, d_out)),
+                         valid * (d_in + d_out) * 2 + 2 * d_in * d_out * out.element_size(),
+                         2 * valid * d_in * d_out)
+                continue
             row, into = {**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags}, lsum
             if site_chunk[i] is not None:
                 c, k = site_chunk[i]
@@ -1114,6 +1128,7 @@ class GhostPlan:
             tabs.append(("lin_prescale", c, xs_pre[c]))
             tabs.append(("lin_sum", c, xs_sum[c]))
         tabs.append(("lin_sum", None, lsum))
+        tabs.append(("lin_moments", None, lmom))
         tab_idx = []
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
@@ -1550,8 +1565,8 @@ class GhostPlan:
         ``events`` may map a stage name ("project", "factor_project",
         "factor", "sqnorm", "nonfinite", "lin_norm", "clip", "scale_sum", "lin_sum") to a
         (start, end) pair of torch.cuda.Event that are recorded around that
-        stage's launches ("lin_sum" spans the clipped sums and their
-        prescale launches).  ``launch_log``, when a
+        stage's launches ("lin_sum" spans the clipped sums of full weights:
+        their prescale, GEMM and moments launches).  ``launch_log``, when a
         list, receives one (stage, key, start, end) entry per table launch
         with freshly recorded timing events, in ``launch_info`` order.
         """
@@ -1647,7 +1662,7 @@ class GhostPlan:
         if "clip" in ev:
             ev["clip"][1].record()
         post = [t for t in self.tables if t[5] > 0 and t[0] in _AFTER_CLIP]
-        stage = [("lin_sum" if t[0] == "lin_prescale" else t[0]) for t in post]
+        stage = [("lin_sum" if t[0] in ("lin_prescale", "lin_moments") else t[0]) for t in post]
         for idx, (name, dt, probs, ws, n, total) in enumerate(post):
             st = stage[idx]
             if st in ev and st not in stage[:idx]:
@@ -1668,6 +1683,11 @@ class GhostPlan:
                                                    self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
                                                    self.n_groups, float(self.clip.normalize_by),
                                                    0 if dt is None else 1), name)
+            elif name == "lin_moments":
+                N.check(lib.odp_linear_moments(stream, probs.data_ptr(), ws.data_ptr(), n, total,
+                                               self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                               self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
+                                               self.n_groups, float(self.clip.normalize_by)), name)
             if end_ev is not None:
                 end_ev.record()
             if st in ev and st not in stage[idx + 1:]:

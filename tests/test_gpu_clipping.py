@@ -385,6 +385,54 @@ def test_full_weight_linear_seams_match_oracle(pe_bytes):
 
 
 @pytest.mark.parametrize("pe_bytes", [None, 0])
+def test_full_weight_second_moment_matches_oracle(pe_bytes):
+    """clipped_grad(second_moment=True) over bf16 full-weight seams: the
+    reference squares every clipped per-example gradient and sums the squares
+    (_clipped_fun.py:675-683,777-782).  pe_bytes None: stored gradients and
+    the scale-sum; 0: nothing stored, the moments kernel forms each example's
+    gradient tile on the fly.  Both moments rel 2e-2 vs the oracle, group
+    norms rel 2e-2, per-example clip masks equal away from the threshold."""
+    print(f"drop-in full-weight second moment: linear_pe_bytes={pe_bytes}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    d, h, n, T = 64, 96, 8, 40
+    params = {"up": (torch.randn(h, d, generator=g) / d**0.5).to(torch.bfloat16),
+              "down": (torch.randn(d, h, generator=g) / h**0.5).to(torch.bfloat16)}
+
+    def make(lin):
+        def loss(p, xi, yi):
+            u = torch.nn.functional.gelu(lin(xi, p["up"], None))
+            return ((lin(u, p["down"], None).float() - yi.float()) ** 2).mean()
+
+        return loss
+
+    def plain(x, W, b):
+        return torch.nn.functional.linear(x, W, b)
+
+    x = (torch.randn(n, T, d, generator=g) * torch.logspace(-1, 0.5, n).view(n, 1, 1)).to(torch.bfloat16)
+    y = torch.randn(n, T, d, generator=g).to(torch.bfloat16)
+    pg = per_group(params, up=0.05, down=0.08)
+    fn, st = clipped_grad(make(capture.linear), clipping_norm=pg, batch_argnums=(1, 2), return_aux=True,
+                          normalize_by=4.0, second_moment=True)
+    if pe_bytes is not None:
+        fn.engine.plan_options["linear_pe_bytes"] = pe_bytes
+    (out, aux), _ = fn({k: v.to(DEV) for k, v in params.items()}, x.to(DEV), y.to(DEV), state=st)
+    assert len(fn.engine._discovery[1].eligible) == 2
+    tables = {t[0] for t in fn.engine._plan.tables if t[5] > 0}
+    assert ("lin_moments" in tables) == (pe_bytes == 0), tables
+    ref, raux = dp_ref.clipped_grad(make(plain), params, (x, y), clipping_norm=pg, normalize_by=4.0,
+                                    second_moment=True)
+    for k in params:
+        assert rel(out.grads.pytree[k], ref[k]) <= 2e-2, (k, rel(out.grads.pytree[k], ref[k]))
+        assert rel(out.squared_grads.pytree[k], raux["squared"][k]) <= 2e-2, k
+    for name, v in raux["group_norms"].items():
+        assert rel(aux.group_norms[name], v) <= 2e-2
+        thr = {"up": 0.05, "down": 0.08}[name]
+        far = ((v.double() - thr).abs() / thr) > 1e-3
+        got = aux.group_norms[name].cpu() > thr
+        assert torch.equal(got[far], (v > thr)[far]), name
+
+
+@pytest.mark.parametrize("pe_bytes", [None, 0])
 def test_full_weight_non_finite_activation(pe_bytes):
     """A NaN in one example's activations: the reference zeroes the non-finite
     entries of that example's weight gradient (nan_to_num,

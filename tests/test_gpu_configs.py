@@ -177,29 +177,37 @@ def _c4_norms(B, T, sites):
     return norms
 
 
-def _c4_sums(B, T, sites, fac):
+def _c4_sums(B, T, sites, fac, squares=False):
     """The reference's clipped sum from per-example M_s: M_s rounded to bf16 as
     vmap(grad) stores it, each scale.to(bf16) * M_s rounded to bf16, fp32 sum,
-    bf16, / 8."""
-    sums = []
+    bf16, / 8.  With squares, also the second moment: each clipped term
+    squared in bf16, summed the same way (_clipped_fun.py:675-683,777-782)."""
+    sums, sums2 = [], []
     for k, (_, x, g) in enumerate(sites):
-        acc = None
+        acc = acc2 = None
         for s in range(B):
             m = torch.matmul(g[s * T : (s + 1) * T].float().t(), x[s * T : (s + 1) * T].float()).to(torch.bfloat16)
-            t = (fac[k, s].to(DEV) * m).float()
+            y = fac[k, s].to(DEV) * m
+            t = y.float()
             acc = t if acc is None else acc + t
+            if squares:
+                t2 = y.square().float()
+                acc2 = t2 if acc2 is None else acc2 + t2
         sums.append((acc.to(torch.bfloat16) / 8.0).cpu())
-    return sums
+        if squares:
+            sums2.append((acc2.to(torch.bfloat16) / 8.0).cpu())
+    return (sums, sums2) if squares else sums
 
 
-@pytest.mark.parametrize("path", ["stored", "gemm", "gram_gate_down"])
+@pytest.mark.parametrize("path", ["stored", "gemm", "gram_gate_down", "moments"])
 def test_config_c4_layer(path):
     """C4 at its workload: one full Llama-3-8B layer (7 full-weight linears),
     batch 8 x 4096, PerGroup with 7 thresholds (one per linear type), on the
-    stored path, the clipped-sum GEMM path and with gate/down forced to the
-    token-Gram norms.  Group norms rel 2e-3 and the clipped sums rel 2e-2
-    against a plain fp32 reference; one example of k also against the fp64
-    CPU oracle."""
+    stored path, the clipped-sum GEMM path, with gate/down forced to the
+    token-Gram norms, and with second moments and nothing stored (the
+    moments kernel).  Group norms rel 2e-3 and the clipped sums (and second
+    moments) rel 2e-2 against a plain fp32 reference; one example of k also
+    against the fp64 CPU oracle."""
     print(f"C4 layer: path={path}", flush=True)
     B, T, sites = _c4_layer(seed=44)
     shapes = [(g.shape[1], x.shape[1]) for _, x, g in sites]
@@ -214,7 +222,7 @@ def test_config_c4_layer(path):
     clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=C, effective=math.sqrt(sum(c * c for c in C)), normalize_by=8.0,
                     guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=Segments.padded(B, T), leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
-                     linear_pe_bytes=None if path == "stored" else 0)
+                     linear_pe_bytes=None if path == "stored" else 0, second_moment=path == "moments")
     res = plan.run()
     torch.cuda.synchronize()
     kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
@@ -227,7 +235,14 @@ def test_config_c4_layer(path):
 
     fac = torch.stack([dp_ref.finalize(torch.tensor(C[k], dtype=torch.float64) / norms[k], torch.bfloat16, rnd, True)
                        for k in range(len(sites))]).to(torch.bfloat16)
-    sums = _c4_sums(B, T, sites, fac)
+    sums, sums2 = _c4_sums(B, T, sites, fac, squares=True) if path == "moments" else (_c4_sums(B, T, sites, fac),
+                                                                                        None)
+    if path == "moments":
+        assert {t[0] for t in plan.tables if t[5] > 0} >= {"lin_moments"}
+        assert not any(t[0] in ("lin_sum", "lin_prescale") and t[5] > 0 for t in plan.tables)
+        for k in range(len(sites)):
+            want, got = sums2[k].double(), res.second_moment[k].double().cpu()
+            assert (got - want).norm() <= 2e-2 * want.norm(), (k, ((got - want).norm() / want.norm()).item())
     got_n = res.group_norms.double().cpu()
     assert torch.allclose(got_n, norms, rtol=2e-3), (got_n / norms - 1).abs().max()
     for k in range(len(sites)):

@@ -333,14 +333,16 @@ def test_stored_linear_gradients_within_a_budget():
         assert torch.equal(res["part"][0][k], res["all"][0][k])
 
 
-def test_stored_linear_gradients_second_moment():
-    print("stored linear gradients: second moment", flush=True)
+@pytest.mark.parametrize("pe_bytes", [None, 0])
+def test_linear_gradients_second_moment(pe_bytes):
+    """Second moments of full weights, with the per-example gradients stored
+    (scale-sum over storage) or not (the moments kernel): both against the
+    oracle's per-example gradients, clipped and squared in bf16."""
+    print(f"linear gradients: second moment, linear_pe_bytes={pe_bytes}", flush=True)
     seg, leaves, lins, clip = _multi_site(seed=29)
-    with pytest.raises(ValueError, match="second moments"):
-        GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
-                  second_moment=True, linear_pe_bytes=0)
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=DEV,
-                     second_moment=True)
+                     second_moment=True, linear_pe_bytes=pe_bytes)
+    assert (plan.lin_pe.numel() > 0) == (pe_bytes is None)
     r = plan.run()
     torch.cuda.synchronize()
     scales = r.scales.cpu()

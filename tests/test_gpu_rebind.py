@@ -67,21 +67,47 @@ def _same(a, b):
         assert torch.equal(u, v), i
 
 
-def test_full_weight_second_moment_without_storage_raises():
-    """Second moments of full weights need every example's gradient; with no
-    room to store them (linear_pe_bytes=0) the plan refuses at build time
-    with a clear error rather than return a partial result."""
+def test_full_weight_second_moment_without_storage():
+    """Second moments of full weights whose per-example gradients are not
+    stored (linear_pe_bytes=0): the moments kernel forms each example's tile
+    of M_s, rounds it to bf16 as the outer-norm kernel stores it and sums
+    c_s m and bf16((c_s m)^2) per segment in order, so it must equal the
+    stored path (outer norm with the bf16 store, then the scale-sum) bit for
+    bit: first and second moments, norms and scales.  One example holds a
+    NaN activation and another a pair of finite values whose product
+    overflows float32; the reference zeroes both by nan_to_num
+    (clipping/_pytree.py:520-527); one segment is empty."""
     print("rebind: second moment without stored full-weight gradients", flush=True)
     leaves, clip = _spec([0.5, 0.8])
-    seg = Segments.padded(4, 64, [64, 10, 33, 64])
+    seg = Segments.padded(4, 64, [64, 0, 33, 64])
     l1, n1, m1 = _inputs(1, gram=False)
-    with pytest.raises(ValueError, match="need their per-example gradients stored"):
-        GhostPlan(clip=clip, lora_sites=l1, linear_sites=n1, materialized=m1, segments=seg, leaves=leaves,
-                  device=DEV, second_moment=True, linear_pe_bytes=0)
+    xl, g0 = n1[0].x.clone(), n1[0].g.clone()
+    xl[5, 17] = float("nan")  # example 0
+    # Example 2, row 131: one entry of M_s is 1e40 (inf in float32); the
+    # rest of the row's products stay small enough to square.
+    xl[131] *= 1e-3
+    g0[131] *= 1e-3
+    xl[131, 40], g0[131, 9] = 1e20, 1e20
+    n1 = [LinearSite(xl, g0, 4, N.FORM_OUTER), LinearSite(xl, n1[1].g, 5, N.FORM_OUTER)]
+    kw = dict(clip=clip, lora_sites=l1, linear_sites=n1, materialized=m1, segments=seg, leaves=leaves,
+              device=DEV, second_moment=True)
+    stored = GhostPlan(linear_pe_bytes=None, **kw)
+    assert stored.lin_pe.numel() > 0
+    want = _snapshot(stored.run())
+    plan = GhostPlan(linear_pe_bytes=0, **kw)
+    assert plan.lin_pe.numel() == 0
+    assert any(t[0] == "lin_moments" and t[5] > 0 for t in plan.tables)
+    assert not any(t[0] in ("lin_sum", "lin_prescale") and t[5] > 0 for t in plan.tables)
+    got = plan.run()
+    torch.cuda.synchronize()
+    _same(_snapshot(got), want)
+    for k in (4, 5):
+        assert torch.isfinite(got.leaves[k].float()).all() and torch.isfinite(got.second_moment[k].float()).all()
+        assert got.second_moment[k].abs().sum() > 0
 
 
 @pytest.mark.parametrize("keyed", [False, True])
-@pytest.mark.parametrize("pe_bytes,second_moment", [(None, False), (0, False), (None, True)])
+@pytest.mark.parametrize("pe_bytes,second_moment", [(None, False), (0, False), (None, True), (0, True)])
 def test_rebind_equals_fresh_plan(pe_bytes, second_moment, keyed):
     print(f"rebind: pe_bytes={pe_bytes} second_moment={second_moment} keyed={keyed}", flush=True)
     leaves, clip1 = _spec([0.5, 0.8])
