@@ -47,6 +47,10 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=None, help="default 16 (c3) / 8 (c4)")
     ap.add_argument("--seq", type=int, default=None, help="default 1024 (c3) / 4096 (c4)")
     ap.add_argument("--rank", type=int, default=16)
+    ap.add_argument("--rank-products", choices=["seam", "recompute"], default="seam",
+                    help="c3: seam = the LoRA seam keeps V = xA (its forward) and U = gB^T (its input-gradient "
+                         "backward) and the step reads them from HBM; recompute = the step projects X and G "
+                         "again (two extra passes over the narrower of each pair)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--linear-pe-gb", type=float, default=None,
                     help="c4: HBM for stored per-example weight gradients (default: free memory after "
@@ -82,7 +86,7 @@ def kernel_label(stage, key):
         return f"k_lin_clip_sum<{'false' if key is None else 'true'}>"
     if key is None:
         return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "nonfinite": "k_nonfinite_cols",
-                "pack": "k_pack_factors",
+                "pack": "k_pack_factors", "planes": "k_pack_planes",
                 "factor_project": "k_factor_project_bf16"}[stage]
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]
@@ -233,35 +237,46 @@ def cpu_baseline(r, seed, lengths):
 def setup_c3(args, dev):
     """C3: captured LoRA seams, AUTO-S, one clip group."""
     from opaque_amd import _native as N
-    from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments, leaves_key, plan_key
+    from opaque_amd.engine import LORA_PTRS, ClipSpec, GhostPlan, LeafOut, LoraSite, Segments, leaves_key, plan_key
     from opaque_amd.guard import guard_constants, leaf_guards
 
     B, T, r = args.batch, args.seq, args.rank
     lengths, sites = build_workload(args.layers, B, T, r, args.seed, dev)
     seg = Segments.padded(B, T, lengths)
+    seam = args.rank_products == "seam"
     leaves, lsites, shapes = [], [], []
     for name, x, gt, A, Bm in sites:
         ia, ib = len(leaves), len(leaves) + 1
         leaves += [LeafOut(tuple(A.shape), torch.bfloat16), LeafOut(tuple(Bm.shape), torch.bfloat16)]
         shapes += [tuple(A.shape), tuple(Bm.shape)]
-        lsites.append(LoraSite(x, gt, A, Bm, 2.0, a_leaf=ia, b_leaf=ib))
+        # The seam's V = x A (LoRA forward) and U = g B^T (its dx backward),
+        # made here as the model would, before the timed region; the step
+        # reads them from HBM.
+        v = torch.matmul(x, A) if seam else None
+        u = torch.matmul(gt, Bm.t().contiguous()) if seam else None
+        lsites.append(LoraSite(x, gt, A, Bm, 2.0, a_leaf=ia, b_leaf=ib, v=v, u=u))
     _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
     rel, ab = guard_constants(torch.bfloat16, rnd)
     clip = ClipSpec(mode=N.CLIP_AUTOS, thresholds=[1.0], effective=1.0, gamma=0.01,
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev)
     valid = sum(lengths)
-    flops = 3 * 2 * valid * r * sum(d_in + d_out for d_in, d_out in LAYER_SHAPES.values()) * args.layers
+    # Per valid token and linear: the dA and dB products (2 N r (d_in + d_out)
+    # each); recomputing V and U adds the prep term, 2 N r (d_in + d_out).
+    terms = 2 if seam else 3
+    flops = terms * 2 * valid * r * sum(d_in + d_out for d_in, d_out in LAYER_SHAPES.values()) * args.layers
     config = {
         "workload": "C3: Llama-3-8B-shaped LoRA r=16, 32 layers x 7 linears, batch 16 x seq 1024, "
                     "ragged lengths U[256,1024], AUTO-S R=1 gamma=0.01, noise multiplier 1.0",
         "global_batch": B, "seq_len": T, "layers": args.layers, "rank": r,
         "valid_tokens": valid, "lengths": lengths, "parallelism": "single GPU",
+        "rank_products": ("from the seam (V = xA kept by the LoRA forward, U = gB^T by its dx backward; "
+                          "read from HBM in the step)" if seam else "recomputed in the step (V = XA, U = GB^T)"),
     }
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B LoRA r=16"
 
     lkey = leaves_key(leaves)
-    ptrs = torch.empty(4 * len(lsites), dtype=torch.int64)
+    ptrs = torch.empty(LORA_PTRS * len(lsites), dtype=torch.int64)
 
     def rebind_once():
         """What a call with new inputs of this structure costs the host
@@ -272,7 +287,8 @@ def setup_c3(args, dev):
             raise RuntimeError("the C3 plan refused its own inputs")
 
     plan.bench_rebind = rebind_once
-    return plan, 1.0 / B, config, metric, flops, ("project", "factor_project", "factor", "clip", "scale_sum", "noise"), "hbm"
+    return (plan, 1.0 / B, config, metric, flops,
+            ("planes", "project", "factor_project", "factor", "clip", "scale_sum", "noise"), "hbm")
 
 
 def dropin_overhead(args, dev, step_ms):

@@ -17,7 +17,7 @@
  * The reference (JetBrains-Research/opaque) is Python; these entry points
  * replace the following internals of its DP-SGD hot path
  * (paths relative to packages/):
- *   odp_project + odp_seg_factor_project + odp_seg_factor
+ *   odp_project or odp_pack_planes, odp_seg_factor_project, odp_seg_factor
  *                                 -> per-sample LoRA factor gradients,
  *       opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176
  *       (dA[i] = s X[i]^T (G[i] B^T), dB[i] = s (X[i] A)^T G[i]) and the
@@ -104,6 +104,34 @@ enum {
 int64_t odp_pack_factors_blocks(int64_t d_in);
 int odp_pack_factors(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                      int32_t n_prob, int32_t total_blocks);
+
+/* ---- odp_pack_planes: Q^T[k][row] = S[row][k] ----------------------------
+ * Lays a rank-space product that the seam already computed (V = X A from
+ * the LoRA forward, U = G B^T from its input-gradient backward) out as the
+ * plane odp_project would have written: rows [0, n_rows), rows outside the
+ * problem's segments 0, one plane [k][ldq] at ODP_PL_DST in the activation
+ * dtype.  With it the factor kernels read each activation and output
+ * gradient once.  The reference computes both products a second time in its
+ * per-sample rule (opaque-patches/src/opaque/api/patches/kernels/lora.py:
+ * 157-176: grad_out @ B.t() for dX and again per sample, X @ A); here the
+ * seam's own are reused.  One workgroup per 256 rows
+ * (odp_pack_planes_blocks).                                                 */
+enum {
+  ODP_PL_SRC = 0,     /* address of S, row-major [n_rows][r], ld = ODP_PL_LDS  */
+  ODP_PL_LDS = 1,     /* elements                                             */
+  ODP_PL_R = 2,       /* r <= 64                                              */
+  ODP_PL_DST = 3,     /* address of the plane                                 */
+  ODP_PL_LDQ = 4,     /* row pitch of the plane (elements)                    */
+  ODP_PL_NROWS = 5,
+  ODP_PL_SEG_FIRST = 6,
+  ODP_PL_NSEG = 7,
+  ODP_PL_DTYPE = 8,   /* odp_dtype of S and the plane: bf16 or f32            */
+  ODP_PL_FIELDS = 12
+};
+int64_t odp_pack_planes_blocks(int64_t n_rows);
+int odp_pack_planes(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                    int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
+                    const int32_t* seg_row_len);
 
 /* ---- odp_project: Q^T[k][row] = sum_j P[row][j] * W[k][j] --------------
  * The LoRA rank-space projections U = G B^T and V = X A for rows

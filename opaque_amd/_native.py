@@ -25,6 +25,8 @@ CLIP_AUTOS = 1
 # Problem-table field layouts (must match include/opaque_dp.h).
 PF_SRC, PF_LD0, PF_LD1, PF_DTYPES, PF_DIN, PF_R, PF_DST = range(7)
 PF_FIELDS = 8
+PL_FIELDS = 12
+PL_SRC, PL_LDS, PL_R, PL_DST, PL_LDQ, PL_NROWS, PL_SEG_FIRST, PL_NSEG, PL_DTYPE = range(9)
 PJ_FIELDS = 12
 PJ_P, PJ_LDP, PJ_D, PJ_W, PJ_R, PJ_Q, PJ_LDQ, PJ_NROWS, PJ_SEG_FIRST, PJ_NSEG = range(10)
 FT_FIELDS = 24
@@ -110,6 +112,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32, _c_i32],
     ),
+    "odp_pack_planes_blocks": (_c_i64, [_c_i64]),
+    "odp_pack_planes": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr]),
     "odp_linear_moments_blocks": (_c_i64, [_c_i64, _c_i64]),
     "odp_linear_moments": (
         _c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32]),

@@ -40,6 +40,8 @@ class SiteRecord:
     w_obj: torch.Tensor | None = None  # full-weight linear: the weight passed ([d_out, d_in])
     w_index: int | None = None  # MoE expert: slice of the stacked weight w_obj ([E, d_out, d_in])
     segments: Any = None  # MoE expert: engine Segments of x's rows (x is then [rows, d_in])
+    v: torch.Tensor | None = None  # LoRA: x A, kept from the forward ([B, *, r])
+    u: torch.Tensor | None = None  # LoRA: g B^T, kept from the backward ([B, *, r])
 
     @property
     def kind(self) -> str:
@@ -82,11 +84,17 @@ def _plain(x, W, A, B, scaling, bias):
 
 
 class _TapLoRA(torch.autograd.Function):
-    """Physical (batch-merged) LoRA op that records x now and g in backward."""
+    """Physical (batch-merged) LoRA op that records x now and g in backward,
+    and with them the rank-space products the op computes anyway: v = x A
+    in the forward, u = g B^T in the backward (the reference's merged dX
+    forms the same grad_out @ B.t(), PAT/kernels/lora.py:157-160)."""
 
     @staticmethod
     def forward(x, W, A, B, scaling, bias, anchor, record):
-        return _plain(x, W, A, B, scaling, bias)
+        xa = x @ A
+        record.v = xa
+        out = F.linear(x, W) + scaling * (xa @ B)
+        return out if bias is None else out + bias
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -101,9 +109,10 @@ class _TapLoRA(torch.autograd.Function):
     def backward(ctx, g):
         W, A, B = ctx.saved_tensors
         ctx.record.g = g.detach()
+        gb = g @ B.t()
+        ctx.record.u = gb.detach()
         dx = None
         if ctx.needs_input_grad[0]:
-            gb = g @ B.t()
             dx = g @ W + ctx.scaling * (gb @ A.t())
         dbias = None
         if ctx.has_bias and ctx.needs_input_grad[5]:

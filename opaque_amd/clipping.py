@@ -37,6 +37,7 @@ from torch.autograd.profiler import record_function
 from opaque_amd import _native as N
 from opaque_amd.capture import CaptureSession, SiteRecord
 from opaque_amd.engine import (
+    LORA_PTRS,
     ClipSpec,
     GhostPlan,
     LeafOut,
@@ -525,8 +526,8 @@ class _ClipEngine:
         # (_clipped_fun.py:115-134): float64 on request, float32 otherwise.
         kw = dict(second_moment=self.second_moment, square_f64=square_f64,
                   sum_f64=self.compute_dtype == torch.float64, **self.plan_options)
-        if self._lora_ptrs.numel() < 4 * len(sites):
-            self._lora_ptrs = torch.empty(4 * len(sites), dtype=torch.int64)
+        if self._lora_ptrs.numel() < LORA_PTRS * len(sites):
+            self._lora_ptrs = torch.empty(LORA_PTRS * len(sites), dtype=torch.int64)
         key = plan_key(segments=segments, leaves=outs, clip=spec, lora_sites=sites, materialized=mats,
                        linear_sites=lins, device=device, leaves_key_=outs_key, lora_ptrs=self._lora_ptrs, **kw)
         plan = None
@@ -722,7 +723,7 @@ class _ClipEngine:
             )
             if kernel_ok:
                 sites.append(LoraSite(x=r.x, g=r.g, A=r.A, B=r.B, scaling=r.scaling, a_leaf=ka, b_leaf=kb,
-                                      a_transposed=r.a_transposed, b_transposed=r.b_transposed))
+                                      a_transposed=r.a_transposed, b_transposed=r.b_transposed, v=r.v, u=r.u))
             else:
                 for k, pe in _site_per_example(r, ka, kb, leaves):
                     mats.append(MaterializedLeaf(per_example=pe.reshape(n, -1), leaf=k))

@@ -46,7 +46,7 @@ void put_shape_device(std::string& out, const at::Tensor& t) {
 // Attribute names, made once (a lookup by a C string builds a new str each time).
 struct Names {
   py::str segments{"segments"}, x{"x"}, g{"g"}, A{"A"}, B{"B"}, scaling{"scaling"}, a_leaf{"a_leaf"},
-      b_leaf{"b_leaf"}, a_transposed{"a_transposed"}, b_transposed{"b_transposed"};
+      b_leaf{"b_leaf"}, a_transposed{"a_transposed"}, b_transposed{"b_transposed"}, v{"v"}, u{"u"};
 };
 const Names& names() {
   static const Names* n = new Names();  // never destroyed: outlives the interpreter's teardown order
@@ -75,14 +75,31 @@ int64_t leaf_field(PyObject* d, const py::str& name) {
   return v == Py_None ? -1 : PyLong_AsLongLong(v);
 }
 
+// An optional tensor attribute (the seam's rank-space products): its key, or
+// a marker when absent; returns its address or 0.
+int64_t put_optional(std::string& out, PyObject* d, const py::str& name) {
+  PyObject* v = field(d, name);
+  if (v == Py_None) {
+    put(out, -1);
+    return 0;
+  }
+  TORCH_CHECK(THPVariable_Check(v), "site attribute ", std::string(py::str(name)), " is not a tensor");
+  const at::Tensor& t = THPVariable_Unpack(v);
+  put_tensor(out, t);
+  return reinterpret_cast<int64_t>(t.data_ptr());
+}
+
+constexpr int64_t kPtrs = 6;  // x, g, A, B, v, u per site
+
 // Structure of a list of LoraSite objects as bytes, and per site the
-// addresses of x, g, A and B written to `ptrs` (an int64 CPU tensor of 4 x
-// the number of sites).  Returns None when a site brings its own segments
-// (the caller then takes the general path).
+// addresses of x, g, A, B, v and u (0 when absent) written to `ptrs` (an
+// int64 CPU tensor of 6 x the number of sites).  Returns None when a site
+// brings its own segments (the caller then takes the general path).
 py::object lora_signature(py::list sites, at::Tensor ptrs) {
   const int64_t n = static_cast<int64_t>(sites.size());
-  TORCH_CHECK(ptrs.scalar_type() == at::kLong && ptrs.is_contiguous() && !ptrs.is_cuda() && ptrs.numel() >= 4 * n,
-              "ptrs must be a contiguous int64 CPU tensor of at least 4 entries per site");
+  TORCH_CHECK(ptrs.scalar_type() == at::kLong && ptrs.is_contiguous() && !ptrs.is_cuda() &&
+                  ptrs.numel() >= kPtrs * n,
+              "ptrs must be a contiguous int64 CPU tensor of at least 6 entries per site");
   int64_t* P = ptrs.data_ptr<int64_t>();
   std::string sig;
   sig.reserve(static_cast<size_t>(n) * 400);
@@ -137,10 +154,13 @@ py::object lora_signature(py::list sites, at::Tensor ptrs) {
     put(sig, leaf_field(d, nm.a_leaf));
     put(sig, leaf_field(d, nm.b_leaf));
     put(sig, (PyObject_IsTrue(field(d, nm.a_transposed)) ? 1 : 0) | (PyObject_IsTrue(field(d, nm.b_transposed)) ? 2 : 0));
-    P[4 * i + 0] = xp;
-    P[4 * i + 1] = reinterpret_cast<int64_t>(g.data_ptr());
-    P[4 * i + 2] = reinterpret_cast<int64_t>(A.data_ptr());
-    P[4 * i + 3] = reinterpret_cast<int64_t>(B.data_ptr());
+    int64_t* Pi = P + kPtrs * i;
+    Pi[0] = xp;
+    Pi[1] = reinterpret_cast<int64_t>(g.data_ptr());
+    Pi[2] = reinterpret_cast<int64_t>(A.data_ptr());
+    Pi[3] = reinterpret_cast<int64_t>(B.data_ptr());
+    Pi[4] = put_optional(sig, d, nm.v);
+    Pi[5] = put_optional(sig, d, nm.u);
   }
   // The distinct activations' keys close the signature.
   put(sig, static_cast<int64_t>(xkeys.size()));

@@ -1073,6 +1073,73 @@ extern "C" int odp_pack_factors(odp_stream_t stream, const int64_t* problems, co
   return odp_check_launch("odp_pack_factors");
 }
 
+// ---------------------------------------------------------------------------
+// Rank-space products from the seam laid out as planes: one thread per row,
+// writing column k of its row to plane row k (each plane row coalesced
+// across the workgroup's threads); rows outside the segments get 0.
+// ---------------------------------------------------------------------------
+constexpr int PL_THREADS = 256;
+
+template <typename T>
+__device__ __forceinline__ void pack_plane_row(const T* __restrict__ s, T* __restrict__ d, int r, int64_t ldq,
+                                               bool in, bool vec) {
+  constexpr int V = 16 / sizeof(T);  // elements per 16-byte load
+  if (in && vec) {
+    for (int k0 = 0; k0 < r; k0 += V) {
+      const u32x4_t w = *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(s + k0);
+      T e[V];
+      __builtin_memcpy(e, &w, 16);
+#pragma unroll
+      for (int i = 0; i < V; ++i) odp_gstore(d + (int64_t)(k0 + i) * ldq, e[i]);
+    }
+    return;
+  }
+  for (int k = 0; k < r; ++k) odp_gstore(d + (int64_t)k * ldq, in ? s[k] : (T)0);
+}
+
+__global__ __launch_bounds__(PL_THREADS) void k_pack_planes(const int64_t* __restrict__ probs,
+                                                            const int32_t* __restrict__ ws, int n_prob,
+                                                            const int32_t* __restrict__ sstart,
+                                                            const int32_t* __restrict__ slen) {
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_PL_FIELDS;
+  const int64_t row = (int64_t)(bid - ws[p]) * PL_THREADS + threadIdx.x;
+  if (row >= f[ODP_PL_NROWS]) return;
+  const int seg_first = (int)f[ODP_PL_SEG_FIRST];
+  const bool in = odp_row_in_segments(row, sstart + seg_first, slen + seg_first, (int)f[ODP_PL_NSEG]);
+  const int64_t lds = f[ODP_PL_LDS], ldq = f[ODP_PL_LDQ];
+  const int r = (int)f[ODP_PL_R];
+  const uintptr_t src = (uintptr_t)f[ODP_PL_SRC];
+  if (f[ODP_PL_DTYPE] == ODP_DTYPE_BF16) {
+    // 16-byte loads when every row starts 16-byte aligned and r fills them.
+    const bool vec = ((src | (uintptr_t)(lds * 2)) & 15) == 0 && (r & 7) == 0;
+    pack_plane_row((const uint16_t*)src + row * lds, (uint16_t*)f[ODP_PL_DST] + row, r, ldq, in, vec);
+  } else {
+    const bool vec = ((src | (uintptr_t)(lds * 4)) & 15) == 0 && (r & 3) == 0;
+    pack_plane_row((const float*)src + row * lds, (float*)f[ODP_PL_DST] + row, r, ldq, in, vec);
+  }
+}
+
+extern "C" int64_t odp_pack_planes_blocks(int64_t n_rows) {
+  return n_rows <= 0 ? 0 : (n_rows + PL_THREADS - 1) / PL_THREADS;
+}
+
+extern "C" int odp_pack_planes(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                               int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
+                               const int32_t* seg_row_len) {
+  int rc = odp_check_table("odp_pack_planes", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_row_start == nullptr || seg_row_len == nullptr) {
+    odp_set_error("odp_pack_planes: null segment arrays");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_pack_planes, dim3(total_blocks), dim3(PL_THREADS), 0, odp_hip_stream(stream), problems,
+                     work_start, n_prob, seg_row_start, seg_row_len);
+  return odp_check_launch("odp_pack_planes");
+}
+
 extern "C" int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r) {
   const int64_t rows = dtype == ODP_DTYPE_BF16 ? 64 * pj_rpw((r + 15) / 16) : PJ_ROWS;
   return n_rows <= 0 ? 0 : (n_rows + rows - 1) / rows;

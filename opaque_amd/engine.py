@@ -185,6 +185,36 @@ class LoraSite:
     a_transposed: bool = False
     b_transposed: bool = False
     segments: Segments | None = None  # rows of x / g; None: the plan's segments
+    # The seam's own rank-space products, when it kept them: v = x A (its
+    # forward) and u = g B^T (its input-gradient backward), [rows, r] in
+    # x's dtype.  With both, for every site of an activation, the plan reads
+    # them instead of projecting X and G again.
+    v: torch.Tensor | None = None
+    u: torch.Tensor | None = None
+
+
+def _seam_rows(t: torch.Tensor) -> torch.Tensor:
+    """2-D row view [rows, r] of a seam product with unit column stride."""
+    t2 = t.reshape(-1, t.shape[-1])
+    return t2 if t2.stride(-1) == 1 else t2.contiguous()
+
+
+def uses_seam_products(chunk: list[LoraSite]) -> bool:
+    """Whether the sites of one activation all bring both seam products in
+    the activation's dtype, one row per activation row."""
+    x = chunk[0].x
+    dt, n_rows = x.dtype, x.numel() // max(x.shape[-1], 1)
+    for s in chunk:
+        r = s.A.shape[1]
+        for t in (s.v, s.u):
+            if t is None or t.dtype != dt or t.device != s.x.device or t.dim() < 1 or t.shape[-1] != r \
+                    or t.numel() != n_rows * r:
+                return False
+    return True
+
+
+# Addresses per LoRA site that plan_key writes to ``lora_ptrs``: x, g, A, B, v, u.
+LORA_PTRS = 6
 
 
 @dataclass
@@ -410,13 +440,13 @@ def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_
     Threshold values, gamma and normalize_by are not part of it.
 
     With the host helper built, the LoRA sites' part is its byte signature
-    (the same fields), and ``lora_ptrs`` (an int64 CPU tensor of at least 4
-    entries per LoRA site) receives the addresses of each site's x, g, A
-    and B for rebind()."""
+    (the same fields), and ``lora_ptrs`` (an int64 CPU tensor of at least
+    LORA_PTRS entries per LoRA site) receives the addresses of each site's
+    x, g, A, B, v and u (0 for a missing product) for rebind()."""
     host = _host.load()
     lora_sig = None
     if host is not None:
-        buf = lora_ptrs if lora_ptrs is not None else torch.empty(4 * len(lora_sites), dtype=torch.int64)
+        buf = lora_ptrs if lora_ptrs is not None else torch.empty(LORA_PTRS * len(lora_sites), dtype=torch.int64)
         lora_sig = host.lora_signature(list(lora_sites), buf)
     firsts: dict[int, int] = {}
     xkeys: list[tuple] = []
@@ -438,7 +468,9 @@ def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_
     else:
         lora = tuple((shared(s.x), _tensor_key(s.g), _tensor_key(s.A), s.B.shape, s.B.get_device(),
                       s.B.dtype, s.B.is_contiguous(), float(s.scaling), s.a_leaf, s.b_leaf, s.a_transposed,
-                      s.b_transposed, None if s.segments is None else _seg_key(s.segments)) for s in lora_sites)
+                      s.b_transposed, None if s.segments is None else _seg_key(s.segments),
+                      None if s.v is None else _tensor_key(s.v), None if s.u is None else _tensor_key(s.u))
+                     for s in lora_sites)
     mats = tuple((_tensor_key(m.per_example), m.leaf, _seg_key(m.segments)) for m in materialized)
     lins = tuple((shared(ls.x), _tensor_key(ls.g), ls.w_leaf, ls.form, ls.index,
                   _seg_key(ls.segments)) for ls in linear_sites)
@@ -602,7 +634,9 @@ class GhostPlan:
         # call's inputs.
         site_index = {id(s): k for k, s in enumerate(sites)}
         self._chunk_sites = [[site_index[id(s)] for s in ch] for ch in chunks]
-        self._lwx_groups = self._factor_groups(chunks)
+        # Chunks whose sites bring the seam's V and U skip the projections.
+        self._chunk_products = [uses_seam_products(ch) for ch in chunks]
+        self._lwx_groups = self._factor_groups(chunks, self._chunk_products)
         self._ext_keys = self._external_keys(chunks, len(mats), len(lins))
         ext = dict(zip(self._ext_keys, self._external_list(chunks, mats, lins)))
         self._ext = ext
@@ -795,11 +829,21 @@ class GhostPlan:
             chunk_layout.append((dt, rtot, rows_alloc, planes, base, base + per, ldq))
             q_need[dt] = base + 2 * per
         self.qbuf = {dt: torch.empty(max(n, 1), dtype=dt, device=dev) for dt, n in q_need.items()}
+        # Where each LoRA site's columns of the V and U planes lie (rank_planes).
+        self._planes_of: dict[int, tuple] = {}
+        for ci, (ch, (dt, _, _, _, vbase, ubase, ldq)) in enumerate(zip(chunks, chunk_layout)):
+            c0 = 0
+            for j, s in enumerate(ch):
+                r = s.A.shape[1]
+                self._planes_of[self._chunk_sites[ci][j]] = (dt, vbase, ubase, c0, r, ldq,
+                                                            reg.view(ch[0].segments).n_rows)
+                c0 += r
 
         # Problem tables, per activation dtype.
         # Tables are keyed by (dtype, rank blocks): one launch per key.
         pj: dict[tuple, _Table] = {}
         ft: dict[tuple, _Table] = {}
+        pl = _Table(N.PL_FIELDS)
         fused_rows: list[tuple] = []
 
         def tab(tables: dict, dt: torch.dtype, r: int, fields: int) -> _Table:
@@ -817,22 +861,28 @@ class GhostPlan:
 
             x = ext[("lx", ci)]
             d_in = x.shape[1]
-            # V = X [A_1 .. A_k]
-            wx = wx_of[ci]
-            if self._mirrored(ch, dt, v):
-                self._mirror_rows(ch[0], x, wx, ext[("lg", ci, 0)], ext[("lwb", ci, 0)], dt, v, qaddr, vbase,
-                                  ubase, ldq, planes, es, pj, ft, tab, fused_rows, slot_base)
-                continue
-            tab(pj, dt, rtot, N.PJ_FIELDS).add(
-                {
-                    N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
-                    N.PJ_W: wx.data_ptr(), N.PJ_R: rtot,
-                    N.PJ_Q: qaddr(vbase, 0),
-                    N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
-                },
-                lib.odp_project_blocks(dtype_code(dt), n_rows, rtot),
-                (valid * d_in + rtot * d_in + planes * rtot * valid) * es,
-            )
+            # The seam's own V and U, when it kept them, become the planes
+            # (odp_pack_planes); then one factor pass over X gives every
+            # site's dA and one over each G its dB, and no activation or
+            # output gradient is read twice.
+            products = self._chunk_products[ci]
+            if not products:
+                # V = X [A_1 .. A_k]
+                wx = wx_of[ci]
+                if self._mirrored(ch, dt, v):
+                    self._mirror_rows(ch[0], x, wx, ext[("lg", ci, 0)], ext[("lwb", ci, 0)], dt, v, qaddr, vbase,
+                                      ubase, ldq, planes, es, pj, ft, tab, fused_rows, slot_base)
+                    continue
+                tab(pj, dt, rtot, N.PJ_FIELDS).add(
+                    {
+                        N.PJ_P: x.data_ptr(), N.PJ_LDP: x.stride(0), N.PJ_D: d_in,
+                        N.PJ_W: wx.data_ptr(), N.PJ_R: rtot,
+                        N.PJ_Q: qaddr(vbase, 0),
+                        N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
+                    },
+                    lib.odp_project_blocks(dtype_code(dt), n_rows, rtot),
+                    (valid * d_in + rtot * d_in + planes * rtot * valid) * es,
+                )
             c0 = 0
             a_leaves = []
             for j, s in enumerate(ch):
@@ -840,6 +890,13 @@ class GhostPlan:
                 g = ext[("lg", ci, j)]
                 wb = ext[("lwb", ci, j)]
                 d_out = g.shape[1]
+                if products:
+                    for pkey, base in (("lv", vbase), ("lu", ubase)):
+                        t = ext[(pkey, ci, j)]
+                        pl.add({N.PL_SRC: t.data_ptr(), N.PL_LDS: t.stride(0), N.PL_R: r,
+                                N.PL_DST: qaddr(base, c0), N.PL_LDQ: ldq, N.PL_NROWS: n_rows,
+                                N.PL_SEG_FIRST: sf, N.PL_NSEG: n_seg, N.PL_DTYPE: dtype_code(dt)},
+                               lib.odp_pack_planes_blocks(n_rows), (valid + n_rows) * r * es)
                 if s.a_leaf is not None:
                     a_leaves.append((s.a_leaf, c0, r))
                 # dB_i^T rows: pe[s][k][m] = scaling * sum_t V[k][t] G[t][m]
@@ -854,7 +911,7 @@ class GhostPlan:
                         N.FT_LEAF0 + 1: 0 | (r << 16) | pe_bits(s.b_leaf),
                         N.FT_LEAF0 + 2: slot_base[s.b_leaf],
                     }
-                if frow is not None and self._fusable(dt, r, v, g):
+                if frow is not None and not products and self._fusable(dt, r, v, g):
                     # U and the dB rows in one pass over G, one workgroup per
                     # segment: a row per segment, so that the launch can run
                     # the longest first (the segment's pe rows start at its
@@ -873,17 +930,18 @@ class GhostPlan:
                                            + (r * d_out * es if j == 0 else 0)))
                     c0 += r
                     continue
-                # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
-                tab(pj, dt, r, N.PJ_FIELDS).add(
-                    {
-                        N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
-                        N.PJ_W: wb.data_ptr(), N.PJ_R: r,
-                        N.PJ_Q: qaddr(ubase, c0),
-                        N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
-                    },
-                    lib.odp_project_blocks(dtype_code(dt), n_rows, r),
-                    (valid * d_out + r * d_out + planes * r * valid) * es,
-                )
+                if not products:
+                    # U_i = G_i B_i^T into columns [c0, c0 + r) of the chunk's U planes.
+                    tab(pj, dt, r, N.PJ_FIELDS).add(
+                        {
+                            N.PJ_P: g.data_ptr(), N.PJ_LDP: g.stride(0), N.PJ_D: d_out,
+                            N.PJ_W: wb.data_ptr(), N.PJ_R: r,
+                            N.PJ_Q: qaddr(ubase, c0),
+                            N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
+                        },
+                        lib.odp_project_blocks(dtype_code(dt), n_rows, r),
+                        (valid * d_out + r * d_out + planes * r * valid) * es,
+                    )
                 if frow is not None:
                     tab(ft, dt, r, N.FT_FIELDS).add(frow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
                                                     (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es)
@@ -1112,7 +1170,7 @@ class GhostPlan:
         idx["seg_len"] = pack.add(seg_ln)
         idx["seg_ex"] = pack.add(seg_ex)
         self._launch: list[tuple] = []
-        tabs = [("pack", None, pft)]
+        tabs = [("pack", None, pft), ("planes", None, pl)]
         for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("project", key, pj[key]))
         tabs.append(("factor_project", None, fp))
@@ -1217,11 +1275,14 @@ class GhostPlan:
                 return False
         if not trusted:
             # The sites of a chunk read one activation (the plan projects it once).
-            for ch in chunks:
+            for ci, ch in enumerate(chunks):
                 x0 = ch[0].x
                 for s in ch[1:]:
                     if s.x.data_ptr() != x0.data_ptr() or s.x.shape != x0.shape or s.x.stride() != x0.stride():
                         return False
+                # A chunk planned on the seam's V and U needs them again.
+                if self._chunk_products[ci] and not uses_seam_products(ch):
+                    return False
         if fast is not None:
             src, n_lora = fast
             outs = list(self._alloc_outputs().values())
@@ -1248,8 +1309,7 @@ class GhostPlan:
         self._pack.refresh()
         return True
 
-    @staticmethod
-    def _ext_sources(chunks: list[list[LoraSite]], mats: list[MaterializedLeaf],
+    def _ext_sources(self, chunks: list[list[LoraSite]], mats: list[MaterializedLeaf],
                      lins: list[LinearSite]) -> dict[tuple, torch.Tensor]:
         """The input tensor each external tensor derives from."""
         src: dict[tuple, torch.Tensor] = {}
@@ -1259,6 +1319,9 @@ class GhostPlan:
                 src[("lg", ci, j)] = s.g
                 src[("lwb", ci, j)] = s.B
                 src[("la", ci, j)] = s.A
+                if self._chunk_products[ci]:
+                    src[("lv", ci, j)] = s.v
+                    src[("lu", ci, j)] = s.u
         for mi, m in enumerate(mats):
             src[("mat", mi)] = m.per_example
         for i, ls in enumerate(lins):
@@ -1269,12 +1332,13 @@ class GhostPlan:
     def _fast_map(self, chunks: list[list[LoraSite]], ext: dict[tuple, torch.Tensor], n_sites: int):
         """Where rebind's fast path finds each LoRA input address: when every
         LoRA input is read in place, the address of ("lx", c), ("lg", c, j),
-        ("lwb", c, j) and ("la", c, j) is the caller's x, g, B or A (entry
-        4 site + 0, 1, 3 or 2 of the host helper's address list).  None when
-        some input was copied at build time, or without the helper."""
+        ("lwb", c, j), ("la", c, j), ("lv", c, j) and ("lu", c, j) is the
+        caller's x, g, B, A, v or u (entry LORA_PTRS site + 0, 1, 3, 2, 4 or
+        5 of the host helper's address list).  None when some input was
+        copied at build time, or without the helper."""
         if _host.load() is None or not chunks:
             return None
-        slot = {"lx": 0, "lg": 1, "la": 2, "lwb": 3}
+        slot = {"lx": 0, "lg": 1, "la": 2, "lwb": 3, "lv": 4, "lu": 5}
         keys = self._ext_keys
         src = np.full(len(keys), -1, dtype=np.int64)
         n_lora = 0
@@ -1286,24 +1350,27 @@ class GhostPlan:
             ci = k[1]
             j = 0 if kind == "lx" else k[2]
             s = chunks[ci][j]
-            t = (s.x, s.g, s.A, s.B)[slot[kind]]
+            t = (s.x, s.g, s.A, s.B, s.v, s.u)[slot[kind]]
             if ext[k].data_ptr() != t.data_ptr():
                 return None
-            src[p] = 4 * self._chunk_sites[ci][j] + slot[kind]
+            src[p] = LORA_PTRS * self._chunk_sites[ci][j] + slot[kind]
         return src, n_lora
 
     @staticmethod
-    def _factor_groups(chunks: list[list[LoraSite]]) -> list[list[int]]:
-        """Chunks whose stacked A^T come out of one copy: same dtype and d_in."""
+    def _factor_groups(chunks: list[list[LoraSite]], products: list[bool]) -> list[list[int]]:
+        """Chunks whose stacked A^T come out of one copy: same dtype and d_in
+        (chunks that read the seam's V and U project nothing and need none)."""
         by_width: dict[tuple, list[int]] = {}
         for ci, ch in enumerate(chunks):
-            by_width.setdefault((ch[0].x.dtype, ch[0].A.shape[0]), []).append(ci)
+            if not products[ci]:
+                by_width.setdefault((ch[0].x.dtype, ch[0].A.shape[0]), []).append(ci)
         return list(by_width.values())
 
     def _external_keys(self, chunks: list[list[LoraSite]], n_mats: int, n_lins: int) -> list[tuple]:
         """Keys of the tensors _external_list returns, in its order: per LoRA
         chunk its activation rows ("lx", c) and per site of the chunk its
-        output gradient rows ("lg", c, j), B ("lwb", c, j) and A ("la", c, j);
+        output gradient rows ("lg", c, j), B ("lwb", c, j) and A ("la", c, j)
+        (and the seam's V ("lv", c, j) and U ("lu", c, j) rows when it uses them);
         materialised leaves ("mat", m) as [n_seg, n]; linear sites' rows
         ("linx", i), ("ling", i)."""
         keys = []
@@ -1311,6 +1378,8 @@ class GhostPlan:
             keys.append(("lx", ci))
             for j in range(len(ch)):
                 keys += [("lg", ci, j), ("lwb", ci, j), ("la", ci, j)]
+                if self._chunk_products[ci]:
+                    keys += [("lv", ci, j), ("lu", ci, j)]
         keys += [("mat", mi) for mi in range(n_mats)]
         for i in range(n_lins):
             keys += [("linx", i), ("ling", i)]
@@ -1324,7 +1393,7 @@ class GhostPlan:
         out: list[torch.Tensor] = []
         p = 0
         with torch.no_grad():
-            for ch in chunks:
+            for ci, ch in enumerate(chunks):
                 dt = ch[0].x.dtype
                 x = ch[0].x
                 out.append(x if direct and direct[p] else _rows(x))
@@ -1335,6 +1404,10 @@ class GhostPlan:
                     out.append(b if b.dtype == dt and b.is_contiguous() else b.to(dt).contiguous())
                     out.append(s.A)  # read in place by odp_pack_factors
                     p += 3
+                    if self._chunk_products[ci]:
+                        out.append(s.v if direct and direct[p] else _seam_rows(s.v))
+                        out.append(s.u if direct and direct[p + 1] else _seam_rows(s.u))
+                        p += 2
         return out + self._other_external(mats, lins, direct, p)
 
     def _other_external(self, mats: list[MaterializedLeaf], lins: list[LinearSite], direct: list[bool] | None,
@@ -1554,6 +1627,19 @@ class GhostPlan:
             ok = ok & (self.nf_mask == 0).all()
         return ok
 
+    def rank_planes(self, site: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The rank-space products of LoRA site ``site`` (its index in the
+        plan's site list) as the last run laid them out: V = x A and
+        U = g B^T, [n_rows, r] views of the plan's planes.  Rows outside the
+        segments are 0 or unspecified."""
+        dt, vbase, ubase, c0, r, ldq, n_rows = self._planes_of[site]
+        q = self.qbuf[dt]
+
+        def view(base: int) -> torch.Tensor:
+            return q[base + c0 * ldq : base + (c0 + r) * ldq].view(r, ldq)[:, :n_rows].t()
+
+        return view(vbase), view(ubase)
+
     def pe_views(self) -> list[torch.Tensor]:
         """The per-example factor gradients each LoRA leaf stored ([n_seg * r * M], parameter dtype)."""
         return [self.pe[dt][o : o + n] for dt, o, n in self._pe_slices]
@@ -1589,6 +1675,9 @@ class GhostPlan:
         def launch(name, dt, probs, ws, n, total, s):
             if name == "pack":
                 N.check(lib.odp_pack_factors(s, probs.data_ptr(), ws.data_ptr(), n, total), name)
+            elif name == "planes":
+                N.check(lib.odp_pack_planes(s, probs.data_ptr(), ws.data_ptr(), n, total,
+                                            self.seg_start.data_ptr(), self.seg_len.data_ptr()), name)
             elif name == "project":
                 N.check(lib.odp_project(s, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                         self.seg_start.data_ptr(), self.seg_len.data_ptr(), dt[1]), name)

@@ -35,7 +35,10 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _lora_sites(shapes, B, T, r, dtype, seed, lengths=None, g_scale=None, shared=None):
+def _lora_sites(shapes, B, T, r, dtype, seed, lengths=None, g_scale=None, shared=None, products=False):
+    """Sites of one layer; with ``products`` each also brings the seam's V = x A
+    and U = g B^T (torch.matmul on the device in the site dtype, as the
+    LoRA forward and its dx backward compute them)."""
     g = torch.Generator().manual_seed(seed)
     seg = Segments.padded(B, T, lengths)
     xs, sites, host = {}, [], []
@@ -52,7 +55,10 @@ def _lora_sites(shapes, B, T, r, dtype, seed, lengths=None, g_scale=None, shared
         A = torch.randn(d_in, r, generator=g) / math.sqrt(d_in)
         Bm = torch.randn(r, d_out, generator=g) * 0.02
         x, gt, A, Bm = (t.to(dtype) for t in (x, gt, A, Bm))
-        sites.append(LoraSite(x.to(DEV), gt.to(DEV), A.to(DEV), Bm.to(DEV), 2.0, a_leaf=2 * li, b_leaf=2 * li + 1))
+        xd, gd, Ad, Bd = x.to(DEV), gt.to(DEV), A.to(DEV), Bm.to(DEV)
+        v = torch.matmul(xd, Ad) if products else None
+        u = torch.matmul(gd, Bd.t()) if products else None
+        sites.append(LoraSite(xd, gd, Ad, Bd, 2.0, a_leaf=2 * li, b_leaf=2 * li + 1, v=v, u=u))
         host.append((x, gt, A, Bm))
     return seg, sites, host
 
@@ -67,12 +73,17 @@ def _oracle(seg, host, s=2.0):
 
 
 def _run(seg, sites, leaves, dtype, mode, C, normalize_by):
+    """Builds and runs the plan; a plan over sites that bring V and U must
+    read them (odp_pack_planes) and project nothing."""
     shapes = [lf.shape for lf in leaves]
     _, rnd = leaf_guards(shapes, [dtype] * len(shapes))
     rel, ab = guard_constants(dtype, rnd)
     clip = ClipSpec(mode=mode, thresholds=[C], effective=C, gamma=0.01, normalize_by=normalize_by,
                     guards=[(rel, ab, dtype)])
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=sites, device=DEV)
+    if sites and all(s.v is not None for s in sites):
+        live = {t[0] for t in plan.tables if t[5] > 0}
+        assert "planes" in live and not live & {"project", "factor_project"}, live
     res = plan.run()
     torch.cuda.synchronize()
     return res
@@ -92,9 +103,10 @@ def _check_lora(seg, host, res, *, mode, C, normalize_by, tol, band):
     return norms
 
 
-def test_config_c1():
+@pytest.mark.parametrize("products", [False, True])
+def test_config_c1(products):
     shapes = {"lin": (768, 768)}
-    seg, sites, host = _lora_sites(shapes, 32, 128, 8, torch.float32, seed=1)
+    seg, sites, host = _lora_sites(shapes, 32, 128, 8, torch.float32, seed=1, products=products)
     leaves = [LeafOut((768, 8), torch.float32), LeafOut((8, 768), torch.float32)]
     res = _run(seg, sites, leaves, torch.float32, N.CLIP_FIXED, 1.0, 32.0)
     _check_lora(seg, host, res, mode=N.CLIP_FIXED, C=1.0, normalize_by=32.0, tol=1e-5, band=1e-6)
@@ -115,12 +127,14 @@ def test_config_c1():
     assert stats.kstest(z, "norm").pvalue > 0.01
 
 
-def test_config_c2_layer():
+@pytest.mark.parametrize("products", [False, True])
+def test_config_c2_layer(products):
     shapes = {"q": (768, 768), "k": (768, 768), "v": (768, 768), "o": (768, 768), "fc": (768, 3072), "proj": (3072, 768)}
     shared = {"k": "q", "v": "q"}
     B, T = 64, 512
     g_scale = torch.exp(torch.randn(B, generator=torch.Generator().manual_seed(7))) * 0.02
-    seg, sites, host = _lora_sites(shapes, B, T, 8, torch.bfloat16, seed=2, g_scale=g_scale, shared=shared)
+    seg, sites, host = _lora_sites(shapes, B, T, 8, torch.bfloat16, seed=2, g_scale=g_scale, shared=shared,
+                                   products=products)
     _, norms0 = _oracle(seg, host)
     C = float(norms0.median())
     leaves = []
@@ -131,13 +145,15 @@ def test_config_c2_layer():
     assert 0 < int((norms > C).sum()) < B  # some examples clip, some do not
 
 
-def test_config_c3_layer():
+@pytest.mark.parametrize("products", [False, True])
+def test_config_c3_layer(products):
     shapes = {"q": (4096, 4096), "k": (4096, 1024), "v": (4096, 1024), "o": (4096, 4096),
               "gate": (4096, 14336), "up": (4096, 14336), "down": (14336, 4096)}
     shared = {"k": "q", "v": "q", "up": "gate"}
     B, T = 16, 1024
     lengths = torch.randint(256, T + 1, (B,), generator=torch.Generator().manual_seed(0)).tolist()
-    seg, sites, host = _lora_sites(shapes, B, T, 16, torch.bfloat16, seed=3, lengths=lengths, shared=shared)
+    seg, sites, host = _lora_sites(shapes, B, T, 16, torch.bfloat16, seed=3, lengths=lengths, shared=shared,
+                                   products=products)
     leaves = []
     for d_in, d_out in shapes.values():
         leaves += [LeafOut((d_in, 16), torch.bfloat16), LeafOut((16, d_out), torch.bfloat16)]

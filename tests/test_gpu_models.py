@@ -82,6 +82,10 @@ def test_hf_llama_lora_matches_oracle(dtype, tol, autos):
     torch.cuda.synchronize()
     disc = fn.engine._discovery[1]
     assert len(disc.eligible) == 28  # every adapter factor went through the seam
+    # The seams kept V = x A and U = g B^T: the step reads them instead of
+    # projecting the activations and output gradients again.
+    live = {t[0] for t in fn.engine._plan.tables if t[5] > 0}
+    assert "planes" in live and not live & {"project", "factor_project"}, live
     summed, aux = dp_ref.clipped_grad(ref_loss, train_cpu, (ids, labels), clipping_norm=C, autos=autos,
                                       normalize_by=n)
     for k, ref in summed.items():

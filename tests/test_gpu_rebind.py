@@ -19,14 +19,15 @@ import torch
 from opaque_amd import _native as N
 from opaque_amd import capture
 from opaque_amd.clipping import auto_clipped_grad, clipped_grad
-from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LinearSite, LoraSite, MaterializedLeaf, Segments, plan_key
+from opaque_amd.engine import (LORA_PTRS, ClipSpec, GhostPlan, LeafOut, LinearSite, LoraSite, MaterializedLeaf,
+                               Segments, plan_key)
 from opaque_amd.guard import guard_constants, leaf_guards
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _inputs(seed, n_ex=4, T=64, gram=True):
+def _inputs(seed, n_ex=4, T=64, gram=True, products=False):
     g = torch.Generator(device=DEV).manual_seed(seed)
     bf = torch.bfloat16
     x = torch.randn(n_ex * T, 256, device=DEV, generator=g).to(bf)
@@ -35,7 +36,10 @@ def _inputs(seed, n_ex=4, T=64, gram=True):
         gt = torch.randn(n_ex * T, d_out, device=DEV, generator=g).to(bf) * 0.1
         A = (torch.randn(256, 16, device=DEV, generator=g) / 16).to(bf)
         B = (torch.randn(16, d_out, device=DEV, generator=g) * 0.02).to(bf)
-        lora.append(LoraSite(x, gt, A, B, 2.0, a_leaf=2 * k, b_leaf=2 * k + 1))
+        # products: the seam's own V = x A and U = g B^T come with the site.
+        v = torch.matmul(x, A) if products else None
+        u = torch.matmul(gt, B.t()) if products else None
+        lora.append(LoraSite(x, gt, A, B, 2.0, a_leaf=2 * k, b_leaf=2 * k + 1, v=v, u=u))
     xl = torch.randn(n_ex * T, 136, device=DEV, generator=g).to(bf)
     lins = [LinearSite(xl, (torch.randn(n_ex * T, 72, device=DEV, generator=g) * 0.05).to(bf), 4),
             LinearSite(xl, (torch.randn(n_ex * T, 40, device=DEV, generator=g) * 0.05).to(bf), 5,
@@ -106,21 +110,23 @@ def test_full_weight_second_moment_without_storage():
         assert got.second_moment[k].abs().sum() > 0
 
 
+@pytest.mark.parametrize("products", [False, True])
 @pytest.mark.parametrize("keyed", [False, True])
 @pytest.mark.parametrize("pe_bytes,second_moment", [(None, False), (0, False), (None, True), (0, True)])
-def test_rebind_equals_fresh_plan(pe_bytes, second_moment, keyed):
-    print(f"rebind: pe_bytes={pe_bytes} second_moment={second_moment} keyed={keyed}", flush=True)
+def test_rebind_equals_fresh_plan(pe_bytes, second_moment, keyed, products):
+    print(f"rebind: pe_bytes={pe_bytes} second_moment={second_moment} keyed={keyed} products={products}",
+          flush=True)
     leaves, clip1 = _spec([0.5, 0.8])
     _, clip2 = _spec([0.3, 1.1])  # thresholds change between calls (adaptive clipping)
     seg = Segments.padded(4, 64, [64, 10, 33, 64])
-    l1, n1, m1 = _inputs(1, gram=not second_moment)
-    l2, n2, m2 = _inputs(2, gram=not second_moment)
+    l1, n1, m1 = _inputs(1, gram=not second_moment, products=products)
+    l2, n2, m2 = _inputs(2, gram=not second_moment, products=products)
     kw = dict(segments=seg, leaves=leaves, device=DEV, second_moment=second_moment, linear_pe_bytes=pe_bytes)
     plan = GhostPlan(clip=clip1, lora_sites=l1, linear_sites=n1, materialized=m1, **kw)
     r1 = plan.run()
     first = _snapshot(r1)
     held = [t for t in r1.leaves]  # the tensors the first call handed out
-    ptrs = torch.empty(4 * len(l2), dtype=torch.int64)
+    ptrs = torch.empty(LORA_PTRS * len(l2), dtype=torch.int64)
     k2 = plan_key(clip=clip2, lora_sites=l2, linear_sites=n2, materialized=m2, lora_ptrs=ptrs, **kw)
     assert plan.key == plan_key(clip=clip1, lora_sites=l1, linear_sites=n1, materialized=m1, **kw) == k2
     # keyed: the fast path when the host helper is built (addresses from plan_key)

@@ -316,11 +316,24 @@ def test_host_signature_tracks_structure_and_addresses():
     helper is built) changes with every field that shapes a plan's tables and
     with nothing else; the addresses it writes are the sites' tensors'."""
     mod = _helper()
-    ptrs = torch.empty(8, dtype=torch.int64)
+    ptrs = torch.empty(12, dtype=torch.int64)
     base = _lora_sites(0)
     sig = mod.lora_signature(base, ptrs)
-    assert ptrs.tolist() == [t.data_ptr() for s in base for t in (s.x, s.g, s.A, s.B)]
-    assert mod.lora_signature(_lora_sites(1), torch.empty(8, dtype=torch.int64)) == sig  # new values, same structure
+    assert ptrs.tolist() == [a for s in base for a in (s.x.data_ptr(), s.g.data_ptr(), s.A.data_ptr(),
+                                                       s.B.data_ptr(), 0, 0)]
+    assert mod.lora_signature(_lora_sites(1), torch.empty(12, dtype=torch.int64)) == sig  # new values, same structure
+    # The seam's rank-space products: their presence and layout are structure,
+    # their addresses are written beside the others.
+    vu = _lora_sites(0)
+    for s_ in vu:
+        s_.v = (s_.x.float() @ s_.A.float()).to(torch.bfloat16)
+        s_.u = (s_.g.float() @ s_.B.float().t()).to(torch.bfloat16)
+    sig_vu = mod.lora_signature(vu, ptrs)
+    assert sig_vu != sig
+    assert ptrs.tolist() == [a for s in vu for a in (s.x.data_ptr(), s.g.data_ptr(), s.A.data_ptr(), s.B.data_ptr(),
+                                                     s.v.data_ptr(), s.u.data_ptr())]
+    vu[1].u = vu[1].u.t().contiguous().t()
+    assert mod.lora_signature(vu, torch.empty(12, dtype=torch.int64)) != sig_vu
     g_t = base[1].g.t().contiguous().t()  # same shape, other strides
     changed = {
         "unshared x": _lora_sites(0, share=False),
@@ -336,7 +349,7 @@ def test_host_signature_tracks_structure_and_addresses():
         "b_transposed": _lora_sites(0, b_transposed=True),
     }
     for what, sites in changed.items():
-        assert mod.lora_signature(sites, torch.empty(8, dtype=torch.int64)) != sig, what
+        assert mod.lora_signature(sites, torch.empty(12, dtype=torch.int64)) != sig, what
     from opaque_amd.engine import Segments
 
     assert mod.lora_signature(_lora_sites(0, segments=Segments.padded(2, 32)), ptrs) is None
