@@ -62,9 +62,6 @@ def parse_args():
     ap.add_argument("--second-moment", action="store_true",
                     help="c4: also sum the squared clipped per-example gradients (second_moment=True); "
                          "sites without stored gradients then take the moments kernel")
-    ap.add_argument("--serial", action="store_true",
-                    help="launch every table on one stream (no side streams for the projection and factor "
-                         "stages)")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--dropin-overhead", choices=["on", "off"], default="on",
                     help="c3: also time the drop-in auto_clipped_grad's per-call host work")
@@ -234,16 +231,15 @@ def cpu_baseline(r, seed, lengths):
     }
 
 
-def setup_c3(args, dev):
-    """C3: captured LoRA seams, AUTO-S, one clip group."""
-    from opaque_amd import _native as N
-    from opaque_amd.engine import LORA_PTRS, ClipSpec, GhostPlan, LeafOut, LoraSite, Segments, leaves_key, plan_key
+def c3_sites(layers, B, T, r, seed, seam, dev):
+    """The C3 inputs as plan sites: (segments, lengths, LoRA sites, output
+    leaves, guard constants).  With ``seam`` every site also brings the
+    seam's V = x A and U = g B^T."""
+    from opaque_amd.engine import LeafOut, LoraSite, Segments
     from opaque_amd.guard import guard_constants, leaf_guards
 
-    B, T, r = args.batch, args.seq, args.rank
-    lengths, sites = build_workload(args.layers, B, T, r, args.seed, dev)
+    lengths, sites = build_workload(layers, B, T, r, seed, dev)
     seg = Segments.padded(B, T, lengths)
-    seam = args.rank_products == "seam"
     leaves, lsites, shapes = [], [], []
     for name, x, gt, A, Bm in sites:
         ia, ib = len(leaves), len(leaves) + 1
@@ -256,7 +252,17 @@ def setup_c3(args, dev):
         u = torch.matmul(gt, Bm.t().contiguous()) if seam else None
         lsites.append(LoraSite(x, gt, A, Bm, 2.0, a_leaf=ia, b_leaf=ib, v=v, u=u))
     _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
-    rel, ab = guard_constants(torch.bfloat16, rnd)
+    return seg, lengths, lsites, leaves, guard_constants(torch.bfloat16, rnd)
+
+
+def setup_c3(args, dev):
+    """C3: captured LoRA seams, AUTO-S, one clip group."""
+    from opaque_amd import _native as N
+    from opaque_amd.engine import LORA_PTRS, ClipSpec, GhostPlan, leaves_key, plan_key
+
+    B, T, r = args.batch, args.seq, args.rank
+    seam = args.rank_products == "seam"
+    seg, lengths, lsites, leaves, (rel, ab) = c3_sites(args.layers, B, T, r, args.seed, seam, dev)
     clip = ClipSpec(mode=N.CLIP_AUTOS, thresholds=[1.0], effective=1.0, gamma=0.01,
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev)
@@ -445,7 +451,6 @@ def main():
         args.seq = 1024 if args.seq is None else args.seq
         plan, sigma, config, metric, flops, stages, bound = setup_c3(args, dev)
     B = args.batch
-    plan.serial = args.serial
     # Stages with no launch in this plan record no events.
     present = ({("lin_sum" if i[0] in ("lin_prescale", "lin_moments") else i[0]) for i in plan.launch_info}
                | {"clip", "noise"})

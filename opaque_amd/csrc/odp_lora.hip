@@ -411,22 +411,24 @@ __device__ __forceinline__ void factor_epilogue(const f32x4_t (&acc)[NJ][NKB], i
       // Columns of frozen factors between leaves belong to no leaf.
       if (k < lc0 || k - lc0 >= lrk) continue;
       (void)lpe;
-      (void)l16;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int64_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
         if (m < M) {
-          // Non-finite entries count as 0 (nan_to_num); squares are taken
+          // The value as stored in the leaf's dtype (the reference squares
+          // its per-example gradient as stored, _pytree.py:224-265);
+          // non-finite entries count as 0 (nan_to_num); squares are taken
           // in fp32 like the reference's float32 accumulation dtype.
-          const float v = scale * acc[j][kb][i];
+          float v = scale * acc[j][kb][i];
+          if (l16) v = odp_bf2f(odp_f2bf(v));
           const float vf = isfinite(v) ? v : 0.f;
           cs[i] += (double)__fmul_rn(vf, vf);
         }
       }
     }
     // The stored copy (summed after clipping) is in the leaf's dtype, as the
-    // reference's per-example gradients are (the norm above uses the fp32
-    // values).  After a quad transpose each lane holds 4 consecutive
+    // reference's per-example gradients are (the norm above squares the same
+    // rounded values).  After a quad transpose each lane holds 4 consecutive
     // columns of one row: 8-byte (bf16) or 16-byte (f32) stores.
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -769,7 +771,8 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
         else
           pend[2 * j + (i >> 1)] = h;
         if (k < r && m < M) {
-          const float vf = isfinite(v) ? v : 0.f;
+          const float vq = odp_bf2f((uint16_t)h);  // the value as stored
+          const float vf = isfinite(vq) ? vq : 0.f;
           cs[i] += (double)__fmul_rn(vf, vf);
         }
       }

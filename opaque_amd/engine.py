@@ -381,23 +381,6 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-# Launches of these stages read and write disjoint buffers (the projection
-# planes of different activations; the per-example gradients and partial
-# slots of different leaves), so the tables of one stage run side by side on
-# forked streams: each launch's last, partly filled round of workgroups then
-# overlaps the others instead of idling the CUs between launches.
-_CONCURRENT = ("project", "factor")
-_SIDE: dict[int, list[torch.cuda.Stream]] = {}
-
-
-def _side_streams(device: torch.device, n: int) -> list[torch.cuda.Stream]:
-    """n streams of the device at the default priority, created once per process."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    have = _SIDE.setdefault(idx, [])
-    while len(have) < n:
-        have.append(torch.cuda.Stream(device=idx))
-    return have[:n]
-
 
 def _layout(ext: dict[tuple, torch.Tensor]) -> list[tuple]:
     """Shapes, strides, dtypes and storage sharing of a plan's input tensors:
@@ -538,9 +521,6 @@ class GhostPlan:
         if dev.type == "cuda" and dev.index is None:
             dev = torch.device("cuda", torch.cuda.current_device())
         self.device = dev
-        # True launches every table on the caller's stream in table order
-        # (the concurrent stages then run one launch at a time).
-        self.serial = False
         self.segments = segments
         self.leaves = leaves
         self.clip = clip
@@ -1702,39 +1682,19 @@ class GhostPlan:
                                               self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                               self.seg_ex.data_ptr(), self.part.data_ptr(), self.n_slots), name)
 
-        # Runs of consecutive tables of one stage; a run of a _CONCURRENT stage
-        # forks: table j > 0 goes to side stream j - 1 after an event of the
-        # caller's stream, and the caller's stream waits for every side stream
-        # before the next stage (so buffers the caller frees afterwards are
-        # only reused behind all of them).
-        runs: list[list[tuple]] = []
-        for t in live:
-            if runs and runs[-1][0][0] == t[0]:
-                runs[-1].append(t)
-            else:
-                runs.append([t])
-        for run_ in runs:
-            name = run_[0][0]
-            if name in ev:
+        # Every table on the caller's stream, in table order.  (Launching the
+        # tables of one stage side by side on forked streams, to overlap each
+        # launch's last round of workgroups with the next, measured no faster
+        # on MI355X.)
+        names = [t[0] for t in live]
+        for idx, (name, dt, probs, ws, n, total) in enumerate(live):
+            if name in ev and name not in names[:idx]:
                 ev[name][0].record(main)
-            side = (_side_streams(self.device, len(run_) - 1)
-                    if name in _CONCURRENT and len(run_) > 1 and not self.serial else [])
-            if side:
-                fork = torch.cuda.Event()
-                fork.record(main)
-            for j, (_, dt, probs, ws, n, total) in enumerate(run_):
-                on = side[j - 1] if side and j > 0 else main
-                if on is not main:
-                    on.wait_event(fork)
-                end_ev = mark(name, dt, on)
-                launch(name, dt, probs, ws, n, total, on.cuda_stream)
-                if end_ev is not None:
-                    end_ev.record(on)
-            for s in side:
-                done = torch.cuda.Event()
-                done.record(s)
-                main.wait_event(done)
-            if name in ev:
+            end_ev = mark(name, dt, main)
+            launch(name, dt, probs, ws, n, total, stream)
+            if end_ev is not None:
+                end_ev.record(main)
+            if name in ev and name not in names[idx + 1:]:
                 ev[name][1].record(main)
         if "clip" in ev:
             ev["clip"][0].record()

@@ -118,6 +118,7 @@ def run_both(dtype, *, n=6, T=16, autos=False, C=None, normalize_by=1.0, second_
     summed, aux = dp_ref.clipped_grad(ref_loss, train, (x, y), clipping_norm=C, autos=autos,
                                       normalize_by=normalize_by, second_moment=second_moment,
                                       dtype=out_dtype)
+    run_both.last_fn = fn
     return out, st, st2, summed, aux, C
 
 
@@ -138,10 +139,15 @@ def test_lora_capture_matches_oracle(dtype, tol, autos):
     assert rel(gaux.loss_values, aux["loss_values"]) <= tol
     assert rel(gaux.clipped_grad_norms, aux["clipped_norms"]) <= max(tol, 1e-5)
     assert gaux.batch_size == 6
-    # Masks agree away from the threshold.
+    # The kernel's per-example clip masks (norm > C, AUTO-S counting the same
+    # way) equal the oracle's for every example away from the threshold band,
+    # and so does the clipping rate when no example lies in the band.
     band = 1e-3 if dtype == torch.bfloat16 else 1e-6
     ref_n = aux["norms"].double()
     far = ((ref_n - C).abs() / C) > band
+    mask = run_both.last_fn.engine._plan.clipped_total.cpu().bool()
+    assert torch.equal(mask[far], (ref_n > C)[far]), (mask, ref_n, C)
+    assert 0 < int((ref_n[far] > C).sum()) < int(far.sum())  # both outcomes occur
     ref_rate = float((ref_n[far] > C).sum()) / len(ref_n)
     if bool(far.all()):
         assert gaux.clipping_rate == pytest.approx(ref_rate)
@@ -382,6 +388,51 @@ def test_full_weight_linear_seams_match_oracle(pe_bytes):
         assert rel(res.pytree[k], ref[k]) <= 2e-2, (k, rel(res.pytree[k], ref[k]))
     for name, v in raux["group_norms"].items():
         assert rel(aux.group_norms[name], v) <= 2e-2
+
+
+@pytest.mark.parametrize("d,h,T,form", [(256, 384, 40, "gram"), (1024, 1024, 600, "gram256")])
+def test_full_weight_gram_norms_through_the_drop_in(d, h, T, form):
+    """Without room to store per-example gradients, short examples against
+    wide weights make the engine take the token-Gram norms (the 128-row
+    kernel below 512 rows, the 256-row-block kernel from 512 rows): the
+    drop-in reaches them and still matches the oracle, group norms and
+    per-example masks included."""
+    from opaque_amd import _native as N
+
+    print(f"drop-in Gram norms: d={d} h={h} T={T} ({form})", flush=True)
+    g = torch.Generator().manual_seed(31)
+    params = {"up": (torch.randn(h, d, generator=g) / d**0.5).to(torch.bfloat16),
+              "down": (torch.randn(d, h, generator=g) / h**0.5).to(torch.bfloat16)}
+
+    def make(lin):
+        def loss(p, xi, yi):
+            u = torch.nn.functional.gelu(lin(xi, p["up"], None))
+            return ((lin(u, p["down"], None).float() - yi.float()) ** 2).mean()
+
+        return loss
+
+    def plain(x, W, b):
+        return torch.nn.functional.linear(x, W, b)
+
+    n = 4
+    x = (torch.randn(n, T, d, generator=g) * torch.logspace(-1, 0.5, n).view(n, 1, 1)).to(torch.bfloat16)
+    y = torch.randn(n, T, d, generator=g).to(torch.bfloat16)
+    _, aux0 = dp_ref.clipped_grad(make(plain), params, (x, y), clipping_norm=float("inf"))
+    C = float(aux0["norms"].median())
+    fn, st = clipped_grad(make(capture.linear), clipping_norm=C, batch_argnums=(1, 2), return_aux=True,
+                          normalize_by=float(n))
+    fn.engine.plan_options["linear_pe_bytes"] = 0
+    (res, aux), _ = fn({k: v.to(DEV) for k, v in params.items()}, x.to(DEV), y.to(DEV), state=st)
+    plan = fn.engine._plan
+    forms = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
+    assert forms == {N.FORM_GRAM if form == "gram" else N.FORM_GRAM256}, forms
+    ref, raux = dp_ref.clipped_grad(make(plain), params, (x, y), clipping_norm=C, normalize_by=float(n))
+    for k in params:
+        assert rel(res.pytree[k], ref[k]) <= 2e-2, (k, rel(res.pytree[k], ref[k]))
+    assert rel(aux.grad_norms, raux["norms"]) <= 2e-2
+    ref_n = raux["norms"].double()
+    far = ((ref_n - C).abs() / C) > 1e-3
+    assert torch.equal(plan.clipped_total.cpu().bool()[far], (ref_n > C)[far])
 
 
 @pytest.mark.parametrize("pe_bytes", [None, 0])

@@ -135,3 +135,29 @@ def test_segment_past_the_fused_limit_takes_the_two_pass_path(d_in, d_out):
     ga, gb = r1.leaves[0].double().cpu(), r1.leaves[1].double().cpu()
     assert (ga - dA.sum(0)).norm() <= 2e-2 * dA.sum(0).norm()
     assert (gb - dB.sum(0)).norm() <= 2e-2 * dB.sum(0).norm()
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4]])
+def test_norms_square_the_stored_values(case, fuse):
+    """The reference squares each per-example gradient as stored in the
+    parameter dtype (clipping/_pytree.py:224-265 squares the bf16 leaf).  The
+    kernels' squared norms must therefore be the fp32 squares of the bf16
+    values they store, summed in fp64: equal to the sum over pe_views up to
+    the fp64 summation order (rel 1e-12).  Squaring the unrounded fp32
+    values instead differs by about 2^-9 / sqrt(n) relative, 1e-5 here."""
+    n_ex, T, lengths, d_in, d_outs, ranks, frozen = case
+    print(f"norms of stored values: fuse={fuse} d_in={d_in} d_outs={d_outs}", flush=True)
+    seg = Segments.padded(n_ex, T, lengths)
+    X, sites, leaves, shapes = _sites(n_ex * T, d_in, d_outs, ranks, frozen, seed=3)
+    plan, res = _plan(X, sites, leaves, shapes, seg, fuse=fuse, C=1e30)
+    want = torch.zeros(n_ex, dtype=torch.float64)
+    for pe, lf in zip(plan.pe_views(), leaves):
+        per = pe.view(n_ex, -1).float()  # one segment per example, in order
+        assert pe.dtype == torch.bfloat16
+        want += per.square().double().sum(1).cpu()
+    got = res.norms.double().cpu().square()
+    assert torch.allclose(got, want, rtol=1e-6, atol=0), (got, want)  # the stored norm is fp32
+    # The fp32-rounded norm leaves 1e-7; the exact check runs on the fp64 partials.
+    part = plan.part.double().sum(1).cpu()
+    assert torch.allclose(part, want, rtol=1e-12, atol=0), ((part / want) - 1).abs().max()

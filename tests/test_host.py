@@ -155,6 +155,11 @@ def test_guard_constants_match_oracle(shapes, dt):
     expect = dp_ref.finalize(ratio, dt, rnd, clamp_one=False)
     got = torch.clamp(ratio * rel - ab, min=0.0)
     assert torch.equal(got, expect)
+    # The magnitude the reference documents (_pytree.py:384-385,492-493): the
+    # shrink 1 - rel is one unit roundoff of the storage dtype plus twice the
+    # norm roundoff -- neither a smaller nor a larger guard passes.
+    eps = torch.finfo(dt).eps
+    assert rnd > 0 and abs((1.0 - rel) - eps) <= 2 * rnd * (1 + 1e-9)
 
 
 # -- validation messages (the reference's tests assert these substrings) --------

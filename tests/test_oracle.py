@@ -152,6 +152,46 @@ def test_oracle_fp32_guard_is_negligible():
     torch.testing.assert_close(out["a"], torch.tensor([0.6, 0.8]), rtol=1e-6, atol=0)
 
 
+# The reference documents what its guard costs a clipped output (the
+# AUTO-S and clip_pytree docstrings, _pytree.py:384-385,492-493): "~0.8% of
+# the output magnitude at bfloat16, ~0.1% at float16 and ~1.2e-7 at float32",
+# i.e. one unit roundoff of the storage dtype (2^-7, 2^-10, 2^-23) plus twice
+# the norm roundoff.  Pinned from both sides, so that a guard made smaller
+# (the bound could break) or larger (outputs shrink for nothing) fails.
+GUARD_SHRINK = {torch.bfloat16: 2.0**-7, torch.float16: 2.0**-10, torch.float32: 2.0**-23}
+
+
+@pytest.mark.parametrize("dt", list(GUARD_SHRINK))
+@pytest.mark.parametrize("shapes", [[(3,)], [(8192, 16), (16, 4096)], [(4096, 16)] * 448])
+def test_oracle_guard_magnitude_matches_reference_docs(dt, shapes):
+    leaves = [torch.zeros(s, dtype=dt) for s in shapes]
+    acc = dp_ref.acc_dtype(leaves, None)
+    rnd = dp_ref.roundoff(acc, len(leaves), dp_ref.reduction_terms(leaves))
+    # The norm roundoff is float32 squares plus float64 sums: a few parts in
+    # 1e8 at most for these trees, far below the storage term.
+    assert 0 < rnd < 1e-7
+    ratio = torch.tensor([2.0, 0.37, 5.0e3], dtype=torch.float64)
+    shrink = 1.0 - dp_ref.finalize(ratio, dt, rnd, clamp_one=False) / ratio
+    eps = GUARD_SHRINK[dt]
+    tiny = torch.finfo(dt).smallest_normal * torch.finfo(dt).eps / 0.37
+    assert ((shrink - eps).abs() <= 2 * rnd + tiny + 1e-15).all(), (shrink, eps, rnd)
+    # The storage term as the docstrings round it: 0.8 %, 0.1 %, 1.2e-7 (at
+    # float32 the norm roundoff, 2 rnd ~ 6e-8, is of the same order and not
+    # included in the documented figure).
+    doc = {torch.bfloat16: 0.008, torch.float16: 0.001, torch.float32: 1.2e-7}[dt]
+    assert abs((float(shrink[0]) - 2 * rnd) / doc - 1.0) < 0.03
+
+
+def test_oracle_clipped_count_counts_strictly_above():
+    """num_clipped = #(norm > C) (_clipped_fun.py:512-523): equality is not
+    clipped; the count is taken in the norms' own dtype."""
+    norms = torch.tensor([0.5, 1.0, 1.00000001, 3.0, float("inf")], dtype=torch.float64)
+    assert dp_ref.clipped_count(norms, 1.0) == 3
+    assert dp_ref.clipped_count(norms.float(), 1.0) == 2  # 1.00000001 rounds to 1.0 in float32
+    assert dp_ref.clipped_count(torch.zeros(0), 1.0) == 0
+    assert dp_ref.clipped_count(norms, float("inf")) == 0
+
+
 def test_oracle_nan_sanitised():
     out, norm, _ = dp_ref.auto_scale_pytree({"a": torch.tensor([float("nan"), float("inf"), 1.0])}, 1.0, 0.01)
     assert torch.isfinite(out["a"]).all()
