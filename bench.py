@@ -63,6 +63,10 @@ def parse_args():
                     help="c4: also sum the squared clipped per-example gradients (second_moment=True); "
                          "sites without stored gradients then take the moments kernel")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--cpu-layers", type=int, default=32,
+                    help="layers of the CPU baseline sample (32: the whole C3 model, about 16 s per run on 16 "
+                         "host threads; fewer are scaled to 32)")
+    ap.add_argument("--cpu-runs", type=int, default=1, help="timed CPU baseline runs (median)")
     ap.add_argument("--dropin-overhead", choices=["on", "off"], default="on",
                     help="c3: also time the drop-in auto_clipped_grad's per-call host work")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -92,8 +96,10 @@ def kernel_label(stage, key):
     return f"{base}_f32"
 
 
-def committed_traffic(label):
-    """HBM bytes per launch of `label` from the committed PMC summary, or None."""
+def committed_traffic(label, design_bytes):
+    """HBM bytes per launch of `label` from the committed PMC summary, or None
+    when there is none for a launch of these design bytes (a summary taken
+    on another plan or workload does not describe this launch)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as f:
@@ -101,7 +107,9 @@ def committed_traffic(label):
     except (OSError, ValueError):
         return None
     entry = data.get("kernels", {}).get(label)
-    return None if entry is None else entry.get("traffic_bytes")
+    if entry is None or entry.get("algorithmic_bytes") != design_bytes:
+        return None
+    return entry.get("traffic_bytes")
 
 
 def copy_calibration(nbytes):
@@ -139,9 +147,22 @@ def build_workload(layers, B, T, r, seed, device):
 
 
 def cpu_model() -> str:
+    """The host CPU as lscpu names it (model, sockets x cores x threads per
+    core), else /proc/cpuinfo's model name."""
+    import subprocess
+
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        f = {k.strip(): v.strip() for k, v in (ln.split(":", 1) for ln in out.splitlines() if ":" in ln)}
+        if "Model name" in f:
+            return (f"{f['Model name']} ({f.get('Vendor ID', '?')}, family {f.get('CPU family', '?')} model "
+                    f"{f.get('Model', '?')}; {f.get('Socket(s)', '?')} socket(s) x {f.get('Core(s) per socket', '?')}"
+                    f" cores x {f.get('Thread(s) per core', '?')} threads; {f.get('CPU(s)', '?')} CPUs)")
+    except (OSError, subprocess.SubprocessError, ValueError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
                 if line.startswith("model name"):
                     return line.split(":", 1)[1].strip()
     except OSError:
@@ -149,15 +170,13 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-CPU_LAYERS = 2  # of the 32: the sample of the CPU baseline
-
-
-def cpu_baseline(r, seed, lengths):
+def cpu_baseline(r, seed, lengths, layers=32, runs=1):
     """The reference algorithm on the host (oracle.dp_ref): vmap(grad)
     per-example LoRA gradients, reference AUTO-S scaling, fp32-accumulated sum
     and mt19937 inverse-CDF noise, for every example of the GPU step at its
-    own valid length (no padding) over CPU_LAYERS of the 32 layers; 2
-    warm-ups, median of 5."""
+    own valid length (no padding), over `layers` of the 32 layers (all of
+    them by default, so nothing is extrapolated); an untimed two-layer
+    warm-up, then the median of `runs` timed runs."""
     from oracle import dp_ref
 
     threads = len(os.sched_getaffinity(0))
@@ -166,14 +185,15 @@ def cpu_baseline(r, seed, lengths):
     names = list(LAYER_SHAPES)
     keys = ("qkv", "o", "gu", "down")
     din = {"qkv": 4096, "o": 4096, "gu": 4096, "down": 14336}
+    per = len(keys) + len(names)
     params = {}
-    for layer in range(CPU_LAYERS):
+    for layer in range(layers):
         for name, (d_in, d_out) in LAYER_SHAPES.items():
             params[f"{layer}.{name}.A"] = (torch.randn(d_in, r, generator=g) / math.sqrt(d_in)).to(torch.bfloat16)
             params[f"{layer}.{name}.B"] = (torch.randn(r, d_out, generator=g) * 0.02).to(torch.bfloat16)
     # Activations and output gradients are windows of one random pool at
     # random offsets: the values only need to be bf16 normals, and drawing
-    # the full 1.4 G of them would take longer than the timed work.
+    # all of them would take longer than the timed work.
     pool = torch.randn(1 << 26, generator=g).to(torch.bfloat16)
 
     def draw(L, d):
@@ -183,51 +203,56 @@ def cpu_baseline(r, seed, lengths):
     examples = []
     for L in lengths:
         batch = []
-        for layer in range(CPU_LAYERS):
+        for layer in range(layers):
             batch += [draw(L, din[k]) for k in keys]
             batch += [draw(L, LAYER_SHAPES[n][1]) for n in names]
         examples.append(tuple(batch))
 
-    def loss(p, *b):
-        tot = 0.0
-        per = len(keys) + len(names)
-        for layer in range(CPU_LAYERS):
-            xs = dict(zip(keys, b[layer * per : layer * per + len(keys)]))
-            gs = dict(zip(names, b[layer * per + len(keys) : (layer + 1) * per]))
-            for name in names:
-                x = xs[SHARED_INPUT[name]]
-                y = 2.0 * (x @ p[f"{layer}.{name}.A"]) @ p[f"{layer}.{name}.B"]
-                tot = tot + (y.float() * gs[name].float()).sum()
-        return tot
+    def make_loss(n_layers):
+        def loss(p, *b):
+            tot = 0.0
+            for layer in range(n_layers):
+                xs = dict(zip(keys, b[layer * per : layer * per + len(keys)]))
+                gs = dict(zip(names, b[layer * per + len(keys) : (layer + 1) * per]))
+                for name in names:
+                    x = xs[SHARED_INPUT[name]]
+                    y = 2.0 * (x @ p[f"{layer}.{name}.A"]) @ p[f"{layer}.{name}.B"]
+                    tot = tot + (y.float() * gs[name].float()).sum()
+            return tot
+
+        return loss
 
     B = len(lengths)
 
-    def once():
+    def once(n_layers):
+        loss = make_loss(n_layers)
+        sub = {k: v for k, v in params.items() if int(k.split(".", 1)[0]) < n_layers}
         total = None
         for batch in examples:  # one example at a time: its own length
-            res, _ = dp_ref.clipped_grad(loss, params, batch, clipping_norm=1.0, normalize_by=float(B), autos=True)
+            res, _ = dp_ref.clipped_grad(loss, sub, batch[: n_layers * per], clipping_norm=1.0,
+                                         normalize_by=float(B), autos=True)
             f = {k: v.float() for k, v in res.items()}
             total = f if total is None else {k: total[k] + f[k] for k in f}
         dp_ref.gaussian_noise_reference({k: v.to(torch.bfloat16) for k, v in total.items()}, 1.0 / B, key=42, step=0)
 
-    for _ in range(2):
-        once()
+    once(min(2, layers))  # warm-up: thread pool and allocator
     times = []
-    for _ in range(5):
+    for _ in range(runs):
         t0 = time.perf_counter()
-        once()
+        once(layers)
         times.append(time.perf_counter() - t0)
     t = sorted(times)[len(times) // 2]
-    value = B / (t * 32 / CPU_LAYERS)  # the 32-layer model's examples/sec
+    value = B / (t * 32 / layers)  # the 32-layer model's examples/sec
+    scaled = "" if layers == 32 else f", scaled by 32/{layers}"
     return {
         "value": value,
         "unit": "examples/sec",
         "cores": threads,
         "kind": "port",
-        "sample": f"{CPU_LAYERS} of 32 Llama-3-8B LoRA r={r} layers, all {B} examples of the GPU step at their "
+        "sample": f"{layers} of 32 Llama-3-8B LoRA r={r} layers, all {B} examples of the GPU step at their "
                   f"valid lengths (sum {sum(lengths)} tokens, no padding), bf16 on the host (oracle vmap(grad) "
-                  f"per example + AUTO-S + fp32 sum + mt19937 noise), median of 5 after 2 warm-ups "
-                  f"({t:.2f} s), scaled by 32/{CPU_LAYERS}; cpu={cpu_model()}",
+                  f"per example + AUTO-S + fp32 sum + mt19937 noise), median of {runs} timed run(s) after a "
+                  f"two-layer warm-up ({t:.2f} s per run){scaled}; cpu={cpu_model()}",
     }
 
 
@@ -486,11 +511,17 @@ def main():
 
     # Per-launch durations (HIP events on the launch stream), algorithmic bytes and flops.
     launches = []
-    for j, (stage, key_, wgs, nbytes, nflops) in enumerate(plan.launch_info):
+    # Per launch: "contract" bytes are what the step's algorithmic byte count
+    # (one read of the unique activations and output gradients plus the
+    # clipped-sum writes) charges to it; "design" bytes add the plan's own
+    # intermediates (rank-space planes, per-example gradients, partials).
+    for j, (stage, key_, wgs, nbytes, nflops, io) in enumerate(plan.launch_info):
         avg = sum(lg[j][2].elapsed_time(lg[j][3]) for lg in logs) / args.steps
         launches.append({"kernel": kernel_label(stage, key_), "stage": stage, "workgroups": wgs,
-                         "algorithmic_bytes": nbytes, "algorithmic_flops": nflops, "avg_ms": avg,
-                         "gbs": nbytes / (avg * 1e-3) / 1e9 if avg > 0 else None,
+                         "contract_bytes": io, "design_bytes": nbytes, "algorithmic_flops": nflops,
+                         "avg_ms": avg,
+                         "gbs": io / (avg * 1e-3) / 1e9 if avg > 0 else None,
+                         "design_gbs": nbytes / (avg * 1e-3) / 1e9 if avg > 0 else None,
                          "tflops": nflops / (avg * 1e-3) / 1e12 if avg > 0 else None})
     dom = max(launches, key=lambda d: d["avg_ms"])
     res = plan.run()
@@ -499,14 +530,17 @@ def main():
     if bound == "hbm":
         roofline = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["gbs"],
                     "peak": MI355X_HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["gbs"] / MI355X_HBM_PEAK_GBS,
-                    "traffic": committed_traffic(dom["kernel"]),
-                    "algorithmic_bytes_per_launch": dom["algorithmic_bytes"], "avg_launch_ms": dom["avg_ms"]}
+                    "traffic": committed_traffic(dom["kernel"], dom["design_bytes"]),
+                    "contract_bytes_per_launch": dom["contract_bytes"],
+                    "design_bytes_per_launch": dom["design_bytes"],
+                    "design_frac": dom["design_gbs"] / MI355X_HBM_PEAK_GBS, "avg_launch_ms": dom["avg_ms"]}
     else:
         roofline = {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["tflops"],
                     "peak": MI355X_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": dom["tflops"] / MI355X_BF16_PEAK_TFLOPS,
-                    "traffic": committed_traffic(dom["kernel"]),
+                    "traffic": committed_traffic(dom["kernel"], dom["design_bytes"]),
                     "algorithmic_flops_per_launch": dom["algorithmic_flops"], "avg_launch_ms": dom["avg_ms"]}
+    executed = sum(i[4] for i in plan.launch_info) / (ms * 1e-3) / 1e12  # matrix work actually issued
     out = {
         "metric": metric,
         "value": B / (ms * 1e-3),
@@ -524,10 +558,15 @@ def main():
         "roofline": roofline,
         "launches": launches,
         "stage_ms": stage_ms,
-        "mfma_frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
+        # The matrix work the step issues, per second of step time, against
+        # the bf16 dense peak.  C4 also reports the contract's min-form count
+        # (the cheaper norm form per example plus the clipped sum), which
+        # credits flops that a step storing its per-example gradients does
+        # not execute.
+        "mfma_frac_of_bf16_peak": executed / MI355X_BF16_PEAK_TFLOPS,
+        "executed_mfma_tflops": executed,
         "algorithmic_tflops": flops / (ms * 1e-3) / 1e12,
-        "executed_mfma_tflops": (sum(f for *_, f in plan.launch_info) / (ms * 1e-3) / 1e12
-                                 if args.workload == "c4" else None),
+        "algorithmic_mfma_frac": flops / (ms * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
         "clipped_fraction": float(res.clipped_total.float().mean().item()),
         "plan_build_ms": plan.build_ms,
     }
@@ -541,7 +580,7 @@ def main():
         if args.dropin_overhead == "on":
             out["dropin_overhead"] = dropin_overhead(args, dev, ms)
     if args.cpu_baseline == "on" and args.workload == "c3":
-        out["cpu_baseline"] = cpu_baseline(args.rank, args.seed, config["lengths"])
+        out["cpu_baseline"] = cpu_baseline(args.rank, args.seed, config["lengths"], args.cpu_layers, args.cpu_runs)
     print(json.dumps(out), flush=True)
 
 

@@ -938,6 +938,17 @@ def _empty_response(args, state, *, argnums, clipping_norm, normalize_by, second
     return grads, state
 
 
+def under_differentiating_transform() -> bool:
+    """Whether an enclosing torch.func grad, vjp or jvp is active (the
+    reference's test, ``ENG/functional/_transform_stack.py:10-21``)."""
+    try:
+        from torch._C._functorch import TransformType, get_interpreter_stack
+    except ImportError:  # pragma: no cover - the functorch C API moved
+        return False
+    stack = get_interpreter_stack() or ()
+    return any(i.key() in (TransformType.Grad, TransformType.Jvp) for i in stack)
+
+
 def _make(loss_fn, argnums, has_aux, *, clipping_norm, autos, gamma, normalize_by, batch_argnums,
           return_aux, return_stats, second_moment, pre_clipping_transform, microbatch_size, dtype,
           compute_dtype, scale_fn, aux_cls, label):
@@ -955,6 +966,13 @@ def _make(loss_fn, argnums, has_aux, *, clipping_norm, autos, gamma, normalize_b
             return _empty_response(args, state, argnums=argnums_t, clipping_norm=clipping_norm,
                                    normalize_by=normalize_by, second_moment=second_moment,
                                    return_aux=return_aux, return_stats=return_stats, aux_cls=aux_cls)
+        # The reference keeps the graph for an enclosing grad/jvp
+        # (_clipped_grad.py:261-265); the clip and sum kernels here have no
+        # derivative, so such a call is refused rather than silently detached.
+        if under_differentiating_transform():
+            raise NotImplementedError(
+                f"{label.split('::')[-1]} cannot run under an enclosing torch.func grad/vjp/jvp: its clip and sum "
+                "kernels are not differentiable (call it outside the transform)")
         with record_function(label):
             out = engine(args, kwargs)
         return out, state

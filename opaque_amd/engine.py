@@ -355,12 +355,18 @@ class _Table:
         self.blocks: list[int] = []
         self.nbytes = 0  # algorithmic HBM bytes of the launch (one read/write of each operand)
         self.nflops = 0  # algorithmic flops of the launch
+        # The part of nbytes that the step's contract counts: reads of the
+        # activations and output gradients (and of materialised per-example
+        # gradients), and the clipped sums written; not the plan's own
+        # intermediates (rank-space planes, stored per-example gradients).
+        self.io_bytes = 0
 
-    def add(self, row: dict[int, int], blocks: int, nbytes: int = 0, nflops: int = 0) -> None:
+    def add(self, row: dict[int, int], blocks: int, nbytes: int = 0, nflops: int = 0, io: int = 0) -> None:
         if blocks <= 0:
             return
         self.nbytes += int(nbytes)
         self.nflops += int(nflops)
+        self.io_bytes += int(io)
         r = [0] * self.fields
         for k, v in row.items():
             r[k] = int(v)
@@ -861,7 +867,8 @@ class GhostPlan:
                         N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                     },
                     lib.odp_project_blocks(dtype_code(dt), n_rows, rtot),
-                    (valid * d_in + rtot * d_in + planes * rtot * valid) * es,
+                    (valid * d_in + rtot * d_in + planes * rtot * valid) * es, 2 * valid * d_in * rtot,
+                    io=valid * d_in * es,
                 )
             c0 = 0
             a_leaves = []
@@ -907,7 +914,8 @@ class GhostPlan:
                         # B itself is counted once per site.
                         fused_rows.append((-ln * d_out, len(fused_rows), row, 1,
                                            (ln * d_out + 2 * planes * r * ln) * es + r * d_out * es
-                                           + (r * d_out * es if j == 0 else 0)))
+                                           + (r * d_out * es if j == 0 else 0), ln * d_out * es,
+                                           4 * ln * d_out * r))
                     c0 += r
                     continue
                 if not products:
@@ -920,11 +928,13 @@ class GhostPlan:
                             N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                         },
                         lib.odp_project_blocks(dtype_code(dt), n_rows, r),
-                        (valid * d_out + r * d_out + planes * r * valid) * es,
+                        (valid * d_out + r * d_out + planes * r * valid) * es, 2 * valid * d_out * r,
+                        io=valid * d_out * es,
                     )
                 if frow is not None:
                     tab(ft, dt, r, N.FT_FIELDS).add(frow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
-                                                    (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es)
+                                                    (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es,
+                                                    2 * valid * d_out * r, io=valid * d_out * es)
                 c0 += r
             if a_leaves:
                 scal = {s.scaling for s in ch if s.a_leaf is not None}
@@ -936,20 +946,22 @@ class GhostPlan:
                             self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, sf, n_seg, sc,
                                         [(s_leaf, col0, r)], pe_off, slot_base),
                             n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
-                            (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * es)
+                            (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * es, 2 * valid * d_in * r,
+                            io=valid * d_in * es)
                 else:
                     tab(ft, dt, rtot, N.FT_FIELDS).add(
                         self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
                                     a_leaves, pe_off, slot_base),
                         n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, rtot),
                         (valid * d_in + planes * rtot * valid) * es
-                        + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * es)
+                        + n_seg * sum(rk for _, _, rk in a_leaves) * d_in * es, 2 * valid * d_in * rtot,
+                        io=valid * d_in * es)
 
         # Most work first (the fused launch has one workgroup per segment, of
         # very different lengths).
         fp = _Table(N.FT_FIELDS)
-        for _, _, row, blocks, nbytes in sorted(fused_rows, key=lambda t: (t[0], t[1])):
-            fp.add(row, blocks, nbytes)
+        for _, _, row, blocks, nbytes, io, fl in sorted(fused_rows, key=lambda t: (t[0], t[1])):
+            fp.add(row, blocks, nbytes, fl, io=io)
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
@@ -965,7 +977,7 @@ class GhostPlan:
                     N.SQ_DTYPE: dtype_code(pe_m.dtype) | ((1 if self.square_f64 else 0) << 8),
                 },
                 n_seg * lib.odp_sqnorm_blocks(n),
-                n_seg * n * pe_m.element_size(),
+                n_seg * n * pe_m.element_size(), io=n_seg * n * pe_m.element_size(),
             )
             mat_pe[m.leaf] = pe_m
 
@@ -1005,7 +1017,8 @@ class GhostPlan:
         for t, v, off in masks.values():
             nft.add({N.NF_P: t.data_ptr(), N.NF_LDP: t.stride(0), N.NF_D: t.shape[1],
                      N.NF_SEG_FIRST: v.first, N.NF_NSEG: v.n_seg, N.NF_MASK: mask_addr(off)},
-                    int(lib.odp_nonfinite_blocks(t.shape[1], v.n_seg)), v.valid * t.shape[1] * 2)
+                    int(lib.odp_nonfinite_blocks(t.shape[1], v.n_seg)), v.valid * t.shape[1] * 2,
+                    io=v.valid * t.shape[1] * 2)
 
         # Clipped sums read X' = c_i x_t (odp_linear_prescale) from a scratch
         # buffer, one X' per (activation, group, class), filled chunk by chunk
@@ -1045,7 +1058,8 @@ class GhostPlan:
                                N.LN_SEG_FIRST: v.first, N.LN_NSEG: v.n_seg, N.LN_NROWS: x.shape[0],
                                N.LN_FLAGS: (lf.group << 8) | (lf.cls << 24), N.LN_OUT: self.xs[off:].data_ptr(),
                                N.LN_XMASK: mask_addr(site_mask[i][0])},
-                              int(lib.odp_linear_prescale_blocks(x.shape[0])), 2 * v.valid * x.shape[1] * 2)
+                              int(lib.odp_linear_prescale_blocks(x.shape[0])), 2 * v.valid * x.shape[1] * 2,
+                              io=v.valid * x.shape[1] * 2)
         lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS),
                N.FORM_GRAM256: _Table(N.LN_FIELDS)}
         # fp32 scratch of the 256-row-block Gram kernel (its X blocks).
@@ -1076,7 +1090,8 @@ class GhostPlan:
             scr_at = self.gram_scr.data_ptr() + lin_scr[i] if i in lin_scr else 0
             lnt[form].add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_off[i], N.LN_NB: nb_max,
                            N.LN_PE: pe_at, N.LN_NFFLAG: self._nf_flag_addr, N.LN_SCRATCH: scr_at}, blocks,
-                          valid * (d_in + d_out) * 2 + (n_seg * d_in * d_out * 2 if pe_at else 0), fl)
+                          valid * (d_in + d_out) * 2 + (n_seg * d_in * d_out * 2 if pe_at else 0), fl,
+                          io=valid * (d_in + d_out) * 2)
             if i in lin_pe:
                 continue
             lf = self.leaves[ls.w_leaf]
@@ -1087,7 +1102,8 @@ class GhostPlan:
                 lmom.add({**common, N.LN_OUT: out.data_ptr(), N.LN_OUT2: o2.data_ptr(), N.LN_FLAGS: flags},
                          int(lib.odp_linear_moments_blocks(d_in, d_out)),
                          valid * (d_in + d_out) * 2 + 2 * d_in * d_out * out.element_size(),
-                         2 * valid * d_in * d_out)
+                         2 * valid * d_in * d_out,
+                         io=valid * (d_in + d_out) * 2 + 2 * d_in * d_out * out.element_size())
                 continue
             row, into = {**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags}, lsum
             if site_chunk[i] is not None:
@@ -1097,7 +1113,9 @@ class GhostPlan:
                 into = xs_sum[c]
             into.add(row, int(lib.odp_linear_sum_blocks(d_in, d_out)),
                      valid * (d_in + d_out) * 2 + d_in * d_out * out.element_size(),
-                     2 * valid * d_in * d_out)
+                     2 * valid * d_in * d_out,
+                     io=(0 if site_chunk[i] is not None else valid * (d_in + d_out) * 2)
+                     + d_in * d_out * out.element_size())
         lin_leaves = {ls.w_leaf for ls in lins}
 
         ss = _Table(N.SS_FIELDS)
@@ -1115,7 +1133,8 @@ class GhostPlan:
             ss.add({N.SS_PE: self.lin_pe[off:].data_ptr(), N.SS_M: M, N.SS_RANK: 1, N.SS_SEG_FIRST: v.first,
                     N.SS_NSEG: v.n_seg, N.SS_OUT: out.data_ptr(), N.SS_FLAGS: flags, N.SS_OUT2: out2},
                    lib.odp_scale_sum_blocks(M),
-                   v.n_seg * M * 2 + M * out.element_size() * (2 if self.out2 is not None else 1))
+                   v.n_seg * M * 2 + M * out.element_size() * (2 if self.out2 is not None else 1),
+                   io=M * out.element_size() * (2 if self.out2 is not None else 1))
         for i, lf in enumerate(self.leaves):
             if i in lin_leaves:
                 continue
@@ -1140,6 +1159,7 @@ class GhostPlan:
                 lib.odp_scale_sum_blocks(rank * M),
                 n_seg * rank * M * (self.pe[pe_dt[i]].element_size() if i not in mat_pe else mat_pe[i].element_size())
                 + rank * M * out.element_size() * (2 if self.out2 is not None else 1),
+                io=rank * M * out.element_size() * (2 if self.out2 is not None else 1),
             )
 
         # Upload everything in one copy.
@@ -1170,7 +1190,8 @@ class GhostPlan:
         tab_idx = []
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
-            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total, (t.nbytes, t.nflops)))
+            tab_idx.append((name, dt, pack.add(probs), pack.add(ws), len(t.rows), total,
+                            (t.nbytes, t.nflops, t.io_bytes)))
         idx["gstart"] = pack.add(gstart)
         idx["thr"] = pack.add(np.asarray(self.clip.thresholds, dtype=np.float64))
         guards = self.clip.guards or [(1.0, 0.0, torch.float32)]
@@ -1190,8 +1211,10 @@ class GhostPlan:
         self.gstart, self.thr = views[idx["gstart"]], views[idx["thr"]]
         self.guard, self.cls_dt = views[idx["guard"]], views[idx["cls_dt"]]
         self.tables = [(name, dt, views[pi], views[wi], n, total) for name, dt, pi, wi, n, total, _ in tab_idx]
-        # Per launch, in launch order: (stage, key, workgroups, algorithmic bytes, algorithmic flops).
-        info = [(name, dt, total, nb[0], nb[1]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
+        # Per launch, in launch order: (stage, key, workgroups, algorithmic bytes, algorithmic flops,
+        # contract bytes: the part of the bytes that reads activations and
+        # output gradients or writes the clipped sums).
+        info = [(name, dt, total, nb[0], nb[1], nb[2]) for name, dt, _, _, _, total, nb in tab_idx if total > 0]
         after_clip = _AFTER_CLIP
         self.launch_info = [i for i in info if i[0] not in after_clip] + [i for i in info if i[0] in after_clip]
 
@@ -1531,7 +1554,7 @@ class GhostPlan:
                 N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
             },
             lib.odp_project_blocks(dtype_code(dt), n_rows, r),
-            (valid * d_out + r * d_out + planes * r * valid) * es,
+            (valid * d_out + r * d_out + planes * r * valid) * es, 2 * valid * d_out * r, io=valid * d_out * es,
         )
         # V = X A and the dA^T rows (scaling * sum_t U[k][t] X[t][m]) in one
         # pass over X: the fused kernel with X, A^T and U in the places of G,
@@ -1553,7 +1576,7 @@ class GhostPlan:
             rj[N.FT_LEAF0] = pe0 + j * r * d_in * pe_es
             fused_rows.append((-ln * d_in, len(fused_rows), rj, 1,
                                (ln * d_in + 2 * planes * r * ln) * es + r * d_in * es
-                               + (r * d_in * es if j == 0 else 0)))
+                               + (r * d_in * es if j == 0 else 0), ln * d_in * es, 4 * ln * d_in * r))
         # dB^T rows from G and V.
         if s.b_leaf is not None:
             tab(ft, dt, r, N.FT_FIELDS).add(
@@ -1567,7 +1590,8 @@ class GhostPlan:
                     N.FT_LEAF0 + 2: slot_base[s.b_leaf],
                 },
                 n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
-                (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es)
+                (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es, 2 * valid * d_out * r,
+                io=valid * d_out * es)
 
     def _fusable(self, dt: torch.dtype, r: int, v: _SegView, g: torch.Tensor) -> bool:
         """Whether a site's G side runs as one odp_seg_factor_project pass."""
