@@ -219,13 +219,15 @@ int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
 /* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
  * For leaves that are not behind a captured linear op, the per-example
  * gradients X[n_seg][n] are materialised; each workgroup sums x^2
- * (non-finite x counted as 0; squared in float32, or in float64 with bit 8
- * of ODP_SQ_DTYPE, as clip_pytree's accumulation dtype does) over a chunk
+ * (non-finite x counted as 0 unless bit 9 of ODP_SQ_DTYPE is set; squared
+ * in float32, or in float64 with bit 8, as clip_pytree's accumulation dtype
+ * does) over a chunk
  * of one segment in fp64 and writes part[seg_example[s] * part_stride +
  * slot + chunk]; a problem uses odp_sqnorm_blocks(n) slots.               */
 enum {
   ODP_SQ_X = 0, ODP_SQ_N = 1, ODP_SQ_NSEG = 2, ODP_SQ_SEG_FIRST = 3,
-  ODP_SQ_SLOT = 4, ODP_SQ_DTYPE = 5, /* x dtype | square in float64 << 8  */
+  ODP_SQ_SLOT = 4, ODP_SQ_DTYPE = 5, /* x dtype | square in float64 << 8
+                                        | keep non-finite x << 9           */
   ODP_SQ_FIELDS = 8
 };
 int64_t odp_sqnorm_blocks(int64_t n);
@@ -262,8 +264,13 @@ int odp_clip_factors(odp_stream_t stream, const double* part, int64_t n_slots, i
  * a static device array of odp_noalloc_max_partials() doubles (8 MiB) that
  * each GPU holds until the process ends, cleared at every call: it returns
  * ODP_ERR_UNSUPPORTED when n_ex * n_slots exceeds that.  Allocates nothing.
- * Calls that overlap on one GPU share the array and race; the stream must
- * belong to the current device.                                          */
+ * A table entry whose example index or slot falls outside the n_ex x
+ * n_slots partials has its write dropped on the device (nothing is written
+ * past the array); the call then reports every example's norm as NaN with
+ * zero scales and clear masks, since its partials are incomplete (the
+ * launch is asynchronous, so no status code can say so).  Calls that
+ * overlap on one GPU share the array and race; the stream must belong to
+ * the current device.                                                     */
 int64_t odp_noalloc_max_partials(void);
 int odp_clip_materialized_noalloc(odp_stream_t stream, const int64_t* sq_problems,
                                   const int32_t* sq_work_start, int32_t sq_n_prob,
@@ -287,9 +294,11 @@ enum {
   ODP_SS_SEG_FIRST = 3, ODP_SS_NSEG = 4,
   ODP_SS_OUT = 5,       /* address of the output leaf                       */
   ODP_SS_FLAGS = 6,     /* out dtype | transpose << 8 | group << 16 | cls << 40
-                           | wide << 48 | pe dtype << 56; transpose 0 writes
-                           [rank][M], 1 writes [M][rank]; non-finite pe
-                           values count 0                                   */
+                           | wide << 48 | raw << 52 | pe dtype << 56;
+                           transpose 0 writes [rank][M], 1 writes [M][rank];
+                           non-finite pe values count 0; raw: the values are
+                           already scaled (a caller's scale function) and
+                           are summed as they are, scale 1, non-finite kept */
   ODP_SS_OUT2 = 7,      /* address of the second-moment output or 0         */
   ODP_SS_FIELDS = 8
 };

@@ -7,6 +7,7 @@ fallback implementation, so a missing library raises immediately.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libopaque_dp.so"
@@ -131,7 +132,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = Path(path) if path is not None else LIB_PATH
+    # OPAQUE_AMD_LIBRARY names another build of the same library (the
+    # sanitizer test loads the instrumented one this way).
+    p = Path(path) if path is not None else Path(os.environ.get("OPAQUE_AMD_LIBRARY") or LIB_PATH)
     if not p.exists():
         raise RuntimeError(
             f"opaque_amd native library not found at {p}. Build it with "

@@ -66,6 +66,44 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+SAN_DIR = PKG_DIR / "_asan_build"
+SAN_LIB = SAN_DIR / LIB_NAME
+# The host side of the library instrumented for address and undefined-
+# behaviour errors (device code is built as usual).  It is loaded only by
+# the CPU test of the C ABI's argument and error handling, in a process
+# that preloads the sanitizer runtime.
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-Xarch_host", "-fsanitize=address",
+             "-Xarch_host", "-fsanitize=undefined"]
+
+
+def sanitizer_runtime() -> Path | None:
+    """The compiler's AddressSanitizer runtime, which a process must preload
+    to load the instrumented library."""
+    llvm = Path(hipcc_path()).resolve().parent.parent / "llvm"
+    for cand in sorted(llvm.glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")) + \
+            sorted(Path("/opt/rocm/llvm").glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")):
+        return cand
+    return None
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    """Compile opaque_amd/_asan_build/libopaque_dp.so with the sanitizers on
+    the host code; skipped when it is newer than every source."""
+    srcs = [CSRC / s for s in SOURCES] + sorted(CSRC.glob("*.h")) + [INCLUDE / "opaque_dp.h"]
+    if SAN_LIB.exists() and SAN_LIB.stat().st_mtime > max(p.stat().st_mtime for p in srcs):
+        return SAN_LIB
+    SAN_DIR.mkdir(exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-O3"] + SAN_FLAGS
+    tmp = SAN_LIB.with_name(LIB_NAME + f".tmp{os.getpid()}")
+    cmd = [hipcc_path(), *flags, f"-I{INCLUDE}", f"-I{CSRC}", *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        tmp.unlink(missing_ok=True)
+        raise RuntimeError(f"hipcc (sanitized) failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, SAN_LIB)
+    return SAN_LIB
+
+
 HOST_SRC = CSRC / "odp_host.cpp"
 HOST_DIR = PKG_DIR / "_host_build"
 HOST_NAME = "_odp_host"

@@ -427,9 +427,10 @@ class _ClipEngine:
         cn = self.clipping_norm
         effective = cn.effective if isinstance(cn, PerGroup) else float(cn)
         if self.scale_fn is not None:
-            # The values arrive already scaled by the caller's _scale_fn: the
-            # kernels sum them with every scale 1 (an infinite threshold
-            # passes a gradient through unchanged, _pytree.py:513-518).
+            # The values arrive already scaled by the caller's _scale_fn; the
+            # plan sums them with scale 1 (raw_values) and the clip factors
+            # only supply their norms (the clipped norms), so no threshold
+            # applies.
             thresholds = [float("inf")] * len(thresholds)
             effective = float("inf")
         spec = ClipSpec(
@@ -524,8 +525,12 @@ class _ClipEngine:
         names, spec, square_f64, outs, outs_key = self._spec_memo[1]
         # The batch sum accumulates in compute_dtype when one is given
         # (_clipped_fun.py:115-134): float64 on request, float32 otherwise.
+        # A caller's _scale_fn already scaled the values: they are summed as
+        # they are (scale 1, non-finite entries kept), as the reference sums
+        # the scale function's output (_clipped_fun.py:673-700, 777-782).
         kw = dict(second_moment=self.second_moment, square_f64=square_f64,
-                  sum_f64=self.compute_dtype == torch.float64, **self.plan_options)
+                  sum_f64=self.compute_dtype == torch.float64, raw_values=self.scale_fn is not None,
+                  **self.plan_options)
         if self._lora_ptrs.numel() < LORA_PTRS * len(sites):
             self._lora_ptrs = torch.empty(LORA_PTRS * len(sites), dtype=torch.int64)
         key = plan_key(segments=segments, leaves=outs, clip=spec, lora_sites=sites, materialized=mats,

@@ -52,14 +52,29 @@ __device__ __forceinline__ double finalize_scale(double ratio, double rel, doubl
 // models) is bound by what one CU can have in flight, so each thread issues
 // CL_DEPTH 16-byte loads at once; the order of additions is fixed (it does
 // not depend on which loads are masked), so runs are bitwise reproducible.
+// `status` (optional): a word that k_sqnorm sets when it dropped a write
+// outside the partials; every example then gets a NaN norm, zero scales and
+// clear masks, since the partials are incomplete.
 __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
     const double* __restrict__ part, int64_t n_slots, int n_ex, const int64_t* __restrict__ gstart, int n_groups,
     const double* __restrict__ thr, double eff_thr, int mode, double gamma, int n_cls,
     const double* __restrict__ guard, const int32_t* __restrict__ cls_dtype,
     double* __restrict__ scale_out, float* __restrict__ norm_out, float* __restrict__ gnorm_out,
-    uint8_t* __restrict__ clip_out, uint8_t* __restrict__ clip_total_out) {
+    uint8_t* __restrict__ clip_out, uint8_t* __restrict__ clip_total_out, const uint32_t* __restrict__ status) {
   const int ex = blockIdx.x;
   const int t = threadIdx.x;
+  if (status != nullptr && *status != 0u) {
+    if (t == 0) {
+      norm_out[ex] = __builtin_nanf("");
+      if (clip_total_out) clip_total_out[ex] = 0;
+    }
+    if (t < n_groups) {
+      if (gnorm_out) gnorm_out[(int64_t)t * n_ex + ex] = __builtin_nanf("");
+      if (clip_out) clip_out[(int64_t)t * n_ex + ex] = 0;
+      for (int k = 0; k < n_cls; ++k) scale_out[((int64_t)k * n_groups + t) * n_ex + ex] = 0.0;
+    }
+    return;
+  }
   __shared__ double red[CL_THREADS / 64];
   __shared__ double gsq[CL_MAX_GROUPS];
   __shared__ double sguard[16];
@@ -79,10 +94,11 @@ __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
 #pragma unroll
     for (int q = 0; q < CL_DEPTH; ++q) a[q] = 0.0;
     // Slots are read in 16-byte pairs from the first 16-byte aligned one
-    // (a leading and a trailing odd slot go to thread 0), and every load of
-    // a round is issued before the first add (masked past the group's end).
+    // (by address, so any 8-byte aligned partials buffer works; a leading
+    // and a trailing odd slot go to thread 0), and every load of a round is
+    // issued before the first add (masked past the group's end).
     const int64_t lo = gstart[g];
-    int64_t la = lo + (((int64_t)ex * n_slots + lo) & 1);
+    int64_t la = lo + (int64_t)((((uintptr_t)(row + lo)) >> 3) & 1u);
     la = la < hi ? la : hi;
     const int64_t npair = (hi - la) >> 1;
     if (t == 0) {
@@ -135,24 +151,28 @@ __global__ __launch_bounds__(CL_THREADS) void k_clip_factors(
 // in segment order.  Each term is scale * value rounded to the value's dtype
 // (clip_pytree's `scale.to(dtype) * leaf`), accumulated in float32, or in
 // float64 (Acc = double) for float64 values or a float64 compute dtype.
-// This element-wise form serves float16/float64 and the float64 sums; the
-// kernel below vectorises float32/bfloat16.
+// This element-wise form serves float16/float64, the float64 sums and raw
+// sums; the kernel below vectorises float32/bfloat16.  `raw`: the values
+// are already scaled (a caller's scale function): each is summed as it is,
+// with scale 1 and no nan_to_num, as the reference sums a scale function's
+// output (_clipped_fun.py:673-700, 777-782).
 template <typename Acc>
 __device__ __forceinline__ void scale_sum_generic(const void* pe, int pdt, int64_t E, int64_t e0, int n_seg,
                                                   int seg_first, const int32_t* __restrict__ sex,
                                                   const double* __restrict__ sc, float normalize_by, void* out,
-                                                  void* out2, int odt, int transpose, int64_t M, int rank) {
+                                                  void* out2, int odt, int transpose, int64_t M, int rank,
+                                                  bool raw) {
   Acc acc[SS_ELEMS], acc2[SS_ELEMS];
 #pragma unroll
   for (int i = 0; i < SS_ELEMS; ++i) acc[i] = acc2[i] = (Acc)0;
   for (int s = 0; s < n_seg; ++s) {
-    const double c = sc[sex[seg_first + s]];
+    const double c = raw ? 1.0 : sc[sex[seg_first + s]];
 #pragma unroll
     for (int i = 0; i < SS_ELEMS; ++i) {
       if (e0 + i >= E) break;
       const double v = odp_load_as_double(pe, (int64_t)s * E + e0 + i, pdt);
       double y = 0.0, yy = 0.0;
-      if (isfinite(v)) {  // nan_to_num of the per-example value
+      if (raw || isfinite(v)) {  // nan_to_num of the per-example value
         if (pdt == ODP_DTYPE_F64) {
           y = c * v;
           yy = y * y;
@@ -374,20 +394,21 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
   const int grp = (int)((flags >> 16) & 0xffffff);
   const int cls = (int)((flags >> 40) & 0xff);
   const int wide = (int)((flags >> 48) & 1);
+  const bool raw = ((flags >> 52) & 1) != 0;
   const int pdt = (int)((flags >> 56) & 0xff);
   const int64_t E = M * rank;
   const double* sc = scales + ((int64_t)cls * n_groups + grp) * n_ex;
-  const bool generic = wide || pdt == ODP_DTYPE_F64 || pdt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F16 ||
+  const bool generic = wide || raw || pdt == ODP_DTYPE_F64 || pdt == ODP_DTYPE_F16 || odt == ODP_DTYPE_F16 ||
                        odt == ODP_DTYPE_F64 || (E & 7) != 0;
   if (generic) {
     const int64_t e0 = ((int64_t)(bid - ws[p]) * SS_THREADS + threadIdx.x) * SS_ELEMS;
     if (e0 >= E) return;
     if (wide || pdt == ODP_DTYPE_F64)
       scale_sum_generic<double>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
-                                M, rank);
+                                M, rank, raw);
     else
       scale_sum_generic<float>(pe, pdt, E, e0, n_seg, seg_first, sex, sc, normalize_by, out, out2, odt, transpose,
-                               M, rank);
+                               M, rank, raw);
     return;
   }
   const bool bf_in = pdt == ODP_DTYPE_BF16;
@@ -437,11 +458,13 @@ __global__ __launch_bounds__(SS_THREADS) void k_scale_sum(
 constexpr int SQ_THREADS = 256;
 constexpr int64_t SQ_CHUNK = 8192;
 
+// Writes outside the partials ([0, n_ex) x [0, part_stride)) are dropped;
+// `status` (optional) is then set to 1.
 __global__ __launch_bounds__(SQ_THREADS) void k_sqnorm(const int64_t* __restrict__ probs,
                                                        const int32_t* __restrict__ ws, int n_prob,
                                                        const int32_t* __restrict__ sex,
                                                        double* __restrict__ part,
-                                                       int64_t part_stride) {
+                                                       int64_t part_stride, int n_ex, uint32_t* status) {
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_SQ_FIELDS;
@@ -451,6 +474,7 @@ __global__ __launch_bounds__(SQ_THREADS) void k_sqnorm(const int64_t* __restrict
   const int64_t slot = f[ODP_SQ_SLOT];
   const int dt = (int)(f[ODP_SQ_DTYPE] & 0xff);
   const bool sq64 = ((f[ODP_SQ_DTYPE] >> 8) & 1) != 0;
+  const bool raw = ((f[ODP_SQ_DTYPE] >> 9) & 1) != 0;  // no nan_to_num
   const int64_t nchunk = (n + SQ_CHUNK - 1) / SQ_CHUNK;
   const int64_t local = bid - ws[p];
   const int64_t seg = local / nchunk, chunk = local % nchunk;
@@ -459,13 +483,13 @@ __global__ __launch_bounds__(SQ_THREADS) void k_sqnorm(const int64_t* __restrict
   if (sq64) {
     for (int64_t i = lo + threadIdx.x; i < hi; i += SQ_THREADS) {
       double x = odp_load_as_double(X, seg * n + i, dt);
-      if (!isfinite(x)) x = 0.0;  // nan_to_num before the norm
+      if (!raw && !isfinite(x)) x = 0.0;  // nan_to_num before the norm
       acc += x * x;
     }
   } else {
     for (int64_t i = lo + threadIdx.x; i < hi; i += SQ_THREADS) {
       float x = odp_load_as_float(X, seg * n + i, dt);
-      if (!isfinite(x)) x = 0.f;
+      if (!raw && !isfinite(x)) x = 0.f;
       acc += (double)__fmul_rn(x, x);
     }
   }
@@ -476,7 +500,13 @@ __global__ __launch_bounds__(SQ_THREADS) void k_sqnorm(const int64_t* __restrict
     if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) part[(int64_t)sex[seg_first + seg] * part_stride + slot + chunk] = red[0];
+  if (threadIdx.x == 0) {
+    const int ex = sex[seg_first + seg];
+    if (ex >= 0 && ex < n_ex && slot >= 0 && slot + chunk < part_stride)
+      part[(int64_t)ex * part_stride + slot + chunk] = red[0];
+    else if (status != nullptr)
+      odp_gstore(status, 1u);  // every such writer stores the same value
+  }
 }
 
 }  // namespace
@@ -496,7 +526,7 @@ extern "C" int odp_sqnorm(odp_stream_t stream, const int64_t* problems, const in
     return ODP_ERR_INVALID_ARGUMENT;
   }
   hipLaunchKernelGGL(k_sqnorm, dim3(total_blocks), dim3(SQ_THREADS), 0, odp_hip_stream(stream),
-                     problems, work_start, n_prob, seg_example, part, part_stride);
+                     problems, work_start, n_prob, seg_example, part, part_stride, INT32_MAX, nullptr);
   return odp_check_launch("odp_sqnorm");
 }
 
@@ -552,7 +582,7 @@ extern "C" int odp_clip_factors(odp_stream_t stream, const double* part, int64_t
   hipLaunchKernelGGL(k_clip_factors, dim3(n_ex), dim3(CL_THREADS), 0, odp_hip_stream(stream), part,
                      n_slots, n_ex, group_slot_start, n_groups, thresholds, effective_threshold, mode,
                      gamma, n_cls, guard, cls_dtype, scale_out, norm_out, group_norm_out,
-                     clipped_out, clipped_total_out);
+                     clipped_out, clipped_total_out, nullptr);
   return odp_check_launch("odp_clip_factors");
 }
 
@@ -595,7 +625,8 @@ extern "C" int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const
 // itself to a kernel.  Every call on a GPU shares that GPU's array, so calls
 // that overlap on one GPU race.
 // ---------------------------------------------------------------------------
-static __device__ __align__(256) double scratch[ODP_NOALLOC_MAX_PARTIALS];
+// The partials, then one status word (k_sqnorm's dropped writes).
+static __device__ __align__(256) double scratch[ODP_NOALLOC_MAX_PARTIALS + 32];
 
 namespace {
 
@@ -630,11 +661,12 @@ int scratch_on_current_device(double** out) {
   return ODP_OK;
 }
 
-// Clears n partials (a kernel, not a memset: the call may be captured into
-// a graph).
-__global__ __launch_bounds__(256) void k_zero_partials(double* __restrict__ p, int64_t n) {
+// Clears n partials and the status word (a kernel, not a memset: the call
+// may be captured into a graph).
+__global__ __launch_bounds__(256) void k_zero_partials(double* __restrict__ p, int64_t n, uint32_t* status) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = 0.0;
+  if (i == 0) *status = 0u;
 }
 
 }  // namespace
@@ -666,21 +698,23 @@ extern "C" int odp_clip_materialized_noalloc(
   double* part = nullptr;
   rc = scratch_on_current_device(&part);
   if (rc != ODP_OK) return rc;
+  uint32_t* status = (uint32_t*)(part + ODP_NOALLOC_MAX_PARTIALS);
   hipStream_t s = odp_hip_stream(stream);
   const int64_t n = (int64_t)n_ex * n_slots;
-  if (n > 0) {
-    hipLaunchKernelGGL(k_zero_partials, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, n);
-    rc = odp_check_launch(what);
-    if (rc != ODP_OK) return rc;
-  }
+  hipLaunchKernelGGL(k_zero_partials, dim3((unsigned)((n + 255) / 256 > 0 ? (n + 255) / 256 : 1)), dim3(256), 0, s,
+                     part, n, status);
+  rc = odp_check_launch(what);
+  if (rc != ODP_OK) return rc;
   if (sq_total_blocks > 0) {
+    // The kernel's bounds checks keep every write inside the n_ex x n_slots
+    // partials (a malformed table cannot write past the static array).
     hipLaunchKernelGGL(k_sqnorm, dim3(sq_total_blocks), dim3(SQ_THREADS), 0, s, sq_problems, sq_work_start,
-                       sq_n_prob, seg_example, part, n_slots);
+                       sq_n_prob, seg_example, part, n_slots, n_ex, status);
     rc = odp_check_launch(what);
     if (rc != ODP_OK) return rc;
   }
   hipLaunchKernelGGL(k_clip_factors, dim3(n_ex), dim3(CL_THREADS), 0, s, part, n_slots, n_ex, group_slot_start,
                      n_groups, thresholds, effective_threshold, mode, gamma, n_cls, guard, cls_dtype, scale_out,
-                     norm_out, group_norm_out, clipped_out, clipped_total_out);
+                     norm_out, group_norm_out, clipped_out, clipped_total_out, status);
   return odp_check_launch(what);
 }

@@ -254,6 +254,21 @@ GRAM256_ITEM_BYTES = 256 * 256 * 4
 GRAM256_FLOP_COST = 1.2
 
 
+def split_budget(avail: int | None, stored: int, prescale_bytes: int) -> tuple[int, int]:
+    """(Gram scratch bytes, prescaled-activation bytes) a plan may use, from
+    the device memory available when it is built (``avail``; None off the
+    GPU: no device limit) once ``stored`` bytes of per-example gradients are
+    placed.  The 256-row Gram kernels' scratch gets up to a quarter of the
+    rest (and at most GRAM256_SCRATCH_BYTES), the prescaled activations up
+    to half of what then remains (and at most ``prescale_bytes``), so the
+    three together never exceed ``avail``."""
+    if avail is None:
+        return GRAM256_SCRATCH_BYTES, prescale_bytes
+    rest = max(0, avail - stored)
+    scr = min(GRAM256_SCRATCH_BYTES, rest // 4)
+    return scr, min(prescale_bytes, (rest - scr) // 2)
+
+
 def choose_form(max_len: int, d_in: int, d_out: int) -> int:
     """The faster form: GRAM costs L^2 (d_in + d_out) flops per example (upper
     triangle) at GRAM_FLOP_COST (GRAM256_FLOP_COST from GRAM256_MIN_LEN rows)
@@ -418,7 +433,7 @@ def leaves_key(leaves: list[LeafOut]) -> tuple:
 
 # GhostPlan's keyword options and their defaults (part of a plan's key).
 _PLAN_OPTIONS = {"second_moment": False, "fuse_g_side": True, "prescale_bytes": 8 << 30,
-                 "linear_pe_bytes": None, "square_f64": False, "sum_f64": False}
+                 "linear_pe_bytes": None, "square_f64": False, "sum_f64": False, "raw_values": False}
 
 
 def plan_key(*, segments: Segments, leaves: list[LeafOut], clip: ClipSpec, lora_sites=(), materialized=(),
@@ -499,6 +514,9 @@ class GhostPlan:
     reference's accumulation dtype when a leaf is float64 or
     compute_dtype=float64); ``sum_f64``: the clipped sums of stored
     gradients accumulate in float64 (compute_dtype=float64).
+    ``raw_values``: the materialised leaves hold values a caller's scale
+    function already scaled: they are summed as they are (scale 1, non-finite
+    entries kept) and their norms taken without nan_to_num.
     ``second_moment``: the plan also sums the squared clipped per-example
     gradients; full-weight sites whose gradients are not stored then take
     the moments kernel instead of the clipped-sum GEMM (both sums in float32).
@@ -520,6 +538,7 @@ class GhostPlan:
         linear_pe_bytes: int | None = None,
         square_f64: bool = False,
         sum_f64: bool = False,
+        raw_values: bool = False,
     ) -> None:
         t_build = time.perf_counter()
         N.load()
@@ -536,6 +555,7 @@ class GhostPlan:
         self.linear_pe_bytes = linear_pe_bytes
         self.square_f64 = bool(square_f64)
         self.sum_f64 = bool(sum_f64)
+        self.raw_values = bool(raw_values)
         self.n_groups = len(clip.thresholds)
         self.n_cls = max(1, len(clip.guards))
         if self.n_groups < 1:
@@ -551,7 +571,8 @@ class GhostPlan:
         self.key = plan_key(segments=segments, leaves=leaves, clip=clip, lora_sites=lora_sites,
                             materialized=materialized, linear_sites=linear_sites, device=dev,
                             second_moment=second_moment, fuse_g_side=fuse_g_side, prescale_bytes=prescale_bytes,
-                            linear_pe_bytes=linear_pe_bytes, square_f64=square_f64, sum_f64=sum_f64)
+                            linear_pe_bytes=linear_pe_bytes, square_f64=square_f64, sum_f64=sum_f64,
+                            raw_values=raw_values)
         self._build(list(lora_sites), list(materialized), list(linear_sites))
         self.build_ms = (time.perf_counter() - t_build) * 1e3  # host time of the construction
 
@@ -707,20 +728,27 @@ class GhostPlan:
         # form, which would still need the clipped-sum GEMM, whatever the
         # sequence length.  The other sites take the faster norm form and
         # the GEMM.
-        budget = self.linear_pe_bytes
-        if budget is None:
-            budget = 0
-            if dev.type == "cuda" and lins:
-                # Free device memory plus what torch's allocator holds unused
-                # (an earlier plan's buffers), so repeated calls see the same
-                # budget.
-                cached = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
-                budget = (torch.cuda.mem_get_info(dev)[0] + cached) // 2
+        # One reading of the device memory available to the plan (free plus
+        # what torch's allocator holds unused, e.g. an earlier plan's
+        # buffers, so repeated calls see the same budgets) is shared by the
+        # stored gradients, the Gram scratch and the prescaled activations.
+        avail = 0
+        if dev.type == "cuda" and lins:
+            cached = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
+            avail = torch.cuda.mem_get_info(dev)[0] + cached
+        budget = self.linear_pe_bytes if self.linear_pe_bytes is not None else avail // 2
         lin_pe: dict[int, int] = {}  # site -> element offset in self.lin_pe
         pe_total = 0
+        for i, ls in enumerate(lins):
+            v = reg.view(ls.segments)
+            n = v.n_seg * ls.x.shape[-1] * ls.g.shape[-1]
+            if ls.form in (None, N.FORM_OUTER) and (pe_total + n) * 2 <= budget:
+                lin_pe[i] = pe_total
+                pe_total += (n + 127) // 128 * 128
+        scr_budget, self._prescale_budget = split_budget(avail if dev.type == "cuda" else None, 2 * pe_total,
+                                                         self.prescale_bytes)
         lin_scr: dict[int, int] = {}  # site -> byte offset in self.gram_scr (GRAM256 sites)
         scr_total = 0
-        scr_budget = None
         lin_form: list[int] = []
         lin_view: list[_SegView] = []
         lin_off: list[int] = []
@@ -729,21 +757,13 @@ class GhostPlan:
         for i, ls in enumerate(lins):
             d_in, d_out = ls.x.shape[-1], ls.g.shape[-1]
             v = reg.view(ls.segments)
-            n = v.n_seg * d_in * d_out
-            if ls.form in (None, N.FORM_OUTER) and (pe_total + n) * 2 <= budget:
-                lin_pe[i] = pe_total
-                pe_total += (n + 127) // 128 * 128
+            if i in lin_pe:
                 form = N.FORM_OUTER
             else:
                 form = ls.form if ls.form is not None else choose_form(v.max_len, d_in, d_out)
             if (form == N.FORM_GRAM and v.max_len >= GRAM256_MIN_LEN) or form == N.FORM_GRAM256:
                 need = v.n_seg * int(lib.odp_linear_tiles(N.FORM_GRAM256, d_in, d_out, v.max_len)) \
                     * GRAM256_ITEM_BYTES
-                if scr_budget is None:
-                    scr_budget = GRAM256_SCRATCH_BYTES
-                    if dev.type == "cuda":
-                        cached = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
-                        scr_budget = min(scr_budget, (torch.cuda.mem_get_info(dev)[0] + cached) // 4)
                 if form == N.FORM_GRAM256 or scr_total + need <= scr_budget:
                     form = N.FORM_GRAM256
                     lin_scr[i] = scr_total
@@ -974,7 +994,8 @@ class GhostPlan:
                 {
                     N.SQ_X: pe_m.data_ptr(), N.SQ_N: n, N.SQ_NSEG: n_seg, N.SQ_SEG_FIRST: v.first,
                     N.SQ_SLOT: slot_base[m.leaf],
-                    N.SQ_DTYPE: dtype_code(pe_m.dtype) | ((1 if self.square_f64 else 0) << 8),
+                    N.SQ_DTYPE: dtype_code(pe_m.dtype) | ((1 if self.square_f64 else 0) << 8)
+                    | ((1 if self.raw_values else 0) << 9),
                 },
                 n_seg * lib.odp_sqnorm_blocks(n),
                 n_seg * n * pe_m.element_size(), io=n_seg * n * pe_m.element_size(),
@@ -1034,12 +1055,12 @@ class GhostPlan:
                 continue
             x, lf = lin_x[i], self.leaves[ls.w_leaf]
             nbytes = -(-x.shape[0] * x.shape[1] * 2 // 256) * 256
-            if nbytes > self.prescale_bytes:
+            if nbytes > self._prescale_budget:
                 site_chunk.append(None)
                 continue
             k = (x.data_ptr(), tuple(x.shape), tuple(x.stride()), lin_view[i].first, lf.group, lf.cls)
             if k not in cur:
-                if cur_bytes + nbytes > self.prescale_bytes:
+                if cur_bytes + nbytes > self._prescale_budget:
                     xs_chunks.append(cur)
                     cur, cur_bytes = {}, 0
                 cur[k] = (cur_bytes // 2, i)
@@ -1150,7 +1171,7 @@ class GhostPlan:
                 transpose = 1 if self._leaf_transposed(i, sites) else 0
                 pdt, pe_a = dtype_code(pe_dt[i]), pe_addr(i)
             flags = (dtype_code(lf.out_dtype) | (transpose << 8) | (lf.group << 16) | (lf.cls << 40)
-                     | (int(self.sum_f64) << 48) | (pdt << 56))
+                     | (int(self.sum_f64) << 48) | (int(self.raw_values and i in mat_pe) << 52) | (pdt << 56))
             ss.add(
                 {
                     N.SS_PE: pe_a, N.SS_M: M, N.SS_RANK: rank, N.SS_SEG_FIRST: v.first,

@@ -283,6 +283,53 @@ def test_custom_scale_fn():
         assert rel(res2.pytree[k], want[k] * 4.0) <= 1e-5, k
 
 
+def test_custom_scale_fn_output_is_summed_as_it_is():
+    """The reference sums a scale function's output as it is
+    (_clipped_fun.py:673-700, 777-782): NaN entries it returns stay NaN in
+    the sum, and values whose squares overflow float32 are still summed
+    (their clipped norms are inf, not a reason to drop the example).  Here
+    the function turns large entries into NaN and multiplies examples above
+    C by 1e30."""
+    import types
+
+    g = torch.Generator().manual_seed(9)
+    params = {"w": torch.randn(12, 5, generator=g), "b": torch.randn(5, generator=g)}
+    x = torch.randn(9, 12, generator=g) * torch.logspace(-1, 1, 9).view(9, 1)
+    y = torch.randn(9, 5, generator=g)
+    C, T = 30.0, 40.0
+
+    def f(p, xi, yi):
+        return ((xi @ p["w"] + p["b"] - yi) ** 2).sum()
+
+    def wild(grad):
+        nrm = torch.sqrt(sum((t.double() ** 2).sum() for t in grad.values()))
+        s = torch.where(nrm > C, torch.full_like(nrm, 1e30), torch.ones_like(nrm)).float()
+        out = {k: torch.where(v.abs() > T, torch.full_like(v, float("nan")), v) * s for k, v in grad.items()}
+        return out, types.SimpleNamespace(norm=nrm, group_norms=None)
+
+    pe = torch.func.vmap(torch.func.grad(f), in_dims=(None, 0, 0))(params, x, y)
+    scaled, norm = torch.func.vmap(lambda gr: (wild(gr)[0], wild(gr)[1].norm))(pe)
+    want = {k: v.sum(0) / 4.0 for k, v in scaled.items()}
+    # global_norm of the scaled gradient: float32 squares and sums.
+    want_cn = torch.sqrt(sum((v.float() ** 2).flatten(1).sum(1) for v in scaled.values()))
+    assert torch.isnan(want["w"]).any() and torch.isfinite(want["w"]).any()
+    assert torch.isinf(want_cn).any() and torch.isfinite(want_cn).any()
+
+    fn, st = clipped_grad(f, clipping_norm=C, batch_argnums=(1, 2), return_aux=True, normalize_by=4.0,
+                          _scale_fn=wild)
+    (res, aux), _ = fn({k: v.to(DEV) for k, v in params.items()}, x.to(DEV), y.to(DEV), state=st)
+    for k in params:
+        got, w = res.pytree[k].cpu(), want[k]
+        assert torch.equal(torch.isnan(got), torch.isnan(w)), k
+        fin = torch.isfinite(w)
+        scale = w[fin].abs().max()
+        assert ((got[fin] - w[fin]).abs() <= 1e-5 * w[fin].abs() + 1e-6 * scale).all(), k
+    cn = aux.clipped_grad_norms.cpu().float()
+    assert torch.equal(torch.isnan(cn), torch.isnan(want_cn)) and torch.equal(torch.isinf(cn), torch.isinf(want_cn))
+    fin = torch.isfinite(want_cn)
+    assert torch.allclose(cn[fin], want_cn[fin], rtol=1e-5)
+
+
 def test_per_group_matches_oracle():
     frozen, train = make_model(torch.float32)
     pg = per_group(train, up=0.3, down=0.2, norm=0.5)

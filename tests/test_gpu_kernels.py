@@ -158,6 +158,37 @@ def test_clip_factor_arithmetic_is_bit_exact():
             assert torch.equal(ct.cpu().bool(), nrm.float() > C)
 
 
+def test_clip_factors_take_partials_at_any_8_byte_offset():
+    """The partials may start 8 bytes past a 16-byte boundary (a sub-view of
+    a caller's buffer): the pair loads follow the address, and the result
+    equals that of an aligned copy up to the fp64 summation order."""
+    g = torch.Generator().manual_seed(2)
+    n_ex, n_slots = 5, 1001
+    sq = torch.rand(n_ex, n_slots, generator=g, dtype=torch.float64)
+    base = torch.zeros(n_ex * n_slots + 2, dtype=torch.float64, device=DEV)
+    out = {}
+    for off in (0, 1):
+        part = base[off : off + n_ex * n_slots]
+        part.copy_(sq.reshape(-1).to(DEV))
+        assert (part.data_ptr() % 16 == 8) == (off == 1)
+        gs = torch.tensor([0, 400, n_slots], dtype=torch.int64, device=DEV)
+        thr = torch.tensor([10.0, 12.0], dtype=torch.float64, device=DEV)
+        guard = torch.tensor([1.0 - 2**-23, 0.0], dtype=torch.float64, device=DEV)
+        cls = torch.tensor([N.DTYPE_F32], dtype=torch.int32, device=DEV)
+        scale = torch.empty((1, 2, n_ex), dtype=torch.float64, device=DEV)
+        norms = torch.empty(n_ex, dtype=torch.float32, device=DEV)
+        gn = torch.empty((2, n_ex), dtype=torch.float32, device=DEV)
+        N.call("odp_clip_factors", _stream(), part.data_ptr(), n_slots, n_ex, gs.data_ptr(), 2, thr.data_ptr(),
+               15.6, N.CLIP_FIXED, 0.0, 1, guard.data_ptr(), cls.data_ptr(), scale.data_ptr(), norms.data_ptr(),
+               gn.data_ptr(), None, None)
+        torch.cuda.synchronize()
+        out[off] = (gn.double().cpu(), scale.cpu())
+    want = torch.stack([sq[:, :400].sum(1), sq[:, 400:].sum(1)]).sqrt()
+    for off in (0, 1):
+        assert torch.allclose(out[off][0], want, rtol=1e-6)
+    assert torch.allclose(out[0][1], out[1][1], rtol=1e-6)
+
+
 @pytest.mark.parametrize("dt,shape", [(torch.float32, (3, 7)), (torch.bfloat16, (3, 7)),
                                       (torch.bfloat16, (6, 40)), (torch.float32, (5, 48))])
 def test_materialized_leaf_path(dt, shape):

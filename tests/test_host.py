@@ -204,6 +204,34 @@ def test_product_refuses_cpu_parameters():
         fn(torch.ones(3), torch.ones(2, 3), state=st)
 
 
+def test_outer_differentiating_transform_is_refused():
+    """The reference keeps the graph when an enclosing torch.func grad/jvp
+    differentiates its clipped gradient (_clipped_grad.py:261-265,
+    functional/_transform_stack.py:10-21).  The kernels here are not
+    differentiable, so such a call raises a named error before any device
+    work; vmap alone and the top level are not differentiating."""
+    from opaque_amd.clipping import under_differentiating_transform
+
+    assert not under_differentiating_transform()
+    seen = []
+    torch.func.vmap(lambda t: seen.append(under_differentiating_transform()) or t)(torch.ones(2))
+    torch.func.grad(lambda t: seen.append(under_differentiating_transform()) or t.sum())(torch.ones(2))
+    torch.func.jvp(lambda t: seen.append(under_differentiating_transform()) or t, (torch.ones(2),), (torch.ones(2),))
+    assert seen == [False, True, True]
+    for make in (lambda: clipped_grad(_loss, clipping_norm=1.0),
+                 lambda: auto_clipped_grad(_loss, R=1.0)):
+        fn, st = make()
+        x = torch.ones(3, 4)
+
+        def outer(p):
+            return fn(p, x, state=st)[0].pytree.sum()
+
+        with pytest.raises(NotImplementedError, match="not differentiable"):
+            torch.func.grad(outer)(torch.ones(4))
+        with pytest.raises(NotImplementedError, match="not differentiable"):
+            torch.func.jvp(outer, (torch.ones(4),), (torch.ones(4),))
+
+
 def test_gaussian_noise_validation():
     with pytest.raises(ValueError, match="non-negative"):
         gaussian_noise(noise_multiplier=-1.0, key=key(0))
@@ -375,6 +403,29 @@ def test_host_view_maker_matches_torch_views():
     d, u = vm2.make([raw])
     assert d.dtype == torch.float64 and torch.equal(d, raw[256 : 256 + 48].view(torch.float64).view(2, 3))
     assert u.dtype == torch.uint8 and torch.equal(u, raw[512:516])
+
+
+@pytest.mark.parametrize("avail_gib", [0, 1, 6, 40, 200, 288])
+@pytest.mark.parametrize("stored_frac", [0.0, 0.5])
+def test_plan_memory_budgets_fit_the_device(avail_gib, stored_frac):
+    """Stored per-example gradients (at most half the available memory by
+    default), the Gram scratch and the prescaled activations come out of one
+    reading of the available memory and never add up to more than it."""
+    from opaque_amd.engine import GRAM256_SCRATCH_BYTES, split_budget
+
+    avail = avail_gib << 30
+    stored = int(avail * stored_frac) // 2 * 2
+    scr, pre = split_budget(avail, stored, 8 << 30)
+    assert 0 <= scr <= GRAM256_SCRATCH_BYTES and 0 <= pre <= 8 << 30
+    assert stored + scr + pre <= avail
+    if avail_gib == 288 and stored_frac == 0.0:
+        assert (scr, pre) == (GRAM256_SCRATCH_BYTES, 8 << 30)  # a whole MI355X: both at their caps
+    # The budgets shrink with what is left: a caller holding most of the
+    # device leaves less to each.
+    if avail_gib:
+        scr2, pre2 = split_budget(avail // 4, stored // 4, 8 << 30)
+        assert scr2 <= scr and pre2 <= pre
+    assert split_budget(None, 0, 123) == (GRAM256_SCRATCH_BYTES, 123)  # off the GPU: no device limit
 
 
 def test_form_choice_at_c4_shapes():

@@ -4,7 +4,10 @@ odp_clip_materialized_noalloc (partials in the library's static device
 array) must give bit-identical scales, norms and masks to odp_sqnorm into a
 caller buffer followed by odp_clip_factors, on two calls in a row (the
 second smaller, so stale partials of the first would show), and refuse a
-problem larger than its array before launching anything.
+problem larger than its array before launching anything.  A table whose
+slot runs past the partials has that write dropped by the kernel's own
+bounds check, and the call reports NaN norms and zero scales; the next
+valid call is unaffected.
 """
 
 from __future__ import annotations
@@ -97,3 +100,30 @@ def test_noalloc_refuses_problems_beyond_its_array():
                                            gs.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), None, None, None)
     assert rc == N.ERR_UNSUPPORTED
     assert "static scratch" in N.last_error()
+
+
+def test_noalloc_drops_writes_outside_its_partials():
+    thr = torch.tensor([1.5, 2.0], dtype=torch.float64, device=DEV)
+    guard = torch.tensor([1 - 2**-8, 1e-40, 1 - 2**-23, 1e-44], dtype=torch.float64, device=DEV)
+    cls = torch.tensor([N.DTYPE_BF16, N.DTYPE_F32], dtype=torch.int32, device=DEV)
+    c = _case(3, [40, 11], [torch.float32, torch.bfloat16], seed=5)
+    bad = c["probs"].clone()
+    bad[1, 4] = c["n_slots"]  # the second leaf's slot: one past the last partial of a row
+    print("no-alloc: slot past the partials", flush=True)
+    o = _outputs(3)
+    N.call("odp_clip_materialized_noalloc", _stream(), bad.data_ptr(), c["ws"].data_ptr(), c["n_prob"],
+           c["total"], c["seg_ex"].data_ptr(), c["n_slots"], 3, *_clip_args(c, o, thr, guard, cls))
+    torch.cuda.synchronize()
+    assert torch.isnan(o["norm"]).all() and torch.isnan(o["gnorm"]).all()
+    assert (o["scale"] == 0).all() and (o["clip"] == 0).all() and (o["clip_t"] == 0).all()
+    # The status is cleared by the next call, which matches the caller-buffer path.
+    a, b = _outputs(3), _outputs(3)
+    part = torch.zeros(3, c["n_slots"], dtype=torch.float64, device=DEV)
+    N.call("odp_sqnorm", _stream(), c["probs"].data_ptr(), c["ws"].data_ptr(), c["n_prob"], c["total"],
+           c["seg_ex"].data_ptr(), part.data_ptr(), c["n_slots"])
+    N.call("odp_clip_factors", _stream(), part.data_ptr(), c["n_slots"], 3, *_clip_args(c, a, thr, guard, cls))
+    N.call("odp_clip_materialized_noalloc", _stream(), c["probs"].data_ptr(), c["ws"].data_ptr(), c["n_prob"],
+           c["total"], c["seg_ex"].data_ptr(), c["n_slots"], 3, *_clip_args(c, b, thr, guard, cls))
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
