@@ -78,11 +78,11 @@ def parse_args():
 def kernel_label(stage, key):
     """Device symbol of a table launch, as rocprofv3 names it."""
     if stage == "lin_norm":
-        return {1: "k_lin_gram_norm", 2: "k_lin_gram2_norm"}.get(key, "k_lin_outer_norm")
+        return {1: "k_lin_gram_norm", 2: "k_lin_gram2_norm", 3: "k_lin_outer_norm_guarded"}.get(key, "k_lin_outer_norm")
     if stage == "lin_prescale":
         return "k_lin_prescale"
     if stage == "lin_moments":
-        return "k_lin_moments"
+        return "k_lin_moments_guarded" if key == 1 else "k_lin_moments"
     if stage == "lin_sum":  # keyed by prescale chunk, None for in-register scaling
         return f"k_lin_clip_sum<{'false' if key is None else 'true'}>"
     if key is None:

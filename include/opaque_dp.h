@@ -73,7 +73,9 @@ typedef enum odp_clip_mode {
 typedef enum odp_norm_form {
   ODP_FORM_OUTER = 0, /* ||sum_t g_t a_t^T||_F^2 */
   ODP_FORM_GRAM = 1,  /* sum_{t,s} (g_t . g_s)(a_t . a_s), 128-row blocks */
-  ODP_FORM_GRAM256 = 2 /* the same sum over 256-row blocks, with scratch  */
+  ODP_FORM_GRAM256 = 2, /* the same sum over 256-row blocks, with scratch */
+  ODP_FORM_OUTER_GUARDED = 3 /* OUTER for the segments at risk of float32
+                                overflow only (see odp_linear_sqnorm)       */
 } odp_norm_form;
 
 /* ---- segments -----------------------------------------------------------
@@ -344,8 +346,22 @@ int odp_scale_sum(odp_stream_t stream, const int64_t* problems, const int32_t* w
  * into nan_to_num(M_s).  odp_nonfinite_columns finds the columns; the Gram
  * norm, the prescale and the clipped sum zero them wherever ODP_LN_XMASK /
  * ODP_LN_GMASK are set (the outer norm zeroes non-finite entries of M_s by
- * itself).  Finite inputs whose per-example product overflows float32 are
- * zeroed by the outer form only.                                            */
+ * itself).
+ *
+ * Overflow.  Where the products of finite inputs may exceed float32 (an
+ * entry of M_s itself, or its square in the norm, or an intermediate Gram
+ * product), the reference's result is that of the materialised M_s (inf
+ * entries zeroed, an inf norm giving scale 0).  odp_nonfinite_columns also
+ * records each segment's largest finite |x| and |g| (ODP_NF_AMAX); a
+ * segment is at risk when, with a = max|x|, b = max|g| and L its length,
+ *   a b max(L, sqrt(d_in d_out)) >= 2^60, d_in a^2 >= 2^124 or d_out b^2 >= 2^124.
+ * With ODP_LN_XAMAX / ODP_LN_GAMAX set, the Gram norms skip such segments
+ * and ODP_FORM_OUTER_GUARDED computes their outer-form partials (which form
+ * M_s tile by tile, as the reference does) into ODP_LN_SLOT + tile; the
+ * clipped sum skips a problem with such a segment and odp_linear_moments
+ * with guarded != 0 writes it instead.  Below the bound no form can
+ * overflow (|M_s| < 2^60, squares and Gram products < 2^124, clipped-sum
+ * terms < 2^60 times the clip factor).                                      */
 enum {
   ODP_LN_X = 0, ODP_LN_LDX = 1, ODP_LN_G = 2, ODP_LN_LDG = 3,
   ODP_LN_DIN = 4, ODP_LN_DOUT = 5, ODP_LN_SEG_FIRST = 6, ODP_LN_NSEG = 7,
@@ -368,7 +384,12 @@ enum {
                         problem ([n_seg][slots][65536], 16-byte aligned)    */
   ODP_LN_OUT2 = 18,  /* moments: address of the second moment [d_out][d_in]
                         (output dtype of ODP_LN_FLAGS) or 0                 */
-  ODP_LN_FIELDS = 20
+  ODP_LN_XAMAX = 19, /* GRAM sqnorm, OUTER_GUARDED sqnorm, clipped sum,
+                        guarded moments: address of the float bits (uint32)
+                        of max |x| per segment of X (ODP_NF_AMAX), or 0 for
+                        no overflow check                                   */
+  ODP_LN_GAMAX = 20, /* the same for G                                      */
+  ODP_LN_FIELDS = 24
 };
 
 /* ---- odp_nonfinite_columns: per-segment masks of non-finite columns ------
@@ -377,10 +398,14 @@ enum {
  * w < ceil(d / 32)) whose bit j is set when column 32 w + j holds a NaN or
  * Inf in one of the segment's rows.  Every word is written, so the masks
  * need no clearing.  One workgroup per (segment, 256 columns)
- * (odp_nonfinite_blocks).  Feeds ODP_LN_XMASK / ODP_LN_GMASK.             */
+ * (odp_nonfinite_blocks).  Feeds ODP_LN_XMASK / ODP_LN_GMASK.  With
+ * ODP_NF_AMAX set it also raises amax[s] (the float bits of a non-negative
+ * value, as uint32; the caller zeroes them first) to the largest |value| of
+ * a finite entry in the segment's rows.                                     */
 enum {
   ODP_NF_P = 0, ODP_NF_LDP = 1, ODP_NF_D = 2, ODP_NF_SEG_FIRST = 3, ODP_NF_NSEG = 4,
   ODP_NF_MASK = 5,   /* address of the uint32 masks [n_seg][ceil(d / 32)]   */
+  ODP_NF_AMAX = 6,   /* address of uint32 [n_seg] (zeroed by the caller) or 0 */
   ODP_NF_FIELDS = 8
 };
 int64_t odp_nonfinite_blocks(int64_t d, int64_t n_seg);
@@ -431,12 +456,16 @@ int odp_linear_clipped_sum(odp_stream_t stream, const int64_t* problems,
  * bit-identical to odp_linear_sqnorm's bf16 store of each M_s followed by
  * odp_scale_sum, without storing M_s.  ODP_LN_OUT2 = 0 writes the first
  * moment only.  One workgroup per 256 x 128 output tile
- * (odp_linear_moments_blocks, padded to a multiple of 8).                  */
-int64_t odp_linear_moments_blocks(int64_t d_in, int64_t d_out);
+ * (odp_linear_moments_blocks, padded to a multiple of 8).  With guarded
+ * != 0 a problem is written only when one of its segments is at risk of
+ * float32 overflow (ODP_LN_XAMAX / GAMAX, the bound above; the clipped sum
+ * skips exactly those problems), by a few workgroups that loop over its
+ * tiles (odp_linear_moments_blocks with guarded != 0).                      */
+int64_t odp_linear_moments_blocks(int64_t d_in, int64_t d_out, int32_t guarded);
 int odp_linear_moments(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                        int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
                        const int32_t* seg_row_len, const int32_t* seg_example, const double* scales,
-                       int32_t n_ex, int32_t n_groups, float normalize_by);
+                       int32_t n_ex, int32_t n_groups, float normalize_by, int32_t guarded);
 
 /* ---- odp_gaussian_noise --------------------------------------------------
  * out[i] = round_out(in[i] + sigma * sqrt(2) * erfinv(2u - 1)) for element

@@ -41,14 +41,15 @@ NZ_FIELDS = 8
 NZ_IN, NZ_OUT, NZ_N, NZ_FLAT_OFFSET, NZ_SIGMA, NZ_DTYPES = range(6)
 SQ_FIELDS = 8
 SQ_X, SQ_N, SQ_NSEG, SQ_SEG_FIRST, SQ_SLOT, SQ_DTYPE = range(6)
-LN_FIELDS = 20
+LN_FIELDS = 24
 LN_X, LN_LDX, LN_G, LN_LDG, LN_DIN, LN_DOUT, LN_SEG_FIRST, LN_NSEG, LN_SLOT, LN_OUT, LN_FLAGS, LN_NB, LN_NROWS, LN_PE = range(14)
-LN_XMASK, LN_GMASK, LN_NFFLAG, LN_SCRATCH, LN_OUT2 = 14, 15, 16, 17, 18
+LN_XMASK, LN_GMASK, LN_NFFLAG, LN_SCRATCH, LN_OUT2, LN_XAMAX, LN_GAMAX = 14, 15, 16, 17, 18, 19, 20
 NF_FIELDS = 8
-NF_P, NF_LDP, NF_D, NF_SEG_FIRST, NF_NSEG, NF_MASK = range(6)
+NF_P, NF_LDP, NF_D, NF_SEG_FIRST, NF_NSEG, NF_MASK, NF_AMAX = range(7)
 FORM_OUTER = 0
 FORM_GRAM = 1
 FORM_GRAM256 = 2
+FORM_OUTER_GUARDED = 3
 
 _c_int = ctypes.c_int
 _c_i32 = ctypes.c_int32
@@ -115,9 +116,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "odp_pack_planes_blocks": (_c_i64, [_c_i64]),
     "odp_pack_planes": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr]),
-    "odp_linear_moments_blocks": (_c_i64, [_c_i64, _c_i64]),
+    "odp_linear_moments_blocks": (_c_i64, [_c_i64, _c_i64, _c_i32]),
     "odp_linear_moments": (
-        _c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32]),
+        _c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32, _c_f32, _c_i32]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -185,6 +185,55 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm(c
 }
 
 // ---------------------------------------------------------------------------
+// ||M_i||^2 partials, outer form, for the segments at risk of float32
+// overflow in the Gram form only (see lin_seg_at_risk).  GUARD_SPLIT
+// workgroups per (problem, segment) exit at once unless the segment is at
+// risk, and otherwise loop over its tiles: cheap when no segment is at risk
+// (the usual case), exact (slow) when one is.
+// ---------------------------------------------------------------------------
+constexpr int GUARD_SPLIT = 8;
+
+__global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm_guarded(
+    const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
+    const int32_t* __restrict__ sstart, const int32_t* __restrict__ slen, const int32_t* __restrict__ sex,
+    double* __restrict__ part, int64_t part_stride) {
+  __shared__ double red[NW];
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
+  const LinProblem P = read_problem(f);
+  const int local = bid - ws[p];
+  const int seg = local / GUARD_SPLIT, j = local % GUARD_SPLIT;
+  if (seg >= P.n_seg) return;
+  const int gs = P.seg_first + seg;
+  const int32_t t_begin = sstart[gs], len = slen[gs];
+  if (!lin_seg_at_risk(f, seg, len, P.d_in, P.d_out)) return;
+  const int ex = sex[gs];
+  const int64_t slot = f[ODP_LN_SLOT];
+  const int tn_count = (int)((P.d_in + ON - 1) / ON);
+  const int tiles = tn_count * (int)((P.d_out + OM - 1) / OM);
+  uint32_t* nfflag = (uint32_t*)f[ODP_LN_NFFLAG];
+  auto next = [](const Step& st) {
+    Step n = st;
+    n.t0 = st.t0 + OK;
+    n.live = n.t0 < st.te ? 1 : 0;
+    return n;
+  };
+  for (int tile = j; tile < tiles; tile += GUARD_SPLIT) {
+    const int64_t o0 = (int64_t)(tile / tn_count) * OM, n0 = (int64_t)(tile % tn_count) * ON;
+    OuterAcc acc;
+    zero_acc(acc);
+    const Step first = {t_begin, t_begin, t_begin + len, seg, 1, 0};
+    dma_mainloop<false, true, false>(P, o0, n0, first, next, [](const Step&) { return 1.0f; },
+                                     [](uint16_t*, const Step&) {}, acc);
+    bool nonfinite = false;
+    const double tot = block_sum(acc_sq(acc, nonfinite), red);
+    if (threadIdx.x == 0) part[(int64_t)ex * part_stride + slot + tile] = tot;
+    if (nfflag != nullptr && nonfinite) odp_gstore(nfflag, 1u);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // ||M_i||^2 partials, token-Gram form, wide tiles.  A workgroup of 8 waves
 // covers token block tb (128 rows) against blocks sb0 and sb0 + 1 (256
 // rows) of one segment, with both Gram products in registers: waves 0-3
@@ -250,6 +299,9 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
   const int gs = P.seg_first + seg;
   const int32_t t_begin = sstart[gs], len = slen[gs];
   const int ex = sex[gs];
+  // A segment at risk of float32 overflow takes the outer form instead
+  // (ODP_FORM_OUTER_GUARDED); its Gram partials stay 0.
+  if (lin_seg_at_risk(f, seg, len, P.d_in, P.d_out)) return;
   double* dst = part + (int64_t)ex * part_stride + slot + item;
   if ((int64_t)sb0 * LT >= len) {  // item past this segment's length
     if (threadIdx.x == 0) *dst = 0.0;
@@ -464,6 +516,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
   const int gs = P.seg_first + seg;
   const int32_t t_begin = sstart[gs], len = slen[gs];
   const int ex = sex[gs];
+  if (lin_seg_at_risk(f, seg, len, P.d_in, P.d_out)) return;  // outer form (guarded) instead
   double* dst = part + (int64_t)ex * part_stride + slot + item;
   if ((int64_t)sb * G2_B >= len) {  // item past this segment's length
     if (threadIdx.x == 0) *dst = 0.0;
@@ -729,6 +782,9 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
   const int tm_count = (int)((P.d_out + OM - 1) / OM);
   const int tile = bid - ws[p];
   if (tile >= tm_count * tn_count) return;  // padding block
+  // A problem with a segment at risk of float32 overflow is written by the
+  // guarded moments kernel instead.
+  if (lin_problem_at_risk(f, slen, P.seg_first, P.n_seg, P.d_in, P.d_out)) return;
   const int64_t o0 = (int64_t)(tile / tn_count) * OM, n0 = (int64_t)(tile % tn_count) * ON;
 
   OuterAcc acc;
@@ -837,6 +893,18 @@ __device__ __forceinline__ uint32_t nonfinite8(u32x4_t v) {
   return b;
 }
 
+// Largest magnitude among the finite bf16 elements of the 8, as bf16 bits.
+__device__ __forceinline__ uint32_t finite_amax8(u32x4_t v) {
+  uint32_t m = 0u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = v[k] & 0xffffu, hi = v[k] >> 16;
+    if ((lo & 0x7f80u) != 0x7f80u) m = max(m, lo & 0x7fffu);
+    if ((hi & 0x7f80u) != 0x7f80u) m = max(m, hi & 0x7fffu);
+  }
+  return m;
+}
+
 __global__ __launch_bounds__(NF_THREADS) void k_nonfinite_cols(const int64_t* __restrict__ probs,
                                                                const int32_t* __restrict__ ws, int n_prob,
                                                                const int32_t* __restrict__ sstart,
@@ -857,17 +925,38 @@ __global__ __launch_bounds__(NF_THREADS) void k_nonfinite_cols(const int64_t* __
   const int len = slen[seg_first + seg];
   const int lane = threadIdx.x & 31, rg = threadIdx.x >> 5;
   const int64_t col = (int64_t)strip * NF_STRIP + 8 * lane;
-  uint32_t bits = 0u;
+  uint32_t* amax = (uint32_t*)f[ODP_NF_AMAX];
+  uint32_t bits = 0u, am = 0u;
   if (col < d) {
     const uint16_t* base = P + t0 * ldp + col;
     auto row = [&](int r) { return *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(base + (int64_t)r * ldp); };
     int r = rg;
     // Four rows in flight per lane.
-    for (; r + 24 < len; r += 32) {
-      const u32x4_t a = row(r), b = row(r + 8), c = row(r + 16), e = row(r + 24);
-      bits |= nonfinite8(a) | nonfinite8(b) | nonfinite8(c) | nonfinite8(e);
+    if (amax != nullptr) {
+      for (; r + 24 < len; r += 32) {
+        const u32x4_t a = row(r), b = row(r + 8), c = row(r + 16), e = row(r + 24);
+        bits |= nonfinite8(a) | nonfinite8(b) | nonfinite8(c) | nonfinite8(e);
+        am = max(max(am, max(finite_amax8(a), finite_amax8(b))), max(finite_amax8(c), finite_amax8(e)));
+      }
+      for (; r < len; r += 8) {
+        const u32x4_t a = row(r);
+        bits |= nonfinite8(a);
+        am = max(am, finite_amax8(a));
+      }
+    } else {
+      for (; r + 24 < len; r += 32) {
+        const u32x4_t a = row(r), b = row(r + 8), c = row(r + 16), e = row(r + 24);
+        bits |= nonfinite8(a) | nonfinite8(b) | nonfinite8(c) | nonfinite8(e);
+      }
+      for (; r < len; r += 8) bits |= nonfinite8(row(r));
     }
-    for (; r < len; r += 8) bits |= nonfinite8(row(r));
+  }
+  if (amax != nullptr) {
+    // The workgroup's largest finite magnitude, as float bits (monotonic
+    // for non-negative values), raised into the segment's word.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) am = max(am, (uint32_t)__shfl_xor((int)am, off));
+    if ((threadIdx.x & 63) == 0 && am != 0u) atomicMax(amax + seg, am << 16);
   }
   red[rg][lane] = bits;
   __syncthreads();
@@ -912,6 +1001,7 @@ extern "C" int odp_nonfinite_columns(odp_stream_t stream, const int64_t* problem
 
 extern "C" int64_t odp_linear_tiles(int form, int64_t d_in, int64_t d_out, int64_t max_seg_len) {
   if (d_in <= 0 || d_out <= 0) return 0;
+  // ODP_FORM_OUTER_GUARDED: the outer tiles.
   if (form == ODP_FORM_GRAM) {
     const int64_t nb = max_seg_len > 0 ? (max_seg_len + LT - 1) / LT : 0;
     return gram_items(nb);
@@ -927,6 +1017,7 @@ extern "C" int64_t odp_linear_norm_blocks(int form, int64_t d_in, int64_t d_out,
                                           int64_t n_seg) {
   const int64_t per = odp_linear_tiles(form, d_in, d_out, max_seg_len);
   if (per <= 0 || n_seg <= 0) return 0;
+  if (form == ODP_FORM_OUTER_GUARDED) return n_seg * GUARD_SPLIT;
   if ((form == ODP_FORM_GRAM || form == ODP_FORM_GRAM256) && n_seg >= 8) return 8 * ((n_seg + 7) / 8) * per;
   return (n_seg * per + 7) / 8 * 8;
 }
@@ -943,7 +1034,8 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
                                  const int32_t* seg_example, double* part, int64_t part_stride) {
   int rc = odp_check_table("odp_linear_sqnorm", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
-  if (form != ODP_FORM_OUTER && form != ODP_FORM_GRAM && form != ODP_FORM_GRAM256) {
+  if (form != ODP_FORM_OUTER && form != ODP_FORM_GRAM && form != ODP_FORM_GRAM256 &&
+      form != ODP_FORM_OUTER_GUARDED) {
     odp_set_error("odp_linear_sqnorm: unknown form %d", form);
     return ODP_ERR_INVALID_ARGUMENT;
   }
@@ -960,6 +1052,9 @@ extern "C" int odp_linear_sqnorm(odp_stream_t stream, int form, const int64_t* p
                        seg_row_start, seg_row_len, seg_example, part, part_stride);
   else if (form == ODP_FORM_GRAM256)
     hipLaunchKernelGGL(k_lin_gram2_norm, grid, dim3(512), 0, s, problems, work_start, n_prob,
+                       seg_row_start, seg_row_len, seg_example, part, part_stride);
+  else if (form == ODP_FORM_OUTER_GUARDED)
+    hipLaunchKernelGGL(k_lin_outer_norm_guarded, grid, block, 0, s, problems, work_start, n_prob,
                        seg_row_start, seg_row_len, seg_example, part, part_stride);
   else
     hipLaunchKernelGGL(k_lin_outer_norm, grid, block, 0, s, problems, work_start, n_prob,

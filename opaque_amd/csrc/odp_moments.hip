@@ -51,16 +51,11 @@ __device__ __forceinline__ void moment_store(void* dst, int64_t at, int odt, flo
   odp_store_from_float(dst, at, odt, x);
 }
 
-// Workgroup = one OM x ON output tile of one weight; the segments of the
-// problem in order.
-__global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_moments(
-    const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
-    const int32_t* __restrict__ sstart, const int32_t* __restrict__ slen, const int32_t* __restrict__ sex,
-    const double* __restrict__ scales, int n_ex, int n_groups, float normalize_by) {
-  const int bid = blockIdx.x;
-  const int p = odp_find_problem(ws, n_prob, bid);
-  const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
-  const LinProblem P = read_problem(f);
+// One OM x ON output tile of problem f: the segments in order.
+__device__ __forceinline__ void moments_tile(const int64_t* __restrict__ f, const LinProblem& P, int tile,
+                                             const int32_t* __restrict__ sstart, const int32_t* __restrict__ slen,
+                                             const int32_t* __restrict__ sex, const double* __restrict__ scales,
+                                             int n_ex, int n_groups, float normalize_by) {
   void* out = (void*)f[ODP_LN_OUT];
   void* out2 = (void*)f[ODP_LN_OUT2];
   const int64_t flags = f[ODP_LN_FLAGS];
@@ -68,9 +63,6 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_moments(
   const int grp = (int)((flags >> 8) & 0xffff);
   const int cls = (int)((flags >> 24) & 0xffff);
   const int tn_count = (int)((P.d_in + ON - 1) / ON);
-  const int tm_count = (int)((P.d_out + OM - 1) / OM);
-  const int tile = bid - ws[p];
-  if (tile >= tm_count * tn_count) return;  // padding block
   const int64_t o0 = (int64_t)(tile / tn_count) * OM, n0 = (int64_t)(tile % tn_count) * ON;
   // Uniform values through the scalar path.
   const ODP_CONST int32_t* cstart = (const ODP_CONST int32_t*)(sstart + P.seg_first);
@@ -119,14 +111,49 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_moments(
   });
 }
 
+// Workgroup = one output tile of one weight.
+__global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_moments(
+    const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
+    const int32_t* __restrict__ sstart, const int32_t* __restrict__ slen, const int32_t* __restrict__ sex,
+    const double* __restrict__ scales, int n_ex, int n_groups, float normalize_by) {
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
+  const LinProblem P = read_problem(f);
+  const int tile = bid - ws[p];
+  if (tile >= (int)((P.d_out + OM - 1) / OM) * (int)((P.d_in + ON - 1) / ON)) return;  // padding block
+  moments_tile(f, P, tile, sstart, slen, sex, scales, n_ex, n_groups, normalize_by);
+}
+
+// The same sums for the problems with a segment at risk of float32
+// overflow only (the clipped-sum GEMM skips exactly those): MOM_SPLIT
+// workgroups per problem exit at once unless it is at risk, and otherwise
+// loop over its tiles.
+constexpr int MOM_SPLIT = 32;
+
+__global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_moments_guarded(
+    const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
+    const int32_t* __restrict__ sstart, const int32_t* __restrict__ slen, const int32_t* __restrict__ sex,
+    const double* __restrict__ scales, int n_ex, int n_groups, float normalize_by) {
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_LN_FIELDS;
+  const LinProblem P = read_problem(f);
+  if (!lin_problem_at_risk(f, slen, P.seg_first, P.n_seg, P.d_in, P.d_out)) return;
+  const int tiles = (int)((P.d_out + OM - 1) / OM) * (int)((P.d_in + ON - 1) / ON);
+  for (int tile = bid - ws[p]; tile < tiles; tile += MOM_SPLIT)
+    moments_tile(f, P, tile, sstart, slen, sex, scales, n_ex, n_groups, normalize_by);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
 
-extern "C" int64_t odp_linear_moments_blocks(int64_t d_in, int64_t d_out) {
+extern "C" int64_t odp_linear_moments_blocks(int64_t d_in, int64_t d_out, int32_t guarded) {
   if (d_in <= 0 || d_out <= 0) return 0;
+  if (guarded) return MOM_SPLIT;
   const int64_t tiles = ((d_out + OM - 1) / OM) * ((d_in + ON - 1) / ON);
   return (tiles + 7) / 8 * 8;
 }
@@ -134,7 +161,7 @@ extern "C" int64_t odp_linear_moments_blocks(int64_t d_in, int64_t d_out) {
 extern "C" int odp_linear_moments(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                                   int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
                                   const int32_t* seg_row_len, const int32_t* seg_example, const double* scales,
-                                  int32_t n_ex, int32_t n_groups, float normalize_by) {
+                                  int32_t n_ex, int32_t n_groups, float normalize_by, int32_t guarded) {
   int rc = odp_check_table("odp_linear_moments", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
   if (!(normalize_by > 0.0f)) {
@@ -147,8 +174,8 @@ extern "C" int odp_linear_moments(odp_stream_t stream, const int64_t* problems, 
     odp_set_error("odp_linear_moments: null segment/scale arrays or empty batch");
     return ODP_ERR_INVALID_ARGUMENT;
   }
-  hipLaunchKernelGGL(k_lin_moments, dim3(total_blocks), dim3(OUTER_THREADS), 0, odp_hip_stream(stream), problems,
-                     work_start, n_prob, seg_row_start, seg_row_len, seg_example, scales, n_ex, n_groups,
-                     normalize_by);
+  hipLaunchKernelGGL(guarded ? k_lin_moments_guarded : k_lin_moments, dim3(total_blocks), dim3(OUTER_THREADS), 0,
+                     odp_hip_stream(stream), problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example,
+                     scales, n_ex, n_groups, normalize_by);
   return odp_check_launch("odp_linear_moments");
 }

@@ -34,6 +34,31 @@ __host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
   return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
 }
 
+// Whether local segment sg (len rows) of problem f may overflow float32 in
+// the Gram or clipped-sum forms: with a = max|x| and b = max|g| over the
+// segment's finite entries (odp_nonfinite_columns), a b max(L, sqrt(d_in
+// d_out)) >= 2^60, d_in a^2 >= 2^124 or d_out b^2 >= 2^124.  False without
+// the per-segment maxima (no check requested).
+__device__ __forceinline__ bool lin_seg_at_risk(const int64_t* f, int sg, int32_t len, int64_t d_in,
+                                                int64_t d_out) {
+  const uint32_t* xa = (const uint32_t*)f[ODP_LN_XAMAX];
+  const uint32_t* ga = (const uint32_t*)f[ODP_LN_GAMAX];
+  if (xa == nullptr || ga == nullptr || len <= 0) return false;
+  const double a = (double)__uint_as_float(xa[sg]), b = (double)__uint_as_float(ga[sg]);
+  const double din = (double)d_in, dout = (double)d_out;
+  const double w = fmax((double)len, sqrt(din * dout));
+  return a * b * w >= 0x1p60 || din * a * a >= 0x1p124 || dout * b * b >= 0x1p124;
+}
+
+// Whether any segment of the problem is at risk.
+__device__ __forceinline__ bool lin_problem_at_risk(const int64_t* f, const int32_t* slen, int seg_first,
+                                                    int n_seg, int64_t d_in, int64_t d_out) {
+  if (f[ODP_LN_XAMAX] == 0 || f[ODP_LN_GAMAX] == 0) return false;
+  for (int sg = 0; sg < n_seg; ++sg)
+    if (lin_seg_at_risk(f, sg, slen[seg_first + sg], d_in, d_out)) return true;
+  return false;
+}
+
 struct LinProblem {
   const uint16_t* X;
   const uint16_t* G;

@@ -752,6 +752,7 @@ class GhostPlan:
         lin_form: list[int] = []
         lin_view: list[_SegView] = []
         lin_off: list[int] = []
+        lin_goff: dict[int, int] = {}  # Gram site -> first slot of its guarded outer-form partials
         others = set(leaf_slots)
         slices: dict[int, set[int]] = {}
         for i, ls in enumerate(lins):
@@ -778,6 +779,11 @@ class GhostPlan:
             taken.add(key)
             lin_off.append(leaf_slots.get(ls.w_leaf, 0))
             leaf_slots[ls.w_leaf] = leaf_slots.get(ls.w_leaf, 0) + tiles
+            if form in (N.FORM_GRAM, N.FORM_GRAM256):
+                # Outer-form slots for the segments whose Gram products could
+                # overflow float32 (odp_linear_sqnorm, ODP_FORM_OUTER_GUARDED).
+                lin_goff[i] = leaf_slots[ls.w_leaf]
+                leaf_slots[ls.w_leaf] += int(lib.odp_linear_tiles(N.FORM_OUTER_GUARDED, d_in, d_out, v.max_len))
         for k, taken in slices.items():
             if -1 not in taken and taken != set(range(self.leaves[k].shape[0])):
                 raise ValueError(f"stacked leaf {k} needs a linear site for every slice")
@@ -1009,16 +1015,26 @@ class GhostPlan:
         # columns holding a non-finite value within each segment (so that the
         # result is nan_to_num of every per-example gradient).  One mask per
         # distinct tensor and segment list, found by odp_nonfinite_columns.
-        masks: dict[tuple, tuple[torch.Tensor, _SegView, int]] = {}
+        # The same pass records each segment's largest finite |value| (one
+        # uint32 per segment, zeroed at every run), from which the Gram and
+        # GEMM kernels tell the segments whose products could overflow
+        # float32; those take the outer form and the moments kernel, which
+        # form M_s as the reference does.
+        masks: dict[tuple, tuple[torch.Tensor, _SegView, int, int]] = {}
         mask_words = 0
+        amax_words = 0
 
         def mask_of(t: torch.Tensor, v: _SegView) -> int:
-            nonlocal mask_words
+            nonlocal mask_words, amax_words
             key = (t.data_ptr(), tuple(t.shape), tuple(t.stride()), v.first)
             if key not in masks:
-                masks[key] = (t, v, mask_words)
+                masks[key] = (t, v, mask_words, amax_words)
                 mask_words += v.n_seg * ((t.shape[1] + 31) // 32)
+                amax_words += v.n_seg
             return masks[key][2]
+
+        def amax_of(t: torch.Tensor, v: _SegView) -> int:
+            return self._amax.data_ptr() + 4 * masks[(t.data_ptr(), tuple(t.shape), tuple(t.stride()), v.first)][3]
 
         # With second moments, sites without stored gradients take the
         # moments kernel (odp_linear_moments), which forms each M_s tile and
@@ -1030,14 +1046,16 @@ class GhostPlan:
                      if i not in lin_pe and (i not in lin_mom or lin_form[i] != N.FORM_OUTER)}
         self.nf_mask = torch.empty(max(mask_words, 1), dtype=torch.int32, device=dev)
         self._has_masks = mask_words > 0
+        self._amax = torch.zeros(amax_words, dtype=torch.int32, device=dev)
 
         def mask_addr(w: int) -> int:
             return self.nf_mask.data_ptr() + 4 * w
 
         nft = _Table(N.NF_FIELDS)
-        for t, v, off in masks.values():
+        for t, v, off, aoff in masks.values():
             nft.add({N.NF_P: t.data_ptr(), N.NF_LDP: t.stride(0), N.NF_D: t.shape[1],
-                     N.NF_SEG_FIRST: v.first, N.NF_NSEG: v.n_seg, N.NF_MASK: mask_addr(off)},
+                     N.NF_SEG_FIRST: v.first, N.NF_NSEG: v.n_seg, N.NF_MASK: mask_addr(off),
+                     N.NF_AMAX: self._amax.data_ptr() + 4 * aoff},
                     int(lib.odp_nonfinite_blocks(t.shape[1], v.n_seg)), v.valid * t.shape[1] * 2,
                     io=v.valid * t.shape[1] * 2)
 
@@ -1083,6 +1101,8 @@ class GhostPlan:
                               io=v.valid * x.shape[1] * 2)
         lnt = {N.FORM_OUTER: _Table(N.LN_FIELDS), N.FORM_GRAM: _Table(N.LN_FIELDS),
                N.FORM_GRAM256: _Table(N.LN_FIELDS)}
+        lng = _Table(N.LN_FIELDS)  # guarded outer-form norms of Gram sites
+        lmg = _Table(N.LN_FIELDS)  # guarded moments (first moment) of clipped-sum GEMM sites
         # fp32 scratch of the 256-row-block Gram kernel (its X blocks).
         self.gram_scr = (torch.empty(scr_total // 4, dtype=torch.float32, device=dev) if scr_total
                          else None)
@@ -1101,6 +1121,8 @@ class GhostPlan:
             if i in site_mask:
                 common[N.LN_XMASK] = mask_addr(site_mask[i][0])
                 common[N.LN_GMASK] = mask_addr(site_mask[i][1])
+                common[N.LN_XAMAX] = amax_of(x, v)
+                common[N.LN_GAMAX] = amax_of(g, v)
             if form in (N.FORM_GRAM, N.FORM_GRAM256):
                 fl = sum(ln * ln for ln in v.segs.lengths) * (d_in + d_out)
             else:
@@ -1113,6 +1135,9 @@ class GhostPlan:
                            N.LN_PE: pe_at, N.LN_NFFLAG: self._nf_flag_addr, N.LN_SCRATCH: scr_at}, blocks,
                           valid * (d_in + d_out) * 2 + (n_seg * d_in * d_out * 2 if pe_at else 0), fl,
                           io=valid * (d_in + d_out) * 2)
+            if i in lin_goff:
+                lng.add({**common, N.LN_SLOT: slot_base[ls.w_leaf] + lin_goff[i], N.LN_NFFLAG: self._nf_flag_addr},
+                        int(lib.odp_linear_norm_blocks(N.FORM_OUTER_GUARDED, d_in, d_out, v.max_len, n_seg)))
             if i in lin_pe:
                 continue
             lf = self.leaves[ls.w_leaf]
@@ -1121,12 +1146,16 @@ class GhostPlan:
             if i in lin_mom:
                 o2 = self.out2[ls.w_leaf] if ls.index is None else self.out2[ls.w_leaf][ls.index]
                 lmom.add({**common, N.LN_OUT: out.data_ptr(), N.LN_OUT2: o2.data_ptr(), N.LN_FLAGS: flags},
-                         int(lib.odp_linear_moments_blocks(d_in, d_out)),
+                         int(lib.odp_linear_moments_blocks(d_in, d_out, 0)),
                          valid * (d_in + d_out) * 2 + 2 * d_in * d_out * out.element_size(),
                          2 * valid * d_in * d_out,
                          io=valid * (d_in + d_out) * 2 + 2 * d_in * d_out * out.element_size())
                 continue
             row, into = {**common, N.LN_OUT: out.data_ptr(), N.LN_FLAGS: flags}, lsum
+            # The same output, written only if a segment is at risk of
+            # float32 overflow (the GEMM then skips the site).
+            lmg.add({**common, N.LN_OUT: out.data_ptr(), N.LN_OUT2: 0, N.LN_FLAGS: flags},
+                    int(lib.odp_linear_moments_blocks(d_in, d_out, 1)))
             if site_chunk[i] is not None:
                 c, k = site_chunk[i]
                 row[N.LN_X] = self.xs[xs_chunks[c][k][0]:].data_ptr()
@@ -1202,12 +1231,14 @@ class GhostPlan:
         tabs.append(("lin_norm", N.FORM_OUTER, lnt[N.FORM_OUTER]))
         tabs.append(("lin_norm", N.FORM_GRAM, lnt[N.FORM_GRAM]))
         tabs.append(("lin_norm", N.FORM_GRAM256, lnt[N.FORM_GRAM256]))
+        tabs.append(("lin_norm", N.FORM_OUTER_GUARDED, lng))
         tabs.append(("scale_sum", None, ss))
         for c in range(len(xs_chunks)):
             tabs.append(("lin_prescale", c, xs_pre[c]))
             tabs.append(("lin_sum", c, xs_sum[c]))
         tabs.append(("lin_sum", None, lsum))
         tabs.append(("lin_moments", None, lmom))
+        tabs.append(("lin_moments", 1, lmg))
         tab_idx = []
         for name, dt, t in tabs:
             probs, ws, total = t.arrays()
@@ -1687,6 +1718,8 @@ class GhostPlan:
         seg = self.segments
         ev = events or {}
         self._part_buf.zero_()
+        if self._amax.numel():
+            self._amax.zero_()
         live = [t for t in self.tables if t[5] > 0 and t[0] not in _AFTER_CLIP]
 
         def mark(name, dt, on):
@@ -1781,7 +1814,8 @@ class GhostPlan:
                 N.check(lib.odp_linear_moments(stream, probs.data_ptr(), ws.data_ptr(), n, total,
                                                self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                                self.seg_ex.data_ptr(), self.scales.data_ptr(), seg.n_ex,
-                                               self.n_groups, float(self.clip.normalize_by)), name)
+                                               self.n_groups, float(self.clip.normalize_by),
+                                               0 if dt is None else 1), name)
             if end_ev is not None:
                 end_ev.record()
             if st in ev and st not in stage[idx + 1:]:

@@ -241,7 +241,7 @@ def test_config_c4_layer(path):
                      linear_pe_bytes=None if path == "stored" else 0, second_moment=path == "moments")
     res = plan.run()
     torch.cuda.synchronize()
-    kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
+    kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0 and t[1] != N.FORM_OUTER_GUARDED}
     # Stored: every site takes the outer form (it stores).  Without storage
     # the engine picks the Gram identity for gate/up/down at T = 4096 (and
     # gate/down are forced to it), on the 256-row-block kernel.

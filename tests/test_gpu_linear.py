@@ -92,12 +92,12 @@ def test_gram256_matches_oracle_and_gram128(n_ex, T, d_in, d_out, lengths, monke
     X, G, seg = _case(n_ex, T, d_in, d_out, lengths, seed=T + d_in)
     _, want = _ref_norms(X, G, seg)
     plan, res, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=N.FORM_GRAM)
-    assert {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0} == {N.FORM_GRAM256}
+    assert {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0 and t[1] != N.FORM_OUTER_GUARDED} == {N.FORM_GRAM256}
     got = res.norms.double().cpu().clone()
     assert torch.allclose(got, want.float().double(), rtol=2e-3, atol=1e-6), (got, want)
     monkeypatch.setattr(engine, "GRAM256_MIN_LEN", 1 << 30)
     plan2, r2, _ = _plan(X, G, seg, C=1e30, mode=N.CLIP_FIXED, form=N.FORM_GRAM)
-    assert {t[1] for t in plan2.tables if t[0] == "lin_norm" and t[5] > 0} == {N.FORM_GRAM}
+    assert {t[1] for t in plan2.tables if t[0] == "lin_norm" and t[5] > 0 and t[1] != N.FORM_OUTER_GUARDED} == {N.FORM_GRAM}
     assert torch.allclose(got, r2.norms.double().cpu(), rtol=1e-5, atol=1e-9)
 
 
@@ -369,7 +369,7 @@ def test_storage_takes_the_outer_form():
     res = {}
     for b in (None, 0):
         plan, r, _ = _plan(X, G, seg, C=5.0, mode=N.CLIP_FIXED, form=None, pe_bytes=b)
-        kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
+        kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0 and t[1] != N.FORM_OUTER_GUARDED}
         assert kinds == ({N.FORM_OUTER} if b is None else {N.FORM_GRAM}), (b, kinds)
         res[b] = (r.leaves[0].double().cpu(), r.norms.double().cpu())
     assert torch.allclose(res[None][1], res[0][1], rtol=1e-4)
@@ -424,7 +424,7 @@ def test_non_finite_entries_are_zeroed(path, kind):
     finite_flag = bool(plan.linear_finite().item())
     torch.cuda.synchronize()
     assert (plan.lin_pe.numel() > 0) == (path == "stored")
-    kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0}
+    kinds = {t[1] for t in plan.tables if t[0] == "lin_norm" and t[5] > 0 and t[1] != N.FORM_OUTER_GUARDED}
     assert kinds == {form if form in (N.FORM_GRAM, N.FORM_GRAM256) else N.FORM_OUTER}
     outs, norms = [], []
     for i in range(n_ex):
@@ -444,3 +444,60 @@ def test_non_finite_entries_are_zeroed(path, kind):
         got_cols = [(s, 32 * w + b) for s in range(n_ex) for w in range(words) for b in range(32)
                     if (int(xmask[s, w]) >> b) & 1]
         assert got_cols == want_cols
+
+
+def _overflow_case(seed=41):
+    """Four examples of 64 rows (one empty).  Example 1: one entry of M is
+    1e40, past float32 (the reference zeroes it; the rest of the example
+    stays small, so its norm is finite).  Example 3: one entry of M is 1e20,
+    whose square overflows float32 (the reference's norm is inf, so its
+    scale is 0).  Example 0 is ordinary."""
+    g = torch.Generator().manual_seed(seed)
+    n_ex, T, d_in, d_out = 4, 64, 192, 136
+    X = torch.randn(n_ex * T, d_in, generator=g)
+    G = torch.randn(n_ex * T, d_out, generator=g) * 0.1
+    seg = Segments.padded(n_ex, T, [64, 50, 0, 64])
+    for row, big in ((T + 7, 1e20), (3 * T + 11, 1e10)):
+        X[row] *= 1e-3
+        G[row] *= 1e-3
+        X[row, 40], G[row, 9] = big, big
+    return X.to(torch.bfloat16), G.to(torch.bfloat16), seg
+
+
+@pytest.mark.parametrize("form", [N.FORM_GRAM, N.FORM_GRAM256, N.FORM_OUTER])
+@pytest.mark.parametrize("mode", [N.CLIP_FIXED, N.CLIP_AUTOS])
+def test_overflowing_segments_take_the_exact_forms(form, mode):
+    """Without stored gradients the Gram norms and the clipped-sum GEMM
+    would carry such products as huge finite values or inf; the segments at
+    risk are routed to the outer-form norms and the moments kernel, which
+    form M_s tile by tile.  Results match the stored path (which forms and
+    stores every M_s): the same inf norm and zero contribution for example
+    3, the same zeroed entry for example 1, all_finite false."""
+    print(f"overflow routing: form={form} mode={mode}", flush=True)
+    X, G, seg = _overflow_case()
+    C = 0.5
+    _, want, _ = _plan(X, G, seg, C=C, mode=mode, form=None, pe_bytes=None, out_dtype=torch.float32)
+    plan, got, _ = _plan(X, G, seg, C=C, mode=mode, form=form, pe_bytes=0, out_dtype=torch.float32)
+    assert plan.lin_pe.numel() == 0
+    live = {(t[0], t[1]) for t in plan.tables if t[5] > 0}
+    if form == N.FORM_OUTER:
+        assert ("lin_moments", 1) in live  # the guarded fallback of the GEMM
+    else:
+        assert ("lin_norm", N.FORM_OUTER_GUARDED) in live
+    wn, gn = want.norms.double().cpu(), got.norms.double().cpu()
+    assert torch.isinf(wn[3]) and torch.isinf(gn[3]) and torch.isfinite(wn[:3]).all()
+    assert torch.allclose(gn[:3], wn[:3], rtol=1e-5), (gn, wn)
+    assert torch.equal(got.scales.cpu()[..., 3], torch.zeros_like(got.scales.cpu()[..., 3]))
+    assert torch.equal(got.clipped_total.cpu(), want.clipped_total.cpu())
+    a, b = got.leaves[0].double().cpu(), want.leaves[0].double().cpu()
+    assert torch.isfinite(a).all()
+    assert (a - b).norm() <= 1e-4 * b.norm(), ((a - b).norm() / b.norm()).item()
+    assert not bool(plan.linear_finite())
+    # The oracle on the CPU: per-example gradients in bf16 (inf where they
+    # overflow), nan_to_num, the reference's clip.
+    pe = lora_ref.linear_per_example(X.float(), G.float(), seg.starts, seg.lengths).float().to(torch.bfloat16)
+    assert torch.isinf(pe[1].float()).any()
+    ref, raux = dp_ref.clipped_grad(lambda p, m: (p * m.float()).sum(), torch.zeros(pe.shape[1:]), (pe,),
+                                    clipping_norm=C, autos=mode == N.CLIP_AUTOS)
+    assert torch.isinf(raux["norms"][3])
+    assert torch.allclose(gn[:3], raux["norms"][:3].double(), rtol=2e-2), (gn, raux["norms"])
