@@ -51,6 +51,10 @@ def parse_args():
                     help="c3: seam = the LoRA seam keeps V = xA (its forward) and U = gB^T (its input-gradient "
                          "backward) and the step reads them from HBM; recompute = the step projects X and G "
                          "again (two extra passes over the narrower of each pair)")
+    ap.add_argument("--stream-factors", choices=["on", "off"], default="on",
+                    help="c3: on = one-leaf factor rows (rank <= 16) stream P through LDS "
+                         "(odp_seg_factor_stream); off = the register-staged odp_seg_factor tiles "
+                         "(bit-identical results)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--linear-pe-gb", type=float, default=None,
                     help="c4: HBM for stored per-example weight gradients (default: free memory after "
@@ -88,7 +92,7 @@ def kernel_label(stage, key):
     if key is None:
         return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "nonfinite": "k_nonfinite_cols",
                 "pack": "k_pack_factors", "planes": "k_pack_planes",
-                "factor_project": "k_factor_project_bf16"}[stage]
+                "factor_project": "k_factor_project_bf16", "factor_stream": "k_factor_stream_bf16"}[stage]
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]
     if dt == torch.bfloat16:
@@ -290,7 +294,8 @@ def setup_c3(args, dev):
     seg, lengths, lsites, leaves, (rel, ab) = c3_sites(args.layers, B, T, r, args.seed, seam, dev)
     clip = ClipSpec(mode=N.CLIP_AUTOS, thresholds=[1.0], effective=1.0, gamma=0.01,
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
-    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev)
+    plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=lsites, device=dev,
+                     stream_factors=args.stream_factors == "on")
     valid = sum(lengths)
     # Per valid token and linear: the dA and dB products (2 N r (d_in + d_out)
     # each); recomputing V and U adds the prep term, 2 N r (d_in + d_out).
@@ -319,7 +324,7 @@ def setup_c3(args, dev):
 
     plan.bench_rebind = rebind_once
     return (plan, 1.0 / B, config, metric, flops,
-            ("planes", "project", "factor_project", "factor", "clip", "scale_sum", "noise"), "hbm")
+            ("planes", "project", "factor_project", "factor_stream", "factor", "clip", "scale_sum", "noise"), "hbm")
 
 
 def dropin_overhead(args, dev, step_ms):

@@ -17,8 +17,8 @@
  * The reference (JetBrains-Research/opaque) is Python; these entry points
  * replace the following internals of its DP-SGD hot path
  * (paths relative to packages/):
- *   odp_project or odp_pack_planes, odp_seg_factor_project, odp_seg_factor
- *                                 -> per-sample LoRA factor gradients,
+ *   odp_project or odp_pack_planes, odp_seg_factor_project, odp_seg_factor,
+ *   odp_seg_factor_stream         -> per-sample LoRA factor gradients,
  *       opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176
  *       (dA[i] = s X[i]^T (G[i] B^T), dB[i] = s (X[i] A)^T G[i]) and the
  *       per-example squared norms of clip_pytree,
@@ -178,8 +178,8 @@ enum {
   ODP_FT_SCALING = 8, /* double bit pattern                                  */
   ODP_FT_NLEAF = 9,   /* 1..4                                                */
   ODP_FT_LEAF0 = 10,  /* per leaf l: [10+3l] pe address ([n_seg][rank][M], f32,
-                         or bf16 when bit 32 of [11+3l] is set; norms always
-                         use the fp32 values), [11+3l] col0 | rank << 16 |
+                         or bf16 when bit 32 of [11+3l] is set; norms square
+                         the values as stored), [11+3l] col0 | rank << 16 |
                          pe_bf16 << 32, [12+3l] slot_base;
                          leaves sorted by col0                               */
   ODP_FT_FIELDS = 24,
@@ -217,6 +217,26 @@ int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
                            const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                            const int32_t* seg_row_start, const int32_t* seg_row_len,
                            const int32_t* seg_example, double* part, int64_t part_stride);
+
+/* ---- odp_seg_factor_stream: factor rows of one leaf from given planes ---
+ * Replaces the same per-sample products as odp_seg_factor
+ * (opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176: dB[i] =
+ * s (X[i] A)^T G[i] with Q = the V plane, or dA[i]^T = s (G[i] B^T)^T X[i]
+ * with Q = the U plane) for bf16 problems with NLEAF == 1, the leaf at
+ * column 0 of Q, r <= 16 and bf16 pe rows: the same rows, squares and
+ * partial slots as odp_seg_factor with nkb = 1, bit for bit, with P streamed
+ * through LDS by buffer loads marked non-temporal.  The row's
+ * ODP_FT_GROUPS field splits each segment's 256-column tiles into that many
+ * groups of consecutive tiles, one workgroup each (1 <= groups <= tiles;
+ * odp_seg_factor_stream_groups(M) is the default): workgroups per problem =
+ * n_seg * groups.  Segments may be at most odp_factor_project_max_len()
+ * rows long (the caller checks).                                          */
+enum { ODP_FT_GROUPS = 23 };
+int64_t odp_seg_factor_stream_groups(int64_t M);
+int odp_seg_factor_stream(odp_stream_t stream, const int64_t* problems,
+                          const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
+                          const int32_t* seg_row_start, const int32_t* seg_row_len,
+                          const int32_t* seg_example, double* part, int64_t part_stride);
 
 /* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
  * For leaves that are not behind a captured linear op, the per-example

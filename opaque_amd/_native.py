@@ -35,6 +35,7 @@ FT_P, FT_LDP, FT_M, FT_Q, FT_LDQ, FT_R, FT_SEG_FIRST, FT_NSEG, FT_SCALING, FT_NL
 FT_LEAF0 = 10
 FT_WAVE_SLOTS = 4  # partial slots per LoRA leaf and M-tile
 FP_W, FP_U = 13, 14
+FT_GROUPS = 23
 SS_FIELDS = 8
 SS_PE, SS_M, SS_RANK, SS_SEG_FIRST, SS_NSEG, SS_OUT, SS_FLAGS, SS_OUT2 = range(8)
 NZ_FIELDS = 8
@@ -75,6 +76,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "odp_factor_project_max_len": (_c_i64, []),
     "odp_seg_factor_project": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
+    "odp_seg_factor_stream_groups": (_c_i64, [_c_i64]),
+    "odp_seg_factor_stream": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
     "odp_sqnorm_blocks": (_c_i64, [_c_i64]),
     "odp_sqnorm": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i64]),
     "odp_clip_factors": (

@@ -665,13 +665,32 @@ constexpr uint32_t ODP_BUFFER_DWORD3 = 0x00020000;  // raw 32-bit dwords (CDNA b
 // which every chunk reads again (4.5 % faster on C3 shapes).
 constexpr int FP_G_NT = 2;
 
-__global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* __restrict__ probs,
-                                                                const int32_t* __restrict__ ws, int n_prob,
-                                                                const int32_t* __restrict__ sstart,
-                                                                const int32_t* __restrict__ slen,
-                                                                const int32_t* __restrict__ sex,
-                                                                double* __restrict__ part,
-                                                                int64_t part_stride) {
+// Default column chunks per workgroup of the streamed factor pass (PROJ =
+// false below; the table row gives the group count): a segment's chunks are
+// split into groups of at most this many, so that the widest rows do not
+// leave a tail of long workgroups.
+#ifndef ODP_FS_GROUP
+#define ODP_FS_GROUP 8  // 4-12 measured alike on C3, 16 and wider slower
+#endif
+__host__ __device__ constexpr int fs_groups(int nchunks) {
+  return nchunks <= 0 ? 1 : (nchunks + ODP_FS_GROUP - 1) / ODP_FS_GROUP;
+}
+
+// One pass over P = G of a segment in 256-column chunks.  PROJ: the fused
+// G side above (dB rows and U = G B^T, one workgroup per segment, all
+// chunks).  !PROJ: the planes are given, so the pass forms only the
+// per-example factor rows pe[k][m] = scaling * sum_t Q[k][t] P[t][m] of a
+// one-leaf problem (dB from G and V, or dA from X and U), the pipeline of
+// the fused kernel without B, U and its registers; a workgroup then takes
+// one of the row's ODP_FT_GROUPS groups of consecutive chunks of its
+// segment.  Both compute
+// each chunk's rows, squares and partial slots exactly as k_factor_bf16<1>
+// does for its 256-column tile (same token blocks, same order).
+template <bool PROJ>
+__device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ probs, const int32_t* __restrict__ ws,
+                                                 int n_prob, const int32_t* __restrict__ sstart,
+                                                 const int32_t* __restrict__ slen, const int32_t* __restrict__ sex,
+                                                 double* __restrict__ part, int64_t part_stride) {
   constexpr int NJ = FP_MT / 64, PP = FP_MT;  // unpadded, XOR-swizzled G rows
   constexpr int QP = FP_T + 8, QROWS = 16;
   constexpr int PTILE = FP_T * PP, STAGE = PTILE + QROWS * QP;
@@ -686,9 +705,25 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   const int32_t ldq = (int32_t)f[ODP_FT_LDQ];
   const int r = (int)f[ODP_FT_R];
   const float scale = (float)__longlong_as_double(f[ODP_FT_SCALING]);
-  const uint16_t* W = (const uint16_t*)f[ODP_FP_W];
+  const uint16_t* W = PROJ ? (const uint16_t*)f[ODP_FP_W] : nullptr;
 
-  const int seg = bid - ws[p];
+  const int nchunks = (M + FP_MT - 1) / FP_MT;
+  const int local = bid - ws[p];
+  int seg, c_begin, c_end;
+  if constexpr (PROJ) {
+    seg = local;
+    c_begin = 0;
+    c_end = nchunks;
+  } else {
+    const int64_t ng = f[ODP_FT_GROUPS] > 0 ? f[ODP_FT_GROUPS] : 1;
+    seg = (int)(local / ng);
+    const int64_t grp = local - seg * ng;
+    c_begin = (int)(grp * nchunks / ng);
+    c_end = (int)((grp + 1) * nchunks / ng);
+    // Workgroups past the row's segments (a table whose work_start counts
+    // more than n_seg * groups) have nothing to do.
+    if (seg >= (int)f[ODP_FT_NSEG]) return;
+  }
   const int gs = (int)f[ODP_FT_SEG_FIRST] + seg;
   const int32_t rs = sstart[gs], len = slen[gs], t_hi = rs + len;
   const int ex = sex[gs];
@@ -696,7 +731,6 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   const int32_t t_lo = rs & ~7;
   int nsteps = len > 0 ? (t_hi - t_lo + FP_T - 1) / FP_T : 0;
   nsteps = nsteps < FP_STEPS ? nsteps : FP_STEPS;  // the host keeps segments within bounds
-  const int nchunks = (M + FP_MT - 1) / FP_MT;
 
   // G through a buffer resource over the segment's rows, loaded straight
   // into LDS: rows outside the segment (offsets below it wrap past the end)
@@ -742,9 +776,9 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
     *(u32x4_t*)(qdst_base + b * STAGE) = v;
   };
 
-  f32x4_t acc_u[FP_STEPS];
+  f32x4_t acc_u[PROJ ? FP_STEPS : 1];
 #pragma unroll
-  for (int st = 0; st < FP_STEPS; ++st) acc_u[st] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int st = 0; st < (PROJ ? FP_STEPS : 1); ++st) acc_u[st] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const FactorLeaves L = read_leaves(f);  // one leaf at column 0, rank r, bf16 rows
 
   // A chunk's dB rows (bf16) and this wave's norm partial wait in registers
@@ -834,8 +868,8 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
 
   u32x4_t qv;
   int buf = 0;
-  if (nsteps > 0 && nchunks > 0) load(lds, t_lo, 0, qv);
-  for (int c = 0; c < nchunks; ++c) {
+  if (nsteps > 0 && c_begin < c_end) load(lds, t_lo, c_begin * FP_MT, qv);
+  for (int c = c_begin; c < c_end; ++c) {
     const int32_t m_base = c * FP_MT;
     // The first token of the steps, re-read per chunk: address arithmetic
     // of the unrolled steps then stays inside the loop instead of being
@@ -856,17 +890,19 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
                     int st) __attribute__((always_inline)) {
       if (st + 1 < nsteps)
         load(nxt, tc0 + (st + 1) * FP_T, m_base, qv);
-      else if (c + 1 < nchunks)
+      else if (c + 1 < c_end)
         load(nxt, tc0, m_base + FP_MT, qv);
       if (st == 0) {
-        // B's loads before the stores: the MFMAs that wait for B then do
-        // not wait for the stores too (memory operations complete in
-        // issue order as far as s_waitcnt counts them).
+        if constexpr (PROJ) {
+          // B's loads before the stores: the MFMAs that wait for B then do
+          // not wait for the stores too (memory operations complete in
+          // issue order as far as s_waitcnt counts them).
 #pragma unroll
-        for (int ks = 0; ks < FP_MT / 32; ++ks) {
-          const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
-          const uint32_t off = m < M ? (wrow + (uint32_t)m) * 2u : 0x80000000u;
-          wf[ks] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)off, 0, 0));
+          for (int ks = 0; ks < FP_MT / 32; ++ks) {
+            const int32_t m = m_base + 32 * ks + 8 * (lane >> 4);
+            const uint32_t off = m < M ? (wrow + (uint32_t)m) * 2u : 0x80000000u;
+            wf[ks] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)off, 0, 0));
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
         flush();
@@ -891,7 +927,7 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
       }
       // U rows 16 wave .. + 15 of the step: A = G rows (8 consecutive
       // columns per lane; a swizzled chunk pair stays contiguous).
-      {
+      if constexpr (PROJ) {
         const int row = 16 * wave + (lane & 15);
 #pragma unroll
         for (int ks = 0; ks < FP_MT / 32; ++ks) {
@@ -938,28 +974,50 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
   // multiple of 4), stored as one 8-byte piece when all four tokens are the
   // segment's; tokens outside the segment belong to other workgroups, so a
   // group that straddles a segment end is stored entry by entry.
-  const int col = lane & 15;
-  if (col < r) {
-    uint16_t* uq = (uint16_t*)f[ODP_FP_U] + (int64_t)col * ldq;
+  if constexpr (PROJ) {
+    const int col = lane & 15;
+    if (col < r) {
+      uint16_t* uq = (uint16_t*)f[ODP_FP_U] + (int64_t)col * ldq;
 #pragma unroll
-    for (int st = 0; st < FP_STEPS; ++st) {
-      if (st < nsteps) {
-        const int32_t tb = t_lo + st * FP_T + 16 * wave + 4 * (lane >> 4);
-        uint32_t h[4];
+      for (int st = 0; st < FP_STEPS; ++st) {
+        if (st < nsteps) {
+          const int32_t tb = t_lo + st * FP_T + 16 * wave + 4 * (lane >> 4);
+          uint32_t h[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = odp_f2bf(acc_u[st][i]);
-        if (tb >= rs && tb + 3 < t_hi) {
-          odp_gstore((u32x2_t*)(uq + tb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
-        } else {
+          for (int i = 0; i < 4; ++i) h[i] = odp_f2bf(acc_u[st][i]);
+          if (tb >= rs && tb + 3 < t_hi) {
+            odp_gstore((u32x2_t*)(uq + tb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+          } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int32_t t = tb + i;
-            if (t >= rs && t < t_hi) odp_gstore(uq + t, (uint16_t)h[i]);
+            for (int i = 0; i < 4; ++i) {
+              const int32_t t = tb + i;
+              if (t >= rs && t < t_hi) odp_gstore(uq + t, (uint16_t)h[i]);
+            }
           }
         }
       }
     }
   }
+}
+
+__global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* __restrict__ probs,
+                                                                const int32_t* __restrict__ ws, int n_prob,
+                                                                const int32_t* __restrict__ sstart,
+                                                                const int32_t* __restrict__ slen,
+                                                                const int32_t* __restrict__ sex,
+                                                                double* __restrict__ part,
+                                                                int64_t part_stride) {
+  factor_pass_bf16<true>(probs, ws, n_prob, sstart, slen, sex, part, part_stride);
+}
+
+__global__ __launch_bounds__(256, 2) void k_factor_stream_bf16(const int64_t* __restrict__ probs,
+                                                               const int32_t* __restrict__ ws, int n_prob,
+                                                               const int32_t* __restrict__ sstart,
+                                                               const int32_t* __restrict__ slen,
+                                                               const int32_t* __restrict__ sex,
+                                                               double* __restrict__ part,
+                                                               int64_t part_stride) {
+  factor_pass_bf16<false>(probs, ws, n_prob, sstart, slen, sex, part, part_stride);
 }
 
 // ---------------------------------------------------------------------------
@@ -1207,6 +1265,28 @@ extern "C" int odp_seg_factor_project(odp_stream_t stream, const int64_t* proble
                      problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part,
                      part_stride);
   return odp_check_launch("odp_seg_factor_project");
+}
+
+extern "C" int64_t odp_seg_factor_stream_groups(int64_t M) {
+  return M <= 0 ? 0 : fs_groups((int)((M + FP_MT - 1) / FP_MT));
+}
+
+extern "C" int odp_seg_factor_stream(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
+                                     int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
+                                     const int32_t* seg_row_len, const int32_t* seg_example, double* part,
+                                     int64_t part_stride) {
+  int rc = odp_check_table("odp_seg_factor_stream", problems, work_start, n_prob, total_blocks);
+  if (rc != ODP_OK) return rc;
+  if (total_blocks == 0) return ODP_OK;
+  if (seg_row_start == nullptr || seg_row_len == nullptr || seg_example == nullptr ||
+      part == nullptr || part_stride <= 0) {
+    odp_set_error("odp_seg_factor_stream: null segment/partial arrays or part_stride <= 0");
+    return ODP_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(k_factor_stream_bf16, dim3(total_blocks), dim3(256), 0, odp_hip_stream(stream),
+                     problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part,
+                     part_stride);
+  return odp_check_launch("odp_seg_factor_stream");
 }
 
 extern "C" int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,

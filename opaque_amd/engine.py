@@ -432,7 +432,7 @@ def leaves_key(leaves: list[LeafOut]) -> tuple:
 
 
 # GhostPlan's keyword options and their defaults (part of a plan's key).
-_PLAN_OPTIONS = {"second_moment": False, "fuse_g_side": True, "prescale_bytes": 8 << 30,
+_PLAN_OPTIONS = {"second_moment": False, "fuse_g_side": True, "stream_factors": True, "prescale_bytes": 8 << 30,
                  "linear_pe_bytes": None, "square_f64": False, "sum_f64": False, "raw_values": False}
 
 
@@ -506,7 +506,9 @@ class GhostPlan:
     was built from stay alive and unchanged in shape.
 
     ``fuse_g_side``: LoRA sites take the single-pass kernels where they can
-    (results are bit-identical either way).  ``linear_pe_bytes``: HBM for
+    (results are bit-identical either way).  ``stream_factors``: one-leaf
+    bf16 factor problems of rank <= 16 take odp_seg_factor_stream instead
+    of odp_seg_factor (bit-identical).  ``linear_pe_bytes``: HBM for
     the stored per-example gradients of full-weight sites (bf16); None uses
     half of the free device memory, 0 stores none.  ``prescale_bytes``: at
     most this much of prescaled activations per clipped-sum chunk.
@@ -534,6 +536,7 @@ class GhostPlan:
         device: torch.device | str = "cuda",
         second_moment: bool = False,
         fuse_g_side: bool = True,
+        stream_factors: bool = True,
         prescale_bytes: int = 8 << 30,
         linear_pe_bytes: int | None = None,
         square_f64: bool = False,
@@ -551,6 +554,7 @@ class GhostPlan:
         self.clip = clip
         self.second_moment = second_moment
         self.fuse_g_side = fuse_g_side
+        self.stream_factors = bool(stream_factors)
         self.prescale_bytes = int(prescale_bytes)
         self.linear_pe_bytes = linear_pe_bytes
         self.square_f64 = bool(square_f64)
@@ -570,7 +574,8 @@ class GhostPlan:
         # key skips re-deriving the input layout.
         self.key = plan_key(segments=segments, leaves=leaves, clip=clip, lora_sites=lora_sites,
                             materialized=materialized, linear_sites=linear_sites, device=dev,
-                            second_moment=second_moment, fuse_g_side=fuse_g_side, prescale_bytes=prescale_bytes,
+                            second_moment=second_moment, fuse_g_side=fuse_g_side, stream_factors=stream_factors,
+                            prescale_bytes=prescale_bytes,
                             linear_pe_bytes=linear_pe_bytes, square_f64=square_f64, sum_f64=sum_f64,
                             raw_values=raw_values)
         self._build(list(lora_sites), list(materialized), list(linear_sites))
@@ -857,6 +862,7 @@ class GhostPlan:
         ft: dict[tuple, _Table] = {}
         pl = _Table(N.PL_FIELDS)
         fused_rows: list[tuple] = []
+        stream_rows: list[tuple] = []
 
         def tab(tables: dict, dt: torch.dtype, r: int, fields: int) -> _Table:
             return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
@@ -883,7 +889,7 @@ class GhostPlan:
                 wx = wx_of[ci]
                 if self._mirrored(ch, dt, v):
                     self._mirror_rows(ch[0], x, wx, ext[("lg", ci, 0)], ext[("lwb", ci, 0)], dt, v, qaddr, vbase,
-                                      ubase, ldq, planes, es, pj, ft, tab, fused_rows, slot_base)
+                                      ubase, ldq, planes, es, pj, ft, tab, fused_rows, slot_base, stream_rows)
                     continue
                 tab(pj, dt, rtot, N.PJ_FIELDS).add(
                     {
@@ -957,7 +963,9 @@ class GhostPlan:
                         (valid * d_out + r * d_out + planes * r * valid) * es, 2 * valid * d_out * r,
                         io=valid * d_out * es,
                     )
-                if frow is not None:
+                if frow is not None and self._streamable(dt, r, v, g):
+                    self._stream_rows(frow, v, d_out, r, es, planes, s.b_leaf, stream_rows)
+                elif frow is not None:
                     tab(ft, dt, r, N.FT_FIELDS).add(frow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
                                                     (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es,
                                                     2 * valid * d_out * r, io=valid * d_out * es)
@@ -968,12 +976,20 @@ class GhostPlan:
                     # Different scalings cannot share one pass: split them.
                     for s_leaf, col0, r in a_leaves:
                         sc = next(s.scaling for s in ch if s.a_leaf == s_leaf)
+                        arow = self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, sf, n_seg, sc,
+                                           [(s_leaf, col0, r)], pe_off, slot_base)
+                        if self._streamable(dt, r, v, x):
+                            self._stream_rows(arow, v, d_in, r, es, planes, s_leaf, stream_rows)
+                            continue
                         tab(ft, dt, r, N.FT_FIELDS).add(
-                            self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, sf, n_seg, sc,
-                                        [(s_leaf, col0, r)], pe_off, slot_base),
-                            n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
+                            arow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
                             (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * es, 2 * valid * d_in * r,
                             io=valid * d_in * es)
+                elif len(a_leaves) == 1 and a_leaves[0][1] == 0 and a_leaves[0][2] == rtot \
+                        and self._streamable(dt, rtot, v, x):
+                    self._stream_rows(self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
+                                                  a_leaves, pe_off, slot_base),
+                                      v, d_in, rtot, es, planes, a_leaves[0][0], stream_rows)
                 else:
                     tab(ft, dt, rtot, N.FT_FIELDS).add(
                         self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
@@ -988,6 +1004,9 @@ class GhostPlan:
         fp = _Table(N.FT_FIELDS)
         for _, _, row, blocks, nbytes, io, fl in sorted(fused_rows, key=lambda t: (t[0], t[1])):
             fp.add(row, blocks, nbytes, fl, io=io)
+        fst = _Table(N.FT_FIELDS)
+        for _, _, row, blocks, nbytes, io, fl in sorted(stream_rows, key=lambda t: (t[0], t[1])):
+            fst.add(row, blocks, nbytes, fl, io=io)
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
@@ -1224,6 +1243,7 @@ class GhostPlan:
         for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("project", key, pj[key]))
         tabs.append(("factor_project", None, fp))
+        tabs.append(("factor_stream", None, fst))
         for key in sorted(ft, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("factor", key, ft[key]))
         tabs.append(("sqnorm", None, sq))
@@ -1591,7 +1611,7 @@ class GhostPlan:
         return x.shape[1] > s.g.shape[-1] and self._fusable(dt, s.A.shape[1], v, x)
 
     def _mirror_rows(self, s, x, wx, g, wb, dt, v, qaddr, vbase, ubase, ldq, planes, es, pj, ft, tab, fused_rows,
-                     slot_base) -> None:
+                     slot_base, stream_rows) -> None:
         lib = N.load()
         r = s.A.shape[1]
         d_in = x.shape[1]
@@ -1631,19 +1651,22 @@ class GhostPlan:
                                + (r * d_in * es if j == 0 else 0), ln * d_in * es, 4 * ln * d_in * r))
         # dB^T rows from G and V.
         if s.b_leaf is not None:
-            tab(ft, dt, r, N.FT_FIELDS).add(
-                {
-                    N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
-                    N.FT_Q: qaddr(vbase, 0),
-                    N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
-                    N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
-                    N.FT_LEAF0: self._pe_addr(s.b_leaf),
-                    N.FT_LEAF0 + 1: 0 | (r << 16) | self._pe_bits(s.b_leaf),
-                    N.FT_LEAF0 + 2: slot_base[s.b_leaf],
-                },
-                n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
-                (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es, 2 * valid * d_out * r,
-                io=valid * d_out * es)
+            brow = {
+                N.FT_P: g.data_ptr(), N.FT_LDP: g.stride(0), N.FT_M: d_out,
+                N.FT_Q: qaddr(vbase, 0),
+                N.FT_LDQ: ldq, N.FT_R: r, N.FT_SEG_FIRST: sf, N.FT_NSEG: n_seg,
+                N.FT_SCALING: _f64_bits(s.scaling), N.FT_NLEAF: 1,
+                N.FT_LEAF0: self._pe_addr(s.b_leaf),
+                N.FT_LEAF0 + 1: 0 | (r << 16) | self._pe_bits(s.b_leaf),
+                N.FT_LEAF0 + 2: slot_base[s.b_leaf],
+            }
+            if self._streamable(dt, r, v, g):
+                self._stream_rows(brow, v, d_out, r, es, planes, s.b_leaf, stream_rows)
+            else:
+                tab(ft, dt, r, N.FT_FIELDS).add(
+                    brow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
+                    (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es, 2 * valid * d_out * r,
+                    io=valid * d_out * es)
 
     def _fusable(self, dt: torch.dtype, r: int, v: _SegView, g: torch.Tensor) -> bool:
         """Whether a site's G side runs as one odp_seg_factor_project pass."""
@@ -1651,6 +1674,31 @@ class GhostPlan:
             return False
         lib = N.load()
         return v.max_len <= lib.odp_factor_project_max_len() and v.max_len * g.stride(0) * 2 < 2**31
+
+    def _streamable(self, dt: torch.dtype, r: int, v: _SegView, p: torch.Tensor) -> bool:
+        """Whether a one-leaf factor problem over P runs as odp_seg_factor_stream."""
+        if not self.stream_factors or dt != torch.bfloat16 or r > 16:
+            return False
+        lib = N.load()
+        return v.max_len <= lib.odp_factor_project_max_len() and v.max_len * p.stride(0) * 2 < 2**31
+
+    def _stream_rows(self, row: dict, v: _SegView, M: int, r: int, es: int, planes: int, leaf: int,
+                     out: list) -> None:
+        """A one-leaf factor problem as odp_seg_factor_stream rows: one per
+        segment, its pe rows at the segment's own offset, so that the launch
+        can run the most work per workgroup first."""
+        lib = N.load()
+        pe0 = self._pe_addr(leaf)
+        pe_es = self.pe[torch.bfloat16].element_size()
+        groups = int(lib.odp_seg_factor_stream_groups(M))
+        for j, ln in enumerate(v.segs.lengths):
+            rj = dict(row)
+            rj[N.FT_SEG_FIRST] = v.first + j
+            rj[N.FT_NSEG] = 1
+            rj[N.FT_LEAF0] = pe0 + j * r * M * pe_es
+            rj[N.FT_GROUPS] = groups
+            out.append((-ln * M / groups, len(out), rj, groups, (ln * M + planes * r * ln) * es + r * M * es, ln * M * es,
+                        2 * ln * M * r))
 
     def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, seg_first, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
@@ -1744,6 +1792,11 @@ class GhostPlan:
                                                    self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                                    self.seg_ex.data_ptr(), self.part.data_ptr(),
                                                    self.n_slots), name)
+            elif name == "factor_stream":
+                N.check(lib.odp_seg_factor_stream(s, probs.data_ptr(), ws.data_ptr(), n, total,
+                                                  self.seg_start.data_ptr(), self.seg_len.data_ptr(),
+                                                  self.seg_ex.data_ptr(), self.part.data_ptr(),
+                                                  self.n_slots), name)
             elif name == "factor":
                 N.check(lib.odp_seg_factor(s, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                            self.seg_start.data_ptr(), self.seg_len.data_ptr(),

@@ -78,6 +78,14 @@ def test_field_indices_match_header():
     assert value("ODP_NF_MASK") == N.NF_MASK
     assert value("ODP_CLIP_AUTOS") == N.CLIP_AUTOS
     assert value("ODP_DTYPE_BF16") == N.DTYPE_BF16
+    assert value("ODP_FP_W") == N.FP_W and value("ODP_FP_U") == N.FP_U
+    assert value("ODP_FT_GROUPS") == N.FT_GROUPS
+    assert value("ODP_FT_GROUPS") >= N.FT_LEAF0 + 3 * 4 and value("ODP_FT_GROUPS") < N.FT_FIELDS  # past 4 leaves
+    assert value("ODP_LN_OUT2") == N.LN_OUT2
+    assert value("ODP_LN_XAMAX") == N.LN_XAMAX and value("ODP_LN_GAMAX") == N.LN_GAMAX
+    assert value("ODP_NF_AMAX") == N.NF_AMAX
+    assert value("ODP_FORM_OUTER_GUARDED") == N.FORM_OUTER_GUARDED
+    assert value("ODP_PL_FIELDS") == N.PL_FIELDS and value("ODP_PL_DTYPE") == N.PL_DTYPE
 
 
 def test_block_helpers_are_pure_host_code(lib):
@@ -96,6 +104,10 @@ def test_block_helpers_are_pure_host_code(lib):
     assert lib.odp_nonfinite_blocks(0, 2) == 0
     assert lib.odp_pack_factors_blocks(0) == 0
     assert lib.odp_pack_factors_blocks(256) == 1 and lib.odp_pack_factors_blocks(257) == 2
+    assert lib.odp_seg_factor_stream_groups(0) == 0
+    assert lib.odp_seg_factor_stream_groups(256) == 1
+    tiles = lib.odp_seg_factor_tiles(N.DTYPE_BF16, 14336, 16)
+    assert 1 < lib.odp_seg_factor_stream_groups(14336) <= tiles
 
 
 def test_linear_norm_slots_per_form(lib):

@@ -1,0 +1,157 @@
+"""The streamed factor pass (odp_seg_factor_stream) against the tiled one
+(odp_seg_factor with one rank block).
+
+Both form a one-leaf problem's per-example rows pe[k][m] = scaling *
+sum_t Q[k][t] P[t][m] from the same 32-token MFMA blocks in the same order,
+then square and store the same bf16 values into the same partial slots, so
+every output of a plan must be bit-identical with the streamed pass on and
+off: per-example rows, norms, scales, clip masks and clipped sums.  Covered:
+dB rows from G and V, dA rows from X and U (a one-site activation, and the
+per-site rows of sites with different scalings), the mirrored order of a
+down projection, sites bringing the seam's V and U, widths that split a
+segment's tiles into several groups with a partial last tile, empty,
+single-row, longest and unaligned segments, and a segment past the length
+limit (that site then keeps the tiled pass).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from opaque_amd import _native as N
+from opaque_amd.engine import ClipSpec, GhostPlan, LeafOut, LoraSite, Segments
+from opaque_amd.guard import guard_constants, leaf_guards
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _sites(n_rows, d_in, outs, ranks, frozen=(), scalings=None, seed=0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    X = torch.randn(n_rows, d_in, device=DEV, generator=g).to(torch.bfloat16)
+    sites, leaves = [], []
+    for i, (d_out, r) in enumerate(zip(outs, ranks)):
+        G = (torch.randn(n_rows, d_out, device=DEV, generator=g) * 0.3).to(torch.bfloat16)
+        A = (torch.randn(d_in, r, device=DEV, generator=g) / math.sqrt(d_in)).to(torch.bfloat16)
+        B = (torch.randn(r, d_out, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+        ia = ib = None
+        if (i, "A") not in frozen:
+            ia = len(leaves)
+            leaves.append(LeafOut(tuple(A.shape), torch.bfloat16))
+        if (i, "B") not in frozen:
+            ib = len(leaves)
+            leaves.append(LeafOut(tuple(B.shape), torch.bfloat16))
+        sc = 2.0 if scalings is None else scalings[i]
+        sites.append(LoraSite(X, G, A, B, sc, a_leaf=ia, b_leaf=ib))
+    return sites, leaves
+
+
+def _plan(seg, sites, leaves, stream, C, fuse=True):
+    shapes = [lf.shape for lf in leaves]
+    _, rnd = leaf_guards(shapes, [torch.bfloat16] * len(shapes))
+    rel, ab = guard_constants(torch.bfloat16, rnd)
+    clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=[C], effective=C, normalize_by=2.0,
+                    guards=[(rel, ab, torch.bfloat16)])
+    return GhostPlan(segments=seg, leaves=leaves, clip=clip, lora_sites=sites, device=DEV,
+                     stream_factors=stream, fuse_g_side=fuse)
+
+
+def _outputs(plan):
+    res = plan.run()
+    torch.cuda.synchronize()
+    out = [t.clone() for t in plan.pe_views()] + [t.clone() for t in res.leaves]
+    return out + [res.norms.clone(), res.scales.clone(), res.clipped.clone()]
+
+
+def _compare(seg, sites, leaves, expect_stream=True, fuse=True):
+    """expect_stream: whether the plan must hold streamed rows (None: either)."""
+    base = _plan(seg, sites, leaves, False, 1e30, fuse)
+    norms = base.run().norms.double().cpu()
+    torch.cuda.synchronize()
+    C = float(norms[norms > 0].median()) if (norms > 0).any() else 1.0  # some examples clipped, some not
+    off = _plan(seg, sites, leaves, False, C, fuse)
+    on = _plan(seg, sites, leaves, True, C, fuse)
+    live_on = {t[0] for t in on.tables if t[5] > 0}
+    live_off = {t[0] for t in off.tables if t[5] > 0}
+    assert "factor_stream" not in live_off
+    if expect_stream is not None:
+        assert ("factor_stream" in live_on) == expect_stream, live_on
+    want, got = _outputs(off), _outputs(on)
+    assert len(got) == len(want)
+    for k, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), k
+    return on
+
+
+CASES = [
+    # n_ex, T, lengths, d_in, d_outs, ranks, frozen
+    (5, 96, [96, 33, 1, 70, 64], 136, [264], [8], ()),             # partial last tile, length 1
+    (3, 1081, [1081, 0, 517], 64, [512], [16], ()),                # longest segment, empty segment
+    (4, 40, [40, 39, 17, 25], 96, [1000, 200], [12, 4], ()),       # two sites on one X: dA stays tiled
+    (3, 64, [64, 50, 9], 128, [256, 136], [8, 8], ((0, "B"), (1, "A"))),  # frozen factors
+    (4, 80, [80, 33, 1, 64], 520, [136], [16], ()),                # mirrored: d_in > d_out
+    (3, 200, [200, 0, 57], 264, [4360], [16], ()),                 # 18 tiles: two groups, partial last
+    (2, 129, [129, 88], 4360, [8200], [16], ()),                   # dA over 18 tiles, dB over 33 (three groups)
+]
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+@pytest.mark.parametrize("n_ex,T,lengths,d_in,d_outs,ranks,frozen", CASES)
+def test_streamed_factor_rows_equal_tiled(n_ex, T, lengths, d_in, d_outs, ranks, frozen, fuse):
+    """With the fused G side off every dB row streams; with it on, the dA
+    rows of one-leaf activations and the dB rows of mirrored sites do."""
+    print(f"factor stream: n_ex={n_ex} T={T} d_in={d_in} d_outs={d_outs} ranks={ranks} fuse={fuse}", flush=True)
+    seg = Segments.padded(n_ex, T, lengths)
+    sites, leaves = _sites(n_ex * T, d_in, d_outs, ranks, frozen)
+    _compare(seg, sites, leaves, expect_stream=None if fuse else True, fuse=fuse)
+
+
+def test_sites_with_different_scalings_stream_their_own_da_rows():
+    print("factor stream: per-site dA rows (different scalings)", flush=True)
+    seg = Segments.padded(3, 72, [72, 40, 5])
+    sites, leaves = _sites(3 * 72, 200, [96, 264], [16, 8], scalings=[2.0, 0.5])
+    _compare(seg, sites, leaves)
+
+
+def test_unaligned_segments():
+    print("factor stream: packed segments at unaligned starts", flush=True)
+    lengths = [13, 37, 77, 0, 100]
+    starts = [0, 13, 50, 127, 127]
+    seg = Segments(starts, lengths, list(range(5)), 5, 240)
+    sites, leaves = _sites(240, 72, [328], [16], seed=5)
+    _compare(seg, sites, leaves)
+
+
+def test_segment_past_the_limit_keeps_the_tiled_pass():
+    limit = int(N.load().odp_factor_project_max_len())
+    T = limit + 21
+    print(f"factor stream: segment of {T} rows (limit {limit})", flush=True)
+    seg = Segments.padded(2, T, [T, 40])
+    sites, leaves = _sites(2 * T, 96, [200], [16], seed=7)
+    _compare(seg, sites, leaves, expect_stream=False)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_seam_products(shared):
+    """Sites bringing V and U: every dB row and the dA rows of one-site
+    activations take the streamed pass."""
+    print(f"factor stream: seam products, shared activation={shared}", flush=True)
+    seg = Segments.padded(4, 96, [96, 0, 41, 77])
+    outs, ranks = ([256, 64, 64], [16, 16, 8]) if shared else ([4360], [16])
+    sites, leaves = _sites(4 * 96, 512 if not shared else 256, outs, ranks, seed=3)
+    proj = _plan(seg, sites, leaves, False, 1.0)
+    proj.run()
+    torch.cuda.synchronize()
+    with_vu = []
+    for i, s in enumerate(sites):
+        v, u = proj.rank_planes(i)
+        with_vu.append(LoraSite(s.x, s.g, s.A, s.B, s.scaling, a_leaf=s.a_leaf, b_leaf=s.b_leaf,
+                                v=v.contiguous(), u=u.contiguous()))
+    on = _compare(seg, with_vu, leaves)
+    live = {t[0] for t in on.tables if t[5] > 0}
+    assert "planes" in live and not live & {"project", "factor_project"}, live
+    if not shared:
+        assert "factor" not in live, live
