@@ -52,9 +52,9 @@ def parse_args():
                          "backward) and the step reads them from HBM; recompute = the step projects X and G "
                          "again (two extra passes over the narrower of each pair)")
     ap.add_argument("--stream-factors", choices=["on", "off"], default="on",
-                    help="c3: on = one-leaf factor rows (rank <= 16) stream P through LDS "
-                         "(odp_seg_factor_stream); off = the register-staged odp_seg_factor tiles "
-                         "(bit-identical results)")
+                    help="c3: on = factor rows whose leaves each take a 16-row block of the plane (rank <= 16, "
+                         "up to three blocks) stream P through LDS (odp_seg_factor_stream); off = the "
+                         "register-staged odp_seg_factor tiles (bit-identical results)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--linear-pe-gb", type=float, default=None,
                     help="c4: HBM for stored per-example weight gradients (default: free memory after "
@@ -92,7 +92,9 @@ def kernel_label(stage, key):
     if key is None:
         return {"sqnorm": "k_sqnorm", "scale_sum": "k_scale_sum", "nonfinite": "k_nonfinite_cols",
                 "pack": "k_pack_factors", "planes": "k_pack_planes",
-                "factor_project": "k_factor_project_bf16", "factor_stream": "k_factor_stream_bf16"}[stage]
+                "factor_project": "k_factor_project_bf16"}[stage]
+    if stage == "factor_stream":  # keyed by rank blocks
+        return f"k_factor_stream_bf16<{key}>"
     dt, nkb = key
     base = {"project": "k_project", "factor": "k_factor"}[stage]
     if dt == torch.bfloat16:

@@ -218,25 +218,26 @@ int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
                            const int32_t* seg_row_start, const int32_t* seg_row_len,
                            const int32_t* seg_example, double* part, int64_t part_stride);
 
-/* ---- odp_seg_factor_stream: factor rows of one leaf from given planes ---
+/* ---- odp_seg_factor_stream: factor rows from given planes, streamed ----
  * Replaces the same per-sample products as odp_seg_factor
  * (opaque-patches/src/opaque/api/patches/kernels/lora.py:164-176: dB[i] =
  * s (X[i] A)^T G[i] with Q = the V plane, or dA[i]^T = s (G[i] B^T)^T X[i]
- * with Q = the U plane) for bf16 problems with NLEAF == 1, the leaf at
- * column 0 of Q, r <= 16 and bf16 pe rows: the same rows, squares and
- * partial slots as odp_seg_factor with nkb = 1, bit for bit, with P streamed
- * through LDS by buffer loads marked non-temporal.  The row's
- * ODP_FT_GROUPS field splits each segment's 256-column tiles into that many
- * groups of consecutive tiles, one workgroup each (1 <= groups <= tiles;
- * odp_seg_factor_stream_groups(M) is the default): workgroups per problem =
- * n_seg * groups.  Segments may be at most odp_factor_project_max_len()
- * rows long (the caller checks).                                          */
+ * with Q = the U plane) for bf16 problems whose leaves each start at a
+ * column of Q that is a multiple of 16, with rank <= 16 (at most one leaf
+ * per 16-row block of Q), bf16 pe rows, and ceil(ODP_FT_R / 16) == nkb
+ * (1..3): the same rows, squares and partial slots as odp_seg_factor with
+ * the same nkb, bit for bit, with P streamed through LDS by buffer loads
+ * marked non-temporal.  The row's ODP_FT_GROUPS field splits each
+ * segment's 256-column tiles into that many groups of consecutive tiles,
+ * one workgroup each (1 <= groups <= tiles; odp_seg_factor_stream_groups(M)
+ * is the default): workgroups per problem = n_seg * groups.  Segments may
+ * be at most odp_factor_project_max_len() rows long (the caller checks).  */
 enum { ODP_FT_GROUPS = 23 };
 int64_t odp_seg_factor_stream_groups(int64_t M);
 int odp_seg_factor_stream(odp_stream_t stream, const int64_t* problems,
                           const int32_t* work_start, int32_t n_prob, int32_t total_blocks,
                           const int32_t* seg_row_start, const int32_t* seg_row_len,
-                          const int32_t* seg_example, double* part, int64_t part_stride);
+                          const int32_t* seg_example, double* part, int64_t part_stride, int32_t nkb);
 
 /* ---- odp_sqnorm: squared norms of materialised per-example tensors -------
  * For leaves that are not behind a captured linear op, the per-example

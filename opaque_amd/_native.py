@@ -77,7 +77,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_factor_project_max_len": (_c_i64, []),
     "odp_seg_factor_project": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
     "odp_seg_factor_stream_groups": (_c_i64, [_c_i64]),
-    "odp_seg_factor_stream": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64]),
+    "odp_seg_factor_stream": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i64, _c_i32]),
     "odp_sqnorm_blocks": (_c_i64, [_c_i64]),
     "odp_sqnorm": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i64]),
     "odp_clip_factors": (

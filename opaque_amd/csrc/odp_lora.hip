@@ -679,23 +679,31 @@ __host__ __device__ constexpr int fs_groups(int nchunks) {
 // One pass over P = G of a segment in 256-column chunks.  PROJ: the fused
 // G side above (dB rows and U = G B^T, one workgroup per segment, all
 // chunks).  !PROJ: the planes are given, so the pass forms only the
-// per-example factor rows pe[k][m] = scaling * sum_t Q[k][t] P[t][m] of a
-// one-leaf problem (dB from G and V, or dA from X and U), the pipeline of
-// the fused kernel without B, U and its registers; a workgroup then takes
-// one of the row's ODP_FT_GROUPS groups of consecutive chunks of its
-// segment.  Both compute
-// each chunk's rows, squares and partial slots exactly as k_factor_bf16<1>
-// does for its 256-column tile (same token blocks, same order).
-template <bool PROJ>
+// per-example factor rows pe[k][m] = scaling * sum_t Q[k][t] P[t][m] (dB
+// from G and V, or dA from X and U) of a problem with NKB 16-row blocks of
+// Q, each holding at most one leaf that starts at the block (rank <= 16):
+// the pipeline of the fused kernel without B, U and its registers.  A
+// workgroup then takes one of the row's ODP_FT_GROUPS groups of
+// consecutive chunks of its segment.  Both compute each chunk's rows,
+// squares and partial slots exactly as k_factor_bf16<NKB> does for its
+// 256-column tile (same token blocks, same order).
+template <bool PROJ, int NKB>
 __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ probs, const int32_t* __restrict__ ws,
                                                  int n_prob, const int32_t* __restrict__ sstart,
                                                  const int32_t* __restrict__ slen, const int32_t* __restrict__ sex,
                                                  double* __restrict__ part, int64_t part_stride) {
+  static_assert(NKB >= 1 && NKB <= 3 && (!PROJ || NKB == 1), "one to three rank blocks; the fused G side has one");
   constexpr int NJ = FP_MT / 64, PP = FP_MT;  // unpadded, XOR-swizzled G rows
-  constexpr int QP = FP_T + 8, QROWS = 16;
+  constexpr int QP = FP_T + 8, QROWS = 16 * NKB;
   constexpr int PTILE = FP_T * PP, STAGE = PTILE + QROWS * QP;
-  constexpr int QPC = FP_T / 8;                // V pieces per row per step
-  static_assert(QPC * QROWS == 128, "one V piece per thread of waves 0 and 1");
+  constexpr int QPC = FP_T / 8;                  // V pieces per row per step
+  constexpr int NQP = QPC * QROWS;               // V pieces per step: 128 per rank block
+  constexpr int NQ = (NQP + 255) / 256;          // per thread (waves past NQP issue none)
+  static_assert(NQP % 128 == 0, "V pieces cover whole waves");
+  // Stores a chunk's flush issues (every one unconditional): NJ rows and a
+  // partial per rank block.  The step-1 wait below encodes it in 4 bits.
+  constexpr int NFLUSH = NKB * (NJ + 1);
+  static_assert(NFLUSH <= 15, "vmcnt immediate");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -742,15 +750,22 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
   // 16 wave + 2 i + (l >> 5), so it fetches the logical slot that the XOR
   // swizzle maps there.
   const int gh = lane >> 5, gslot = lane & 31;
-  // Waves 0 and 1 load V, one piece per thread: rank row and 8 tokens of a
-  // step (`vown` is wave-uniform, so the V loads and stores are scalar
-  // branches and waves 2 and 3 issue none).
-  const bool vown = __builtin_amdgcn_readfirstlane(wave) < 2;
-  const int qrow = (tid % (QPC * QROWS)) / QPC, qpc = tid % QPC;
-  const uint16_t* qsrc = (const uint16_t*)f[ODP_FT_Q] + (int64_t)qrow * ldq;
-  uint16_t* const qdst_base = lds + PTILE + qrow * QP + 8 * qpc;
+  // V pieces (a rank row and 8 tokens of a step) go to threads in order,
+  // 128 per rank block: with one block waves 0 and 1 load them.  `vown` is
+  // wave-uniform, so the V loads and stores are scalar branches.
+  const int qpc = tid % QPC;
+  bool vown[NQ];
+  const uint16_t* qsrc[NQ];
+  uint16_t* qdst_base[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    vown[i] = __builtin_amdgcn_readfirstlane(wave) * 64 + 256 * i < NQP;
+    const int qrow = ((tid + 256 * i) % NQP) / QPC;
+    qsrc[i] = (const uint16_t*)f[ODP_FT_Q] + (int64_t)qrow * ldq;
+    qdst_base[i] = lds + PTILE + qrow * QP + 8 * qpc;
+  }
 
-  auto load = [&](uint16_t* stage, int32_t t0, int32_t m_base, u32x4_t& qv) {
+  auto load = [&](uint16_t* stage, int32_t t0, int32_t m_base, u32x4_t (&qv)[NQ]) {
     uint16_t* dst = stage + 16 * wave * PP;
 #pragma unroll
     for (int i = 0; i < FP_T / 4 / 2; ++i) {
@@ -761,100 +776,140 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
       __builtin_amdgcn_raw_ptr_buffer_load_lds(grsrc, (ODP_LDS void*)(dst + 2 * i * PP), 16, off, 0, 0, FP_G_NT);
     }
     const int32_t tq = t0 + 8 * qpc;
-    if (vown) qv = ld16(qsrc + (tq < t_hi ? tq : t_lo));
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      if (vown[i]) qv[i] = ld16(qsrc[i] + (tq < t_hi ? tq : t_lo));
   };
   // V's tokens outside [rs, t_hi) are zeroed when its piece is written.
-  auto store_q = [&](int b, int32_t t0, u32x4_t v) {
-    if (!vown) return;
+  auto store_q = [&](int b, int32_t t0, const u32x4_t (&qv)[NQ]) {
     const int32_t tq = t0 + 8 * qpc;
+    uint32_t mask[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const int32_t ta = tq + 2 * w;
-      v[w] &= ((ta >= rs && ta < t_hi) ? 0x0000ffffu : 0u) |
-              ((ta + 1 >= rs && ta + 1 < t_hi) ? 0xffff0000u : 0u);
+      mask[w] = ((ta >= rs && ta < t_hi) ? 0x0000ffffu : 0u) | ((ta + 1 >= rs && ta + 1 < t_hi) ? 0xffff0000u : 0u);
     }
-    *(u32x4_t*)(qdst_base + b * STAGE) = v;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (!vown[i]) continue;
+      u32x4_t v = qv[i];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[w] &= mask[w];
+      *(u32x4_t*)(qdst_base[i] + b * STAGE) = v;
+    }
   };
 
   f32x4_t acc_u[PROJ ? FP_STEPS : 1];
 #pragma unroll
   for (int st = 0; st < (PROJ ? FP_STEPS : 1); ++st) acc_u[st] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const FactorLeaves L = read_leaves(f);  // one leaf at column 0, rank r, bf16 rows
+  // The leaf of each rank block (bf16 rows): the one that starts at column
+  // 16 kb of Q, if any (rank 0 otherwise: nothing stored, no partial).
+  const FactorLeaves L = read_leaves(f);
+  uint16_t* lpe[NKB];
+  int lrank[NKB];
+  int64_t lslot[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    lpe[kb] = nullptr;
+    lrank[kb] = 0;
+    lslot[kb] = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < L.n && L.col0[q] == 16 * kb) {
+        lpe[kb] = (uint16_t*)L.pe[q];
+        lrank[kb] = L.rank[q] < 16 ? L.rank[q] : 16;
+        lslot[kb] = L.slot[q];
+      }
+  }
 
-  // A chunk's dB rows (bf16) and this wave's norm partial wait in registers
+  // A chunk's rows (bf16) and this wave's norm partials wait in registers
   // and are stored after the next step's barrier: a barrier waits for every
   // memory operation in flight, so stores issued just before one would
   // stall it for their whole latency.  The arithmetic is factor_epilogue's
-  // for one leaf, in the same order.
-  uint32_t pend[NJ * 2];
-  double pend_sq = 0.0;
+  // for one leaf per rank block, in the same order.
+  uint32_t pend[NKB][NJ * 2];
+  double pend_sq[NKB];
   int32_t pend_m0 = -1, pend_tile = 0;  // pend_m0 < 0: nothing pending
-  auto hold = [&](const f32x4_t (&acc)[NJ][1], int32_t m_base, int tile) {
-    double wsum = 0.0, cs[4];
+  auto hold = [&](const f32x4_t (&acc)[NJ][NKB], int32_t m_base, int tile) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      cs[i] = 0.0;
-      const int k = 4 * (lane >> 4) + i;
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int rk = lrank[kb];
+      double wsum = 0.0, cs[4];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int32_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
-        const float v = scale * acc[j][0][i];
-        const uint32_t h = odp_f2bf(v);
-        if (i & 1)
-          pend[2 * j + (i >> 1)] |= h << 16;
-        else
-          pend[2 * j + (i >> 1)] = h;
-        if (k < r && m < M) {
-          const float vq = odp_bf2f((uint16_t)h);  // the value as stored
-          const float vf = isfinite(vq) ? vq : 0.f;
-          cs[i] += (double)__fmul_rn(vf, vf);
+      for (int i = 0; i < 4; ++i) {
+        cs[i] = 0.0;
+        const int k = 4 * (lane >> 4) + i;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int32_t m = m_base + (NJ * wave + j) * 16 + (lane & 15);
+          const float v = scale * acc[j][kb][i];
+          const uint32_t h = odp_f2bf(v);
+          if (i & 1)
+            pend[kb][2 * j + (i >> 1)] |= h << 16;
+          else
+            pend[kb][2 * j + (i >> 1)] = h;
+          if (k < rk && m < M) {
+            const float vq = odp_bf2f((uint16_t)h);  // the value as stored
+            const float vf = isfinite(vq) ? vq : 0.f;
+            cs[i] += (double)__fmul_rn(vf, vf);
+          }
         }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const double v = row_sum16(cs[i]);
-      if (4 * (lane >> 4) + i < r) wsum += v;
+      for (int i = 0; i < 4; ++i) {
+        const double v = row_sum16(cs[i]);
+        if (4 * (lane >> 4) + i < rk) wsum += v;
+      }
+      pend_sq[kb] = rows_sum4(wsum);
     }
-    pend_sq = rows_sum4(wsum);
     pend_m0 = m_base;
     pend_tile = tile;
   };
-  // Each 16 x 16 block of dB rows leaves as 8-byte pieces: a 4 x 4
-  // transpose within each quad of lanes (two exchanges) turns lane
-  // (g, 4q + t)'s column of rows 4g .. 4g + 3 into row 4g + t, columns
-  // 4q .. 4q + 3.  The stores are buffer stores issued unconditionally
-  // (an offset past the end drops a store with nothing to write): the
-  // compiler then knows that exactly NJ + 1 of them follow B's loads, and
-  // the MFMAs that wait for B do not wait for the stores.
-  const __amdgpu_buffer_rsrc_t pe_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((uint16_t*)L.pe[0] + (int64_t)seg * r * M), (short)0, (int)((uint32_t)r * (uint32_t)M * 2u),
-      ODP_BUFFER_DWORD3);
-  const __amdgpu_buffer_rsrc_t part_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(part + (int64_t)ex * part_stride + L.slot[0]), (short)0,
-      (int)(ODP_FT_WAVE_SLOTS * (uint32_t)nchunks * 8u), ODP_BUFFER_DWORD3);
+  // Each 16 x 16 block of rows leaves as 8-byte pieces: a 4 x 4 transpose
+  // within each quad of lanes (two exchanges) turns lane (g, 4q + t)'s
+  // column of rows 4g .. 4g + 3 into row 4g + t, columns 4q .. 4q + 3.  The
+  // stores are buffer stores issued unconditionally (an offset past the end
+  // drops a store with nothing to write): the compiler then knows that
+  // exactly NFLUSH of them follow B's loads, and the MFMAs that wait for B
+  // do not wait for the stores.
+  __amdgpu_buffer_rsrc_t pe_rsrc[NKB], part_rsrc[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    pe_rsrc[kb] = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(lpe[kb] + (int64_t)seg * lrank[kb] * M), (short)0,
+        (int)((uint32_t)lrank[kb] * (uint32_t)M * 2u), ODP_BUFFER_DWORD3);
+    part_rsrc[kb] = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(part + (int64_t)ex * part_stride + lslot[kb]), (short)0,
+        lrank[kb] > 0 ? (int)(ODP_FT_WAVE_SLOTS * (uint32_t)nchunks * 8u) : 0, ODP_BUFFER_DWORD3);
+  }
   auto flush = [&]() {
     const bool live = pend_m0 >= 0;
     const int t = lane & 3, tl = t & 1, th = t >> 1;
     const int k = 4 * (lane >> 4) + t;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const uint32_t h0 = pend[2 * j] & 0xffffu, h1 = pend[2 * j] >> 16;
-      const uint32_t h2 = pend[2 * j + 1] & 0xffffu, h3 = pend[2 * j + 1] >> 16;
-      // Rows of the other parity to the odd/even neighbour.
-      const uint32_t r1 = quad_x1(tl ? (h0 | (h2 << 16)) : (h1 | (h3 << 16)));
-      // Rows 4g + 2a + tl, columns of this lane pair (low half: even column).
-      const uint32_t p0 = tl ? ((r1 & 0xffffu) | (h1 << 16)) : (h0 | (r1 << 16));
-      const uint32_t p1 = tl ? ((r1 >> 16) | (h3 << 16)) : (h2 | (r1 & 0xffff0000u));
-      // Row pairs across the two lane pairs of the quad.
-      const uint32_t r2 = quad_x2(th ? p0 : p1);
-      const uint32_t keep = th ? p1 : p0;
-      const int32_t m = pend_m0 + (NJ * wave + j) * 16 + 4 * ((lane & 15) >> 2);
-      const uint32_t off = live && k < r && m < M ? ((uint32_t)k * (uint32_t)M + (uint32_t)m) * 2u : 0x80000000u;
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{th ? r2 : keep, th ? keep : r2}, pe_rsrc, (int)off, 0, 0);
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const uint32_t h0 = pend[kb][2 * j] & 0xffffu, h1 = pend[kb][2 * j] >> 16;
+        const uint32_t h2 = pend[kb][2 * j + 1] & 0xffffu, h3 = pend[kb][2 * j + 1] >> 16;
+        // Rows of the other parity to the odd/even neighbour.
+        const uint32_t r1 = quad_x1(tl ? (h0 | (h2 << 16)) : (h1 | (h3 << 16)));
+        // Rows 4g + 2a + tl, columns of this lane pair (low half: even column).
+        const uint32_t p0 = tl ? ((r1 & 0xffffu) | (h1 << 16)) : (h0 | (r1 << 16));
+        const uint32_t p1 = tl ? ((r1 >> 16) | (h3 << 16)) : (h2 | (r1 & 0xffff0000u));
+        // Row pairs across the two lane pairs of the quad.
+        const uint32_t r2 = quad_x2(th ? p0 : p1);
+        const uint32_t keep = th ? p1 : p0;
+        const int32_t m = pend_m0 + (NJ * wave + j) * 16 + 4 * ((lane & 15) >> 2);
+        const uint32_t off =
+            live && k < lrank[kb] && m < M ? ((uint32_t)k * (uint32_t)M + (uint32_t)m) * 2u : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{th ? r2 : keep, th ? keep : r2}, pe_rsrc[kb], (int)off, 0, 0);
+      }
+      const uint32_t poff =
+          live && lane == 0 ? (uint32_t)(ODP_FT_WAVE_SLOTS * pend_tile + wave) * 8u : 0x80000000u;
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, pend_sq[kb]), part_rsrc[kb], (int)poff, 0,
+                                            0);
     }
-    const uint32_t poff = live && lane == 0 ? (uint32_t)(ODP_FT_WAVE_SLOTS * pend_tile + wave) * 8u : 0x80000000u;
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, pend_sq), part_rsrc, (int)poff, 0, 0);
     pend_m0 = -1;
   };
   // B's chunk as MFMA B operands: k-step ks covers columns 32 ks .. + 31,
@@ -866,7 +921,7 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
       (void*)W, (short)0, (int)((uint32_t)r * (uint32_t)M * 2u), ODP_BUFFER_DWORD3);
   const uint32_t wrow = (lane & 15) < r ? (uint32_t)(lane & 15) * (uint32_t)M : 0x40000000u;
 
-  u32x4_t qv;
+  u32x4_t qv[NQ];
   int buf = 0;
   if (nsteps > 0 && c_begin < c_end) load(lds, t_lo, c_begin * FP_MT, qv);
   for (int c = c_begin; c < c_end; ++c) {
@@ -877,9 +932,11 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
     int32_t tc0 = t_lo;
     __asm__ volatile("" : "+s"(tc0));
     bf16x8_t wf[FP_MT / 32];
-    f32x4_t acc[NJ][1];
+    f32x4_t acc[NJ][NKB];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) acc[j][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // One step: the next stage's loads go into `nxt` while the step reads
     // `sp`.  The two are restrict-qualified, so the compiler's scoped alias
@@ -908,11 +965,13 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
         flush();
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-      // dB rows: B operand = G columns by transposing reads, A = V.
+      // Factor rows: B operand = P columns by transposing reads, A = Q.
 #pragma unroll
       for (int u = 0; u < FP_T / 32; ++u) {
         const int tc = 32 * u + 8 * (lane >> 4);
-        const u32x4_t vv = *(const u32x4_t*)&sp[PTILE + (lane & 15) * QP + tc];
+        u32x4_t vv[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) vv[kb] = *(const u32x4_t*)&sp[PTILE + (16 * kb + (lane & 15)) * QP + tc];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const int m0 = (NJ * wave + j) * 16, cc = lane & 15;
@@ -921,8 +980,10 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
           const v4i16_t t0 = lds_tr16(src), t1 = lds_tr16(src + 4 * PP);
           const v4i16_t tt[2] = {t0, t1};
           const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, tt);
-          acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vv), bop,
-                                                              acc[j][0], 0, 0, 0);
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+            acc[j][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vv[kb]), bop,
+                                                                 acc[j][kb], 0, 0, 0);
         }
       }
       // U rows 16 wave .. + 15 of the step: A = G rows (8 consecutive
@@ -946,14 +1007,14 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
       if constexpr (st < FP_STEPS) {
         if (st < nsteps) {
           store_q(buf, tc0 + st * FP_T, qv);
-          // The stage's loads (this wave's) must have landed and its V piece
+          // The stage's loads (this wave's) must have landed and its V pieces
           // be written before the barrier.  Vector memory operations complete
           // in issue order as s_waitcnt counts them, and step 0 issues the
-          // stage's loads before B's loads and the NJ + 1 stores of the
-          // previous chunk: at step 1, vmcnt <= NJ + 1 covers the stage while
+          // stage's loads before B's loads and the NFLUSH stores of the
+          // previous chunk: at step 1, vmcnt <= NFLUSH covers the stage while
           // the stores drain.  Other steps wait for everything.
           if (st == 1)
-            __builtin_amdgcn_s_waitcnt(0x0070 | (NJ + 1));  // vmcnt(NJ + 1) lgkmcnt(0)
+            __builtin_amdgcn_s_waitcnt(0x0070 | NFLUSH);  // vmcnt(NFLUSH) lgkmcnt(0)
           else
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
           __asm__ volatile("s_barrier" ::: "memory");
@@ -1007,9 +1068,10 @@ __global__ __launch_bounds__(256, 2) void k_factor_project_bf16(const int64_t* _
                                                                 const int32_t* __restrict__ sex,
                                                                 double* __restrict__ part,
                                                                 int64_t part_stride) {
-  factor_pass_bf16<true>(probs, ws, n_prob, sstart, slen, sex, part, part_stride);
+  factor_pass_bf16<true, 1>(probs, ws, n_prob, sstart, slen, sex, part, part_stride);
 }
 
+template <int NKB>
 __global__ __launch_bounds__(256, 2) void k_factor_stream_bf16(const int64_t* __restrict__ probs,
                                                                const int32_t* __restrict__ ws, int n_prob,
                                                                const int32_t* __restrict__ sstart,
@@ -1017,7 +1079,7 @@ __global__ __launch_bounds__(256, 2) void k_factor_stream_bf16(const int64_t* __
                                                                const int32_t* __restrict__ sex,
                                                                double* __restrict__ part,
                                                                int64_t part_stride) {
-  factor_pass_bf16<false>(probs, ws, n_prob, sstart, slen, sex, part, part_stride);
+  factor_pass_bf16<false, NKB>(probs, ws, n_prob, sstart, slen, sex, part, part_stride);
 }
 
 // ---------------------------------------------------------------------------
@@ -1274,18 +1336,26 @@ extern "C" int64_t odp_seg_factor_stream_groups(int64_t M) {
 extern "C" int odp_seg_factor_stream(odp_stream_t stream, const int64_t* problems, const int32_t* work_start,
                                      int32_t n_prob, int32_t total_blocks, const int32_t* seg_row_start,
                                      const int32_t* seg_row_len, const int32_t* seg_example, double* part,
-                                     int64_t part_stride) {
+                                     int64_t part_stride, int32_t nkb) {
   int rc = odp_check_table("odp_seg_factor_stream", problems, work_start, n_prob, total_blocks);
   if (rc != ODP_OK) return rc;
+  if (nkb < 1 || nkb > 3) {
+    odp_set_error("odp_seg_factor_stream: nkb=%d outside [1, 3]", nkb);
+    return ODP_ERR_UNSUPPORTED;
+  }
   if (total_blocks == 0) return ODP_OK;
   if (seg_row_start == nullptr || seg_row_len == nullptr || seg_example == nullptr ||
       part == nullptr || part_stride <= 0) {
     odp_set_error("odp_seg_factor_stream: null segment/partial arrays or part_stride <= 0");
     return ODP_ERR_INVALID_ARGUMENT;
   }
-  hipLaunchKernelGGL(k_factor_stream_bf16, dim3(total_blocks), dim3(256), 0, odp_hip_stream(stream),
-                     problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part,
-                     part_stride);
+  hipStream_t s = odp_hip_stream(stream);
+  const dim3 grid(total_blocks), block(256);
+  switch (nkb) {
+    case 1: hipLaunchKernelGGL(k_factor_stream_bf16<1>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+    case 2: hipLaunchKernelGGL(k_factor_stream_bf16<2>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+    default: hipLaunchKernelGGL(k_factor_stream_bf16<3>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len, seg_example, part, part_stride); break;
+  }
   return odp_check_launch("odp_seg_factor_stream");
 }
 

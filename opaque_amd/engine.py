@@ -862,7 +862,7 @@ class GhostPlan:
         ft: dict[tuple, _Table] = {}
         pl = _Table(N.PL_FIELDS)
         fused_rows: list[tuple] = []
-        stream_rows: list[tuple] = []
+        stream_rows: dict[int, list[tuple]] = {}  # per rank-block count
 
         def tab(tables: dict, dt: torch.dtype, r: int, fields: int) -> _Table:
             return tables.setdefault((dt, (r + 15) // 16), _Table(fields))
@@ -963,8 +963,8 @@ class GhostPlan:
                         (valid * d_out + r * d_out + planes * r * valid) * es, 2 * valid * d_out * r,
                         io=valid * d_out * es,
                     )
-                if frow is not None and self._streamable(dt, r, v, g):
-                    self._stream_rows(frow, v, d_out, r, es, planes, s.b_leaf, stream_rows)
+                if frow is not None and self._streamable(dt, [(0, r)], v, g):
+                    self._stream_rows(frow, v, d_out, es, planes, stream_rows)
                 elif frow is not None:
                     tab(ft, dt, r, N.FT_FIELDS).add(frow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
                                                     (valid * d_out + planes * r * valid) * es + n_seg * r * d_out * es,
@@ -978,18 +978,18 @@ class GhostPlan:
                         sc = next(s.scaling for s in ch if s.a_leaf == s_leaf)
                         arow = self._a_row(x, d_in, qaddr, ubase, col0, r, ldq, sf, n_seg, sc,
                                            [(s_leaf, col0, r)], pe_off, slot_base)
-                        if self._streamable(dt, r, v, x):
-                            self._stream_rows(arow, v, d_in, r, es, planes, s_leaf, stream_rows)
+                        if self._streamable(dt, [(0, r)], v, x):
+                            self._stream_rows(arow, v, d_in, es, planes, stream_rows)
                             continue
                         tab(ft, dt, r, N.FT_FIELDS).add(
                             arow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_in, r),
                             (valid * d_in + planes * r * valid) * es + n_seg * r * d_in * es, 2 * valid * d_in * r,
                             io=valid * d_in * es)
-                elif len(a_leaves) == 1 and a_leaves[0][1] == 0 and a_leaves[0][2] == rtot \
-                        and self._streamable(dt, rtot, v, x):
+                elif self._streamable(dt, [(c, rk) for _, c, rk in a_leaves], v, x) and (rtot + 15) // 16 <= 3:
+                    # One leaf per 16-row block of U (q/k/v, gate/up at rank 16).
                     self._stream_rows(self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
                                                   a_leaves, pe_off, slot_base),
-                                      v, d_in, rtot, es, planes, a_leaves[0][0], stream_rows)
+                                      v, d_in, es, planes, stream_rows)
                 else:
                     tab(ft, dt, rtot, N.FT_FIELDS).add(
                         self._a_row(x, d_in, qaddr, ubase, 0, rtot, ldq, sf, n_seg, scal.pop(),
@@ -1004,9 +1004,11 @@ class GhostPlan:
         fp = _Table(N.FT_FIELDS)
         for _, _, row, blocks, nbytes, io, fl in sorted(fused_rows, key=lambda t: (t[0], t[1])):
             fp.add(row, blocks, nbytes, fl, io=io)
-        fst = _Table(N.FT_FIELDS)
-        for _, _, row, blocks, nbytes, io, fl in sorted(stream_rows, key=lambda t: (t[0], t[1])):
-            fst.add(row, blocks, nbytes, fl, io=io)
+        fst: dict[int, _Table] = {}
+        for nkb in sorted(stream_rows):
+            fst[nkb] = _Table(N.FT_FIELDS)
+            for _, _, row, blocks, nbytes, io, fl in sorted(stream_rows[nkb], key=lambda t: (t[0], t[1])):
+                fst[nkb].add(row, blocks, nbytes, fl, io=io)
 
         sq = _Table(N.SQ_FIELDS)
         mat_pe: dict[int, torch.Tensor] = {}
@@ -1243,7 +1245,8 @@ class GhostPlan:
         for key in sorted(pj, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("project", key, pj[key]))
         tabs.append(("factor_project", None, fp))
-        tabs.append(("factor_stream", None, fst))
+        for nkb in sorted(fst):
+            tabs.append(("factor_stream", nkb, fst[nkb]))
         for key in sorted(ft, key=lambda k: (str(k[0]), k[1])):
             tabs.append(("factor", key, ft[key]))
         tabs.append(("sqnorm", None, sq))
@@ -1660,8 +1663,8 @@ class GhostPlan:
                 N.FT_LEAF0 + 1: 0 | (r << 16) | self._pe_bits(s.b_leaf),
                 N.FT_LEAF0 + 2: slot_base[s.b_leaf],
             }
-            if self._streamable(dt, r, v, g):
-                self._stream_rows(brow, v, d_out, r, es, planes, s.b_leaf, stream_rows)
+            if self._streamable(dt, [(0, r)], v, g):
+                self._stream_rows(brow, v, d_out, es, planes, stream_rows)
             else:
                 tab(ft, dt, r, N.FT_FIELDS).add(
                     brow, n_seg * lib.odp_seg_factor_tiles(dtype_code(dt), d_out, r),
@@ -1675,30 +1678,36 @@ class GhostPlan:
         lib = N.load()
         return v.max_len <= lib.odp_factor_project_max_len() and v.max_len * g.stride(0) * 2 < 2**31
 
-    def _streamable(self, dt: torch.dtype, r: int, v: _SegView, p: torch.Tensor) -> bool:
-        """Whether a one-leaf factor problem over P runs as odp_seg_factor_stream."""
-        if not self.stream_factors or dt != torch.bfloat16 or r > 16:
+    def _streamable(self, dt: torch.dtype, leaves: list[tuple[int, int]], v: _SegView, p: torch.Tensor) -> bool:
+        """Whether a factor problem over P whose leaves sit at these (column
+        in Q, rank) pairs runs as odp_seg_factor_stream: bf16, every leaf on
+        a 16-row block of its own, segments within the kernel's length."""
+        if not self.stream_factors or dt != torch.bfloat16:
+            return False
+        if not leaves or any(c % 16 or rk > 16 for c, rk in leaves):
             return False
         lib = N.load()
         return v.max_len <= lib.odp_factor_project_max_len() and v.max_len * p.stride(0) * 2 < 2**31
 
-    def _stream_rows(self, row: dict, v: _SegView, M: int, r: int, es: int, planes: int, leaf: int,
-                     out: list) -> None:
-        """A one-leaf factor problem as odp_seg_factor_stream rows: one per
-        segment, its pe rows at the segment's own offset, so that the launch
+    def _stream_rows(self, row: dict, v: _SegView, M: int, es: int, planes: int, out: dict) -> None:
+        """A factor problem as odp_seg_factor_stream rows: one per segment,
+        each leaf's pe rows at the segment's own offset, so that the launch
         can run the most work per workgroup first."""
         lib = N.load()
-        pe0 = self._pe_addr(leaf)
+        r = int(row[N.FT_R])
         pe_es = self.pe[torch.bfloat16].element_size()
         groups = int(lib.odp_seg_factor_stream_groups(M))
+        ranks = [(row[N.FT_LEAF0 + 3 * li + 1] >> 16) & 0xFFFF for li in range(int(row[N.FT_NLEAF]))]
+        lst = out.setdefault((r + 15) // 16, [])
         for j, ln in enumerate(v.segs.lengths):
             rj = dict(row)
             rj[N.FT_SEG_FIRST] = v.first + j
             rj[N.FT_NSEG] = 1
-            rj[N.FT_LEAF0] = pe0 + j * r * M * pe_es
+            for li, rk in enumerate(ranks):
+                rj[N.FT_LEAF0 + 3 * li] = row[N.FT_LEAF0 + 3 * li] + j * rk * M * pe_es
             rj[N.FT_GROUPS] = groups
-            out.append((-ln * M / groups, len(out), rj, groups, (ln * M + planes * r * ln) * es + r * M * es, ln * M * es,
-                        2 * ln * M * r))
+            lst.append((-ln * M / groups, len(lst), rj, groups,
+                        (ln * M + planes * r * ln) * es + sum(ranks) * M * es, ln * M * es, 2 * ln * M * r))
 
     def _a_row(self, x, d_in, qaddr, ubase, col0, r, ldq, seg_first, n_seg, scaling, leaves, pe_off, slot_base):
         row = {
@@ -1796,7 +1805,7 @@ class GhostPlan:
                 N.check(lib.odp_seg_factor_stream(s, probs.data_ptr(), ws.data_ptr(), n, total,
                                                   self.seg_start.data_ptr(), self.seg_len.data_ptr(),
                                                   self.seg_ex.data_ptr(), self.part.data_ptr(),
-                                                  self.n_slots), name)
+                                                  self.n_slots, dt), name)
             elif name == "factor":
                 N.check(lib.odp_seg_factor(s, dtype_code(dt[0]), probs.data_ptr(), ws.data_ptr(), n, total,
                                            self.seg_start.data_ptr(), self.seg_len.data_ptr(),

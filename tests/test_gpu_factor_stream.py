@@ -1,17 +1,19 @@
 """The streamed factor pass (odp_seg_factor_stream) against the tiled one
-(odp_seg_factor with one rank block).
+(odp_seg_factor with the same number of rank blocks).
 
-Both form a one-leaf problem's per-example rows pe[k][m] = scaling *
-sum_t Q[k][t] P[t][m] from the same 32-token MFMA blocks in the same order,
-then square and store the same bf16 values into the same partial slots, so
-every output of a plan must be bit-identical with the streamed pass on and
-off: per-example rows, norms, scales, clip masks and clipped sums.  Covered:
-dB rows from G and V, dA rows from X and U (a one-site activation, and the
-per-site rows of sites with different scalings), the mirrored order of a
-down projection, sites bringing the seam's V and U, widths that split a
-segment's tiles into several groups with a partial last tile, empty,
-single-row, longest and unaligned segments, and a segment past the length
-limit (that site then keeps the tiled pass).
+Both form a problem's per-example rows pe[k][m] = scaling * sum_t Q[k][t]
+P[t][m] from the same 32-token MFMA blocks in the same order, then square
+and store the same bf16 values into the same partial slots, so every output
+of a plan must be bit-identical with the streamed pass on and off:
+per-example rows, norms, scales, clip masks and clipped sums.  Covered: dB
+rows from G and V, dA rows from X and U (a one-site activation, the per-site
+rows of sites with different scalings, and activations shared by two or
+three sites of rank 16, one of them with a frozen A: a rank block without a
+leaf), the mirrored order of a down projection, sites bringing the seam's V
+and U, widths that split a segment's tiles into several groups with a
+partial last tile, empty, single-row, longest and unaligned segments, and
+the cases that keep the tiled pass (leaves off the 16-row blocks, a segment
+past the length limit).
 """
 
 from __future__ import annotations
@@ -95,6 +97,9 @@ CASES = [
     (4, 80, [80, 33, 1, 64], 520, [136], [16], ()),                # mirrored: d_in > d_out
     (3, 200, [200, 0, 57], 264, [4360], [16], ()),                 # 18 tiles: two groups, partial last
     (2, 129, [129, 88], 4360, [8200], [16], ()),                   # dA over 18 tiles, dB over 33 (three groups)
+    (3, 128, [128, 77, 0], 256, [256, 64, 64], [16, 16, 16], ()),  # q/k/v: dA in three rank blocks
+    (3, 128, [128, 5, 90], 256, [256, 64, 64], [16, 16, 8], ((1, "A"),)),  # a rank block without a leaf
+    (3, 96, [96, 50, 3], 128, [512, 512], [16, 8], ()),            # gate/up: two rank blocks, rank 8 last
 ]
 
 
@@ -152,6 +157,6 @@ def test_seam_products(shared):
                                 v=v.contiguous(), u=u.contiguous()))
     on = _compare(seg, with_vu, leaves)
     live = {t[0] for t in on.tables if t[5] > 0}
-    assert "planes" in live and not live & {"project", "factor_project"}, live
-    if not shared:
-        assert "factor" not in live, live
+    assert "planes" in live and not live & {"project", "factor_project", "factor"}, live
+    keys = {t[1] for t in on.tables if t[0] == "factor_stream" and t[5] > 0}
+    assert keys == ({1, 3} if shared else {1}), keys
