@@ -261,7 +261,16 @@ __host__ __device__ constexpr int64_t gram_items(int64_t nb) {
 
 static_assert(GR_K == 32, "one 32-bit column-mask word per Gram step");
 
+// Rows are 64 bytes (four 16-byte slots); slot k of row r lives at slot
+// k ^ gr_swz(r).  An MFMA operand read (ds_read_b128) takes slot kq of 16
+// consecutive rows per 16 lanes.  Measured with SQ_LDS_BANK_CONFLICT on
+// gfx950: this swizzle reads at full rate, while (r >> 2) & 3, no swizzle,
+// and ((r >> 1) ^ (r >> 3)) & 3 all take twice the LDS cycles per read.
+#ifdef ODP_GR_SWZ_ROW4
 __device__ __forceinline__ int gr_swz(int row) { return (row >> 2) & 3; }
+#else
+__device__ __forceinline__ int gr_swz(int row) { return (row >> 1) & 3; }
+#endif
 __device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ gr_swz(row)); }
 
 __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restrict__ probs,
