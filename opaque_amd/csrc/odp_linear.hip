@@ -242,9 +242,8 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_outer_norm_g
 // G).  The 384 rows x 32 features of a step arrive by buffer loads straight
 // into a ring of GR_RING LDS stages (GR_RING - 1 steps in flight), the X
 // steps then the G steps as one sequence.  Rows past the segment and
-// features past d arrive as zeros.  Rows are 64 bytes; the 16-byte slot k
-// of row r sits at k ^ ((r >> 2) & 3), which spreads the 16 rows of a
-// fragment read over the LDS banks.
+// features past d arrive as zeros.  Rows are 64 bytes, swizzled in 16-byte
+// slots by gr_swz below.
 // ---------------------------------------------------------------------------
 constexpr int GR_K = 32;                   // features per step
 constexpr int GR_ROWS = 3 * LT;            // t block + two s blocks
@@ -266,11 +265,7 @@ static_assert(GR_K == 32, "one 32-bit column-mask word per Gram step");
 // consecutive rows per 16 lanes.  Measured with SQ_LDS_BANK_CONFLICT on
 // gfx950: this swizzle reads at full rate, while (r >> 2) & 3, no swizzle,
 // and ((r >> 1) ^ (r >> 3)) & 3 all take twice the LDS cycles per read.
-#ifdef ODP_GR_SWZ_ROW4
-__device__ __forceinline__ int gr_swz(int row) { return (row >> 2) & 3; }
-#else
 __device__ __forceinline__ int gr_swz(int row) { return (row >> 1) & 3; }
-#endif
 __device__ __forceinline__ int gr_at(int row, int slot) { return row * GR_K + 8 * (slot ^ gr_swz(row)); }
 
 __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restrict__ probs,
