@@ -670,7 +670,7 @@ constexpr int FP_G_NT = 2;
 // split into groups of at most this many, so that the widest rows do not
 // leave a tail of long workgroups.
 #ifndef ODP_FS_GROUP
-#define ODP_FS_GROUP 8  // 4-12 measured alike on C3, 16 and wider slower
+#define ODP_FS_GROUP 4  // C3: 4 best for three rank blocks (6 % over 8), 4-12 alike for one, 16+ slower
 #endif
 __host__ __device__ constexpr int fs_groups(int nchunks) {
   return nchunks <= 0 ? 1 : (nchunks + ODP_FS_GROUP - 1) / ODP_FS_GROUP;
@@ -1197,51 +1197,81 @@ extern "C" int odp_pack_factors(odp_stream_t stream, const int64_t* problems, co
 }
 
 // ---------------------------------------------------------------------------
-// Rank-space products from the seam laid out as planes: one thread per row,
-// writing column k of its row to plane row k (each plane row coalesced
-// across the workgroup's threads); rows outside the segments get 0.
+// Rank-space products from the seam laid out as planes.  A workgroup takes
+// PL_THREADS consecutive rows, PL_K columns at a time: each thread reads its
+// row's columns (16-byte loads where rows are aligned), the block is
+// transposed through LDS, and each plane row leaves as 16-byte pieces of
+// consecutive rows.  Rows outside the segments get 0.
 // ---------------------------------------------------------------------------
 constexpr int PL_THREADS = 256;
+constexpr int PL_K = 16;  // plane rows per pass
 
 template <typename T>
-__device__ __forceinline__ void pack_plane_row(const T* __restrict__ s, T* __restrict__ d, int r, int64_t ldq,
-                                               bool in, bool vec) {
-  constexpr int V = 16 / sizeof(T);  // elements per 16-byte load
-  if (in && vec) {
-    for (int k0 = 0; k0 < r; k0 += V) {
-      const u32x4_t w = *(const ODP_GLOBAL u32x4_t*)(const ODP_GLOBAL void*)(s + k0);
-      T e[V];
-      __builtin_memcpy(e, &w, 16);
+__device__ __forceinline__ void pack_planes_tile(const T* __restrict__ src, int64_t lds, T* __restrict__ dst,
+                                                 int64_t ldq, int r, int64_t row0, int64_t n_rows, bool in,
+                                                 T* __restrict__ tile) {
+  constexpr int V = 16 / sizeof(T);       // elements per 16-byte piece
+  constexpr int TP = PL_THREADS + V;       // LDS pitch of a plane row
+  constexpr int PIECES = PL_THREADS / V;   // 16-byte pieces per plane row
+  const int t = threadIdx.x;
+  const T* s = src + (row0 + t) * lds;
+  const bool vec = (((uintptr_t)src | (uintptr_t)(lds * (int64_t)sizeof(T))) & 15) == 0;
+  const bool dvec = (((uintptr_t)dst | (uintptr_t)(ldq * (int64_t)sizeof(T))) & 15) == 0;
+  for (int k0 = 0; k0 < r; k0 += PL_K) {
+    T e[PL_K];
+    if (in && vec && k0 + PL_K <= r) {
 #pragma unroll
-      for (int i = 0; i < V; ++i) odp_gstore(d + (int64_t)(k0 + i) * ldq, e[i]);
+      for (int q = 0; q < PL_K / V; ++q) {
+        const u32x4_t w = ld16(s + k0 + q * V);
+        __builtin_memcpy(e + q * V, &w, 16);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < PL_K; ++c) e[c] = in && k0 + c < r ? s[k0 + c] : (T)0;
     }
-    return;
+    if (k0 > 0) __syncthreads();  // the previous pass has read the tile
+#pragma unroll
+    for (int c = 0; c < PL_K; ++c) tile[c * TP + t] = e[c];
+    __syncthreads();
+#pragma unroll
+    for (int i = t; i < PL_K * PIECES; i += PL_THREADS) {
+      const int c = i / PIECES, pc = i % PIECES;
+      const int64_t r0 = row0 + (int64_t)pc * V;
+      if (k0 + c >= r || r0 >= n_rows) continue;
+      T* d = dst + (int64_t)(k0 + c) * ldq + r0;
+      const T* sp = tile + c * TP + pc * V;
+      if (dvec && r0 + V <= n_rows) {
+        u32x4_t w;
+        __builtin_memcpy(&w, sp, 16);
+        odp_gstore((u32x4_t*)d, w);
+      } else {
+        for (int q = 0; q < V && r0 + q < n_rows; ++q) odp_gstore(d + q, sp[q]);
+      }
+    }
   }
-  for (int k = 0; k < r; ++k) odp_gstore(d + (int64_t)k * ldq, in ? s[k] : (T)0);
 }
 
 __global__ __launch_bounds__(PL_THREADS) void k_pack_planes(const int64_t* __restrict__ probs,
                                                             const int32_t* __restrict__ ws, int n_prob,
                                                             const int32_t* __restrict__ sstart,
                                                             const int32_t* __restrict__ slen) {
+  __shared__ __attribute__((aligned(16))) uint32_t tile[PL_K * (PL_THREADS + 4)];  // f32: pitch 260
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
   const int64_t* f = probs + (int64_t)p * ODP_PL_FIELDS;
-  const int64_t row = (int64_t)(bid - ws[p]) * PL_THREADS + threadIdx.x;
-  if (row >= f[ODP_PL_NROWS]) return;
+  const int64_t n_rows = f[ODP_PL_NROWS];
+  const int64_t row0 = (int64_t)(bid - ws[p]) * PL_THREADS, row = row0 + threadIdx.x;
   const int seg_first = (int)f[ODP_PL_SEG_FIRST];
-  const bool in = odp_row_in_segments(row, sstart + seg_first, slen + seg_first, (int)f[ODP_PL_NSEG]);
+  const bool in = row < n_rows &&
+                  odp_row_in_segments(row, sstart + seg_first, slen + seg_first, (int)f[ODP_PL_NSEG]);
   const int64_t lds = f[ODP_PL_LDS], ldq = f[ODP_PL_LDQ];
   const int r = (int)f[ODP_PL_R];
-  const uintptr_t src = (uintptr_t)f[ODP_PL_SRC];
-  if (f[ODP_PL_DTYPE] == ODP_DTYPE_BF16) {
-    // 16-byte loads when every row starts 16-byte aligned and r fills them.
-    const bool vec = ((src | (uintptr_t)(lds * 2)) & 15) == 0 && (r & 7) == 0;
-    pack_plane_row((const uint16_t*)src + row * lds, (uint16_t*)f[ODP_PL_DST] + row, r, ldq, in, vec);
-  } else {
-    const bool vec = ((src | (uintptr_t)(lds * 4)) & 15) == 0 && (r & 3) == 0;
-    pack_plane_row((const float*)src + row * lds, (float*)f[ODP_PL_DST] + row, r, ldq, in, vec);
-  }
+  if (f[ODP_PL_DTYPE] == ODP_DTYPE_BF16)
+    pack_planes_tile((const uint16_t*)f[ODP_PL_SRC], lds, (uint16_t*)f[ODP_PL_DST], ldq, r, row0, n_rows, in,
+                     (uint16_t*)tile);
+  else
+    pack_planes_tile((const float*)f[ODP_PL_SRC], lds, (float*)f[ODP_PL_DST], ldq, r, row0, n_rows, in,
+                     (float*)tile);
 }
 
 extern "C" int64_t odp_pack_planes_blocks(int64_t n_rows) {

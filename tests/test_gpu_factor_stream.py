@@ -95,8 +95,8 @@ CASES = [
     (4, 40, [40, 39, 17, 25], 96, [1000, 200], [12, 4], ()),       # two sites on one X: dA stays tiled
     (3, 64, [64, 50, 9], 128, [256, 136], [8, 8], ((0, "B"), (1, "A"))),  # frozen factors
     (4, 80, [80, 33, 1, 64], 520, [136], [16], ()),                # mirrored: d_in > d_out
-    (3, 200, [200, 0, 57], 264, [4360], [16], ()),                 # 18 tiles: two groups, partial last
-    (2, 129, [129, 88], 4360, [8200], [16], ()),                   # dA over 18 tiles, dB over 33 (three groups)
+    (3, 200, [200, 0, 57], 264, [4360], [16], ()),                 # 18 tiles in several groups, partial last
+    (2, 129, [129, 88], 4360, [8200], [16], ()),                   # dA over 18 tiles, dB over 33 (uneven groups)
     (3, 128, [128, 77, 0], 256, [256, 64, 64], [16, 16, 16], ()),  # q/k/v: dA in three rank blocks
     (3, 128, [128, 5, 90], 256, [256, 64, 64], [16, 16, 8], ((1, "A"),)),  # a rank block without a leaf
     (3, 96, [96, 50, 3], 128, [512, 512], [16, 8], ()),            # gate/up: two rank blocks, rank 8 last
