@@ -160,6 +160,11 @@ def test_kernel_argument_checks(lib):
          N.ERR_UNSUPPORTED, "nkb=0")
     _err(lib, lib.odp_seg_factor_project(None, _BAD, _BAD, 1, 1, None, None, None, None, 1),
          N.ERR_INVALID_ARGUMENT, "null segment")
+    _err(lib, lib.odp_seg_factor_stream(None, _BAD, _BAD, 1, 1, None, None, None, None, 1, 1),
+         N.ERR_INVALID_ARGUMENT, "null segment")
+    _err(lib, lib.odp_seg_factor_stream(None, _BAD, _BAD, 1, 1, _BAD, _BAD, _BAD, _BAD, 1, 4),
+         N.ERR_UNSUPPORTED, "nkb=4")
+    _err(lib, lib.odp_pack_planes(None, _BAD, _BAD, 1, 1, None, None), N.ERR_INVALID_ARGUMENT, "null segment")
     _err(lib, lib.odp_linear_sqnorm(None, 9, None, None, 0, 0, None, None, None, None, 1),
          N.ERR_INVALID_ARGUMENT, "unknown form 9")
     _err(lib, lib.odp_scale_sum(None, None, None, 0, 0, None, None, 1, 1, 0.0), N.ERR_INVALID_ARGUMENT,
