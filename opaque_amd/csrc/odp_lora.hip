@@ -33,14 +33,19 @@ namespace {
 #ifndef ODP_FT_T
 #define ODP_FT_T 32  // tokens per bf16 factor step (a multiple of the MFMA K, 32)
 #endif
+#ifndef ODP_PJ_RPW_2
+#define ODP_PJ_RPW_2 3  // 16-row blocks per wave for two rank blocks (W re-read per workgroup)
+#endif
 #ifndef ODP_PJ_RPW_WIDE
-#define ODP_PJ_RPW_WIDE 2  // 16-row blocks per wave for rank blocks >= 2 (W re-read per workgroup)
+#define ODP_PJ_RPW_WIDE 2  // ... and for three or four
 #endif
 constexpr int PJ_ROWS = 64;   // rows per fp32 project workgroup (4 waves x 16)
 // bf16 projection: 16-row MFMA blocks per wave.  One block for rank <= 16
 // (two measured slower there); wider ranks re-read a larger W tile per
-// workgroup, so they take more rows per workgroup.
-__host__ __device__ constexpr int pj_rpw(int nkb) { return nkb >= 2 ? ODP_PJ_RPW_WIDE : 1; }
+// workgroup, so they take more rows per workgroup: three blocks per wave for
+// two rank blocks (C3 gate/up V: 0.60-0.63 -> 0.52-0.53 ms against two; four
+// slower), two for three rank blocks (three and four no faster).
+__host__ __device__ constexpr int pj_rpw(int nkb) { return nkb == 2 ? ODP_PJ_RPW_2 : nkb > 2 ? ODP_PJ_RPW_WIDE : 1; }
 constexpr int FT_T = ODP_FT_T;
 constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 
@@ -72,6 +77,13 @@ __device__ __forceinline__ u32x4_t ld16_nt(const void* p) {
 // column i of 4 consecutive rows: the K-contiguous MFMA operand layout.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 #define ODP_LDS __attribute__((address_space(3)))
+
+// LDS row pitch, in bf16 elements, for tiles whose MFMA operands are read
+// as 16-byte pieces of 16 consecutive rows at one column (ds_read_b128):
+// measured on gfx950 (SQ_LDS_BANK_CONFLICT), such a read runs at full rate
+// when the pitch is an odd multiple of 32 bytes and at half rate otherwise
+// (e.g. 80, 144 or 272 bytes).  The smallest such pitch >= `cols`.
+__host__ __device__ constexpr int lds_pitch(int cols) { return ((cols + 15) / 32) * 32 + 16; }
 __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((ODP_LDS v4i16_t*)(ODP_LDS void*)p);
 }
@@ -90,7 +102,7 @@ __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
 // extra loads in flight measured 1-5 % faster (one rank block of the factor
 // kernel: no difference, left to the compiler; three rank blocks: two
 // workgroups, the registers of a 256-wide tile without spills).
-__host__ __device__ constexpr int pj_min_blocks(int nkb) { return nkb == 1 ? 6 : nkb == 2 ? 3 : 1; }
+__host__ __device__ constexpr int pj_min_blocks(int nkb) { return nkb == 1 ? 6 : nkb == 2 ? 2 : 1; }
 __host__ __device__ constexpr int ft_min_blocks(int nkb) { return nkb == 2 ? 3 : nkb == 3 ? 2 : 1; }
 
 template <int NKB>
@@ -98,6 +110,9 @@ __global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const 
                                                       const int32_t* __restrict__ ws, int n_prob,
                                                       const int32_t* __restrict__ sstart,
                                                       const int32_t* __restrict__ slen) {
+  // Pitch KS + 8 (272 bytes): its operand reads take two LDS passes, but the
+  // conflict-free lds_pitch(KS) measured no faster here (and fits six
+  // one-block workgroups per CU only with this one).
   constexpr int KS = ODP_PJ_KS, WPITCH = KS + 8, PPITCH = KS + 8, RP = 16 * NKB;
   constexpr int RB = pj_rpw(NKB), WR = 16 * RB;  // row blocks and rows per wave
   constexpr int NPR = RB * KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
@@ -503,7 +518,7 @@ __global__ __launch_bounds__(256, ft_min_blocks(NKB)) void k_factor_bf16(const i
                                                      const int32_t* __restrict__ sex,
                                                      double* __restrict__ part, int64_t part_stride) {
   constexpr int NJ = ft_nj(NKB), MT = 64 * NJ, PP = MT;  // unpadded, XOR-swizzled rows
-  constexpr int QP = FT_T + 8, QROWS = 16 * NKB;
+  constexpr int QP = lds_pitch(FT_T), QROWS = 16 * NKB;
   constexpr int PTILE = FT_T * PP, STAGE = PTILE + QROWS * QP;
   constexpr int NPP = NJ * FT_T / 32;             // P pieces per thread per step
   constexpr int QPC = FT_T / 8;                   // Q pieces per row per step
@@ -694,7 +709,7 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
                                                  double* __restrict__ part, int64_t part_stride) {
   static_assert(NKB >= 1 && NKB <= 3 && (!PROJ || NKB == 1), "one to three rank blocks; the fused G side has one");
   constexpr int NJ = FP_MT / 64, PP = FP_MT;  // unpadded, XOR-swizzled G rows
-  constexpr int QP = FP_T + 8, QROWS = 16 * NKB;
+  constexpr int QP = lds_pitch(FP_T), QROWS = 16 * NKB;
   constexpr int PTILE = FP_T * PP, STAGE = PTILE + QROWS * QP;
   constexpr int QPC = FP_T / 8;                  // V pieces per row per step
   constexpr int NQP = QPC * QROWS;               // V pieces per step: 128 per rank block
