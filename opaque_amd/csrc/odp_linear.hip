@@ -466,25 +466,39 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram_norm(const int64_t* __restr
 // Gram form over 256-row blocks (ODP_FORM_GRAM256).  Item (tb, sb), tb <= sb,
 // of a segment pairs the t block (rows 256 tb ..) with the s block (rows
 // 256 sb ..); eight waves in 2 x 4 each own 128 x 64 of the 256 x 256 block
-// pair, as in the outer-form kernels, and a step moves 512 rows x 64 bytes
-// into LDS: 128 flop per byte loaded against 87 for the 128 x 256 pairs of
-// k_lin_gram_norm, whose loads into LDS bound it.  The two Gram blocks of a
+// pair, as in the outer-form kernels, and a step moves 512 rows x G2_K
+// features into LDS: 128 flop per byte loaded against 87 for the 128 x 256
+// pairs of k_lin_gram_norm, whose loads into LDS bound it.  With 64
+// features per step each row piece is a whole 128-byte line (32 features
+// fetched every line twice, doubling the L2 requests per flop), in a ring
+// of two 64 KB stages.  The two Gram blocks of a
 // 256 x 256 pair do not fit in registers together, so the X block
 // P = X_t X_s^T is accumulated first and written to the item's fp32 scratch
 // in register order (each lane its own 16-byte pieces, 1 KB per wave and
 // block), then G's block Q is accumulated and the item's partial
 // sum_{t,s} P Q is formed against the scratch read back by the same lanes.
 // A diagonal item (tb == sb) loads its rows once and reads both operands
-// from them.  Same row swizzle, non-finite column handling and work order
-// as k_lin_gram_norm.
+// from them.  Same non-finite column handling and work order as
+// k_lin_gram_norm.
 // ---------------------------------------------------------------------------
+#ifndef ODP_G2_K
+#define ODP_G2_K 64  // features per step: 64 (128-byte rows, two stages) or 32 (64-byte rows, four)
+#endif
 constexpr int G2_B = 256;                                 // rows per block
 constexpr int G2_ROWS = 2 * G2_B;                         // t block + s block
-constexpr int G2_STAGE = G2_ROWS * GR_K;                  // elements (32 KB)
-constexpr int G2_RING = 4;
-constexpr int G2_LOADS = G2_ROWS * GR_K * 2 / 1024 / 8;  // 1 KB loads per wave per step
+constexpr int G2_K = ODP_G2_K;
+constexpr int G2_SLOTS = G2_K / 8;                        // 16-byte slots per row
+constexpr int G2_STAGE = G2_ROWS * G2_K;                  // elements (64 or 32 KB)
+constexpr int G2_RING = G2_K == 64 ? 2 : 4;               // 128 KB of LDS either way
+constexpr int G2_LOADS = G2_ROWS * G2_K * 2 / 1024 / 8;   // 1 KB loads per wave per step
+constexpr int G2_RPL = 64 / G2_SLOTS;                     // rows per load
+constexpr int G2_WORDS = G2_K / 32;                       // column-mask words per step
 constexpr int64_t G2_SCRATCH = (int64_t)G2_B * G2_B;      // floats per (segment, item)
-static_assert(G2_LOADS == 4, "four loads per wave per step");
+static_assert((G2_K == 32 || G2_K == 64) && G2_LOADS * G2_RPL == 64, "each wave loads 64 rows per step");
+// Slot k of row r at k ^ g2_swz(r): 16 rows read at one slot hit the LDS at
+// full rate (measured; for 64-byte rows as gr_swz).
+__device__ __forceinline__ int g2_swz(int row) { return (row >> 1) & (G2_SLOTS - 1); }
+__device__ __forceinline__ int g2_at(int row, int slot) { return row * G2_K + 8 * (slot ^ g2_swz(row)); }
 
 __host__ __device__ constexpr int64_t gram2_items(int64_t nb) { return nb * (nb + 1) / 2; }
 
@@ -496,10 +510,9 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
                                                               double* __restrict__ part, int64_t part_stride) {
   __shared__ __attribute__((aligned(16))) uint16_t q0[G2_STAGE];
   __shared__ __attribute__((aligned(16))) uint16_t q1[G2_STAGE];
-  __shared__ __attribute__((aligned(16))) uint16_t q2[G2_STAGE];
-  __shared__ __attribute__((aligned(16))) uint16_t q3[G2_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t q2[G2_RING > 2 ? G2_STAGE : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t q3[G2_RING > 2 ? G2_STAGE : 8];
   __shared__ double red[8];
-  static_assert(G2_RING == 4, "four ring stages");
   auto stage = [&](int k) -> uint16_t* { return k == 0 ? q0 : k == 1 ? q1 : k == 2 ? q2 : q3; };
   const int bid = blockIdx.x;
   const int p = odp_find_problem(ws, n_prob, bid);
@@ -544,15 +557,15 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
   }
 
   // Stage rows 0..255: block tb; 256..511: block sb (not loaded for a
-  // diagonal item).  Wave w loads rows 64 w .. + 63, 16 per load.
+  // diagonal item).  Wave w loads rows 64 w .. + 63, G2_RPL per load.
   uint32_t lbase[G2_LOADS];
   int lslot[G2_LOADS];
   bool lload[G2_LOADS];
 #pragma unroll
   for (int i = 0; i < G2_LOADS; ++i) {
-    const int row = 64 * wave + 16 * i + (lane >> 2);
+    const int row = 64 * wave + G2_RPL * i + lane / G2_SLOTS;
     lbase[i] = (uint32_t)((row < G2_B ? tb : sb) * G2_B + (row & (G2_B - 1)));
-    lslot[i] = (lane & 3) ^ gr_swz(row);
+    lslot[i] = (lane % G2_SLOTS) ^ g2_swz(row);
     lload[i] = row < G2_B || !diag;
   }
   const uint32_t nrow = (uint32_t)len;
@@ -560,7 +573,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
       (void*)(P.X + (int64_t)t_begin * P.ldx), (short)0, (int)(nrow * (uint32_t)P.ldx * 2u), LIN_BUF_DWORD3);
   const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(P.G + (int64_t)t_begin * P.ldg), (short)0, (int)(nrow * (uint32_t)P.ldg * 2u), LIN_BUF_DWORD3);
-  const int nx = (int)((P.d_in + GR_K - 1) / GR_K), ng = (int)((P.d_out + GR_K - 1) / GR_K);
+  const int nx = (int)((P.d_in + G2_K - 1) / G2_K), ng = (int)((P.d_out + G2_K - 1) / G2_K);
   const int px = (nx + G2_RING - 1) / G2_RING * G2_RING;
   const int total = px + (ng + G2_RING - 1) / G2_RING * G2_RING;
   const uint32_t ldx = (uint32_t)P.ldx, ldg = (uint32_t)P.ldg;
@@ -569,7 +582,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
   auto issue = [&](uint16_t* st, int x) __attribute__((always_inline)) {
     const bool isx = x < px;
     const int32_t kx = isx ? x : x - px;
-    const int32_t k0 = kx * GR_K;
+    const int32_t k0 = kx * G2_K;
     const int32_t d = x < total && kx < (isx ? nx : ng) ? (isx ? din : dout) : 0;
     const uint32_t ld = isx ? ldx : ldg;
     const __amdgpu_buffer_rsrc_t rs = isx ? xr : gr;
@@ -578,8 +591,8 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
       const int32_t col = k0 + 8 * lslot[i];
       const uint32_t o = (lbase[i] * ld + (uint32_t)col) * 2u;
       const uint32_t off = col < d && lload[i] ? o : LIN_OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (ODP_LDS void*)(st + (64 * wave + 16 * i) * GR_K), 16, off, 0,
-                                               0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (ODP_LDS void*)(st + (64 * wave + G2_RPL * i) * G2_K), 16, off,
+                                               0, 0, 0);
     }
   };
 
@@ -588,22 +601,28 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
   const int wt = 128 * (wave & 1), wsr = (diag ? 0 : G2_B) + 64 * (wave >> 1);
   f32x4_t acc[8][4];
   zero_acc(acc);
+  // One step: G2_K / 32 MFMA K blocks in feature order (the same order of
+  // 32-feature blocks whatever G2_K, so results do not depend on it).
   auto compute = [&](const uint16_t* st, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
-    const int r = lane & 15, kq = lane >> 4;
-    bf16x8_t b[4];
+    const int r = lane & 15;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wsr + 16 * j + r, kq)]);
-    // A fragments stream one ahead of the MFMAs that consume them.
-    bf16x8_t a[2];
-    a[0] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wt + r, kq)]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i + 1 < 8)
-        a[(i + 1) & 1] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[gr_at(wt + 16 * (i + 1) + r, kq)]);
+    for (int h = 0; h < G2_K / 32; ++h) {
+      const int kq = 4 * h + (lane >> 4);
+      bf16x8_t b[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i & 1], b[j], acc[i][j], 0, 0, 0);
+        b[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[g2_at(wsr + 16 * j + r, kq)]);
+      // A fragments stream one ahead of the MFMAs that consume them.
+      bf16x8_t a[2];
+      a[0] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[g2_at(wt + r, kq)]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i + 1 < 8)
+          a[(i + 1) & 1] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)&st[g2_at(wt + 16 * (i + 1) + r, kq)]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i & 1], b[j], acc[i][j], 0, 0, 0);
+      }
     }
   };
   auto step = [&](uint16_t* __restrict__ nxt, const uint16_t* __restrict__ cur, int x, bool live,
@@ -611,12 +630,14 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
     issue(nxt, x);
     if (live) compute(cur, acc);
   };
-  auto zero_features = [&](uint16_t* st, uint32_t word) __attribute__((always_inline)) {
-    const int fc = threadIdx.x & 31;
-    if ((word >> fc) & 1u)
-      for (int r = threadIdx.x >> 5; r < G2_ROWS; r += 16) st[gr_at(r, fc >> 3) + (fc & 7)] = 0;
+  // Zeroes the step's masked features (bit f of word w: feature 32 w + f).
+  auto zero_features = [&](uint16_t* st, const uint32_t (&word)[G2_WORDS]) __attribute__((always_inline)) {
+    const int fc = threadIdx.x % G2_K;
+    if ((word[fc >> 5] >> (fc & 31)) & 1u)
+      for (int r = threadIdx.x / G2_K; r < G2_ROWS; r += 512 / G2_K) st[g2_at(r, fc >> 3) + (fc & 7)] = 0;
   };
-  auto phase = [&](int lo, int hi, int live, const uint32_t* mask, f32x4_t(&acc)[8][4]) __attribute__((always_inline)) {
+  auto phase = [&](int lo, int hi, int live, const uint32_t* mask, int mwords, f32x4_t(&acc)[8][4])
+      __attribute__((always_inline)) {
     for (int g0 = lo; g0 < hi; g0 += G2_RING) {
 #pragma unroll
       for (int k = 0; k < G2_RING; ++k) {
@@ -624,8 +645,15 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
         __builtin_amdgcn_s_waitcnt(vmcnt_imm((G2_RING - 2) * G2_LOADS));
         __asm__ volatile("s_barrier" ::: "memory");
         if (fix && mask != nullptr && g - lo < live) {
-          const uint32_t word = mask[g - lo];
-          if (word != 0u) {
+          uint32_t word[G2_WORDS];
+          uint32_t any = 0u;
+#pragma unroll
+          for (int w = 0; w < G2_WORDS; ++w) {
+            const int wi = G2_WORDS * (g - lo) + w;
+            word[w] = wi < mwords ? mask[wi] : 0u;
+            any |= word[w];
+          }
+          if (any != 0u) {
             zero_features(stage(k), word);
             __syncthreads();
           }
@@ -636,7 +664,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
   };
 #pragma unroll
   for (int x = 0; x < G2_RING - 1; ++x) issue(stage(x), x);
-  phase(0, px, nx, xm, acc);
+  phase(0, px, nx, xm, xw, acc);
   // P leaves in register order; lane l of wave w holds block (i, j) at
   // ((w * 8 + i) * 4 + j) * 64 + l (16 bytes each).
   f32x4_t ODP_GLOBAL* sp = (f32x4_t ODP_GLOBAL*)(ODP_GLOBAL void*)scr + wave * 8 * 4 * 64 + lane;
@@ -648,7 +676,7 @@ __global__ __launch_bounds__(512, 1) void k_lin_gram2_norm(const int64_t* __rest
       acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
   __asm__ volatile("" ::: "memory");  // P is read back from memory, not kept live
-  phase(px, total, ng, gm, acc);
+  phase(px, total, ng, gm, gw, acc);
   __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
 
   // P comes back four pieces at a time (the fence keeps the compiler from

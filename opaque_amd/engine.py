@@ -250,8 +250,8 @@ GRAM256_MIN_LEN = 512
 GRAM256_SCRATCH_BYTES = 32 << 30
 GRAM256_ITEM_BYTES = 256 * 256 * 4
 # Its time per flop relative to the outer form, measured on MI355X (C4
-# gate/up/down at 4096 tokens: 1010 vs 1209 TFLOP/s).
-GRAM256_FLOP_COST = 1.2
+# gate/up/down at 4096 tokens: 1090 vs 1233-1262 TFLOP/s).
+GRAM256_FLOP_COST = 1.15
 
 
 def split_budget(avail: int | None, stored: int, prescale_bytes: int) -> tuple[int, int]:
