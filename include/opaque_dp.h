@@ -206,8 +206,9 @@ int odp_seg_factor(odp_stream_t stream, int dtype, const int64_t* problems,
  * fields below; one workgroup per segment (total blocks = sum of n_seg).
  * U is written for the rows of the segments only, as odp_project's planes
  * (same ldq as Q).  Segments may be at most odp_factor_project_max_len()
- * rows long (the caller checks; longer segments use odp_project +
- * odp_seg_factor).  Partial slots and pe layout are odp_seg_factor's.    */
+ * rows long (longer segments use odp_project + odp_seg_factor); a longer
+ * one that does not fit gets NaN partials and nothing else written.
+ * Partial slots and pe layout are odp_seg_factor's.                       */
 enum {
   ODP_FP_W = 13,    /* address of B [r][M] bf16 row-major                      */
   ODP_FP_U = 14     /* plane of U [k][ldq], bf16                              */
@@ -231,7 +232,8 @@ int odp_seg_factor_project(odp_stream_t stream, const int64_t* problems,
  * segment's 256-column tiles into that many groups of consecutive tiles,
  * one workgroup each (1 <= groups <= tiles; odp_seg_factor_stream_groups(M)
  * is the default): workgroups per problem = n_seg * groups.  Segments may
- * be at most odp_factor_project_max_len() rows long (the caller checks).  */
+ * be at most odp_factor_project_max_len() rows long; a longer one that
+ * does not fit gets NaN partials and nothing else written.               */
 enum { ODP_FT_GROUPS = 23 };
 int64_t odp_seg_factor_stream_groups(int64_t M);
 int odp_seg_factor_stream(odp_stream_t stream, const int64_t* problems,

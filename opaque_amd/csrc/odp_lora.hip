@@ -836,6 +836,19 @@ __device__ __forceinline__ void factor_pass_bf16(const int64_t* __restrict__ pro
         lslot[kb] = L.slot[q];
       }
   }
+  // A segment longer than FP_STEPS steps does not fit this pass (the host
+  // keeps segments within odp_factor_project_max_len()): its partial slots
+  // become NaN, so that its norm and clip factor show it, and nothing else
+  // is written.
+  if (len > 0 && (t_hi - t_lo + FP_T - 1) / FP_T > FP_STEPS) {
+    if (lane == 0)
+      for (int kb = 0; kb < NKB; ++kb)
+        if (lrank[kb] > 0)
+          for (int c = c_begin; c < c_end; ++c)
+            odp_gstore(part + (int64_t)ex * part_stride + lslot[kb] + ODP_FT_WAVE_SLOTS * c + wave,
+                       __builtin_nan(""));
+    return;
+  }
 
   // A chunk's rows (bf16) and this wave's norm partials wait in registers
   // and are stored after the next step's barrier: a barrier waits for every

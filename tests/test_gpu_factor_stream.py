@@ -160,3 +160,69 @@ def test_seam_products(shared):
     assert "planes" in live and not live & {"project", "factor_project", "factor"}, live
     keys = {t[1] for t in on.tables if t[0] == "factor_stream" and t[5] > 0}
     assert keys == ({1, 3} if shared else {1}), keys
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+@pytest.mark.parametrize("entry", ["stream", "fused"])
+def test_segment_past_the_limit_gets_nan_partials(entry):
+    """Called directly (the engine never does this) with a segment longer
+    than the single-pass kernels hold (odp_factor_project_max_len() rows
+    whatever the alignment; 17 steps of 64 rows from an 8-aligned start),
+    every partial slot of that example becomes NaN and the other segment's
+    slots are computed as usual."""
+    lib = N.load()
+    limit = int(lib.odp_factor_project_max_len())
+    lens = [limit + 8, 40]  # 1089 rows from row 0: 18 steps
+    starts = [0, limit + 1]
+    n_rows = sum(lens)
+    print(f"factor {entry}: segment of {lens[0]} rows (limit {limit})", flush=True)
+    M, r = 512, 16
+    ldq = (n_rows + 32 + 7) // 8 * 8
+    g = torch.Generator(device=DEV).manual_seed(9)
+    P = torch.randn(n_rows, M, device=DEV, generator=g).to(torch.bfloat16)
+    Q = torch.randn(32, ldq, device=DEV, generator=g).to(torch.bfloat16)  # rows 16.. are read, not used
+    W = torch.randn(r, M, device=DEV, generator=g).to(torch.bfloat16)
+    U = torch.zeros(32, ldq, device=DEV, dtype=torch.bfloat16)
+    pe = torch.zeros(2, r, M, device=DEV, dtype=torch.bfloat16)
+    tiles = int(lib.odp_seg_factor_tiles(N.DTYPE_BF16, M, r))
+    n_slots = N.FT_WAVE_SLOTS * tiles
+    part = torch.zeros(2, n_slots, device=DEV, dtype=torch.float64)
+    sst = torch.tensor(starts, device=DEV, dtype=torch.int32)
+    sln = torch.tensor(lens, device=DEV, dtype=torch.int32)
+    sex = torch.tensor([0, 1], device=DEV, dtype=torch.int32)
+    rows = []
+    for j in range(2):
+        row = [0] * N.FT_FIELDS
+        row[N.FT_P], row[N.FT_LDP], row[N.FT_M] = _ptr(P), M, M
+        row[N.FT_Q], row[N.FT_LDQ], row[N.FT_R] = _ptr(Q), ldq, r
+        row[N.FT_SEG_FIRST], row[N.FT_NSEG] = j, 1
+        row[N.FT_SCALING] = int(torch.tensor([2.0], dtype=torch.float64).view(torch.int64).item())
+        row[N.FT_NLEAF] = 1
+        row[N.FT_LEAF0] = _ptr(pe) + j * r * M * 2
+        row[N.FT_LEAF0 + 1] = 0 | (r << 16) | (1 << 32)
+        row[N.FT_LEAF0 + 2] = 0
+        if entry == "fused":
+            row[N.FP_W], row[N.FP_U] = _ptr(W), _ptr(U)
+        else:
+            row[N.FT_GROUPS] = int(lib.odp_seg_factor_stream_groups(M))
+        rows.append(row)
+    probs = torch.tensor(rows, dtype=torch.int64).view(-1).to(DEV)
+    per = 1 if entry == "fused" else int(lib.odp_seg_factor_stream_groups(M))
+    ws = torch.tensor([0, per, 2 * per], dtype=torch.int32, device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    if entry == "fused":
+        rc = lib.odp_seg_factor_project(s, _ptr(probs), _ptr(ws), 2, 2 * per, _ptr(sst), _ptr(sln), _ptr(sex),
+                                        _ptr(part), n_slots)
+    else:
+        rc = lib.odp_seg_factor_stream(s, _ptr(probs), _ptr(ws), 2, 2 * per, _ptr(sst), _ptr(sln), _ptr(sex),
+                                       _ptr(part), n_slots, 1)
+    N.check(rc, entry)
+    torch.cuda.synchronize()
+    assert torch.isnan(part[0]).all(), part[0]
+    assert torch.isfinite(part[1]).all() and (part[1] > 0).any(), part[1]
+    # The short segment's squared norm: the sum of squares of its stored rows.
+    want = pe[1].float().square().double().sum()
+    assert torch.allclose(part[1].sum(), want, rtol=1e-9), (part[1].sum(), want)
