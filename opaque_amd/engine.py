@@ -506,9 +506,10 @@ class GhostPlan:
     was built from stay alive and unchanged in shape.
 
     ``fuse_g_side``: LoRA sites take the single-pass kernels where they can
-    (results are bit-identical either way).  ``stream_factors``: one-leaf
-    bf16 factor problems of rank <= 16 take odp_seg_factor_stream instead
-    of odp_seg_factor (bit-identical).  ``linear_pe_bytes``: HBM for
+    (results are bit-identical either way).  ``stream_factors``: bf16
+    factor problems whose leaves each take a 16-row block of the rank plane
+    (rank <= 16, at most three blocks) take odp_seg_factor_stream instead of
+    odp_seg_factor (bit-identical).  ``linear_pe_bytes``: HBM for
     the stored per-example gradients of full-weight sites (bf16); None uses
     half of the free device memory, 0 stores none.  ``prescale_bytes``: at
     most this much of prescaled activations per clipped-sum chunk.
