@@ -882,7 +882,7 @@ __global__ __launch_bounds__(OUTER_THREADS, ODP_LIN_OCC) void k_lin_clip_sum(con
   const ODP_CONST double* csc = (const ODP_CONST double*)sc;
   auto scale = [&](const Step& st) { return (float)csc[cex[st.seg]]; };
   // PRESCALED: X already holds c_i x_t (odp_linear_prescale).
-  dma_mainloop<!PRESCALED, false, true>(P, o0, n0, at_segment(0), next, scale, fixup, acc);
+  dma_mainloop<!PRESCALED, true, true>(P, o0, n0, at_segment(0), next, scale, fixup, acc);
 
   // Lane holds D[4 (lane >> 4) + e][lane & 15] of each 16 x 16 block.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
