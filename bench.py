@@ -66,6 +66,12 @@ def parse_args():
     ap.add_argument("--second-moment", action="store_true",
                     help="c4: also sum the squared clipped per-example gradients (second_moment=True); "
                          "sites without stored gradients then take the moments kernel")
+    ap.add_argument("--mfma-calibration", action="store_true",
+                    help="only time the library's MFMA calibration kernel (no memory traffic, operands that "
+                         "change per MFMA) at 1, 2 and 4 waves per SIMD and print its rates")
+    ap.add_argument("--vendor-gemm", choices=["on", "off"], default="off",
+                    help="c4: also time the vendor GEMM library (torch.matmul / torch.bmm, hipBLASLt) on the same "
+                         "products, as a reference rate for the MFMA kernels")
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--cpu-layers", type=int, default=32,
                     help="layers of the CPU baseline sample (32: the whole C3 model, about 16 s per run on 16 "
@@ -127,6 +133,88 @@ def copy_calibration(nbytes):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": n * 4, "launches": 5}), flush=True)
+
+
+def mfma_calibration():
+    """Dense bf16 MFMA rate with no memory traffic (odp_calibrate_mfma).
+
+    One workgroup of 4 waves per CU puts one wave on each SIMD; 2 and 4 per
+    CU give 2 and 4 waves per SIMD (the full-weight kernels run 8 waves per
+    CU, 2 per SIMD).  Each launch runs about 5-20 ms.
+    """
+    from opaque_amd import _native as N
+
+    lib = N.load()
+    dev = torch.device("cuda", 0)
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev)
+    rows = []
+    for per_cu in (1, 2, 4):
+        wgs, iters = n_cu * per_cu, 20000
+        sink = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+        N.check(lib.odp_calibrate_mfma(stream.cuda_stream, wgs, 100, sink.data_ptr()), "odp_calibrate_mfma")
+        times = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            N.check(lib.odp_calibrate_mfma(stream.cuda_stream, wgs, iters, sink.data_ptr()), "odp_calibrate_mfma")
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        ms = sorted(times)[1]
+        tf = lib.odp_calibrate_mfma_flops(wgs, iters) / (ms * 1e-3) / 1e12
+        rows.append({"waves_per_simd": per_cu, "workgroups": wgs, "ms": ms, "tflops": tf,
+                     "frac_of_bf16_peak": tf / MI355X_BF16_PEAK_TFLOPS})
+    print(json.dumps({"mfma_calibration": rows, "peak_tflops": MI355X_BF16_PEAK_TFLOPS,
+                      "kernel": "k_mfma_calibrate (v_mfma_f32_16x16x32_bf16, 16 chains per wave, no memory)"}),
+          flush=True)
+
+
+def vendor_gemm(B, T, dev, reps=10):
+    """The vendor library's rate on C4's matrix products, per linear shape.
+
+    `clip_sum`: the clipped sum as one plain GEMM, X'^T G with X'^T stored
+    d_in x (B T) and G (B T) x d_out (torch.matmul, row-major operands in the
+    library's fastest NN layout); `per_example`: the B per-example products
+    X_s^T G_s (d_in x T times T x d_out) as one batched GEMM (torch.bmm,
+    contiguous operands), the matrix work of the outer-form norm without the
+    norm or the store.  Reference rates only: the DP step never calls these.
+    """
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    rows, tot = {}, {"clip_sum_ms": 0.0, "per_example_ms": 0.0, "flops": 0}
+    for name, (d_in, d_out) in LAYER_SHAPES.items():
+        fl = 2 * B * T * d_in * d_out
+        a = torch.randn(d_in, B * T, dtype=torch.bfloat16, device=dev, generator=g)
+        b = torch.randn(B * T, d_out, dtype=torch.bfloat16, device=dev, generator=g)
+        cs = timed(lambda: a @ b)
+        xa = a.view(d_in, B, T).permute(1, 0, 2).contiguous()
+        gb = b.view(B, T, d_out)
+        pe = timed(lambda: torch.bmm(xa, gb))
+        rows[name] = {"d_in": d_in, "d_out": d_out,
+                      "clip_sum_ms": cs, "clip_sum_tflops": fl / (cs * 1e-3) / 1e12,
+                      "per_example_ms": pe, "per_example_tflops": fl / (pe * 1e-3) / 1e12}
+        tot["clip_sum_ms"] += cs
+        tot["per_example_ms"] += pe
+        tot["flops"] += fl
+        del a, b, xa, gb
+    return {"library": "torch.matmul / torch.bmm (hipBLASLt), bf16 in, bf16 out, fp32 accumulate",
+            "per_linear": rows,
+            "clip_sum_tflops": tot["flops"] / (tot["clip_sum_ms"] * 1e-3) / 1e12,
+            "per_example_tflops": tot["flops"] / (tot["per_example_ms"] * 1e-3) / 1e12,
+            "clip_sum_frac": tot["flops"] / (tot["clip_sum_ms"] * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS,
+            "per_example_frac": tot["flops"] / (tot["per_example_ms"] * 1e-3) / 1e12 / MI355X_BF16_PEAK_TFLOPS}
 
 
 def build_workload(layers, B, T, r, seed, device):
@@ -465,6 +553,9 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
+    if args.mfma_calibration:
+        mfma_calibration()
+        return
 
     from opaque_amd import _native as N
     from opaque_amd.noise import add_noise_tree
@@ -586,6 +677,8 @@ def main():
         out["plan_rebind_ms"] = sorted(t_rb)[2]
         if args.dropin_overhead == "on":
             out["dropin_overhead"] = dropin_overhead(args, dev, ms)
+    if args.vendor_gemm == "on" and args.workload == "c4":
+        out["vendor_gemm"] = vendor_gemm(B, args.seq, dev)
     if args.cpu_baseline == "on" and args.workload == "c3":
         out["cpu_baseline"] = cpu_baseline(args.rank, args.seed, config["lengths"], args.cpu_layers, args.cpu_runs)
     print(json.dumps(out), flush=True)

@@ -532,6 +532,17 @@ int odp_philox_words(odp_stream_t stream, uint64_t ctr0, uint32_t ctr2, uint32_t
  * accuracy tests against a float64 erfinv.                               */
 int odp_noise_icdf(odp_stream_t stream, uint32_t k0, int64_t n, float* out);
 
+/* ---- measurement aid (no counterpart in the reference) --------------------
+ * The dense bf16 MFMA rate the GPU sustains with no memory traffic: each of
+ * `workgroups` workgroups of 4 waves runs 16 independent chains of
+ * v_mfma_f32_16x16x32_bf16 for `iters` rounds on operands that change from
+ * one MFMA to the next, and writes one float per thread to sink
+ * [workgroups * 256].  odp_calibrate_mfma_flops gives the launch's flops.
+ * Used by bench.py to read the full-weight kernels' rates against what the
+ * chip holds under a full MFMA load, beside the published peak.           */
+int odp_calibrate_mfma(odp_stream_t stream, int32_t workgroups, int32_t iters, float* sink);
+int64_t odp_calibrate_mfma_flops(int32_t workgroups, int32_t iters);
+
 /* ---- library -------------------------------------------------------------- */
 int odp_abi_version(void);
 const char* odp_last_error(void);

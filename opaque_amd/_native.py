@@ -105,6 +105,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _c_u64, _c_u32, _c_i32, _c_i32, _c_f64, _c_f64]),
     "odp_philox_words": (_c_int, [_ptr, _c_u64, _c_u32, _c_u32, _c_u64, _c_i64, _ptr]),
     "odp_noise_icdf": (_c_int, [_ptr, _c_u32, _c_i64, _ptr]),
+    "odp_calibrate_mfma": (_c_int, [_ptr, _c_i32, _c_i32, _ptr]),
+    "odp_calibrate_mfma_flops": (_c_i64, [_c_i32, _c_i32]),
     "odp_linear_tiles": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64]),
     "odp_linear_prescale_blocks": (_c_i64, [_c_i64]),
     "odp_linear_prescale": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _ptr, _ptr, _c_i32, _c_i32]),

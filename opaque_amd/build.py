@@ -17,7 +17,8 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libopaque_dp.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["odp_abi.hip", "odp_lora.hip", "odp_clip.hip", "odp_noise.hip", "odp_linear.hip", "odp_moments.hip"]
+SOURCES = ["odp_abi.hip", "odp_lora.hip", "odp_clip.hip", "odp_noise.hip", "odp_linear.hip", "odp_moments.hip",
+           "odp_calib.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -172,6 +172,15 @@ def test_kernel_argument_checks(lib):
     _err(lib, lib.odp_linear_clipped_sum(None, None, None, 0, 0, None, None, None, None, 1, 1, -1.0, 0),
          N.ERR_INVALID_ARGUMENT, "normalize_by must be > 0")
     _err(lib, lib.odp_philox_words(None, 0, 0, 0, 0, -1, None), N.ERR_INVALID_ARGUMENT, "bad n")
+    _err(lib, lib.odp_calibrate_mfma(None, 0, 1, _BAD), N.ERR_INVALID_ARGUMENT, "workgroups (0)")
+    _err(lib, lib.odp_calibrate_mfma(None, 1, 1 << 25, _BAD), N.ERR_INVALID_ARGUMENT, "iters")
+    _err(lib, lib.odp_calibrate_mfma(None, 1, 1, None), N.ERR_INVALID_ARGUMENT, "null sink")
+
+
+def test_calibration_flops(lib):
+    # 4 waves x 16 chains x one 16x16x32 MFMA (16384 flops) per round.
+    assert lib.odp_calibrate_mfma_flops(1, 1) == 4 * 16 * 16384
+    assert lib.odp_calibrate_mfma_flops(512, 1000) == 512 * 1000 * 4 * 16 * 16384
 
 
 def test_clip_factor_argument_checks(lib):
