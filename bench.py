@@ -102,10 +102,10 @@ def kernel_label(stage, key):
     if stage == "factor_stream":  # keyed by rank blocks
         return f"k_factor_stream_bf16<{key}>"
     dt, nkb = key
-    base = {"project": "k_project", "factor": "k_factor"}[stage]
+    base = {"project": "k_project_stream", "factor": "k_factor"}[stage]
     if dt == torch.bfloat16:
         return f"{base}_bf16<{nkb}>"
-    return f"{base}_f32"
+    return f"{base.replace('_stream', '')}_f32"
 
 
 def committed_traffic(label, design_bytes):

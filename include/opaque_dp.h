@@ -136,11 +136,18 @@ int odp_pack_planes(odp_stream_t stream, const int64_t* problems, const int32_t*
                     const int32_t* seg_row_len);
 
 /* ---- odp_project: Q^T[k][row] = sum_j P[row][j] * W[k][j] --------------
- * The LoRA rank-space projections U = G B^T and V = X A for rows
- * [0, n_rows); rows outside the problem's segments get 0.  Only columns
- * k < r are written, as one plane [k][ldq] at ODP_PJ_Q in P's dtype (bf16
- * P: the fp32 sums rounded to bf16, as the reference's bf16 X A and
- * G B^T are).                                                           */
+ * The LoRA rank-space projections U = G B^T and V = X A for the rows of
+ * the problem's segments.  Only columns k < r are written, as one plane
+ * [k][ldq] at ODP_PJ_Q in P's dtype (bf16 P: the fp32 sums rounded to
+ * bf16, as the reference's bf16 X A and G B^T are).
+ * bf16 P: the workgroups walk the problem's covered rows (each segment
+ *   widened to whole 8-row groups, [start & ~7, ceil8(start + len)),
+ *   concatenated in segment order), odp_project_blocks(dtype, covered, r)
+ *   of them, covered = odp_project_covered_rows of the problem's segments
+ *   (n_rows also works: the surplus workgroups exit).  Rows of a covered
+ *   group outside the segments get their products too; other rows are not
+ *   written.
+ * f32 P: rows [0, n_rows) (pass n_rows); rows outside the segments get 0. */
 enum {
   ODP_PJ_P = 0,      /* address of P, row-major, ld = ODP_PJ_LDP elements     */
   ODP_PJ_LDP = 1,
@@ -155,6 +162,8 @@ enum {
   ODP_PJ_FIELDS = 12
 };
 int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r);
+/* Host arrays of one problem's segments (no device access). */
+int64_t odp_project_covered_rows(const int32_t* seg_row_start, const int32_t* seg_row_len, int32_t n_seg);
 /* Every problem of one table must have ceil(ODP_PJ_R / 16) == nkb (1..4). */
 int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,
                 const int32_t* work_start, int32_t n_prob, int32_t total_blocks,

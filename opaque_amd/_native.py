@@ -68,6 +68,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "odp_pack_factors_blocks": (_c_i64, [_c_i64]),
     "odp_pack_factors": (_c_int, [_ptr, _ptr, _ptr, _c_i32, _c_i32]),
     "odp_project_blocks": (_c_i64, [_c_int, _c_i64, _c_i32]),
+    "odp_project_covered_rows": (_c_i64, [_ptr, _ptr, _c_i32]),
     "odp_project": (_c_int, [_ptr, _c_int, _ptr, _ptr, _c_i32, _c_i32, _ptr, _ptr, _c_i32]),
     "odp_seg_factor_tiles": (_c_i64, [_c_int, _c_i64, _c_i32]),
     "odp_seg_factor": (

@@ -27,6 +27,11 @@ __device__ __forceinline__ float odp_round_bf16(float f) {
   return odp_bf2f(__builtin_bit_cast(uint16_t, (__bf16)f));
 }
 
+// s_waitcnt immediate: vmcnt <= n (0..63), lgkmcnt and expcnt not waited on.
+__host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
+  return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
+}
+
 // Largest p in [0, n) with start[p] <= x. `start` is non-decreasing with
 // start[0] == 0 and x < start[n].
 __device__ __forceinline__ int odp_find_problem(const int32_t* __restrict__ start, int n, int x) {

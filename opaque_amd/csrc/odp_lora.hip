@@ -24,28 +24,16 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 namespace {
 
-#ifndef ODP_PJ_KS
-#define ODP_PJ_KS 128  // contraction elements per bf16 project step
-#endif
-#ifndef ODP_PJ_DEPTH
-#define ODP_PJ_DEPTH 2  // project steps of P loads in flight per wave (1 or 2)
-#endif
 #ifndef ODP_FT_T
 #define ODP_FT_T 32  // tokens per bf16 factor step (a multiple of the MFMA K, 32)
 #endif
-#ifndef ODP_PJ_RPW_2
-#define ODP_PJ_RPW_2 3  // 16-row blocks per wave for two rank blocks (W re-read per workgroup)
-#endif
-#ifndef ODP_PJ_RPW_WIDE
-#define ODP_PJ_RPW_WIDE 2  // ... and for three or four
-#endif
 constexpr int PJ_ROWS = 64;   // rows per fp32 project workgroup (4 waves x 16)
-// bf16 projection: 16-row MFMA blocks per wave.  One block for rank <= 16
-// (two measured slower there); wider ranks re-read a larger W tile per
-// workgroup, so they take more rows per workgroup: three blocks per wave for
-// two rank blocks (C3 gate/up V: 0.60-0.63 -> 0.52-0.53 ms against two; four
-// slower), two for three rank blocks (three and four no faster).
-__host__ __device__ constexpr int pj_rpw(int nkb) { return nkb == 2 ? ODP_PJ_RPW_2 : nkb > 2 ? ODP_PJ_RPW_WIDE : 1; }
+// Workgroups per CU the compiler must fit registers for in k_factor_bf16:
+// each fits its LDS tiles that many times in 160 KB without spilling, and
+// the extra loads in flight measured 1-5 % faster (one rank block: no
+// difference, left to the compiler; three rank blocks: two workgroups, the
+// registers of a 256-wide tile without spills).
+__host__ __device__ constexpr int ft_min_blocks(int nkb) { return nkb == 2 ? 3 : nkb == 3 ? 2 : 1; }
 constexpr int FT_T = ODP_FT_T;
 constexpr int FT_M_F32 = 128; // M columns per fp32 factor workgroup
 
@@ -89,201 +77,6 @@ __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
 }
 
 // ---------------------------------------------------------------------------
-// Projection, bf16: MFMA 16x16x32 bf16 with fp32 accumulation.  Each wave
-// owns 16 rows and the full contraction.  P is read with fully coalesced
-// loads (each instruction covers 4 rows x 256 contiguous bytes) into
-// registers one step ahead, then written to a wave-private LDS tile from
-// which each lane picks its MFMA A operand (row lane & 15, 8 consecutive k).
-// W is staged through LDS once per workgroup per step.  All loads are
-// branch-free (clamped addresses, data zeroed when consumed).
-// ---------------------------------------------------------------------------
-// Workgroups per CU the compiler must fit registers for: each of these
-// fits its LDS tiles that many times in 160 KB without spilling, and the
-// extra loads in flight measured 1-5 % faster (one rank block of the factor
-// kernel: no difference, left to the compiler; three rank blocks: two
-// workgroups, the registers of a 256-wide tile without spills).
-__host__ __device__ constexpr int pj_min_blocks(int nkb) { return nkb == 1 ? 6 : nkb == 2 ? 2 : 1; }
-__host__ __device__ constexpr int ft_min_blocks(int nkb) { return nkb == 2 ? 3 : nkb == 3 ? 2 : 1; }
-
-template <int NKB>
-__global__ __launch_bounds__(256, pj_min_blocks(NKB)) void k_project_bf16(const int64_t* __restrict__ probs,
-                                                      const int32_t* __restrict__ ws, int n_prob,
-                                                      const int32_t* __restrict__ sstart,
-                                                      const int32_t* __restrict__ slen) {
-  // Pitch KS + 8 (272 bytes): its operand reads take two LDS passes, but the
-  // conflict-free lds_pitch(KS) measured no faster here (and fits six
-  // one-block workgroups per CU only with this one).
-  constexpr int KS = ODP_PJ_KS, WPITCH = KS + 8, PPITCH = KS + 8, RP = 16 * NKB;
-  constexpr int RB = pj_rpw(NKB), WR = 16 * RB;  // row blocks and rows per wave
-  constexpr int NPR = RB * KS / 32;  // P pieces per lane per step (4 rows x 16 lanes each)
-  constexpr int NW = (RP * (KS / 8) + 255) / 256;  // W pieces per thread per step
-  static_assert(KS % 128 == 0, "each P load covers 128 columns of 4 rows (16 lanes x 16 B per row)");
-  __shared__ __attribute__((aligned(16))) uint16_t wlds[2 * RP * WPITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t plds[4 * WR * PPITCH];
-  const int bid = blockIdx.x;
-  const int p = odp_find_problem(ws, n_prob, bid);
-  const int64_t* f = probs + (int64_t)p * ODP_PJ_FIELDS;
-  const uint16_t* P = (const uint16_t*)f[ODP_PJ_P];
-  const int64_t ldp = f[ODP_PJ_LDP], d = f[ODP_PJ_D];
-  const uint16_t* W = (const uint16_t*)f[ODP_PJ_W];
-  const int r = (int)f[ODP_PJ_R];
-  uint16_t* Q = (uint16_t*)f[ODP_PJ_Q];
-  const int64_t ldq = f[ODP_PJ_LDQ], n_rows = f[ODP_PJ_NROWS];
-  const int seg_first = (int)f[ODP_PJ_SEG_FIRST], n_seg = (int)f[ODP_PJ_NSEG];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row0 = (int64_t)(bid - ws[p]) * (4 * WR) + WR * wave;
-  // Lane i < WR tests row row0 + i; the wave shares the answers as a bit mask.
-  const int64_t test_row = row0 + (lane % WR);
-  const bool tvalid = test_row < n_rows &&
-                      odp_row_in_segments(test_row, sstart + seg_first, slen + seg_first, n_seg);
-  const uint64_t vmask = __ballot(tvalid && lane < WR);
-  if (!__syncthreads_or(vmask != 0 ? 1 : 0)) return;  // the whole block is padding
-
-  // Load mapping: instruction i covers rows 4(i % (4 RB)) + (lane >> 4),
-  // 16 lanes x 16 B per row, at column block i / (4 RB) of the step.
-  const int lr = lane >> 4, piece = lane & 15;
-  constexpr int NRL = 4 * RB;  // row groups of 4 per wave
-  const uint16_t* prow[NRL];
-  bool rowok[NRL];
-#pragma unroll
-  for (int i = 0; i < NRL; ++i) {
-    const int rl = 4 * i + lr;
-    rowok[i] = (vmask >> rl) & 1;
-    prow[i] = P + (rowok[i] ? row0 + rl : 0) * ldp;
-  }
-  uint16_t* pw = plds + wave * WR * PPITCH;
-  const int kq = (lane >> 4) * 8;
-  const int64_t nsteps = (d + KS - 1) / KS;
-
-  f32x4_t acc[RB][NKB];
-#pragma unroll
-  for (int b = 0; b < RB; ++b)
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) acc[b][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto load_p = [&](int64_t s, u32x4_t(&pr)[NPR]) {
-#pragma unroll
-    for (int i = 0; i < NPR; ++i) {
-      const int64_t k = s * KS + 128 * (i / NRL) + 8 * piece;
-      pr[i] = ld16(prow[i % NRL] + (k < d ? k : d - 8));
-    }
-  };
-  auto store_p = [&](int64_t s, const u32x4_t(&pr)[NPR]) {
-#pragma unroll
-    for (int i = 0; i < NPR; ++i) {
-      const int c = 128 * (i / NRL) + 8 * piece;
-      const bool ok = rowok[i % NRL] && s * KS + c < d;
-      *(u32x4_t*)&pw[(4 * (i % NRL) + lr) * PPITCH + c] = ok ? pr[i] : u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  auto load_w = [&](int64_t s, u32x4_t(&wr)[NW]) {
-#pragma unroll
-    for (int q = 0; q < NW; ++q) {
-      const int id = (tid + 256 * q) % (RP * (KS / 8));
-      const int row = id / (KS / 8), col = (id % (KS / 8)) * 8;
-      const int64_t k = s * KS + col;
-      wr[q] = ld16(W + (int64_t)(row < r ? row : 0) * d + (k < d ? k : d - 8));
-    }
-  };
-  auto store_w = [&](int b, int64_t s, const u32x4_t(&wr)[NW]) {
-#pragma unroll
-    for (int q = 0; q < NW; ++q) {
-      const int id = tid + 256 * q;
-      if (id < RP * (KS / 8)) {
-        const int row = id / (KS / 8), col = (id % (KS / 8)) * 8;
-        const bool ok = row < r && s * KS + col < d;
-        *(u32x4_t*)&wlds[(b * RP + row) * WPITCH + col] = ok ? wr[q] : u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  auto compute = [&](int b) {
-#pragma unroll
-    for (int i = 0; i < KS / 32; ++i) {
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const u32x4_t bv =
-            *(const u32x4_t*)&wlds[(b * RP + kb * 16 + (lane & 15)) * WPITCH + 32 * i + kq];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const u32x4_t av = *(const u32x4_t*)&pw[(16 * rb + (lane & 15)) * PPITCH + 32 * i + kq];
-          acc[rb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv), acc[rb][kb], 0, 0, 0);
-        }
-      }
-    }
-  };
-
-  // W of a step is issued before its P rows; prefetch indices are clamped to
-  // the last step instead of branching (surplus loads are discarded).
-  const int64_t last = nsteps - 1;
-#if ODP_PJ_DEPTH == 1
-  u32x4_t pr[NPR], wr[NW];
-  load_w(0, wr);
-  load_p(0, pr);
-  for (int64_t s = 0; s < nsteps; ++s) {
-    const int b = (int)(s & 1);
-    store_w(b, s, wr);
-    store_p(s, pr);
-    __syncthreads();
-    const int64_t nx = s + 1 < last ? s + 1 : last;
-    load_w(nx, wr);
-    load_p(nx, pr);
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-    compute(b);
-  }
-#else
-  // Two steps of P in flight: P(s+2) is issued while P(s+1) is still loading.
-  u32x4_t pa[NPR], pb[NPR], wr[NW];
-  load_w(0, wr);
-  load_p(0, pa);
-  load_p(1 < last ? 1 : last, pb);
-  for (int64_t s = 0; s < nsteps; s += 2) {
-    store_w(0, s, wr);
-    store_p(s, pa);
-    __syncthreads();
-    load_w(s + 1 < last ? s + 1 : last, wr);
-    load_p(s + 2 < last ? s + 2 : last, pa);
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-    compute(0);
-    if (s + 1 >= nsteps) break;
-    store_w(1, s + 1, wr);
-    store_p(s + 1, pb);
-    __syncthreads();
-    load_w(s + 2 < last ? s + 2 : last, wr);
-    load_p(s + 3 < last ? s + 3 : last, pb);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(1);
-  }
-#endif
-
-  // lane holds D[4*(lane>>4) + i][lane & 15] of each 16x16 block: 4
-  // consecutive rows of one rank column, which are 4 consecutive entries of
-  // that column's plane row, rounded to bf16 (the rank-space products of the
-  // reference's per-sample rule, X A and G B^T, are bf16 tensors) and stored
-  // as one 8-byte piece (2-byte stores cost these kernels several % of
-  // their time).  rb is a multiple of
-  // 4 and ldq (a multiple of 8) exceeds n_rows by at least 32, so a group
-  // that runs past n_rows stays inside the plane row; its rows past n_rows
-  // hold zero P rows (rowok), and no kernel reads plane entries of rows
-  // outside segments.
-#pragma unroll
-  for (int b = 0; b < RB; ++b) {
-    const int64_t rb = row0 + 16 * b + 4 * (lane >> 4);
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const int col = kb * 16 + (lane & 15);
-      if (col < r && rb < n_rows) {
-        uint32_t h[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = odp_f2bf(acc[b][kb][i]);
-        odp_gstore((u32x2_t*)(Q + (int64_t)col * ldq + rb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Projection, fp32 inputs: MFMA 16x16x4 f32.  Each wave owns 16 rows; each
 // lane loads 4 consecutive contraction elements and feeds them to 4 MFMAs
 // (MFMA q uses element q).
@@ -308,16 +101,18 @@ __global__ __launch_bounds__(256) void k_project_f32(const int64_t* __restrict__
   const int64_t my_row = row0 + (lane & 15);
   const bool valid = my_row < n_rows &&
                      odp_row_in_segments(my_row, sstart + seg_first, slen + seg_first, n_seg);
-  if (!__syncthreads_or(valid ? 1 : 0)) return;
+  // A block without segment rows reads nothing and stores its zeros.
+  const bool live = __syncthreads_or(valid ? 1 : 0) != 0;
   const int nkb = (r + 15) >> 4;
   const int kq = (lane >> 4) * 4;
   const float* prow = P + (valid ? my_row : 0) * ldp;
+  const int64_t dl = live ? d : 0;
 
   f32x4_t acc[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) acc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t k0 = kq; k0 < d; k0 += 16) {
+  for (int64_t k0 = kq; k0 < dl; k0 += 16) {
     const f32x4_t a = valid ? *(const f32x4_t*)(prow + k0) : f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -1111,6 +906,210 @@ __global__ __launch_bounds__(256, 2) void k_factor_stream_bf16(const int64_t* __
 }
 
 // ---------------------------------------------------------------------------
+// Projection, bf16: MFMA 16x16x32 bf16 with fp32 accumulation, the
+// contraction 32 columns at a time in order, with P and W moved by buffer
+// loads straight into a ring of LDS stages, PS_RING - 1 steps ahead of the
+// compute.  A workgroup owns
+// PS_ROWS = 256 rows, each wave 64 of them (four 16-row MFMA blocks), and
+// walks the contraction PS_KC = 64 columns per step.  Each wave loads, and
+// reads, only its own rows of P (1 KB = 8 rows per load); the step's W tile
+// (16 NKB rank rows) is loaded a quarter per wave, 4 bytes per lane.  Rows
+// outside the segments or past n_rows, rank rows past r and columns past d
+// get offsets past the buffers' ends, so they arrive as zeros and cost no
+// HBM traffic.  LDS rows are 128 bytes, unpadded, with 16-byte slot q of
+// row t at slot q ^ (t & 7): the operand reads (16 rows at one slot) then
+// run without bank conflicts.
+// ---------------------------------------------------------------------------
+constexpr int PS_ROWS = 256, PS_KC = 64;
+// Ring stages per rank block count: as many 32 KB steps of P in flight as
+// the 160 KB of LDS hold (one workgroup per CU).
+#ifndef ODP_PS_RING
+#define ODP_PS_RING 4
+#endif
+__host__ __device__ constexpr int ps_ring(int nkb) { return nkb <= 3 ? ODP_PS_RING : 3; }
+
+// One step: loads for a later step into `nxt`, then this step's MFMAs from
+// `cur`.  Both are restrict parameters of one inlined call, so that the
+// compiler's alias scopes keep the reads of `cur` from waiting for the loads
+// into `nxt`.
+template <int NKB, typename Issue>
+__device__ __forceinline__ void ps_step(uint16_t* __restrict__ nxt, const uint16_t* __restrict__ cur, Issue issue,
+                                        f32x4_t (&acc)[4][NKB]) {
+  constexpr int XT = PS_ROWS * PS_KC;
+  issue(nxt);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sw = lane & 7;  // t & 7 of every row this lane reads
+#pragma unroll
+  for (int h = 0; h < PS_KC / 32; ++h) {
+    const int q = 4 * h + (lane >> 4);
+    u32x4_t bv[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      bv[kb] = *(const u32x4_t*)&cur[XT + (16 * kb + (lane & 15)) * PS_KC + 8 * (q ^ sw)];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const u32x4_t av = *(const u32x4_t*)&cur[(64 * wave + 16 * rb + (lane & 15)) * PS_KC + 8 * (q ^ sw)];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        acc[rb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                              __builtin_bit_cast(bf16x8_t, bv[kb]), acc[rb][kb], 0,
+                                                              0, 0);
+    }
+  }
+}
+
+template <int NKB>
+__global__ __launch_bounds__(256, ps_ring(NKB) == 2 ? 2 : 1) void k_project_stream_bf16(
+    const int64_t* __restrict__ probs, const int32_t* __restrict__ ws, int n_prob,
+    const int32_t* __restrict__ sstart, const int32_t* __restrict__ slen) {
+  static_assert(NKB >= 1 && NKB <= 4, "one to four rank blocks");
+  constexpr int PS_RING = ps_ring(NKB);
+  static_assert(PS_RING >= 2 && PS_RING <= 4, "two to four ring stages");
+  constexpr int XT = PS_ROWS * PS_KC, STAGE = XT + 16 * NKB * PS_KC;
+  static_assert(PS_RING * STAGE * 2 <= 156 * 1024, "the ring fits in LDS");
+  constexpr int XD = PS_ROWS / 4 / 8;  // 1 KB loads of P per wave per step
+  constexpr int WD = 2 * NKB;          // 256-byte loads of W per wave per step
+  constexpr int NDMA = XD + WD;
+  static_assert(NDMA < 64, "vmcnt range");
+  constexpr uint32_t OOB = 0x80000000u;
+  __shared__ __attribute__((aligned(16))) uint16_t ps0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t ps1[STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t ps2[PS_RING > 2 ? STAGE : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t ps3[PS_RING > 3 ? STAGE : 8];
+  auto stage = [&](int k) -> uint16_t* { return k == 0 ? ps0 : k == 1 ? ps1 : k == 2 ? ps2 : ps3; };
+
+  const int bid = blockIdx.x;
+  const int p = odp_find_problem(ws, n_prob, bid);
+  const int64_t* f = probs + (int64_t)p * ODP_PJ_FIELDS;
+  const uint16_t* P = (const uint16_t*)f[ODP_PJ_P];
+  const int64_t ldp = f[ODP_PJ_LDP], d = f[ODP_PJ_D];
+  const uint16_t* W = (const uint16_t*)f[ODP_PJ_W];
+  const int r = (int)f[ODP_PJ_R];
+  uint16_t* Q = (uint16_t*)f[ODP_PJ_Q];
+  const int64_t ldq = f[ODP_PJ_LDQ], n_rows = f[ODP_PJ_NROWS];
+  const int seg_first = (int)f[ODP_PJ_SEG_FIRST], n_seg = (int)f[ODP_PJ_NSEG];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Rows: the problem's covered rows (each segment widened to whole 8-row
+  // groups, [start & ~7, ceil8(start + len)), concatenated in segment
+  // order) in blocks of PS_ROWS, so that padding between segments costs no
+  // workgroups.  Wave w takes groups 8 w .. 8 w + 7 of its block; lane j < 8
+  // finds the first row of group 8 w + j (-1 past the covered rows).  The
+  // walk over the segments is the same for every lane.
+  const int64_t v0 = (int64_t)(bid - ws[p]) * PS_ROWS;
+  int32_t gfirst = -1;
+  {
+    const int64_t v = v0 + 64 * wave + 8 * (lane & 7);
+    int64_t cum = 0;
+    for (int sg = 0; sg < n_seg && cum < v0 + PS_ROWS; ++sg) {
+      const int64_t st = sstart[seg_first + sg], ln = slen[seg_first + sg];
+      if (ln <= 0) continue;
+      const int64_t a = st & ~(int64_t)7, cov = ((st + ln + 7) & ~(int64_t)7) - a;
+      if (v >= cum && v < cum + cov) gfirst = (int32_t)(a + (v - cum));
+      cum += cov;
+    }
+  }
+  int32_t gb[XD];
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < XD; ++i) {
+    gb[i] = __builtin_amdgcn_readlane(gfirst, i);
+    any |= gb[i] >= 0;
+  }
+  // A block past the covered rows loads and stores nothing.
+  const bool live = __syncthreads_or(any ? 1 : 0) != 0;
+
+  // P: load i fills group i of the wave (8 rows of 128 bytes) through a
+  // buffer resource over the group's rows; lane l fills physical slot l & 7
+  // of row l / 8, which holds logical slot (l & 7) ^ (l / 8).
+  __amdgpu_buffer_rsrc_t prs[XD];
+#pragma unroll
+  for (int i = 0; i < XD; ++i) {
+    const int64_t rows = gb[i] < 0 ? 0 : (n_rows - gb[i] < 8 ? n_rows - gb[i] : 8);
+    prs[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(P + (gb[i] < 0 ? 0 : (int64_t)gb[i]) * ldp), (short)0,
+                                               rows > 0 ? (int)((uint32_t)rows * (uint32_t)ldp * 2u) : 0,
+                                               ODP_BUFFER_DWORD3);
+  }
+  const uint32_t xrow = (uint32_t)(lane >> 3) * (uint32_t)ldp * 2u;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)W, (short)0, (int)((uint32_t)r * (uint32_t)d * 2u), ODP_BUFFER_DWORD3);
+  const int xcol = 8 * ((lane & 7) ^ ((lane >> 3) & 7));
+  // W: load j covers rank rows 4 NKB wave + 2 j + lane / 32, 4 bytes per
+  // lane: word lane & 3 of physical slot (lane & 31) / 4.
+  uint32_t wrow[WD];
+  int wcol[WD];
+#pragma unroll
+  for (int j = 0; j < WD; ++j) {
+    const int k = 4 * NKB * wave + 2 * j + (lane >> 5);
+    wcol[j] = 8 * (((lane & 31) >> 2) ^ (k & 7));
+    wrow[j] = k < r ? (uint32_t)k * (uint32_t)d * 2u + 4u * (uint32_t)(lane & 3) : OOB;
+  }
+  // Loads of the step at column c0 (c0 >= d: none, every offset past the end).
+  auto issue = [&](uint16_t* st, int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < XD; ++i) {
+      const int64_t c = c0 + xcol;
+      const uint32_t off = c < d ? xrow + (uint32_t)c * 2u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(prs[i], (ODP_LDS void*)(st + (64 * wave + 8 * i) * PS_KC), 16, off,
+                                               0, 0, FP_G_NT);
+    }
+#pragma unroll
+    for (int j = 0; j < WD; ++j) {
+      const int64_t c = c0 + wcol[j];
+      const uint32_t off = wrow[j] != OOB && c < d ? wrow[j] + (uint32_t)c * 2u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (ODP_LDS void*)(st + XT + (4 * NKB * wave + 2 * j) * PS_KC), 4,
+                                               off, 0, 0, 0);
+    }
+  };
+
+  f32x4_t acc[4][NKB];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc[b][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int64_t nsteps = live ? (d + PS_KC - 1) / PS_KC : 0;
+#pragma unroll
+  for (int q = 0; q < PS_RING - 1; ++q)
+    if (live) issue(stage(q), q < nsteps ? q * PS_KC : d);
+  for (int64_t s = 0; s < nsteps;) {
+#pragma unroll
+    for (int k = 0; k < PS_RING; ++k) {
+      if (s >= nsteps) break;
+      // This step's loads (this wave's) have landed; the later ones may fly.
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((PS_RING - 2) * NDMA));
+      __asm__ volatile("s_barrier" ::: "memory");
+      const int64_t nx = s + PS_RING - 1;
+      const int64_t c0 = nx < nsteps ? nx * PS_KC : d;
+      ps_step<NKB>(stage((k + PS_RING - 1) % PS_RING), stage(k), [&](uint16_t* st) { issue(st, c0); }, acc);
+      ++s;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load into LDS may outlive the workgroup
+
+  // 4 consecutive rows of one rank column per lane (rows 4 (lane / 16) ..
+  // + 3 of block b: half of group 2 b + lane / 32), which are 4 consecutive
+  // entries of that column's plane row, rounded to bf16 (the rank-space
+  // products of the reference's per-sample rule, X A and G B^T, are bf16
+  // tensors) and stored as one 8-byte piece.  ldq exceeds n_rows by at
+  // least 32, so a piece that starts below n_rows stays inside the plane.
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int32_t g0 = (lane >> 5) ? gb[2 * b + 1] : gb[2 * b];
+    const int64_t rb = g0 < 0 ? n_rows : (int64_t)g0 + 4 * ((lane >> 4) & 1);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int col = kb * 16 + (lane & 15);
+      if (col < r && rb < n_rows) {
+        uint32_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = odp_f2bf(acc[b][kb][i]);
+        odp_gstore((u32x2_t*)(Q + (int64_t)col * ldq + rb), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Factor gradients, fp32 P: MFMA 16x16x4 f32 with K = 16 tokens per step in
 // four MFMAs; operands come straight from global memory (P rows are read
 // 64 bytes per 16 lanes, which coalesces).
@@ -1321,8 +1320,19 @@ extern "C" int odp_pack_planes(odp_stream_t stream, const int64_t* problems, con
   return odp_check_launch("odp_pack_planes");
 }
 
+extern "C" int64_t odp_project_covered_rows(const int32_t* seg_row_start, const int32_t* seg_row_len,
+                                            int32_t n_seg) {
+  int64_t cov = 0;
+  for (int32_t s = 0; s < n_seg; ++s) {
+    const int64_t st = seg_row_start[s], ln = seg_row_len[s];
+    if (ln > 0) cov += ((st + ln + 7) & ~(int64_t)7) - (st & ~(int64_t)7);
+  }
+  return cov;
+}
+
 extern "C" int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r) {
-  const int64_t rows = dtype == ODP_DTYPE_BF16 ? 64 * pj_rpw((r + 15) / 16) : PJ_ROWS;
+  (void)r;
+  const int64_t rows = dtype == ODP_DTYPE_BF16 ? PS_ROWS : PJ_ROWS;
   return n_rows <= 0 ? 0 : (n_rows + rows - 1) / rows;
 }
 
@@ -1354,10 +1364,10 @@ extern "C" int odp_project(odp_stream_t stream, int dtype, const int64_t* proble
   const dim3 grid(total_blocks), block(256);
   if (dtype == ODP_DTYPE_BF16) {
     switch (nkb) {
-      case 1: hipLaunchKernelGGL(k_project_bf16<1>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
-      case 2: hipLaunchKernelGGL(k_project_bf16<2>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
-      case 3: hipLaunchKernelGGL(k_project_bf16<3>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
-      default: hipLaunchKernelGGL(k_project_bf16<4>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      case 1: hipLaunchKernelGGL(k_project_stream_bf16<1>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      case 2: hipLaunchKernelGGL(k_project_stream_bf16<2>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      case 3: hipLaunchKernelGGL(k_project_stream_bf16<3>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
+      default: hipLaunchKernelGGL(k_project_stream_bf16<4>, grid, block, 0, s, problems, work_start, n_prob, seg_row_start, seg_row_len); break;
     }
   } else {
     hipLaunchKernelGGL(k_project_f32, grid, block, 0, s, problems, work_start, n_prob,

@@ -29,11 +29,6 @@ __device__ __forceinline__ v4i16_t lds_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((ODP_LDS v4i16_t*)(ODP_LDS void*)p);
 }
 
-// s_waitcnt immediate: vmcnt <= n (0..63), lgkmcnt and expcnt not waited on.
-__host__ __device__ constexpr uint32_t vmcnt_imm(int n) {
-  return (uint32_t)(n & 15) | ((uint32_t)(n >> 4) << 14) | 0x0F70u;
-}
-
 // Whether local segment sg (len rows) of problem f may overflow float32 in
 // the Gram or clipped-sum forms: with a = max|x| and b = max|g| over the
 // segment's finite entries (odp_nonfinite_columns), a b max(L, sqrt(d_in

@@ -106,6 +106,11 @@ class Segments:
         return cls([i * seq_len for i in range(n_ex)], lens, list(range(n_ex)), n_ex, n_ex * seq_len)
 
 
+def _pj_rows(dt: torch.dtype, v: "_SegView") -> int:
+    """The rows odp_project's workgroups walk: the covered rows for bf16, all rows for f32."""
+    return v.covered if dt == torch.bfloat16 else v.n_rows
+
+
 @dataclass
 class _SegView:
     """A segment list as laid out in the plan's device segment arrays."""
@@ -128,6 +133,12 @@ class _SegView:
     @property
     def max_len(self) -> int:
         return max(self.segs.lengths, default=0)
+
+    @property
+    def covered(self) -> int:
+        """Rows of the segments widened to whole 8-row groups (odp_project_covered_rows)."""
+        return int(sum(((st + ln + 7) & ~7) - (st & ~7)
+                       for st, ln in zip(self.segs.starts, self.segs.lengths) if ln > 0))
 
 
 class _SegRegistry:
@@ -899,7 +910,7 @@ class GhostPlan:
                         N.PJ_Q: qaddr(vbase, 0),
                         N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                     },
-                    lib.odp_project_blocks(dtype_code(dt), n_rows, rtot),
+                    lib.odp_project_blocks(dtype_code(dt), _pj_rows(dt, v), rtot),
                     (valid * d_in + rtot * d_in + planes * rtot * valid) * es, 2 * valid * d_in * rtot,
                     io=valid * d_in * es,
                 )
@@ -960,7 +971,7 @@ class GhostPlan:
                             N.PJ_Q: qaddr(ubase, c0),
                             N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
                         },
-                        lib.odp_project_blocks(dtype_code(dt), n_rows, r),
+                        lib.odp_project_blocks(dtype_code(dt), _pj_rows(dt, v), r),
                         (valid * d_out + r * d_out + planes * r * valid) * es, 2 * valid * d_out * r,
                         io=valid * d_out * es,
                     )
@@ -1629,7 +1640,7 @@ class GhostPlan:
                 N.PJ_Q: qaddr(ubase, 0),
                 N.PJ_LDQ: ldq, N.PJ_NROWS: n_rows, N.PJ_SEG_FIRST: sf, N.PJ_NSEG: n_seg,
             },
-            lib.odp_project_blocks(dtype_code(dt), n_rows, r),
+            lib.odp_project_blocks(dtype_code(dt), _pj_rows(dt, v), r),
             (valid * d_out + r * d_out + planes * r * valid) * es, 2 * valid * d_out * r, io=valid * d_out * es,
         )
         # V = X A and the dA^T rows (scaling * sum_t U[k][t] X[t][m]) in one

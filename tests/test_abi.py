@@ -177,6 +177,22 @@ def test_kernel_argument_checks(lib):
     _err(lib, lib.odp_calibrate_mfma(None, 1, 1, None), N.ERR_INVALID_ARGUMENT, "null sink")
 
 
+def test_project_covered_rows(lib):
+    import numpy as np
+
+    from opaque_amd.engine import Segments, _SegView
+
+    starts = np.asarray([3, 253, 266, 270, 1024], dtype=np.int32)
+    lens = np.asarray([250, 13, 0, 601, 8], dtype=np.int32)
+    # [0, 256) + [248, 272) + nothing + [264, 872) + [1024, 1032): 8-row groups, overlaps counted twice.
+    want = 256 + 24 + 608 + 8
+    got = lib.odp_project_covered_rows(starts.ctypes.data, lens.ctypes.data, len(starts))
+    assert got == want
+    view = _SegView(Segments(starts.tolist(), lens.tolist(), list(range(5)), 5, 1100), 0)
+    assert view.covered == want
+    assert lib.odp_project_covered_rows(None, None, 0) == 0
+
+
 def test_calibration_flops(lib):
     # 4 waves x 16 chains x one 16x16x32 MFMA (16384 flops) per round.
     assert lib.odp_calibrate_mfma_flops(1, 1) == 4 * 16 * 16384
