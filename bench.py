@@ -59,6 +59,9 @@ def parse_args():
     ap.add_argument("--linear-pe-gb", type=float, default=None,
                     help="c4: HBM for stored per-example weight gradients (default: free memory after "
                          "the inputs less 32 GiB; 0: clipped-sum GEMM for every site)")
+    ap.add_argument("--prescale-gb", type=float, default=8.0,
+                    help="c4: GiB of prescaled activations per clipped-sum chunk (0: the GEMM scales its operand "
+                         "tiles in registers instead)")
     ap.add_argument("--norm-form", choices=["auto", "rule"], default="auto",
                     help="c4: auto = the engine's choice (fewer flops at the measured kernel speeds, outer form "
                          "with stored gradients while the budget lasts); rule = Gram where T^2 < d_in*d_out, else "
@@ -517,7 +520,8 @@ def setup_c4(args, dev):
     clip = ClipSpec(mode=N.CLIP_FIXED, thresholds=thr, effective=math.sqrt(sum(v * v for v in thr)),
                     normalize_by=float(B), guards=[(rel, ab, torch.bfloat16)])
     plan = GhostPlan(segments=seg, leaves=leaves, clip=clip, linear_sites=lins, device=dev,
-                     linear_pe_bytes=pe_bytes, second_moment=args.second_moment)
+                     linear_pe_bytes=pe_bytes, second_moment=args.second_moment,
+                     prescale_bytes=int(args.prescale_gb * 2**30))
     # Algorithmic flops of the C4 step: per example and weight the cheaper
     # norm form, min(2 L d_in d_out, 2 L^2 (d_in + d_out)), plus the clipped
     # sum's 2 L d_in d_out, whichever kernels run.
@@ -535,6 +539,7 @@ def setup_c4(args, dev):
         "second_moment": args.second_moment,
         "norm_forms": {n: ("gram" if f == N.FORM_GRAM else "outer") for n, f in forms.items()} or "engine",
         "stored_per_example_gb": round(plan.lin_pe.numel() * 2 / 2**30, 1),
+        "prescale_gb": args.prescale_gb,
     }
     metric = "DP-SGD clip+noise examples/sec and % bf16 MFMA peak, Llama-3-8B full-weight per-example clipping"
     sigma = 1.0 * clip.effective / B
