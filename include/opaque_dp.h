@@ -162,7 +162,8 @@ enum {
   ODP_PJ_FIELDS = 12
 };
 int64_t odp_project_blocks(int dtype, int64_t n_rows, int32_t r);
-/* Host arrays of one problem's segments (no device access). */
+/* Host arrays of one problem's segments (no device access); -1 (and the
+ * error text) for null arrays with n_seg > 0. */
 int64_t odp_project_covered_rows(const int32_t* seg_row_start, const int32_t* seg_row_len, int32_t n_seg);
 /* Every problem of one table must have ceil(ODP_PJ_R / 16) == nkb (1..4). */
 int odp_project(odp_stream_t stream, int dtype, const int64_t* problems,

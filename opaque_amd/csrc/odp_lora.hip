@@ -1322,6 +1322,10 @@ extern "C" int odp_pack_planes(odp_stream_t stream, const int64_t* problems, con
 
 extern "C" int64_t odp_project_covered_rows(const int32_t* seg_row_start, const int32_t* seg_row_len,
                                             int32_t n_seg) {
+  if (n_seg > 0 && (seg_row_start == nullptr || seg_row_len == nullptr)) {
+    odp_set_error("odp_project_covered_rows: null segment arrays");
+    return -1;
+  }
   int64_t cov = 0;
   for (int32_t s = 0; s < n_seg; ++s) {
     const int64_t st = seg_row_start[s], ln = seg_row_len[s];

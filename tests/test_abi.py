@@ -191,6 +191,8 @@ def test_project_covered_rows(lib):
     view = _SegView(Segments(starts.tolist(), lens.tolist(), list(range(5)), 5, 1100), 0)
     assert view.covered == want
     assert lib.odp_project_covered_rows(None, None, 0) == 0
+    assert lib.odp_project_covered_rows(None, None, 2) == -1
+    assert "null segment arrays" in N.last_error()
 
 
 def test_calibration_flops(lib):
